@@ -1,0 +1,468 @@
+#!/usr/bin/env python3
+"""Per-op HBM bandwidth of the gfx950 tensor-op library on one MI355X.
+
+A step is one pass of the elementwise/broadcast batch on [4096, 1536]
+(configs[1]): add, mul, SiLU, fused SwiGLU, stride-0 bias add and cast, in
+f32 and f16, plus contiguous of a [1, 9, 4096, 64] transposed view and
+repeat_kv 3 -> 9 heads -- 16 kernel launches.  Inputs are resident in HBM
+before timing.  Each step uses the next of several buffer sets (>= 1 GiB in
+total, four times the 256 MB Infinity Cache) so that reads come from HBM,
+not from the cache.  Steps are replayed as recorded graphs and timed with
+stream events.
+
+GB/s = algorithmic bytes (inputs read once + outputs written once) / time.
+The JSON line's `value` is the whole step's aggregate; `per_op` lists each
+op, and the RMSNorm, softmax and decoder-layer shapes of the other configs
+are timed the same way as extra lines in `per_op`.
+
+    python bench.py [--steps K] [--warmup W] [--sets R] [--no-cpu] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from rustllm_amd import abi, synth  # noqa: E402
+
+PEAK_GBS = 8000.0
+METRIC = "achieved HBM GB/s & % of MI355X peak per op (RMSNorm, softmax, SwiGLU, RoPE)"
+F32, F16 = np.float32, np.float16
+T, H = 4096, 1536
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Op:
+    """One kernel launch on one buffer set: `launch(ctx, bufs)` and its bytes."""
+
+    def __init__(self, name, dtype, shape, nbytes, launch):
+        self.name, self.dtype, self.shape, self.nbytes, self.launch = (name, dtype, shape, nbytes,
+                                                                       launch)
+
+
+def config2_inputs(seed_tag: str):
+    """Host arrays of configs[1] (N(0,1) values)."""
+    arrs = {}
+    for dt in (F32, F16):
+        tag = np.dtype(dt).name
+        arrs[f"a_{tag}"] = synth.normal(synth.seed_for("c2", "a", tag, seed_tag), (T, H), 0, 1, dt)
+        arrs[f"b_{tag}"] = synth.normal(synth.seed_for("c2", "b", tag, seed_tag), (T, H), 0, 1, dt)
+        arrs[f"bias_{tag}"] = synth.normal(synth.seed_for("c2", "bias", tag, seed_tag), (H,), 0, 1,
+                                           dt)
+        arrs[f"view_{tag}"] = synth.normal(synth.seed_for("c2", "view", tag, seed_tag),
+                                           (1, 4096, 9, 64), 0, 1, dt)
+        arrs[f"kv_{tag}"] = synth.normal(synth.seed_for("c2", "kv", tag, seed_tag),
+                                         (1, 3, 4096, 64), 0, 1, dt)
+    return arrs
+
+
+VIEW_DIMS = [1, 9, 4096, 64]
+VIEW_STRIDES = [4096 * 9 * 64, 64, 9 * 64, 1]
+
+
+def config2_ops():
+    ops = []
+    n = T * H
+    for dt in (F32, F16):
+        tag = np.dtype(dt).name
+        es = np.dtype(dt).itemsize
+        sfx = "f16" if dt == F16 else "f32"
+
+        def mk(kind, tag=tag):
+            return lambda c, b: kind(c, b, tag)
+
+        ops.append(Op(f"add_{sfx}", sfx, [T, H], 3 * n * es,
+                      mk(lambda c, b, t: c.add(b[f"a_{t}"], b[f"b_{t}"], b[f"o1_{t}"]))))
+        ops.append(Op(f"mul_{sfx}", sfx, [T, H], 3 * n * es,
+                      mk(lambda c, b, t: c.mul(b[f"a_{t}"], b[f"b_{t}"], b[f"o2_{t}"]))))
+        ops.append(Op(f"silu_{sfx}", sfx, [T, H], 2 * n * es,
+                      mk(lambda c, b, t: c.silu(b[f"a_{t}"], b[f"o3_{t}"]))))
+        ops.append(Op(f"swiglu_{sfx}", sfx, [T, H], 3 * n * es,
+                      mk(lambda c, b, t: c.swiglu(b[f"a_{t}"], b[f"b_{t}"], b[f"o4_{t}"]))))
+        ops.append(Op(f"add_broadcast_{sfx}", sfx, [T, H], 2 * n * es + H * es,
+                      mk(lambda c, b, t: c.add_broadcast(b[f"a_{t}"], b[f"bias_{t}"],
+                                                         b[f"o5_{t}"]))))
+    ops.append(Op("cast_f32_to_f16", "f32->f16", [T, H], n * 6,
+                  lambda c, b: c.cast(b["a_float32"], F16, b["cast_h"])))
+    ops.append(Op("cast_f16_to_f32", "f16->f32", [T, H], n * 6,
+                  lambda c, b: c.cast(b["a_float16"], F32, b["cast_f"])))
+    nv = 9 * 4096 * 64
+    nkv = 3 * 4096 * 64
+    for dt in (F32, F16):
+        tag = np.dtype(dt).name
+        es = np.dtype(dt).itemsize
+        sfx = "f16" if dt == F16 else "f32"
+        ops.append(Op(f"contiguous_{sfx}", sfx, VIEW_DIMS, 2 * nv * es,
+                      lambda c, b, t=tag: c.contiguous(b[f"view_{t}"], VIEW_DIMS, VIEW_STRIDES,
+                                                       b[f"vo_{t}"])))
+        ops.append(Op(f"repeat_kv_{sfx}", sfx, [1, 3, 4096, 64], (nkv + 3 * nkv) * es,
+                      lambda c, b, t=tag: c.repeat_kv(b[f"kv_{t}"], 3, b[f"kvo_{t}"])))
+    return ops
+
+
+def config2_set(ctx, host):
+    """Device buffers of one set: the inputs plus one output per op."""
+    b = {k: ctx.upload(v) for k, v in host.items()}
+    for dt in (F32, F16):
+        tag = np.dtype(dt).name
+        for i in range(1, 6):
+            b[f"o{i}_{tag}"] = ctx.empty((T, H), dt)
+        b[f"vo_{tag}"] = ctx.empty(VIEW_DIMS, dt)
+        b[f"kvo_{tag}"] = ctx.empty((1, 9, 4096, 64), dt)
+    b["cast_h"] = ctx.empty((T, H), F16)
+    b["cast_f"] = ctx.empty((T, H), F32)
+    return b
+
+
+def set_bytes(b) -> int:
+    return sum(v.byte_len for v in b.values())
+
+
+def time_graphs(ctx, graphs, launches_per_graph, reps, warmup=2):
+    """Replays `graphs` round-robin `reps` times; returns ms per launch."""
+    for i in range(warmup):
+        ctx.graph_launch(graphs[i % len(graphs)])
+    ctx.finish()
+    start, end = ctx.event(), ctx.event()
+    ctx.record(start)
+    for i in range(reps):
+        ctx.graph_launch(graphs[i % len(graphs)])
+    ctx.record(end)
+    ms = ctx.elapsed_ms(start, end)
+    ctx.destroy_event(start)
+    ctx.destroy_event(end)
+    return ms / (reps * launches_per_graph)
+
+
+def capture(ctx, fn):
+    ctx.capture_begin()
+    try:
+        fn()
+    finally:
+        g = ctx.capture_end()
+    return g
+
+
+def per_op_rows(ctx, ops, sets, reps):
+    """Each op alone: a graph of len(sets) launches (one per buffer set) replayed."""
+    rows = []
+    for op in ops:
+        graph = capture(ctx, lambda: [op.launch(ctx, s) for s in sets])
+        ms = time_graphs(ctx, [graph], len(sets), reps)
+        ctx.graph_destroy(graph)
+        gbs = op.nbytes / (ms * 1e-3) / 1e9
+        rows.append({"op": op.name, "dtype": op.dtype, "shape": op.shape, "bytes": op.nbytes,
+                     "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                     "pct_peak": round(100 * gbs / PEAK_GBS, 1)})
+        log(f"  {op.name:24s} {str(op.shape):22s} {ms * 1e3:9.2f} us {gbs:8.1f} GB/s "
+            f"({100 * gbs / PEAK_GBS:5.1f}%)")
+    return rows
+
+
+# ----------------------------------------------------- other configs' shapes
+
+def extra_rows(ctx, reps, quick):
+    """RMSNorm, scale/mask + softmax and the decoder
+    layer chain -- same method, rotated buffer sets."""
+    rows = []
+
+    def measure(name, dtype, shape, nbytes, make_set, launch, nsets):
+        sets = [make_set(i) for i in range(nsets)]
+        graph = capture(ctx, lambda: [launch(s) for s in sets])
+        ms = time_graphs(ctx, [graph], nsets, reps)
+        ctx.graph_destroy(graph)
+        del sets
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append({"op": name, "dtype": dtype, "shape": shape, "bytes": nbytes,
+                     "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                     "pct_peak": round(100 * gbs / PEAK_GBS, 1)})
+        log(f"  {name:24s} {str(shape):22s} {ms * 1e3:9.2f} us {gbs:8.1f} GB/s "
+            f"({100 * gbs / PEAK_GBS:5.1f}%)")
+
+    def nsets_for(footprint):
+        return int(min(64, max(4, -(-(1 << 30) // max(footprint, 1)))))
+
+    tokens_list = [4096, 16384] if quick else [1, 16, 256, 4096, 16384]
+    for dt in (F32, F16):
+        es = np.dtype(dt).itemsize
+        sfx = "f16" if dt == F16 else "f32"
+        for hidden in (576, 768, 960):
+            w = ctx.upload(synth.uniform_range(synth.seed_for("w", hidden), (hidden,), 0.5, 1.5,
+                                               dt))
+            for tokens in tokens_list:
+                x = synth.normal(synth.seed_for("rms", tokens, hidden, sfx), (tokens, hidden), 0,
+                                 2.0, dt)
+                nbytes = tokens * hidden * 2 * es + hidden * es
+                measure(f"rmsnorm_{sfx}", sfx, [tokens, hidden], nbytes,
+                        lambda i, x=x, tokens=tokens, hidden=hidden, dt=dt:
+                        (ctx.upload(x), ctx.empty((tokens, hidden), dt)),
+                        lambda s, w=w: ctx.rmsnorm(s[0], w, 1e-5, s[1]),
+                        nsets_for(x.nbytes * 2))
+
+    # prefill [9, 2048, 2048] causal, scale 1/8; decode [9, 1, 2048]
+    def logits(shape, dt=F32):
+        x = synth.normal(synth.seed_for("logits", *shape), shape, 0, 4.0, F32)
+        u = synth.uniform(synth.seed_for("spike", *shape), x.size).reshape(shape)
+        x[u < 0.01] = 20.0
+        return x.astype(dt)
+
+    pre = logits((9, 2048, 2048))
+    n = pre.size
+    unmasked = 9 * (2048 * 2049 // 2)
+    for name, nbytes, fn in [
+        ("attention_softmax_f32", unmasked * 4 + n * 4,
+         lambda s: ctx.attention_softmax(s[0], 0.125, 0, s[1])),
+        ("attention_scale_mask_f32", unmasked * 4 + n * 4,
+         lambda s: ctx.scale_mask(s[0], 0.125, 0, s[1])),
+        ("softmax_f32", 2 * n * 4, lambda s: ctx.softmax(s[0], s[1])),
+    ]:
+        measure(name, "f32", [9, 2048, 2048], nbytes,
+                lambda i: (ctx.upload(pre), ctx.empty(pre.shape, F32)), fn,
+                nsets_for(2 * pre.nbytes))
+    dec = logits((9, 1, 2048))
+    measure("attention_softmax_f32", "f32", [9, 1, 2048], 2 * dec.size * 4,
+            lambda i: (ctx.upload(dec), ctx.empty(dec.shape, F32)),
+            lambda s: ctx.attention_softmax(s[0], 0.125, 2047, s[1]), 16)
+
+    # SmolLM2-360M layer, f16, 4096 tokens
+    hid, qh, kvh, hd, ffn, tok = 960, 15, 5, 64, 2560, 4096
+    c, s_ = _rope_table(hd, tok)
+    dc, ds = ctx.upload(c), ctx.upload(s_)
+    wn = ctx.upload(synth.uniform_range(1, (hid,), 0.5, 1.5, F16))
+    x = synth.normal(synth.seed_for("c5", "x"), (tok, hid), 0, 1, F16)
+    measure("c5.1 rmsnorm_f16", "f16", [tok, hid], tok * hid * 4 + hid * 2,
+            lambda i: (ctx.upload(x), ctx.empty((tok, hid), F16)),
+            lambda s: ctx.rmsnorm(s[0], wn, 1e-5, s[1]), 16)
+    for heads, label in ((qh, "Q"), (kvh, "K")):
+        proj = synth.normal(synth.seed_for("c5", label), (1, tok, heads, hd), 0, 1, F16)
+        dims, strides = [1, heads, tok, hd], [tok * heads * hd, hd, heads * hd, 1]
+        nbytes = 2 * proj.size * 2
+        measure(f"c5.2 rope_{label}_f16 (fused gather)", "f16", dims, nbytes,
+                lambda i, proj=proj, dims=dims: (ctx.upload(proj), ctx.empty(dims, F16)),
+                lambda s, dims=dims, strides=strides: ctx.rope_strided(s[0], dims, strides, dc,
+                                                                        ds, 0, s[1]), 16)
+        cont = np.ascontiguousarray(proj.transpose(0, 2, 1, 3))
+        measure(f"c5.2 rope_{label}_f16", "f16", list(cont.shape), nbytes,
+                lambda i, cont=cont: (ctx.upload(cont), ctx.empty(cont.shape, F16)),
+                lambda s: ctx.rope(s[0], dc, ds, 0, s[1]), 16)
+    kv = synth.normal(synth.seed_for("c5", "kv"), (1, kvh, tok, hd), 0, 1, F16)
+    measure("c5.3 repeat_kv_f16", "f16", [1, kvh, tok, hd], (kv.size + 3 * kv.size) * 2,
+            lambda i: (ctx.upload(kv), ctx.empty((1, qh, tok, hd), F16)),
+            lambda s: ctx.repeat_kv(s[0], 3, s[1]), 16)
+    if not quick:
+        rng = np.random.default_rng(5)
+        sc = rng.standard_normal((qh, tok, tok), dtype=np.float32).astype(F16)
+        n = sc.size
+        unm = qh * (tok * (tok + 1) // 2)
+        measure("c5.4 attention_softmax_f16", "f16", [qh, tok, tok], unm * 2 + n * 2,
+                lambda i: (ctx.upload(sc), ctx.empty(sc.shape, F16)),
+                lambda s: ctx.attention_softmax(s[0], 0.125, 0, s[1]), 3)
+        del sc
+    g = synth.normal(synth.seed_for("c5", "g"), (tok, ffn), 0, 1, F16)
+    u = synth.normal(synth.seed_for("c5", "u"), (tok, ffn), 0, 1, F16)
+    measure("c5.5 swiglu_f16", "f16", [tok, ffn], 3 * g.size * 2,
+            lambda i: (ctx.upload(g), ctx.upload(u), ctx.empty(g.shape, F16)),
+            lambda s: ctx.swiglu(s[0], s[1], s[2]), 8)
+    r = synth.normal(synth.seed_for("c5", "r"), (tok, hid), 0, 1, F16)
+    measure("c5.6 residual add_f16", "f16", [tok, hid], 3 * r.size * 2,
+            lambda i: (ctx.upload(x), ctx.upload(r), ctx.empty(r.shape, F16)),
+            lambda s: ctx.add(s[0], s[1], s[2]), 16)
+    # configs[0] shape, fused add + RMSNorm (writes the sum and the norm)
+    x0 = synth.normal(1, (64, 768), 0, 1, F32)
+    w0 = ctx.upload(synth.uniform_range(2, (768,), 0.5, 1.5, F32))
+    measure("add_rmsnorm_f32", "f32", [64, 768], 64 * 768 * 4 * 4 + 768 * 4,
+            lambda i: (ctx.upload(x0), ctx.upload(x0), ctx.empty(x0.shape, F32),
+                       ctx.empty(x0.shape, F32)),
+            lambda s: ctx.add_rmsnorm(s[0], s[1], w0, 1e-5, s[2], s[3]), 16)
+    return rows
+
+
+def _rope_table(head_dim, max_seq, theta=10000.0):
+    """RotaryEmbedding::new's table (nn/rope.rs:44-62) in float32."""
+    half = head_dim // 2
+    pos = np.arange(max_seq, dtype=np.float32)[:, None]
+    expo = (2 * np.arange(half, dtype=np.float32)) / np.float32(head_dim)
+    inv = np.float32(1.0) / np.power(np.float32(theta), expo, dtype=np.float32)
+    ang = (pos * inv[None, :]).astype(np.float32)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+# --------------------------------------------------------------- CPU leg
+
+def cpu_baseline(host, budget_s: float):
+    """The oracle (scalar C restatement of the reference ops, 1 thread) on
+    whole configs[1] steps until `budget_s` seconds of CPU work have run."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as o
+
+    o.set_threads(1)
+    a32, b32, a16, b16 = host["a_float32"], host["b_float32"], host["a_float16"], host["b_float16"]
+    outs = {}
+
+    def step():
+        for t, a, b in (("float32", a32, b32), ("float16", a16, b16)):
+            outs[f"add_{t}"] = o.add(a, b)
+            outs[f"mul_{t}"] = o.mul(a, b)
+            outs[f"silu_{t}"] = o.silu(a)
+            outs[f"swiglu_{t}"] = o.swiglu(a, b)
+            outs[f"bias_{t}"] = o.add_broadcast(a, host[f"bias_{t}"])
+            outs[f"view_{t}"] = o.contiguous(host[f"view_{t}"].ravel(), VIEW_DIMS, VIEW_STRIDES)
+            outs[f"kv_{t}"] = o.repeat_kv(host[f"kv_{t}"], 3)
+        outs["cast_h"] = o.cast(a32, F16)
+        outs["cast_f"] = o.cast(a16, F32)
+
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        step()
+        steps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    elapsed = time.perf_counter() - t0
+    return steps, elapsed, outs
+
+
+def check_outputs(ctx, dev, outs) -> list[str]:
+    """Compares the first buffer set's outputs with the oracle's; returns failures."""
+    bad = []
+
+    def same(name, got, ref, exact=True):
+        if exact:
+            ok = np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+        elif got.dtype == np.float16:
+            gi = got.view(np.int16).astype(np.int32)
+            ri = ref.view(np.int16).astype(np.int32)
+            gi = np.where(gi < 0, -(gi & 0x7FFF), gi)
+            ri = np.where(ri < 0, -(ri & 0x7FFF), ri)
+            ok = int(np.max(np.abs(gi - ri))) <= 2
+        else:
+            ok = float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1.18e-38))) <= 1e-5
+        if not ok:
+            bad.append(name)
+
+    for t in ("float32", "float16"):
+        same(f"add_{t}", dev[f"o1_{t}"].numpy(), outs[f"add_{t}"])
+        same(f"mul_{t}", dev[f"o2_{t}"].numpy(), outs[f"mul_{t}"])
+        same(f"silu_{t}", dev[f"o3_{t}"].numpy(), outs[f"silu_{t}"], exact=False)
+        same(f"swiglu_{t}", dev[f"o4_{t}"].numpy(), outs[f"swiglu_{t}"], exact=False)
+        same(f"bias_{t}", dev[f"o5_{t}"].numpy(), outs[f"bias_{t}"])
+        same(f"contiguous_{t}", dev[f"vo_{t}"].numpy(), outs[f"view_{t}"])
+        same(f"repeat_kv_{t}", dev[f"kvo_{t}"].numpy(), outs[f"kv_{t}"])
+    same("cast_f32_to_f16", dev["cast_h"].numpy(), outs["cast_h"])
+    same("cast_f16_to_f32", dev["cast_f"].numpy(), outs["cast_f"])
+    return bad
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=4, help="buffer sets rotated across steps")
+    ap.add_argument("--op-reps", type=int, default=50, help="graph replays per op line")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
+    ap.add_argument("--quick", action="store_true", help="fewer extra shapes")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: every op runs on one MI355X and shards across GPUs "
+              "without any exchange, so no multi-GPU figure is produced (use --gpus 1).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    ctx = abi.Context(0)
+    host = config2_inputs("bench")
+    ops = config2_ops()
+    log(f"uploading {args.sets} buffer sets")
+    sets = [config2_set(ctx, host) for _ in range(args.sets)]
+    footprint = sum(set_bytes(s) for s in sets)
+    step_bytes = sum(op.nbytes for op in ops)
+    log(f"footprint {footprint / 2**30:.2f} GiB, {step_bytes / 1e6:.1f} MB per step")
+
+    graphs = [capture(ctx, lambda s=s: [op.launch(ctx, s) for op in ops]) for s in sets]
+    for i in range(args.warmup):
+        ctx.graph_launch(graphs[i % len(graphs)])
+    ctx.finish()
+    start, end = ctx.event(), ctx.event()
+    ctx.record(start)
+    for i in range(args.steps):
+        ctx.graph_launch(graphs[i % len(graphs)])
+    ctx.record(end)
+    ms_total = ctx.elapsed_ms(start, end)
+    ctx.finish()
+    ms_step = ms_total / args.steps
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"step: {ms_step * 1e3:.1f} us, {value:.1f} GB/s ({100 * value / PEAK_GBS:.1f}% of peak)")
+    for g in graphs:
+        ctx.graph_destroy(g)
+
+    log("per op (configs[1]):")
+    rows = per_op_rows(ctx, ops, sets, args.op_reps)
+    dominant = max(rows, key=lambda r: r["us"])
+    roofline = {"bound": "hbm", "kernel": dominant["op"], "achieved": dominant["GB/s"],
+                "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(dominant["GB/s"] / PEAK_GBS, 4),
+                "bytes_per_launch": dominant["bytes"], "us_per_launch": dominant["us"],
+                "traffic": None}
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"cpu baseline: oracle, 1 thread, ~{args.cpu_seconds:.0f} s of whole steps")
+        steps, elapsed, outs = cpu_baseline(host, args.cpu_seconds)
+        bad = check_outputs(ctx, sets[0], outs)
+        cpu_gbs = step_bytes * steps / elapsed / 1e9
+        cpu = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{steps} whole configs[1] steps (16 ops on [4096,1536] and the "
+                         f"view/KV shapes) in {elapsed:.1f} s",
+               "gpu_outputs_match_oracle": not bad}
+        if bad:
+            log(f"MISMATCH against the oracle: {bad}")
+        log(f"cpu: {cpu_gbs:.2f} GB/s over {steps} steps")
+
+    extra = [] if args.no_extra else extra_rows(ctx, max(5, args.op_reps // 5), args.quick)
+    del sets
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: elementwise+broadcast batch [4096,1536], f32 and "
+                               "f16 storage (add, mul, silu, swiglu, bias add, casts, "
+                               "contiguous [1,9,4096,64] view, repeat_kv 3->9)",
+                   "ops_per_step": len(ops), "bytes_per_step": step_bytes,
+                   "buffer_sets": args.sets, "footprint_gib": round(footprint / 2**30, 2)},
+        "pct_of_peak": round(100 * value / PEAK_GBS, 1),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_op": rows + extra,
+    }
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,289 @@
+/*
+ * rustllm_hip.h -- C ABI of the MI355X (gfx950) tensor-op library.
+ *
+ * This is the drop-in boundary under RustLLM's `src/ops` / `src/tensor`
+ * API: every entry point below replaces one Metal-side item of
+ * Lee-Dongwook/RustLLM, cited as file:line relative to that repository.
+ * The Rust side binds these with an `extern "C"` block and keeps its public
+ * signatures; the C++ mirror in rustllm_amd/host/ is the same layer
+ * restated in C++.
+ *
+ * Conventions
+ *  - Every fallible call returns an rl_status (0 = RL_OK).  The codes map
+ *    one-to-one onto the TinyError variants the op layer can raise
+ *    (src/error.rs:4-43); RL_ERR_DEVICE stands in for TinyError::Metal.
+ *    rl_last_error_message() returns the thread's message for the last
+ *    failure.
+ *  - Validation runs before anything is enqueued and has no side effects,
+ *    in the reference's order (e.g. src/ops/softmax.rs:91-108).  An op called
+ *    with ctx == NULL validates its arguments and then returns
+ *    RL_ERR_DEVICE, so argument checking is testable without a GPU.
+ *  - Ops are the `_encode` twins: they enqueue on the context's stream and
+ *    return without waiting.  rl_execution_finish() is the commit + wait of
+ *    MetalExecution::finish (src/metal/execution.rs:30-36).  The synchronous
+ *    reference ops (e.g. ops::add_f32, src/ops/add.rs:8-16) are
+ *    begin + op + finish.
+ *  - Output buffers are passed in by the caller, allocated with
+ *    rl_buffer_empty() exactly where the reference calls MetalBuffer::empty /
+ *    empty_with_element_size (src/metal/buffer.rs:111-142).  Each op checks
+ *    the output's len and byte_len.
+ *  - f16 is IEEE binary16.  All arithmetic is float32; f16 results are
+ *    rounded to nearest even.
+ *  - One context per thread; a context is not thread-safe (MetalContext is
+ *    !Sync, src/metal/context.rs:14-17).  All work of a context runs in
+ *    order on its one stream.
+ */
+#ifndef RUSTLLM_HIP_H
+#define RUSTLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status codes */
+typedef int32_t rl_status;
+#define RL_OK 0
+#define RL_ERR_INVALID_ARGUMENT 1      /* TinyError::InvalidArgument      src/error.rs:5   */
+#define RL_ERR_INVALID_SHAPE 2         /* TinyError::InvalidShape         src/error.rs:6   */
+#define RL_ERR_SHAPE_MISMATCH 3        /* TinyError::ShapeMismatch        src/error.rs:7-10 */
+#define RL_ERR_INVALID_DIMENSION 4     /* TinyError::InvalidDimension     src/error.rs:11  */
+#define RL_ERR_UNSUPPORTED_DTYPE 5     /* TinyError::UnsupportedDType     src/error.rs:18  */
+#define RL_ERR_NON_CONTIGUOUS 6        /* TinyError::NonContiguousTensor  src/error.rs:19  */
+#define RL_ERR_POSITION_OUT_OF_RANGE 7 /* TinyError::PositionOutOfRange   src/error.rs:20-24 */
+#define RL_ERR_MODEL_FORMAT 8          /* TinyError::ModelFormat          src/error.rs:32  */
+#define RL_ERR_DEVICE 9                /* TinyError::Metal                src/error.rs:38  */
+
+/* --------------------------------------------------------------- handles */
+typedef struct rl_context rl_context; /* MetalContext   src/metal/context.rs:10-18 */
+typedef struct rl_graph rl_graph;     /* a recorded command buffer, replayable */
+typedef struct rl_event rl_event;     /* a stream timestamp */
+
+/* A device buffer.  Same three fields as MetalBuffer (src/metal/buffer.rs:8-12):
+ * `len` is the element count, `byte_len` the size in bytes. */
+typedef struct rl_buffer {
+    void* data;
+    uint64_t len;
+    uint64_t byte_len;
+} rl_buffer;
+
+/* Submission counters: MetalDecodeProfile, src/profile.rs:7-16. */
+typedef struct rl_profile {
+    uint64_t command_buffers;
+    uint64_t compute_encoders;
+    uint64_t kernel_dispatches;
+    uint64_t commits;
+    uint64_t waits;
+    uint64_t buffer_allocations;
+    uint64_t allocated_bytes;
+} rl_profile;
+
+/* ---------------------------------------------------------------- errors */
+/* Message of the calling thread's last failure ("" if none). */
+const char* rl_last_error_message(void);
+/* Library version string. */
+const char* rl_version(void);
+
+/* --------------------------------------------------------------- context */
+/* MetalContext::new (src/metal/context.rs:27-44): opens `device` and makes one
+ * in-order stream at the default priority. */
+rl_status rl_context_create(int32_t device, rl_context** out);
+/* As rl_context_create, but enqueues on an existing HIP stream (hipStream_t
+ * passed as void*).  The stream stays owned by the caller. */
+rl_status rl_context_create_on_stream(int32_t device, void* stream, rl_context** out);
+/* Frees pooled memory and the stream; buffers still held become invalid. */
+void rl_context_destroy(rl_context* ctx);
+/* The hipStream_t the context enqueues on. */
+void* rl_context_stream(const rl_context* ctx);
+/* Number of visible devices (0 when no GPU is present). */
+int32_t rl_device_count(void);
+
+/* ---------------------------------------------------------------- buffers */
+/* MetalBuffer::empty_with_element_size (src/metal/buffer.rs:127-142): `len`
+ * elements of `element_size` bytes from the context's stream-ordered pool.
+ * Contents are undefined.  len and element_size must be > 0. */
+rl_status rl_buffer_empty(rl_context* ctx, uint64_t len, uint64_t element_size, rl_buffer* out);
+/* MetalBuffer::from_slice / from_f16_slice (src/metal/buffer.rs:15-34,57-73):
+ * allocate and copy `len` elements from host memory; returns after the copy. */
+rl_status rl_buffer_from_host(rl_context* ctx, const void* host, uint64_t len,
+                              uint64_t element_size, rl_buffer* out);
+/* MetalBuffer::as_slice / as_f16_slice (src/metal/buffer.rs:160-169): waits for
+ * the stream, then copies `byte_len` bytes to host memory. */
+rl_status rl_buffer_to_host(rl_context* ctx, const rl_buffer* buffer, void* host,
+                            uint64_t byte_len);
+/* Stream-ordered copy of `byte_len` bytes between device buffers. */
+rl_status rl_buffer_copy(rl_context* ctx, const rl_buffer* src, const rl_buffer* dst,
+                         uint64_t byte_len);
+/* Drop of MetalBuffer: returns the block to the pool (stream-ordered reuse)
+ * and zeroes *buffer. */
+void rl_buffer_release(rl_context* ctx, rl_buffer* buffer);
+/* Returns unused pooled blocks to the device. */
+rl_status rl_context_trim(rl_context* ctx);
+
+/* ------------------------------------------------------------- execution */
+/* MetalExecution::new (src/metal/execution.rs:11-20): opens a batch; ops
+ * enqueued until finish form one submission. */
+rl_status rl_execution_begin(rl_context* ctx);
+/* MetalExecution::finish (src/metal/execution.rs:30-36): waits for every
+ * enqueued op and reports any device error (the reference never checks). */
+rl_status rl_execution_finish(rl_context* ctx);
+
+/* Records the ops enqueued between begin and end as a replayable graph (the
+ * HIP counterpart of re-encoding one command buffer).  Buffers used while
+ * recording must stay allocated while the graph is replayed. */
+rl_status rl_graph_capture_begin(rl_context* ctx);
+rl_status rl_graph_capture_end(rl_context* ctx, rl_graph** out);
+rl_status rl_graph_launch(rl_context* ctx, rl_graph* graph);
+void rl_graph_destroy(rl_graph* graph);
+
+/* Stream timestamps for measuring device time. */
+rl_status rl_event_create(rl_context* ctx, rl_event** out);
+rl_status rl_event_record(rl_context* ctx, rl_event* event);
+rl_status rl_event_elapsed_ms(rl_event* start, rl_event* end, float* ms);
+void rl_event_destroy(rl_event* event);
+
+/* ----------------------------------------------------------- profiling */
+/* MetalContext::begin_decode_submission_profile (src/metal/context.rs:48-50). */
+void rl_profile_begin(rl_context* ctx);
+/* MetalContext::take_decode_submission_profile (src/metal/context.rs:52-54):
+ * returns 1 and fills *out if profiling was active, else 0. */
+int32_t rl_profile_take(rl_context* ctx, rl_profile* out);
+/* Dispatch count of one kernel family by name (e.g. "add_f32") in the active
+ * profile: MetalDecodeProfile::kernel_dispatches_by_name (src/profile.rs:15). */
+uint64_t rl_profile_dispatches(const rl_context* ctx, const char* kernel_name);
+
+/* =========================================================== element-wise */
+/* ops::add_f32_encode (src/ops/add.rs:18-49): out = a + b. */
+rl_status rl_add_f32(rl_context* ctx, const rl_buffer* a, const rl_buffer* b,
+                     const rl_buffer* out);
+/* ops::add_f16_encode (src/ops/add.rs:61-101): out = half(float(a) + float(b)). */
+rl_status rl_add_f16(rl_context* ctx, const rl_buffer* a, const rl_buffer* b,
+                     const rl_buffer* out);
+/* ops::mul_f32_encode (src/ops/mul.rs:20-68). */
+rl_status rl_mul_f32(rl_context* ctx, const rl_buffer* a, const rl_buffer* b,
+                     const rl_buffer* out);
+/* ops::mul_f16_encode (src/ops/mul.rs:80-119). */
+rl_status rl_mul_f16(rl_context* ctx, const rl_buffer* a, const rl_buffer* b,
+                     const rl_buffer* out);
+/* ops::silu_f32_encode (src/ops/silu.rs:20-63): x * (1 / (1 + exp(-x))). */
+rl_status rl_silu_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* out);
+/* ops::silu_f16_encode (src/ops/silu.rs:75-109): half(x / (1 + exp(-x))). */
+rl_status rl_silu_f16(rl_context* ctx, const rl_buffer* input, const rl_buffer* out);
+/* ops::swiglu_f16_encode (src/ops/swiglu.rs:8-34): half(silu(gate) * up), one rounding. */
+rl_status rl_swiglu_f16(rl_context* ctx, const rl_buffer* gate, const rl_buffer* up,
+                        const rl_buffer* out);
+/* SwiGlu::forward_encode F32 branch (src/nn/swiglu.rs:15-37: silu_f32 then mul_f32)
+ * fused into one pass; bit-identical to the two-kernel composition. */
+rl_status rl_swiglu_f32(rl_context* ctx, const rl_buffer* gate, const rl_buffer* up,
+                        const rl_buffer* out);
+/* ops::cast F32 -> F16 (src/ops/cast.rs:10-83, kernels/cast.metal:5-11), RNE. */
+rl_status rl_cast_f32_to_f16(rl_context* ctx, const rl_buffer* input, const rl_buffer* out);
+/* ops::cast F16 -> F32 (src/ops/cast.rs:10-83, kernels/cast.metal:13-19), exact. */
+rl_status rl_cast_f16_to_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* out);
+/* Tensor::add with a row-broadcast right operand (a [cols] bias seen through a
+ * stride-0 view): the reference materialises the view with contiguous.metal
+ * and adds (src/tensor/elementwise.rs:108-132); this is that composition in
+ * one pass.  out[r, c] = x[r, c] + bias[c]. */
+rl_status rl_add_broadcast_f32(rl_context* ctx, const rl_buffer* x, const rl_buffer* bias,
+                               uint64_t rows, uint64_t cols, const rl_buffer* out);
+rl_status rl_add_broadcast_f16(rl_context* ctx, const rl_buffer* x, const rl_buffer* bias,
+                               uint64_t rows, uint64_t cols, const rl_buffer* out);
+
+/* ========================================================== data movement */
+/* ops::materialize_contiguous_f32_encode (src/ops/contiguous.rs:28-44,85-154):
+ * out[i] = src[sum_d coord_d(i) * strides[d]] for the `rank`-dim view `dims`.
+ * Strides may be 0 (broadcast). */
+rl_status rl_contiguous_f32(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                            const uint64_t* strides, uint32_t rank, const rl_buffer* out);
+/* ops::materialize_contiguous_f16_encode (src/ops/contiguous.rs:67-83). */
+rl_status rl_contiguous_f16(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                            const uint64_t* strides, uint32_t rank, const rl_buffer* out);
+/* tensor::repeat_kv dispatch (src/tensor/repeat_kv.rs:13-130): contiguous
+ * [batch, kv_heads, seq, head_dim] -> [batch, kv_heads*repeats, seq, head_dim],
+ * out[b, h] = in[b, h / repeats].  repeats must be >= 1 (the Tensor layer
+ * returns its input unchanged for 1). */
+rl_status rl_repeat_kv_f32(rl_context* ctx, const rl_buffer* input, uint64_t batch,
+                           uint64_t kv_heads, uint64_t seq_len, uint64_t head_dim,
+                           uint64_t repeats, const rl_buffer* out);
+rl_status rl_repeat_kv_f16(rl_context* ctx, const rl_buffer* input, uint64_t batch,
+                           uint64_t kv_heads, uint64_t seq_len, uint64_t head_dim,
+                           uint64_t repeats, const rl_buffer* out);
+
+/* ============================================================= reductions */
+/* ops::rmsnorm_f32_encode (src/ops/rmsnorm.rs:38-116): per row of `hidden`,
+ * y = x * rsqrt(mean(x^2) + eps) * w. */
+rl_status rl_rmsnorm_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* weight,
+                         uint64_t rows, uint64_t hidden, float eps, const rl_buffer* out);
+/* ops::rmsnorm_f16_encode (src/ops/rmsnorm.rs:142-206). */
+rl_status rl_rmsnorm_f16(rl_context* ctx, const rl_buffer* input, const rl_buffer* weight,
+                         uint64_t rows, uint64_t hidden, float eps, const rl_buffer* out);
+/* Residual add then RMSNorm, the adjacent calls of src/nn/transformer_block.rs:148-152
+ * fused: sum_out = x + residual (rounded to the dtype), norm_out = RMSNorm(sum_out) * w. */
+rl_status rl_add_rmsnorm_f32(rl_context* ctx, const rl_buffer* x, const rl_buffer* residual,
+                             const rl_buffer* weight, uint64_t rows, uint64_t hidden, float eps,
+                             const rl_buffer* sum_out, const rl_buffer* norm_out);
+rl_status rl_add_rmsnorm_f16(rl_context* ctx, const rl_buffer* x, const rl_buffer* residual,
+                             const rl_buffer* weight, uint64_t rows, uint64_t hidden, float eps,
+                             const rl_buffer* sum_out, const rl_buffer* norm_out);
+
+/* ops::softmax_f32_encode (src/ops/softmax.rs:27-49): row softmax over `width`;
+ * a row whose max is -inf yields NaN, as kernels/softmax.metal:7-132. */
+rl_status rl_softmax_f32(rl_context* ctx, const rl_buffer* input, uint64_t rows, uint64_t width,
+                         const rl_buffer* out);
+/* ops::softmax_f16_encode (src/ops/softmax.rs:67-89): a row whose max is -inf
+ * is written as zeros (kernels/softmax.metal:166-173). */
+rl_status rl_softmax_f16(rl_context* ctx, const rl_buffer* input, uint64_t rows, uint64_t width,
+                         const rl_buffer* out);
+
+/* ops::attention_scale_mask_f32_encode (src/ops/attention_scale_mask.rs:35-58):
+ * on [..., query_len, key_len] scores, out = key > start + q ? -inf : x * scale. */
+rl_status rl_attention_scale_mask_f32(rl_context* ctx, const rl_buffer* input, float scale,
+                                      uint64_t query_len, uint64_t key_len,
+                                      uint64_t query_start_pos, const rl_buffer* out);
+/* ops::attention_scale_mask_f16_encode (src/ops/attention_scale_mask.rs:92-116). */
+rl_status rl_attention_scale_mask_f16(rl_context* ctx, const rl_buffer* input, float scale,
+                                      uint64_t query_len, uint64_t key_len,
+                                      uint64_t query_start_pos, const rl_buffer* out);
+/* attention_scale_mask then softmax_last_dim, the adjacent calls of
+ * src/nn/attention.rs:233-240, in one pass: masked keys are never read and
+ * come out as exact zeros.  Same validation as the scale/mask op; results
+ * equal the two-op composition (f16: the scaled score is rounded to f16
+ * before the softmax, as the composition does). */
+rl_status rl_attention_softmax_f32(rl_context* ctx, const rl_buffer* input, float scale,
+                                   uint64_t query_len, uint64_t key_len,
+                                   uint64_t query_start_pos, const rl_buffer* out);
+rl_status rl_attention_softmax_f16(rl_context* ctx, const rl_buffer* input, float scale,
+                                   uint64_t query_len, uint64_t key_len,
+                                   uint64_t query_start_pos, const rl_buffer* out);
+
+/* ================================================================== RoPE */
+/* ops::rope_f32_encode (src/ops/rope.rs:38-151): contiguous [..., seq_len,
+ * head_dim] input, f32 [table_rows, head_dim/2] cos/sin tables; position of
+ * row r is r % seq_len + start_pos. */
+rl_status rl_rope_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* cos_table,
+                      const rl_buffer* sin_table, uint64_t seq_len, uint64_t head_dim,
+                      uint64_t start_pos, const rl_buffer* out);
+/* ops::rope_f16_encode (src/ops/rope.rs:177-277); tables stay f32. */
+rl_status rl_rope_f16(rl_context* ctx, const rl_buffer* input, const rl_buffer* cos_table,
+                      const rl_buffer* sin_table, uint64_t seq_len, uint64_t head_dim,
+                      uint64_t start_pos, const rl_buffer* out);
+/* ops::rope_encode on a strided view (src/ops/rope.rs:303-370): the
+ * contiguous_encode gather of :345 and the rotation in one pass.  The view is
+ * `dims`/`strides` of rank >= 2 with strides[rank-1] == 1; the output is the
+ * contiguous [dims] tensor; `table_rows` is the cos/sin row count. */
+rl_status rl_rope_strided_f32(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                              const uint64_t* strides, uint32_t rank, const rl_buffer* cos_table,
+                              const rl_buffer* sin_table, uint64_t table_rows,
+                              uint64_t start_pos, const rl_buffer* out);
+rl_status rl_rope_strided_f16(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                              const uint64_t* strides, uint32_t rank, const rl_buffer* cos_table,
+                              const rl_buffer* sin_table, uint64_t table_rows,
+                              uint64_t start_pos, const rl_buffer* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RUSTLLM_HIP_H */

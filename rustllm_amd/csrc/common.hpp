@@ -1,0 +1,172 @@
+// common.hpp -- shared pieces of the gfx950 tensor-op library: the context
+// struct behind rl_context, error reporting, launch bookkeeping, and the
+// device helpers (16-byte packs, f16 conversion, wave64 reductions, fast
+// 32-bit division by a runtime constant).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <string>
+#include <unordered_map>
+
+#include "rustllm_hip.h"
+
+namespace rl {
+
+// ------------------------------------------------------------------ errors
+
+rl_status fail(rl_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// ------------------------------------------------------------------ pool
+
+// Stream-ordered caching allocator.  All work of a context runs in order on
+// one stream, so a block released by the host can be handed to the next
+// allocation at once: any kernel that still reads it was enqueued earlier
+// and finishes before anything enqueued later touches the block.
+struct BufferPool {
+    std::multimap<uint64_t, void*> free_blocks;    // size class -> block
+    std::unordered_map<void*, uint64_t> block_size;  // every live or free block
+    uint64_t reserved_bytes = 0;
+
+    static uint64_t size_class(uint64_t bytes);
+    rl_status allocate(uint64_t bytes, void** out);
+    void release(void* ptr);
+    void trim();
+    ~BufferPool();
+};
+
+}  // namespace rl
+
+struct rl_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool owns_stream = false;
+    int num_cus = 256;
+    rl::BufferPool pool;
+
+    int active_executions = 0;
+    bool capturing = false;
+
+    bool profiling = false;
+    rl_profile profile{};
+    std::map<std::string, uint64_t> dispatches_by_name;
+};
+
+namespace rl {
+
+// Common prologue of every op: after validation, a NULL context is reported
+// as a device error (validation itself needs no device).
+inline rl_status require_context(rl_context* ctx) {
+    if (ctx == nullptr) return fail(RL_ERR_DEVICE, "no HIP context (validation passed)");
+    return RL_OK;
+}
+
+// Makes the context's device current for the calling thread.
+rl_status activate(rl_context* ctx);
+
+// Bookkeeping after a kernel launch: launch errors become RL_ERR_DEVICE and
+// the dispatch is counted in an active profile.
+rl_status after_launch(rl_context* ctx, const char* kernel_name);
+
+inline bool aligned_to(const void* p, uint64_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// Buffer checks shared by the ops; messages follow the reference's wording.
+rl_status check_buffer(const rl_buffer* b, const char* what);
+rl_status check_output(const rl_buffer* out, uint64_t len, uint64_t element_size,
+                       const char* op);
+
+// ------------------------------------------------------------ fast divmod
+
+// Division of a 32-bit numerator by a runtime-constant 32-bit divisor with a
+// multiply-high, a 64-bit add and a shift (Granlund & Montgomery, "Division
+// by invariant integers using multiplication", PLDI 1994, unsigned case with
+// a 33-bit magic whose top bit is the explicit "+ n").
+struct FastDiv {
+    uint32_t divisor;
+    uint32_t magic;
+    uint32_t shift;
+
+    FastDiv() : divisor(1), magic(1), shift(0) {}
+    explicit FastDiv(uint32_t d) : divisor(d) {
+        uint32_t s = 0;
+        while ((uint64_t(1) << s) < d) ++s;
+        shift = s;
+        magic = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1);
+    }
+    __host__ __device__ inline uint32_t div(uint32_t n) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+        uint32_t hi = __umulhi(n, magic);
+#else
+        uint32_t hi = uint32_t((uint64_t(n) * magic) >> 32);
+#endif
+        return uint32_t((uint64_t(hi) + n) >> shift);
+    }
+    __host__ __device__ inline void divmod(uint32_t n, uint32_t& q, uint32_t& r) const {
+        q = div(n);
+        r = n - q * divisor;
+    }
+};
+
+}  // namespace rl
+
+// ------------------------------------------------------------ device side
+
+namespace rl {
+
+typedef _Float16 half_t;
+
+template <typename T, int N>
+struct VecOf {
+    typedef T type __attribute__((ext_vector_type(N)));
+};
+
+// One 16-byte pack of T.
+template <typename T>
+struct Pack16 {
+    static constexpr int N = 16 / sizeof(T);
+    typedef typename VecOf<T, N>::type type;
+};
+
+__device__ inline float to_float(float v) { return v; }
+__device__ inline float to_float(half_t v) { return static_cast<float>(v); }
+
+template <typename T>
+__device__ inline T from_float(float v);
+template <>
+__device__ inline float from_float<float>(float v) { return v; }
+template <>
+__device__ inline half_t from_float<half_t>(float v) { return static_cast<half_t>(v); }  // RNE
+
+template <typename V>
+__device__ inline V load_stream(const V* p) {
+    return __builtin_nontemporal_load(p);
+}
+
+template <typename V>
+__device__ inline void store_stream(V* p, V v) {
+    __builtin_nontemporal_store(v, p);
+}
+
+// wave64 butterfly reductions (every lane ends with the result).
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
+    return v;
+}
+
+}  // namespace rl

@@ -1,0 +1,389 @@
+// elementwise.hip -- add, mul, SiLU, SwiGLU, f32<->f16 cast and row-broadcast
+// add for gfx950.
+//
+// Every op here is a pure stream: HBM-bound, a few VALU ops per element.
+// Each thread moves UNROLL packs of 16 bytes per operand (float4 / 8 halves;
+// casts use 8-element packs on both sides), issuing all loads of a tile
+// before any arithmetic so each wave keeps UNROLL x 1 KiB per operand in
+// flight.  Tiles are laid out so that one load instruction of a wave covers
+// 1 KiB of contiguous memory.  Loads and stores are non-temporal: nothing
+// is reused, so the data should not displace L2 contents.  The few elements
+// past the last whole pack are handled by block 0.
+#include "common.hpp"
+
+namespace rl {
+namespace {
+
+constexpr int kThreads = 256;
+
+// ------------------------------------------------------------ element ops
+// Each is the reference shader's expression, evaluated in float32.
+
+struct AddOp {  // vector_add.metal:11,20
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct MulOp {  // mul.metal:18-19,34-35
+    __device__ float operator()(float a, float b) const { return a * b; }
+};
+struct SiluF32Op {  // silu.metal:17-23: x * (1 / (1 + exp(-x)))
+    __device__ float operator()(float x, float) const {
+        float sigmoid = 1.0f / (1.0f + expf(-x));
+        return x * sigmoid;
+    }
+};
+struct SiluF16Op {  // silu.metal:31-35: x / (1 + exp(-x))
+    __device__ float operator()(float x, float) const { return x / (1.0f + expf(-x)); }
+};
+struct SwigluF16Op {  // silu.metal:44-45: (g / (1 + exp(-g))) * u, rounded once
+    __device__ float operator()(float g, float u) const { return (g / (1.0f + expf(-g))) * u; }
+};
+struct SwigluF32Op {  // nn/swiglu.rs:15-37 F32 branch: silu_f32(g) then mul_f32
+    __device__ float operator()(float g, float u) const {
+        float sigmoid = 1.0f / (1.0f + expf(-g));
+        return (g * sigmoid) * u;
+    }
+};
+struct CopyOp {  // cast.metal:10,18: the conversion happens on store/load
+    __device__ float operator()(float x, float) const { return x; }
+};
+
+// out[i] = op(a[i], b[i]) for ARITY 2, op(a[i]) for ARITY 1.
+template <typename TIn, typename TOut, int N, int UNROLL, int ARITY, typename Op>
+__global__ __launch_bounds__(kThreads) void k_map(const TIn* __restrict__ a,
+                                                  const TIn* __restrict__ b,
+                                                  TOut* __restrict__ out, uint64_t n_packs,
+                                                  uint32_t tail, Op op) {
+    typedef typename VecOf<TIn, N>::type VI;
+    typedef typename VecOf<TOut, N>::type VO;
+    const VI* va = reinterpret_cast<const VI*>(a);
+    const VI* vb = reinterpret_cast<const VI*>(b);
+    VO* vo = reinterpret_cast<VO*>(out);
+    const uint64_t tile = uint64_t(kThreads) * UNROLL;
+    const uint64_t step = uint64_t(gridDim.x) * tile;
+    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_packs;
+         base += step) {
+        VI ra[UNROLL], rb[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_packs) {
+                ra[u] = load_stream(va + i);
+                if constexpr (ARITY == 2) rb[u] = load_stream(vb + i);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_packs) {
+                VO r;
+#pragma unroll
+                for (int k = 0; k < N; ++k) {
+                    float x = to_float(ra[u][k]);
+                    float y = 0.0f;
+                    if constexpr (ARITY == 2) y = to_float(rb[u][k]);
+                    r[k] = from_float<TOut>(op(x, y));
+                }
+                store_stream(vo + i, r);
+            }
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x < tail) {
+        uint64_t i = n_packs * N + threadIdx.x;
+        float y = 0.0f;
+        if constexpr (ARITY == 2) y = to_float(b[i]);
+        out[i] = from_float<TOut>(op(to_float(a[i]), y));
+    }
+}
+
+// out[r, c] = x[r, c] + bias[c] on packs; col_packs = cols / N.
+template <typename T, int N, int UNROLL>
+__global__ __launch_bounds__(kThreads) void k_add_broadcast(const T* __restrict__ x,
+                                                            const T* __restrict__ bias,
+                                                            T* __restrict__ out,
+                                                            uint64_t n_packs, FastDiv col_packs) {
+    typedef typename VecOf<T, N>::type V;
+    const V* vx = reinterpret_cast<const V*>(x);
+    const V* vbias = reinterpret_cast<const V*>(bias);
+    V* vo = reinterpret_cast<V*>(out);
+    const uint64_t tile = uint64_t(kThreads) * UNROLL;
+    const uint64_t step = uint64_t(gridDim.x) * tile;
+    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_packs;
+         base += step) {
+        V rx[UNROLL], rb[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_packs) {
+                uint32_t row, col;
+                col_packs.divmod(uint32_t(i), row, col);
+                rx[u] = load_stream(vx + i);
+                rb[u] = vbias[col];  // a few KiB, stays in L2
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_packs) {
+                V r;
+#pragma unroll
+                for (int k = 0; k < N; ++k)
+                    r[k] = from_float<T>(to_float(rx[u][k]) + to_float(rb[u][k]));
+                store_stream(vo + i, r);
+            }
+        }
+    }
+}
+
+// Scalar fallback for buffers that are not pack-aligned or too large for
+// 32-bit pack indices.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void k_add_broadcast_scalar(const T* __restrict__ x,
+                                                                   const T* __restrict__ bias,
+                                                                   T* __restrict__ out,
+                                                                   uint64_t n, uint64_t cols) {
+    const uint64_t step = uint64_t(gridDim.x) * kThreads;
+    for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += step)
+        out[i] = from_float<T>(to_float(x[i]) + to_float(bias[i % cols]));
+}
+
+// Blocks for a grid-stride stream over `items` work items of `per_block` each.
+inline unsigned grid_for(uint64_t items, uint64_t per_block) {
+    uint64_t blocks = ceil_div(items, per_block);
+    if (blocks < 1) blocks = 1;
+    if (blocks > (1u << 30)) blocks = 1u << 30;
+    return unsigned(blocks);
+}
+
+template <typename TIn, typename TOut, int ARITY, typename Op>
+rl_status launch_map(rl_context* ctx, const char* name, const void* a, const void* b, void* out,
+                     uint64_t n, Op op) {
+    if (n == 0) return RL_OK;
+    if (rl_status st = activate(ctx)) return st;
+    constexpr int N = (sizeof(TIn) == 4 && sizeof(TOut) == 4) ? 4 : 8;
+    constexpr int UNROLL = 4;
+    const bool vec = aligned_to(a, N * sizeof(TIn)) &&
+                     (ARITY < 2 || aligned_to(b, N * sizeof(TIn))) &&
+                     aligned_to(out, N * sizeof(TOut));
+    const TIn* pa = static_cast<const TIn*>(a);
+    const TIn* pb = static_cast<const TIn*>(b);
+    TOut* po = static_cast<TOut*>(out);
+    if (vec) {
+        uint64_t n_packs = n / N;
+        uint32_t tail = uint32_t(n - n_packs * N);
+        hipLaunchKernelGGL((k_map<TIn, TOut, N, UNROLL, ARITY, Op>),
+                           dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads),
+                           0, ctx->stream, pa, pb, po, n_packs, tail, op);
+    } else {
+        hipLaunchKernelGGL((k_map<TIn, TOut, 1, UNROLL, ARITY, Op>),
+                           dim3(grid_for(n, uint64_t(kThreads) * UNROLL)), dim3(kThreads), 0,
+                           ctx->stream, pa, pb, po, n, 0u, op);
+    }
+    return after_launch(ctx, name);
+}
+
+template <typename T>
+rl_status launch_add_broadcast(rl_context* ctx, const char* name, const rl_buffer* x,
+                               const rl_buffer* bias, uint64_t rows, uint64_t cols,
+                               const rl_buffer* out) {
+    uint64_t n = rows * cols;
+    if (n == 0) return RL_OK;
+    if (rl_status st = activate(ctx)) return st;
+    constexpr int N = 16 / sizeof(T);
+    constexpr int UNROLL = 4;
+    const T* px = static_cast<const T*>(x->data);
+    const T* pbias = static_cast<const T*>(bias->data);
+    T* po = static_cast<T*>(out->data);
+    const bool vec = cols % N == 0 && aligned_to(px, 16) && aligned_to(pbias, 16) &&
+                     aligned_to(po, 16) && n / N <= UINT32_MAX;
+    if (vec) {
+        uint64_t n_packs = n / N;
+        hipLaunchKernelGGL((k_add_broadcast<T, N, UNROLL>),
+                           dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads),
+                           0, ctx->stream, px, pbias, po, n_packs, FastDiv(uint32_t(cols / N)));
+    } else {
+        hipLaunchKernelGGL((k_add_broadcast_scalar<T>), dim3(grid_for(n, kThreads * 4)),
+                           dim3(kThreads), 0, ctx->stream, px, pbias, po, n, cols);
+    }
+    return after_launch(ctx, name);
+}
+
+rl_status check_input(const rl_buffer* b, uint64_t element_size, const char* what) {
+    if (rl_status st = check_buffer(b, what)) return st;
+    if (b->byte_len < b->len * element_size)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "%s buffer holds %llu bytes, fewer than %llu elements of %llu bytes", what,
+                    (unsigned long long)b->byte_len, (unsigned long long)b->len,
+                    (unsigned long long)element_size);
+    return RL_OK;
+}
+
+}  // namespace
+}  // namespace rl
+
+using namespace rl;
+
+extern "C" {
+
+// src/ops/add.rs:18-49
+rl_status rl_add_f32(rl_context* ctx, const rl_buffer* a, const rl_buffer* b,
+                     const rl_buffer* out) {
+    if (rl_status st = check_input(a, 4, "left")) return st;
+    if (rl_status st = check_input(b, 4, "right")) return st;
+    if (a->len != b->len)
+        return fail(RL_ERR_INVALID_SHAPE, "add requires equal buffer lengths, got %llu and %llu",
+                    (unsigned long long)a->len, (unsigned long long)b->len);
+    if (rl_status st = check_output(out, a->len, 4, "add")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<float, float, 2>(ctx, "add_f32", a->data, b->data, out->data, a->len,
+                                       AddOp{});
+}
+
+// src/ops/add.rs:61-101
+rl_status rl_add_f16(rl_context* ctx, const rl_buffer* a, const rl_buffer* b,
+                     const rl_buffer* out) {
+    if (rl_status st = check_buffer(a, "left")) return st;
+    if (rl_status st = check_buffer(b, "right")) return st;
+    if (a->len != b->len || a->byte_len != a->len * 2 || b->byte_len != b->len * 2)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "F16 add requires equal F16 buffers, got %llu elements/%llu bytes and %llu "
+                    "elements/%llu bytes",
+                    (unsigned long long)a->len, (unsigned long long)a->byte_len,
+                    (unsigned long long)b->len, (unsigned long long)b->byte_len);
+    if (rl_status st = check_output(out, a->len, 2, "add")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<half_t, half_t, 2>(ctx, "add_f16", a->data, b->data, out->data, a->len,
+                                         AddOp{});
+}
+
+// src/ops/mul.rs:20-68
+rl_status rl_mul_f32(rl_context* ctx, const rl_buffer* a, const rl_buffer* b,
+                     const rl_buffer* out) {
+    if (rl_status st = check_input(a, 4, "left")) return st;
+    if (rl_status st = check_input(b, 4, "right")) return st;
+    if (a->len != b->len)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "element-wise multiply requires equal buffer lengths, got %llu and %llu",
+                    (unsigned long long)a->len, (unsigned long long)b->len);
+    if (rl_status st = check_output(out, a->len, 4, "multiply")) return st;
+    if (a->len > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "multiply input size exceeds u32");
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<float, float, 2>(ctx, "mul_f32", a->data, b->data, out->data, a->len,
+                                       MulOp{});
+}
+
+// src/ops/mul.rs:80-119
+rl_status rl_mul_f16(rl_context* ctx, const rl_buffer* a, const rl_buffer* b,
+                     const rl_buffer* out) {
+    if (rl_status st = check_input(a, 2, "left")) return st;
+    if (rl_status st = check_input(b, 2, "right")) return st;
+    if (a->len != b->len)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "element-wise multiply requires equal buffer lengths, got %llu and %llu",
+                    (unsigned long long)a->len, (unsigned long long)b->len);
+    if (rl_status st = check_output(out, a->len, 2, "multiply")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<half_t, half_t, 2>(ctx, "mul_f16", a->data, b->data, out->data, a->len,
+                                         MulOp{});
+}
+
+// src/ops/silu.rs:20-63
+rl_status rl_silu_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* out) {
+    if (rl_status st = check_input(input, 4, "input")) return st;
+    if (input->len == 0) return fail(RL_ERR_INVALID_SHAPE, "SiLU input cannot be empty");
+    if (rl_status st = check_output(out, input->len, 4, "SiLU")) return st;
+    if (input->len > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "SiLU input size exceeds u32");
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<float, float, 1>(ctx, "silu_f32", input->data, nullptr, out->data,
+                                       input->len, SiluF32Op{});
+}
+
+// src/ops/silu.rs:75-109
+rl_status rl_silu_f16(rl_context* ctx, const rl_buffer* input, const rl_buffer* out) {
+    if (rl_status st = check_input(input, 2, "input")) return st;
+    if (input->len == 0) return fail(RL_ERR_INVALID_SHAPE, "SiLU input cannot be empty");
+    if (rl_status st = check_output(out, input->len, 2, "SiLU")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<half_t, half_t, 1>(ctx, "silu_f16", input->data, nullptr, out->data,
+                                         input->len, SiluF16Op{});
+}
+
+// src/ops/swiglu.rs:8-34
+rl_status rl_swiglu_f16(rl_context* ctx, const rl_buffer* gate, const rl_buffer* up,
+                        const rl_buffer* out) {
+    if (rl_status st = check_buffer(gate, "gate")) return st;
+    if (rl_status st = check_buffer(up, "up")) return st;
+    if (gate->len != up->len || gate->byte_len != gate->len * 2 || up->byte_len != up->len * 2)
+        return fail(RL_ERR_INVALID_SHAPE, "SwiGLU requires equal F16 buffers");
+    if (rl_status st = check_output(out, gate->len, 2, "SwiGLU")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<half_t, half_t, 2>(ctx, "swiglu_f16", gate->data, up->data, out->data,
+                                         gate->len, SwigluF16Op{});
+}
+
+// src/nn/swiglu.rs:15-37 (F32: silu_f32 then mul_f32, fused)
+rl_status rl_swiglu_f32(rl_context* ctx, const rl_buffer* gate, const rl_buffer* up,
+                        const rl_buffer* out) {
+    if (rl_status st = check_buffer(gate, "gate")) return st;
+    if (rl_status st = check_buffer(up, "up")) return st;
+    if (gate->len != up->len || gate->byte_len != gate->len * 4 || up->byte_len != up->len * 4)
+        return fail(RL_ERR_INVALID_SHAPE, "SwiGLU requires equal F32 buffers");
+    if (gate->len == 0) return fail(RL_ERR_INVALID_SHAPE, "SiLU input cannot be empty");
+    if (rl_status st = check_output(out, gate->len, 4, "SwiGLU")) return st;
+    if (gate->len > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "SiLU input size exceeds u32");
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<float, float, 2>(ctx, "swiglu_f32", gate->data, up->data, out->data,
+                                       gate->len, SwigluF32Op{});
+}
+
+// src/ops/cast.rs:28-83
+rl_status rl_cast_f32_to_f16(rl_context* ctx, const rl_buffer* input, const rl_buffer* out) {
+    if (rl_status st = check_input(input, 4, "input")) return st;
+    if (rl_status st = check_output(out, input->len, 2, "cast")) return st;
+    if (input->len > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "cast element count exceeds u32");
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<float, half_t, 1>(ctx, "cast_f32_to_f16", input->data, nullptr, out->data,
+                                        input->len, CopyOp{});
+}
+
+rl_status rl_cast_f16_to_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* out) {
+    if (rl_status st = check_input(input, 2, "input")) return st;
+    if (rl_status st = check_output(out, input->len, 4, "cast")) return st;
+    if (input->len > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "cast element count exceeds u32");
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_map<half_t, float, 1>(ctx, "cast_f16_to_f32", input->data, nullptr, out->data,
+                                        input->len, CopyOp{});
+}
+
+static rl_status validate_broadcast(const rl_buffer* x, const rl_buffer* bias, uint64_t rows,
+                                    uint64_t cols, const rl_buffer* out, uint64_t es) {
+    if (rl_status st = check_input(x, es, "input")) return st;
+    if (rl_status st = check_input(bias, es, "bias")) return st;
+    if (rows == 0 || cols == 0)
+        return fail(RL_ERR_INVALID_SHAPE, "shape dimensions must be greater than zero");
+    if (rows > UINT64_MAX / cols || x->len != rows * cols)
+        return fail(RL_ERR_INVALID_SHAPE, "input has %llu elements, expected %llu x %llu",
+                    (unsigned long long)x->len, (unsigned long long)rows,
+                    (unsigned long long)cols);
+    if (bias->len != cols)
+        return fail(RL_ERR_SHAPE_MISMATCH, "bias has %llu elements, expected %llu",
+                    (unsigned long long)bias->len, (unsigned long long)cols);
+    return check_output(out, x->len, es, "add");
+}
+
+rl_status rl_add_broadcast_f32(rl_context* ctx, const rl_buffer* x, const rl_buffer* bias,
+                               uint64_t rows, uint64_t cols, const rl_buffer* out) {
+    if (rl_status st = validate_broadcast(x, bias, rows, cols, out, 4)) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_add_broadcast<float>(ctx, "add_broadcast_f32", x, bias, rows, cols, out);
+}
+
+rl_status rl_add_broadcast_f16(rl_context* ctx, const rl_buffer* x, const rl_buffer* bias,
+                               uint64_t rows, uint64_t cols, const rl_buffer* out) {
+    if (rl_status st = validate_broadcast(x, bias, rows, cols, out, 2)) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_add_broadcast<half_t>(ctx, "add_broadcast_f16", x, bias, rows, cols, out);
+}
+
+}  // extern "C"

@@ -1,0 +1,347 @@
+// movement.hip -- contiguous (strided gather of a view) and repeat_kv for
+// gfx950.
+//
+// contiguous: the view is first simplified on the host (size-1 dims dropped,
+// dims whose strides chain are merged).  If the innermost dim has stride 1
+// the copy is a gather of rows: each row's source offset is decoded once per
+// 16-byte pack with 32-bit multiply-high division, and rows move as whole
+// packs, so every wave load covers runs of at least one row (256 B for a
+// 64-wide f32 head).  Anything else falls back to a per-element gather.
+//
+// repeat_kv: each thread reads one pack of the KV input once and writes it
+// to the `repeats` query heads that share it, so HBM sees the minimum
+// traffic (input once + output once).
+#include <type_traits>
+#include <vector>
+
+#include "common.hpp"
+
+namespace rl {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxRank = 16;
+
+// Outer dimensions of a view, innermost first.
+struct OuterDims {
+    uint32_t rank;
+    FastDiv dim[kMaxRank];
+    uint64_t stride[kMaxRank];
+
+    __device__ inline uint64_t offset(uint32_t index) const {
+        uint64_t off = 0;
+#pragma unroll 4
+        for (uint32_t d = 0; d < rank; ++d) {
+            uint32_t q, r;
+            dim[d].divmod(index, q, r);
+            off += uint64_t(r) * stride[d];
+            index = q;
+        }
+        return off;
+    }
+};
+
+// dst[i] = src[offset(row) + pack], rows of `row_packs` packs of N elements.
+template <typename T, int N, int UNROLL>
+__global__ __launch_bounds__(kThreads) void k_gather_rows(const T* __restrict__ src,
+                                                          T* __restrict__ dst, uint32_t n_packs,
+                                                          FastDiv row_packs, OuterDims outer) {
+    typedef typename VecOf<T, N>::type V;
+    V* vdst = reinterpret_cast<V*>(dst);
+    const uint64_t tile = uint64_t(kThreads) * UNROLL;
+    const uint64_t step = uint64_t(gridDim.x) * tile;
+    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_packs;
+         base += step) {
+        V r[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_packs) {
+                uint32_t row, p;
+                row_packs.divmod(uint32_t(i), row, p);
+                uint64_t off = outer.offset(row) + uint64_t(p) * N;
+                r[u] = *reinterpret_cast<const V*>(src + off);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_packs) store_stream(vdst + i, r[u]);
+        }
+    }
+}
+
+// Per-element gather over all dims (innermost first in `dims`).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void k_gather_elems(const T* __restrict__ src,
+                                                           T* __restrict__ dst, uint32_t numel,
+                                                           OuterDims dims) {
+    const uint64_t step = uint64_t(gridDim.x) * kThreads;
+    for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < numel; i += step)
+        dst[i] = src[dims.offset(uint32_t(i))];
+}
+
+// out[(head * repeats + r) * head_packs + p] = in[head * head_packs + p],
+// head = b * kv_heads + kv_head.
+template <typename T, int N, int UNROLL>
+__global__ __launch_bounds__(kThreads) void k_repeat_kv(const T* __restrict__ in,
+                                                        T* __restrict__ out, uint64_t n_packs,
+                                                        uint64_t head_packs, FastDiv head_div,
+                                                        uint32_t repeats, bool small_index) {
+    typedef typename VecOf<T, N>::type V;
+    const V* vin = reinterpret_cast<const V*>(in);
+    V* vout = reinterpret_cast<V*>(out);
+    const uint64_t tile = uint64_t(kThreads) * UNROLL;
+    const uint64_t step = uint64_t(gridDim.x) * tile;
+    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_packs;
+         base += step) {
+        V r[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_packs) r[u] = load_stream(vin + i);
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_packs) {
+                uint64_t head, p;
+                if (small_index) {
+                    uint32_t q, rem;
+                    head_div.divmod(uint32_t(i), q, rem);
+                    head = q;
+                    p = rem;
+                } else {
+                    head = i / head_packs;
+                    p = i - head * head_packs;
+                }
+                V* dst = vout + head * repeats * head_packs + p;
+                for (uint32_t k = 0; k < repeats; ++k) store_stream(dst + k * head_packs, r[u]);
+            }
+        }
+    }
+}
+
+inline unsigned grid_for(uint64_t items, uint64_t per_block) {
+    uint64_t blocks = ceil_div(items, per_block);
+    if (blocks < 1) blocks = 1;
+    if (blocks > (1u << 30)) blocks = 1u << 30;
+    return unsigned(blocks);
+}
+
+// A view after dropping size-1 dims and merging dims whose strides chain
+// (strides[i] == strides[i+1] * dims[i+1]); iteration order is unchanged.
+struct SimpleView {
+    std::vector<uint64_t> dims, strides;  // outermost first
+};
+
+SimpleView simplify(const uint64_t* dims, const uint64_t* strides, uint32_t rank) {
+    SimpleView v;
+    for (uint32_t d = 0; d < rank; ++d) {
+        if (dims[d] == 1) continue;
+        if (!v.dims.empty() && v.strides.back() == strides[d] * dims[d]) {
+            v.dims.back() *= dims[d];
+            v.strides.back() = strides[d];
+        } else {
+            v.dims.push_back(dims[d]);
+            v.strides.push_back(strides[d]);
+        }
+    }
+    if (v.dims.empty()) {  // a single element
+        v.dims.push_back(1);
+        v.strides.push_back(1);
+    }
+    return v;
+}
+
+template <typename T>
+rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* dst,
+                            const SimpleView& v, uint64_t numel) {
+    if (rl_status st = activate(ctx)) return st;
+    const uint32_t rank = uint32_t(v.dims.size());
+    const uint64_t inner = v.dims[rank - 1];
+    if (v.strides[rank - 1] == 1) {
+        // Largest pack (<= 16 B) dividing the row, every outer stride and
+        // both base addresses.
+        int n = 16 / int(sizeof(T));
+        while (n > 1) {
+            bool ok = inner % n == 0 && aligned_to(src, n * sizeof(T)) &&
+                      aligned_to(dst, n * sizeof(T));
+            for (uint32_t d = 0; d + 1 < rank && ok; ++d) ok = v.strides[d] % n == 0;
+            if (ok) break;
+            n >>= 1;
+        }
+        OuterDims outer{};
+        outer.rank = rank - 1;
+        for (uint32_t d = 0; d + 1 < rank; ++d) {
+            outer.dim[d] = FastDiv(uint32_t(v.dims[rank - 2 - d]));
+            outer.stride[d] = v.strides[rank - 2 - d];
+        }
+        const uint64_t n_packs = numel / n;
+        const FastDiv row_packs(uint32_t(inner / n));
+        constexpr int U = 4;
+        const dim3 grid(grid_for(n_packs, uint64_t(kThreads) * U)), block(kThreads);
+        switch (n) {
+            case 8:
+                hipLaunchKernelGGL((k_gather_rows<T, 8, U>), grid, block, 0, ctx->stream, src, dst,
+                                   uint32_t(n_packs), row_packs, outer);
+                break;
+            case 4:
+                hipLaunchKernelGGL((k_gather_rows<T, 4, U>), grid, block, 0, ctx->stream, src, dst,
+                                   uint32_t(n_packs), row_packs, outer);
+                break;
+            case 2:
+                hipLaunchKernelGGL((k_gather_rows<T, 2, U>), grid, block, 0, ctx->stream, src, dst,
+                                   uint32_t(n_packs), row_packs, outer);
+                break;
+            default:
+                hipLaunchKernelGGL((k_gather_rows<T, 1, U>), grid, block, 0, ctx->stream, src, dst,
+                                   uint32_t(n_packs), row_packs, outer);
+                break;
+        }
+    } else {
+        OuterDims all{};
+        all.rank = rank;
+        for (uint32_t d = 0; d < rank; ++d) {
+            all.dim[d] = FastDiv(uint32_t(v.dims[rank - 1 - d]));
+            all.stride[d] = v.strides[rank - 1 - d];
+        }
+        hipLaunchKernelGGL((k_gather_elems<T>), dim3(grid_for(numel, kThreads * 4)),
+                           dim3(kThreads), 0, ctx->stream, src, dst, uint32_t(numel), all);
+    }
+    return after_launch(ctx, name);
+}
+
+// src/ops/contiguous.rs:85-154, in the reference's order, plus two checks
+// that keep every read inside the source buffer.
+rl_status contiguous_impl(rl_context* ctx, const char* name, const rl_buffer* src,
+                          const uint64_t* dims, const uint64_t* strides, uint32_t rank,
+                          const rl_buffer* out, uint64_t es) {
+    if (rl_status st = check_buffer(src, "source")) return st;
+    if (rank == 0) return fail(RL_ERR_INVALID_SHAPE, "shape cannot be empty");
+    if (dims == nullptr || strides == nullptr)
+        return fail(RL_ERR_INVALID_SHAPE, "shape rank and strides rank differ");
+    if (rank > kMaxRank) return fail(RL_ERR_INVALID_SHAPE, "tensor rank exceeds %d", kMaxRank);
+    uint64_t numel = 1;
+    for (uint32_t d = 0; d < rank; ++d) {
+        if (dims[d] == 0)
+            return fail(RL_ERR_INVALID_SHAPE, "shape dimensions must be greater than zero");
+        if (numel > UINT64_MAX / dims[d])
+            return fail(RL_ERR_INVALID_SHAPE, "tensor element count exceeds u32");
+        numel *= dims[d];
+    }
+    // The reference also requires src->len >= numel; that holds for every view
+    // its API can form (permute / transpose / narrow of a whole tensor).  The
+    // exact bound below replaces it so that stride-0 (broadcast) views, whose
+    // storage is smaller than the view, can be materialised too.
+    if (src->byte_len != src->len * es)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "source buffer does not match contiguous materialization dtype");
+    for (uint32_t d = 0; d < rank; ++d)
+        if (dims[d] > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "shape dimension exceeds u32");
+    for (uint32_t d = 0; d < rank; ++d)
+        if (strides[d] > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "stride exceeds u32");
+    if (numel > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "tensor element count exceeds u32");
+    unsigned __int128 last = 0;
+    for (uint32_t d = 0; d < rank; ++d) last += (unsigned __int128)(dims[d] - 1) * strides[d];
+    if (last >= src->len)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "view reaches element %llu of a %llu-element source buffer",
+                    (unsigned long long)(last > UINT64_MAX ? UINT64_MAX : uint64_t(last)),
+                    (unsigned long long)src->len);
+    if (rl_status st = check_output(out, numel, es, "contiguous")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    SimpleView v = simplify(dims, strides, rank);
+    if (es == 4)
+        return launch_contiguous<float>(ctx, name, static_cast<const float*>(src->data),
+                                        static_cast<float*>(out->data), v, numel);
+    return launch_contiguous<half_t>(ctx, name, static_cast<const half_t*>(src->data),
+                                     static_cast<half_t*>(out->data), v, numel);
+}
+
+// src/tensor/repeat_kv.rs:13-130 (buffer level: rank-4 and contiguity are
+// the Tensor layer's checks; repeats == 0 is rejected here as there).
+rl_status repeat_kv_impl(rl_context* ctx, const char* name, const rl_buffer* in, uint64_t batch,
+                         uint64_t kv_heads, uint64_t seq_len, uint64_t head_dim, uint64_t repeats,
+                         const rl_buffer* out, uint64_t es) {
+    if (rl_status st = check_buffer(in, "input")) return st;
+    if (repeats == 0)
+        return fail(RL_ERR_MODEL_FORMAT, "repeat_kv repeats must be greater than zero");
+    if (batch == 0 || kv_heads == 0 || seq_len == 0 || head_dim == 0)
+        return fail(RL_ERR_INVALID_SHAPE, "shape dimensions must be greater than zero");
+    if (kv_heads > UINT64_MAX / repeats)
+        return fail(RL_ERR_MODEL_FORMAT, "repeat_kv head count overflow");
+    const uint64_t dims[4] = {kv_heads, seq_len, head_dim, repeats};
+    for (uint64_t d : dims)
+        if (d > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "repeat_kv dimension exceeds u32");
+    const uint64_t head = seq_len * head_dim;
+    const uint64_t in_numel = batch * kv_heads * head;
+    if (in->len != in_numel || in->byte_len != in_numel * es)
+        return fail(RL_ERR_INVALID_SHAPE, "repeat_kv input has %llu elements, expected %llu",
+                    (unsigned long long)in->len, (unsigned long long)in_numel);
+    if (rl_status st = check_output(out, in_numel * repeats, es, "repeat_kv")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    if (rl_status st = activate(ctx)) return st;
+
+    const void* src = in->data;
+    void* dst = out->data;
+    constexpr int U = 2;
+    auto launch = [&](auto tag, auto n_const) {
+        typedef decltype(tag) T;
+        constexpr int N = decltype(n_const)::value;
+        const uint64_t head_packs = head / N;
+        const uint64_t n_packs = in_numel / N;
+        const bool small = n_packs <= UINT32_MAX && head_packs <= UINT32_MAX;
+        hipLaunchKernelGGL((k_repeat_kv<T, N, U>), dim3(grid_for(n_packs, kThreads * U)),
+                           dim3(kThreads), 0, ctx->stream, static_cast<const T*>(src),
+                           static_cast<T*>(dst), n_packs, head_packs,
+                           FastDiv(small ? uint32_t(head_packs) : 1u), uint32_t(repeats), small);
+    };
+    const bool aligned16 = aligned_to(src, 16) && aligned_to(dst, 16);
+    if (es == 4) {
+        if (head % 4 == 0 && aligned16)
+            launch(float(), std::integral_constant<int, 4>());
+        else
+            launch(float(), std::integral_constant<int, 1>());
+    } else {
+        if (head % 8 == 0 && aligned16)
+            launch(half_t(), std::integral_constant<int, 8>());
+        else
+            launch(half_t(), std::integral_constant<int, 1>());
+    }
+    return after_launch(ctx, name);
+}
+
+}  // namespace
+}  // namespace rl
+
+using namespace rl;
+
+extern "C" {
+
+rl_status rl_contiguous_f32(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                            const uint64_t* strides, uint32_t rank, const rl_buffer* out) {
+    return contiguous_impl(ctx, "contiguous_f32", src, dims, strides, rank, out, 4);
+}
+
+rl_status rl_contiguous_f16(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                            const uint64_t* strides, uint32_t rank, const rl_buffer* out) {
+    return contiguous_impl(ctx, "contiguous_f16", src, dims, strides, rank, out, 2);
+}
+
+rl_status rl_repeat_kv_f32(rl_context* ctx, const rl_buffer* input, uint64_t batch,
+                           uint64_t kv_heads, uint64_t seq_len, uint64_t head_dim,
+                           uint64_t repeats, const rl_buffer* out) {
+    return repeat_kv_impl(ctx, "repeat_kv_f32", input, batch, kv_heads, seq_len, head_dim,
+                          repeats, out, 4);
+}
+
+rl_status rl_repeat_kv_f16(rl_context* ctx, const rl_buffer* input, uint64_t batch,
+                           uint64_t kv_heads, uint64_t seq_len, uint64_t head_dim,
+                           uint64_t repeats, const rl_buffer* out) {
+    return repeat_kv_impl(ctx, "repeat_kv_f16", input, batch, kv_heads, seq_len, head_dim,
+                          repeats, out, 2);
+}
+
+}  // extern "C"

@@ -1,0 +1,255 @@
+// rmsnorm.hip -- RMSNorm and fused residual-add + RMSNorm for gfx950.
+//
+// y = x * rsqrt(sum(x^2) / h + eps) * w per row of h elements
+// (kernels/rmsnorm.metal:7-126).  The reference gives each row a 256-thread
+// group with an 8-barrier shared-memory tree and reads x twice.  Here one
+// wave64 owns one row: it loads the row once into VGPRs as 16-byte packs
+// (h <= 64 * 16 packs), reduces the sum of squares with a butterfly of
+// cross-lane shuffles (no LDS, no barrier), and writes y from registers, so
+// x is read from HBM exactly once.  Four rows share a 256-thread block.
+// Rows longer than the register budget fall back to a block per row with
+// an LDS step across its four waves and a second (L2-resident) read.
+//
+// The fused variant first forms s = x + r rounded to the dtype (the add
+// kernel's result), writes s and normalises it: the two adjacent calls of
+// nn/transformer_block.rs:148-152 in one pass.
+#include "common.hpp"
+
+namespace rl {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+constexpr int kRowsPerBlock = kThreads / kWave;
+
+template <typename T, int N, int NV, bool ADD>
+__global__ __launch_bounds__(kThreads) void k_rmsnorm_wave(
+    const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ weight,
+    T* __restrict__ sum_out, T* __restrict__ y, uint32_t rows, uint32_t h_packs, float hidden,
+    float eps) {
+    typedef typename VecOf<T, N>::type V;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t row = blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
+    if (row >= rows) return;  // whole wave leaves together; no block barrier below
+    const uint64_t row_off = uint64_t(row) * h_packs;
+    const V* xr = reinterpret_cast<const V*>(x) + row_off;
+    V v[NV];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = lane + k * kWave;
+        if (p < h_packs) v[k] = load_stream(xr + p);
+    }
+    if constexpr (ADD) {
+        const V* rr = reinterpret_cast<const V*>(residual) + row_off;
+        V* sr = reinterpret_cast<V*>(sum_out) + row_off;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const uint32_t p = lane + k * kWave;
+            if (p < h_packs) {
+                V r = load_stream(rr + p);
+                V s;
+#pragma unroll
+                for (int j = 0; j < N; ++j) s[j] = from_float<T>(to_float(v[k][j]) + to_float(r[j]));
+                v[k] = s;
+                store_stream(sr + p, s);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = lane + k * kWave;
+        if (p < h_packs) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float f = to_float(v[k][j]);
+                ss = fmaf(f, f, ss);
+            }
+        }
+    }
+    ss = wave_sum(ss);
+    const float inverse_rms = rsqrtf(ss / hidden + eps);  // rmsnorm.metal:55-60
+    const V* wr = reinterpret_cast<const V*>(weight);
+    V* yr = reinterpret_cast<V*>(y) + row_off;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = lane + k * kWave;
+        if (p < h_packs) {
+            V w = wr[p];  // h elements, shared by every row: L2-resident
+            V o;
+#pragma unroll
+            for (int j = 0; j < N; ++j)
+                o[j] = from_float<T>(to_float(v[k][j]) * inverse_rms * to_float(w[j]));
+            store_stream(yr + p, o);
+        }
+    }
+}
+
+// One 256-thread block per row, any h: pass 1 sums squares (and writes s for
+// the fused add), pass 2 re-reads the row (from L2 for these sizes).
+template <typename T, bool ADD>
+__global__ __launch_bounds__(kThreads) void k_rmsnorm_block(
+    const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ weight,
+    T* __restrict__ sum_out, T* __restrict__ y, uint32_t rows, uint32_t h, float eps) {
+    __shared__ float partial[kThreads / kWave];
+    const uint32_t row = blockIdx.x;
+    const uint64_t off = uint64_t(row) * h;
+    const T* src = ADD ? sum_out : x;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < h; i += kThreads) {
+        float f;
+        if constexpr (ADD) {
+            T s = from_float<T>(to_float(x[off + i]) + to_float(residual[off + i]));
+            sum_out[off + i] = s;
+            f = to_float(s);
+        } else {
+            f = to_float(x[off + i]);
+        }
+        ss = fmaf(f, f, ss);
+    }
+    ss = wave_sum(ss);
+    if (threadIdx.x % kWave == 0) partial[threadIdx.x / kWave] = ss;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) total += partial[w];
+    const float inverse_rms = rsqrtf(total / float(h) + eps);
+    // Each thread re-reads only elements it wrote itself in pass 1.
+    for (uint32_t i = threadIdx.x; i < h; i += kThreads)
+        y[off + i] = from_float<T>(to_float(src[off + i]) * inverse_rms * to_float(weight[i]));
+}
+
+template <typename T, bool ADD>
+rl_status launch_rmsnorm(rl_context* ctx, const char* name, const T* x, const T* residual,
+                         const T* weight, T* sum_out, T* y, uint64_t rows, uint64_t hidden,
+                         float eps) {
+    if (rl_status st = activate(ctx)) return st;
+    constexpr int N = 16 / sizeof(T);
+    const bool packs_ok = hidden % N == 0 && aligned_to(x, 16) && aligned_to(weight, 16) &&
+                          aligned_to(y, 16) && (!ADD || (aligned_to(residual, 16) &&
+                                                         aligned_to(sum_out, 16)));
+    const uint64_t h_packs = hidden / N;
+    const uint32_t r32 = uint32_t(rows);
+    if (packs_ok && h_packs <= 16 * kWave) {
+        const dim3 grid(unsigned(ceil_div(rows, kRowsPerBlock))), block(kThreads);
+        const uint32_t hp = uint32_t(h_packs);
+        const float hf = float(hidden);
+        if (h_packs <= 1 * kWave)
+            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 1, ADD>), grid, block, 0, ctx->stream, x,
+                               residual, weight, sum_out, y, r32, hp, hf, eps);
+        else if (h_packs <= 2 * kWave)
+            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 2, ADD>), grid, block, 0, ctx->stream, x,
+                               residual, weight, sum_out, y, r32, hp, hf, eps);
+        else if (h_packs <= 4 * kWave)
+            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 4, ADD>), grid, block, 0, ctx->stream, x,
+                               residual, weight, sum_out, y, r32, hp, hf, eps);
+        else if (h_packs <= 8 * kWave)
+            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 8, ADD>), grid, block, 0, ctx->stream, x,
+                               residual, weight, sum_out, y, r32, hp, hf, eps);
+        else
+            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 16, ADD>), grid, block, 0, ctx->stream, x,
+                               residual, weight, sum_out, y, r32, hp, hf, eps);
+    } else {
+        hipLaunchKernelGGL((k_rmsnorm_block<T, ADD>), dim3(r32), dim3(kThreads), 0, ctx->stream,
+                           x, residual, weight, sum_out, y, r32, uint32_t(hidden), eps);
+    }
+    return after_launch(ctx, name);
+}
+
+// src/ops/rmsnorm.rs:38-116 / :142-206 in order, plus eps (checked by the
+// Tensor-level ops::rmsnorm at :226-230) and the row-count limits of the grid.
+rl_status validate(const rl_buffer* input, const rl_buffer* weight, uint64_t rows,
+                   uint64_t hidden, float eps, uint64_t es) {
+    if (rl_status st = check_buffer(input, "input")) return st;
+    if (rl_status st = check_buffer(weight, "weight")) return st;
+    if (hidden == 0)
+        return fail(RL_ERR_INVALID_SHAPE, "RMSNorm hidden size cannot be zero");
+    if (rows > UINT64_MAX / hidden || input->len != rows * hidden)
+        return fail(RL_ERR_INVALID_SHAPE, "RMSNorm input has %llu elements, expected %llu",
+                    (unsigned long long)input->len,
+                    (unsigned long long)(rows > UINT64_MAX / hidden ? 0 : rows * hidden));
+    if (weight->len != hidden)
+        return fail(RL_ERR_INVALID_SHAPE, "RMSNorm weight has %llu elements, expected %llu",
+                    (unsigned long long)weight->len, (unsigned long long)hidden);
+    if (input->byte_len < input->len * es || weight->byte_len < weight->len * es)
+        return fail(RL_ERR_INVALID_SHAPE, "RMSNorm buffers do not hold %llu-byte elements",
+                    (unsigned long long)es);
+    if (hidden > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "RMSNorm hidden size exceeds u32");
+    if (rows > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "RMSNorm row count exceeds u32");
+    if (!(eps > 0.0f) || eps == INFINITY)
+        return fail(RL_ERR_INVALID_SHAPE, "RMSNorm epsilon must be positive and finite, got %g",
+                    double(eps));
+    return RL_OK;
+}
+
+template <typename T>
+rl_status rmsnorm_entry(rl_context* ctx, const char* name, const rl_buffer* input,
+                        const rl_buffer* weight, uint64_t rows, uint64_t hidden, float eps,
+                        const rl_buffer* out) {
+    if (rl_status st = validate(input, weight, rows, hidden, eps, sizeof(T))) return st;
+    if (rl_status st = check_output(out, input->len, sizeof(T), "RMSNorm")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    if (rows == 0) return RL_OK;
+    return launch_rmsnorm<T, false>(ctx, name, static_cast<const T*>(input->data), nullptr,
+                                    static_cast<const T*>(weight->data), nullptr,
+                                    static_cast<T*>(out->data), rows, hidden, eps);
+}
+
+template <typename T>
+rl_status add_rmsnorm_entry(rl_context* ctx, const char* name, const rl_buffer* x,
+                            const rl_buffer* residual, const rl_buffer* weight, uint64_t rows,
+                            uint64_t hidden, float eps, const rl_buffer* sum_out,
+                            const rl_buffer* norm_out) {
+    if (rl_status st = check_buffer(residual, "residual")) return st;
+    if (rl_status st = check_buffer(x, "input")) return st;
+    if (x->len != residual->len)  // Tensor::add: shapes must match (elementwise.rs:249-254)
+        return fail(RL_ERR_SHAPE_MISMATCH, "add requires equal buffer lengths, got %llu and %llu",
+                    (unsigned long long)x->len, (unsigned long long)residual->len);
+    if (residual->byte_len < residual->len * sizeof(T))
+        return fail(RL_ERR_INVALID_SHAPE, "residual buffer does not hold %zu-byte elements",
+                    sizeof(T));
+    if (rl_status st = validate(x, weight, rows, hidden, eps, sizeof(T))) return st;
+    if (rl_status st = check_output(sum_out, x->len, sizeof(T), "add")) return st;
+    if (rl_status st = check_output(norm_out, x->len, sizeof(T), "RMSNorm")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    if (rows == 0) return RL_OK;
+    return launch_rmsnorm<T, true>(ctx, name, static_cast<const T*>(x->data),
+                                   static_cast<const T*>(residual->data),
+                                   static_cast<const T*>(weight->data),
+                                   static_cast<T*>(sum_out->data), static_cast<T*>(norm_out->data),
+                                   rows, hidden, eps);
+}
+
+}  // namespace
+}  // namespace rl
+
+using namespace rl;
+
+extern "C" {
+
+rl_status rl_rmsnorm_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* weight,
+                         uint64_t rows, uint64_t hidden, float eps, const rl_buffer* out) {
+    return rmsnorm_entry<float>(ctx, "rmsnorm_f32", input, weight, rows, hidden, eps, out);
+}
+
+rl_status rl_rmsnorm_f16(rl_context* ctx, const rl_buffer* input, const rl_buffer* weight,
+                         uint64_t rows, uint64_t hidden, float eps, const rl_buffer* out) {
+    return rmsnorm_entry<half_t>(ctx, "rmsnorm_f16", input, weight, rows, hidden, eps, out);
+}
+
+rl_status rl_add_rmsnorm_f32(rl_context* ctx, const rl_buffer* x, const rl_buffer* residual,
+                             const rl_buffer* weight, uint64_t rows, uint64_t hidden, float eps,
+                             const rl_buffer* sum_out, const rl_buffer* norm_out) {
+    return add_rmsnorm_entry<float>(ctx, "add_rmsnorm_f32", x, residual, weight, rows, hidden,
+                                    eps, sum_out, norm_out);
+}
+
+rl_status rl_add_rmsnorm_f16(rl_context* ctx, const rl_buffer* x, const rl_buffer* residual,
+                             const rl_buffer* weight, uint64_t rows, uint64_t hidden, float eps,
+                             const rl_buffer* sum_out, const rl_buffer* norm_out) {
+    return add_rmsnorm_entry<half_t>(ctx, "add_rmsnorm_f16", x, residual, weight, rows, hidden,
+                                     eps, sum_out, norm_out);
+}
+
+}  // extern "C"

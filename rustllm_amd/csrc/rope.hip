@@ -1,0 +1,299 @@
+// rope.hip -- rotary position embedding for gfx950.
+//
+// For row r of [..., S, D] at position p = (r mod S) + start and pair
+// i < D/2: (a, b) = (x[i], x[i + D/2]) -> (a*c - b*s, b*c + a*s) with
+// c, s = table[p, i] (kernels/rope.metal:23-63, 82-96).  Each thread rotates
+// a pack of N pairs: one 16-byte-or-smaller load from each half of the row
+// plus N cos and N sin values.  The f32 tables are [table_rows, D/2] (1 MiB
+// for 4096 x 32 x 2) and stay in L2, so HBM traffic is the input and output
+// rows only.  Contraction into FMA is off: each product and difference is
+// rounded once, as in the reference expression.
+//
+// The input may be a strided view whose innermost stride is 1 (the
+// [1, H, S, D] permute of [1, S, H, D] the attention path rotates): the
+// gather that ops::rope_encode does first with contiguous_encode
+// (src/ops/rope.rs:345) happens in the same pass, rows being decoded with
+// 32-bit multiply-high division.
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace rl {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxRank = 16;
+
+// Row dims of the view (all but the innermost), innermost first; dim[0] is
+// the sequence dim.
+struct RowDims {
+    uint32_t rank;
+    FastDiv dim[kMaxRank];
+    uint64_t stride[kMaxRank];
+};
+
+template <typename T, int N, int UNROLL>
+__global__ __launch_bounds__(kThreads) void k_rope(const T* __restrict__ src,
+                                                   const float* __restrict__ cos_table,
+                                                   const float* __restrict__ sin_table,
+                                                   T* __restrict__ out, uint32_t n_items,
+                                                   FastDiv packs_per_row, RowDims rd,
+                                                   uint32_t half_dim, uint32_t start) {
+    typedef typename VecOf<T, N>::type V;
+    typedef typename VecOf<float, N>::type VF;
+    const uint64_t tile = uint64_t(kThreads) * UNROLL;
+    const uint64_t step = uint64_t(gridDim.x) * tile;
+    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_items;
+         base += step) {
+        V a[UNROLL], b[UNROLL];
+        VF c[UNROLL], s[UNROLL];
+        uint64_t dst_off[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_items) {
+                uint32_t row, pp;
+                packs_per_row.divmod(uint32_t(i), row, pp);
+                // Decode the row: the innermost row dim is the sequence position.
+                uint64_t src_off = 0;
+                uint32_t position = 0;
+                uint32_t rest = row;
+                for (uint32_t d = 0; d < rd.rank; ++d) {
+                    uint32_t q, r;
+                    rd.dim[d].divmod(rest, q, r);
+                    if (d == 0) position = r;
+                    src_off += uint64_t(r) * rd.stride[d];
+                    rest = q;
+                }
+                const uint32_t pair = pp * N;
+                const uint64_t t = uint64_t(start + position) * half_dim + pair;
+                a[u] = *reinterpret_cast<const V*>(src + src_off + pair);
+                b[u] = *reinterpret_cast<const V*>(src + src_off + half_dim + pair);
+                c[u] = *reinterpret_cast<const VF*>(cos_table + t);
+                s[u] = *reinterpret_cast<const VF*>(sin_table + t);
+                dst_off[u] = uint64_t(row) * (2 * half_dim) + pair;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint64_t i = base + uint64_t(u) * kThreads;
+            if (i < n_items) {
+                V o1, o2;
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    const float first = to_float(a[u][j]);
+                    const float second = to_float(b[u][j]);
+                    o1[j] = from_float<T>(first * c[u][j] - second * s[u][j]);
+                    o2[j] = from_float<T>(second * c[u][j] + first * s[u][j]);
+                }
+                store_stream(reinterpret_cast<V*>(out + dst_off[u]), o1);
+                store_stream(reinterpret_cast<V*>(out + dst_off[u] + half_dim), o2);
+            }
+        }
+    }
+}
+
+inline unsigned grid_for(uint64_t items, uint64_t per_block) {
+    uint64_t blocks = ceil_div(items, per_block);
+    if (blocks < 1) blocks = 1;
+    if (blocks > (1u << 30)) blocks = 1u << 30;
+    return unsigned(blocks);
+}
+
+// dims/strides: the view, outermost first, rank >= 2, strides[rank-1] == 1.
+template <typename T>
+rl_status launch_rope(rl_context* ctx, const char* name, const T* src, const uint64_t* dims,
+                      const uint64_t* strides, uint32_t rank, const float* cos_table,
+                      const float* sin_table, uint64_t start, T* out) {
+    if (rl_status st = activate(ctx)) return st;
+    const uint64_t head_dim = dims[rank - 1];
+    const uint64_t half = head_dim / 2;
+    uint64_t rows = 1;
+    for (uint32_t d = 0; d + 1 < rank; ++d) rows *= dims[d];
+    // Widest pack of pairs (<= 16 B of T, <= 4 or 8 lanes) that keeps every
+    // access aligned.
+    int n = 16 / int(sizeof(T));
+    while (n > 1) {
+        bool ok = half % n == 0 && aligned_to(src, n * sizeof(T)) &&
+                  aligned_to(out, n * sizeof(T)) && aligned_to(cos_table, n * 4) &&
+                  aligned_to(sin_table, n * 4);
+        for (uint32_t d = 0; d + 1 < rank && ok; ++d) ok = strides[d] % n == 0;
+        if (ok) break;
+        n >>= 1;
+    }
+    RowDims rd{};
+    rd.rank = rank - 1;
+    for (uint32_t d = 0; d + 1 < rank; ++d) {
+        rd.dim[d] = FastDiv(uint32_t(dims[rank - 2 - d]));
+        rd.stride[d] = strides[rank - 2 - d];
+    }
+    const uint64_t n_items = rows * (half / n);
+    const FastDiv ppr(uint32_t(half / n));
+    constexpr int U = 2;
+    const dim3 grid(grid_for(n_items, uint64_t(kThreads) * U)), block(kThreads);
+    const uint32_t h32 = uint32_t(half), s32 = uint32_t(start), ni = uint32_t(n_items);
+    switch (n) {
+        case 8:
+            hipLaunchKernelGGL((k_rope<T, 8, U>), grid, block, 0, ctx->stream, src, cos_table,
+                               sin_table, out, ni, ppr, rd, h32, s32);
+            break;
+        case 4:
+            hipLaunchKernelGGL((k_rope<T, 4, U>), grid, block, 0, ctx->stream, src, cos_table,
+                               sin_table, out, ni, ppr, rd, h32, s32);
+            break;
+        case 2:
+            hipLaunchKernelGGL((k_rope<T, 2, U>), grid, block, 0, ctx->stream, src, cos_table,
+                               sin_table, out, ni, ppr, rd, h32, s32);
+            break;
+        default:
+            hipLaunchKernelGGL((k_rope<T, 1, U>), grid, block, 0, ctx->stream, src, cos_table,
+                               sin_table, out, ni, ppr, rd, h32, s32);
+            break;
+    }
+    return after_launch(ctx, name);
+}
+
+rl_status check_tables(const rl_buffer* cos_table, const rl_buffer* sin_table,
+                       uint64_t table_rows, uint64_t half, uint64_t start, uint64_t seq_len) {
+    if (rl_status st = check_buffer(cos_table, "cos table")) return st;
+    if (rl_status st = check_buffer(sin_table, "sin table")) return st;
+    // ops::rope_encode (src/ops/rope.rs:329-343): equal [rows, D/2] f32 tables
+    // covering positions start .. start + seq_len.
+    if (cos_table->byte_len != cos_table->len * 4 || sin_table->byte_len != sin_table->len * 4)
+        return fail(RL_ERR_UNSUPPORTED_DTYPE, "RoPE requires F32 cos/sin tables");
+    if (table_rows > UINT64_MAX / half || cos_table->len != table_rows * half ||
+        sin_table->len != cos_table->len)
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE cos/sin tables must have equal rank-2 shapes");
+    if (start > UINT64_MAX - seq_len || start + seq_len > table_rows)
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE cos/sin table shape or position range is invalid");
+    return RL_OK;
+}
+
+// src/ops/rope.rs:38-151 / :177-277 in order, plus the table bounds above.
+template <typename T>
+rl_status rope_entry(rl_context* ctx, const char* name, const rl_buffer* input,
+                     const rl_buffer* cos_table, const rl_buffer* sin_table, uint64_t seq_len,
+                     uint64_t head_dim, uint64_t start, const rl_buffer* out) {
+    if (rl_status st = check_buffer(input, "input")) return st;
+    if (head_dim == 0 || head_dim % 2 != 0)
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE head dimension must be positive and even, got %llu",
+                    (unsigned long long)head_dim);
+    if (seq_len == 0) return fail(RL_ERR_INVALID_SHAPE, "RoPE sequence length cannot be zero");
+    if (input->len % head_dim != 0)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "RoPE input length %llu is not divisible by head dimension %llu",
+                    (unsigned long long)input->len, (unsigned long long)head_dim);
+    const uint64_t half = head_dim / 2;
+    const uint64_t rows = input->len / head_dim;
+    if (rows % seq_len != 0)
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE input rows are incompatible with sequence length");
+    if (input->byte_len < input->len * sizeof(T))
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE input does not hold %zu-byte elements", sizeof(T));
+    if (rl_status st = check_output(out, input->len, sizeof(T), "RoPE")) return st;
+    if (seq_len > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE sequence length exceeds u32");
+    if (head_dim > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "RoPE head dimension exceeds u32");
+    if (start > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "RoPE start position exceeds u32");
+    if (rows * half > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "RoPE work size exceeds u32");
+    const uint64_t table_rows = cos_table ? (cos_table->len / half) : 0;
+    if (rl_status st = check_tables(cos_table, sin_table, table_rows, half, start, seq_len))
+        return st;
+    if (rl_status st = require_context(ctx)) return st;
+    if (input->len == 0) return RL_OK;
+    const uint64_t dims[3] = {rows / seq_len, seq_len, head_dim};
+    const uint64_t strides[3] = {seq_len * head_dim, head_dim, 1};
+    return launch_rope<T>(ctx, name, static_cast<const T*>(input->data), dims, strides, 3,
+                          static_cast<const float*>(cos_table->data),
+                          static_cast<const float*>(sin_table->data), start,
+                          static_cast<T*>(out->data));
+}
+
+// ops::rope_encode on a view (src/ops/rope.rs:303-370): the Tensor-level
+// checks (rank >= 2, even head_dim, tables) and the view's own bounds.
+template <typename T>
+rl_status rope_strided_entry(rl_context* ctx, const char* name, const rl_buffer* src,
+                             const uint64_t* dims, const uint64_t* strides, uint32_t rank,
+                             const rl_buffer* cos_table, const rl_buffer* sin_table,
+                             uint64_t table_rows, uint64_t start, const rl_buffer* out) {
+    if (rl_status st = check_buffer(src, "input")) return st;
+    if (dims == nullptr || strides == nullptr)
+        return fail(RL_ERR_INVALID_ARGUMENT, "dims or strides is null");
+    if (rank < 2)
+        return fail(RL_ERR_INVALID_DIMENSION,
+                    "RoPE expects [..., sequence, head_dim], got rank %u", rank);
+    if (rank > kMaxRank + 1) return fail(RL_ERR_INVALID_SHAPE, "tensor rank exceeds %d", kMaxRank + 1);
+    const uint64_t seq_len = dims[rank - 2], head_dim = dims[rank - 1];
+    if (head_dim == 0 || head_dim % 2 != 0)
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE head dimension must be positive and even, got %llu",
+                    (unsigned long long)head_dim);
+    const uint64_t half = head_dim / 2;
+    uint64_t numel = 1;
+    for (uint32_t d = 0; d < rank; ++d) {
+        if (dims[d] == 0)
+            return fail(RL_ERR_INVALID_SHAPE, "shape dimensions must be greater than zero");
+        if (numel > UINT64_MAX / dims[d])
+            return fail(RL_ERR_INVALID_SHAPE, "RoPE work size exceeds u32");
+        numel *= dims[d];
+    }
+    if (rl_status st = check_tables(cos_table, sin_table, table_rows, half, start, seq_len))
+        return st;
+    if (strides[rank - 1] != 1)
+        return fail(RL_ERR_NON_CONTIGUOUS, "RoPE view must have a unit innermost stride");
+    if (src->byte_len < src->len * sizeof(T))
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE input does not hold %zu-byte elements", sizeof(T));
+    for (uint32_t d = 0; d < rank; ++d)
+        if (dims[d] > UINT32_MAX || strides[d] > UINT32_MAX)
+            return fail(RL_ERR_INVALID_SHAPE, "shape dimension exceeds u32");
+    if (numel / 2 > UINT32_MAX || start > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE work size exceeds u32");
+    unsigned __int128 last = 0;
+    for (uint32_t d = 0; d < rank; ++d) last += (unsigned __int128)(dims[d] - 1) * strides[d];
+    if (last >= src->len)
+        return fail(RL_ERR_INVALID_SHAPE, "view reaches past the end of its %llu-element buffer",
+                    (unsigned long long)src->len);
+    if (rl_status st = check_output(out, numel, sizeof(T), "RoPE")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_rope<T>(ctx, name, static_cast<const T*>(src->data), dims, strides, rank,
+                          static_cast<const float*>(cos_table->data),
+                          static_cast<const float*>(sin_table->data), start,
+                          static_cast<T*>(out->data));
+}
+
+}  // namespace
+}  // namespace rl
+
+using namespace rl;
+
+extern "C" {
+
+rl_status rl_rope_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* cos_table,
+                      const rl_buffer* sin_table, uint64_t seq_len, uint64_t head_dim,
+                      uint64_t start_pos, const rl_buffer* out) {
+    return rope_entry<float>(ctx, "rope_f32", input, cos_table, sin_table, seq_len, head_dim,
+                             start_pos, out);
+}
+
+rl_status rl_rope_f16(rl_context* ctx, const rl_buffer* input, const rl_buffer* cos_table,
+                      const rl_buffer* sin_table, uint64_t seq_len, uint64_t head_dim,
+                      uint64_t start_pos, const rl_buffer* out) {
+    return rope_entry<half_t>(ctx, "rope_f16", input, cos_table, sin_table, seq_len, head_dim,
+                              start_pos, out);
+}
+
+rl_status rl_rope_strided_f32(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                              const uint64_t* strides, uint32_t rank, const rl_buffer* cos_table,
+                              const rl_buffer* sin_table, uint64_t table_rows,
+                              uint64_t start_pos, const rl_buffer* out) {
+    return rope_strided_entry<float>(ctx, "rope_strided_f32", src, dims, strides, rank, cos_table,
+                                     sin_table, table_rows, start_pos, out);
+}
+
+rl_status rl_rope_strided_f16(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                              const uint64_t* strides, uint32_t rank, const rl_buffer* cos_table,
+                              const rl_buffer* sin_table, uint64_t table_rows,
+                              uint64_t start_pos, const rl_buffer* out) {
+    return rope_strided_entry<half_t>(ctx, "rope_strided_f16", src, dims, strides, rank,
+                                      cos_table, sin_table, table_rows, start_pos, out);
+}
+
+}  // extern "C"

@@ -1,0 +1,529 @@
+// softmax.hip -- row softmax, attention scale/mask, and the two fused, for
+// gfx950.
+//
+// Softmax (kernels/softmax.metal) reads each row three times through a
+// 256-thread group with two 8-barrier shared-memory trees.  Here a row of up
+// to 64 x 16 packs (4096 f32 / 8192 f16) is owned by one wave64 and held in
+// VGPRs: one HBM read, a butterfly max, exp in registers, a butterfly sum,
+// one write.  Longer rows use a whole 256-thread block per row (LDS only for
+// the cross-wave step) while they fit its registers, and beyond that a
+// streaming kernel with an online max/sum (m, s) merge and a second read.
+//
+// Scale/mask + softmax fused (the adjacent calls at nn/attention.rs:233-240):
+// for query row q the keys past start + q are masked, so their scores are
+// never read; the kept scores are scaled (and, for f16, rounded to f16 as
+// the scale/mask kernel's output would be) before the softmax.  Masked
+// outputs are 0 * (1 / sum): exact zeros, or NaN exactly where the two-op
+// composition gives NaN.
+//
+// The standalone scale/mask op also skips reading masked scores: its output
+// there is -inf whatever the input.
+#include "common.hpp"
+
+namespace rl {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+constexpr int kRowsPerBlock = kThreads / kWave;
+
+struct MaskParams {
+    float scale;
+    FastDiv query_len;
+    uint32_t start;
+};
+
+// Score as the scale/mask op would store it, widened back to float.
+template <typename T>
+__device__ inline float scaled_score(T raw, float scale) {
+    return to_float(from_float<T>(to_float(raw) * scale));
+}
+
+template <typename T>
+__device__ inline bool is_f16() {
+    return sizeof(T) == 2;
+}
+
+// Number of unmasked keys of a row: keys 0 ..= start + q are kept.
+__device__ inline uint32_t kept_keys(uint32_t row, uint32_t width, const MaskParams& mp) {
+    uint32_t q, qi;
+    mp.query_len.divmod(row, q, qi);
+    uint64_t kept = uint64_t(mp.start) + qi + 1;
+    return kept < width ? uint32_t(kept) : width;
+}
+
+// ------------------------------------------------ one wave per row, in VGPRs
+
+template <typename T, int N, int NV, bool MASK>
+__global__ __launch_bounds__(kThreads) void k_softmax_wave(const T* __restrict__ in,
+                                                           T* __restrict__ out, uint32_t rows,
+                                                           uint32_t width, MaskParams mp) {
+    typedef typename VecOf<T, N>::type V;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t row = blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
+    if (row >= rows) return;  // whole wave leaves together
+    const uint32_t w_packs = width / N;
+    const uint64_t row_off = uint64_t(row) * w_packs;
+    const V* src = reinterpret_cast<const V*>(in) + row_off;
+    V* dst = reinterpret_cast<V*>(out) + row_off;
+    const uint32_t kept = MASK ? kept_keys(row, width, mp) : width;
+
+    float v[NV][N];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = lane + k * kWave;
+        if (p < w_packs && (!MASK || p * N < kept)) {
+            V raw = load_stream(src + p);
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float f;
+                if constexpr (MASK)
+                    f = (p * N + j < kept) ? scaled_score(raw[j], mp.scale) : -INFINITY;
+                else
+                    f = to_float(raw[j]);
+                v[k][j] = f;
+                m = fmaxf(m, f);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) v[k][j] = -INFINITY;
+        }
+    }
+    m = wave_max(m);
+    if (is_f16<T>() && m == -INFINITY) {  // softmax.metal:166-173
+        V z;
+#pragma unroll
+        for (int j = 0; j < N; ++j) z[j] = from_float<T>(0.0f);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const uint32_t p = lane + k * kWave;
+            if (p < w_packs) store_stream(dst + p, z);
+        }
+        return;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = lane + k * kWave;
+        if (p < w_packs && (!MASK || p * N < kept)) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float e = expf(v[k][j] - m);
+                v[k][j] = e;
+                s += e;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) v[k][j] = 0.0f;
+        }
+    }
+    s = wave_sum(s);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = lane + k * kWave;
+        if (p < w_packs) {
+            V o;
+#pragma unroll
+            for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
+            store_stream(dst + p, o);
+        }
+    }
+}
+
+// --------------------------------------- 256 threads per row, in VGPRs + LDS
+
+__device__ inline float block_max(float v, float* lds) {
+    v = wave_max(v);
+    __syncthreads();  // lds may still be read from a previous reduction
+    if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float r = lds[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / kWave; ++w) r = fmaxf(r, lds[w]);
+    return r;
+}
+
+__device__ inline float block_sum(float v, float* lds) {
+    v = wave_sum(v);
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float r = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) r += lds[w];
+    return r;
+}
+
+template <typename T, int N, int NV, bool MASK>
+__global__ __launch_bounds__(kThreads) void k_softmax_block(const T* __restrict__ in,
+                                                            T* __restrict__ out, uint32_t rows,
+                                                            uint32_t width, MaskParams mp) {
+    typedef typename VecOf<T, N>::type V;
+    __shared__ float lds[kThreads / kWave];
+    // Rows are uniform per block, so the barriers inside stay uniform too.
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const uint32_t w_packs = width / N;
+    const uint64_t row_off = uint64_t(row) * w_packs;
+    const V* src = reinterpret_cast<const V*>(in) + row_off;
+    V* dst = reinterpret_cast<V*>(out) + row_off;
+    const uint32_t kept = MASK ? kept_keys(row, width, mp) : width;
+
+    float v[NV][N];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = threadIdx.x + k * kThreads;
+        if (p < w_packs && (!MASK || p * N < kept)) {
+            V raw = load_stream(src + p);
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float f;
+                if constexpr (MASK)
+                    f = (p * N + j < kept) ? scaled_score(raw[j], mp.scale) : -INFINITY;
+                else
+                    f = to_float(raw[j]);
+                v[k][j] = f;
+                m = fmaxf(m, f);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) v[k][j] = -INFINITY;
+        }
+    }
+    m = block_max(m, lds);
+    if (is_f16<T>() && m == -INFINITY) {
+        V z;
+#pragma unroll
+        for (int j = 0; j < N; ++j) z[j] = from_float<T>(0.0f);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const uint32_t p = threadIdx.x + k * kThreads;
+            if (p < w_packs) store_stream(dst + p, z);
+        }
+        continue;  // uniform across the block: every thread saw the same m
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = threadIdx.x + k * kThreads;
+        if (p < w_packs && (!MASK || p * N < kept)) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float e = expf(v[k][j] - m);
+                v[k][j] = e;
+                s += e;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) v[k][j] = 0.0f;
+        }
+    }
+    s = block_sum(s, lds);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = threadIdx.x + k * kThreads;
+        if (p < w_packs) {
+            V o;
+#pragma unroll
+            for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
+            store_stream(dst + p, o);
+        }
+    }
+    }
+}
+
+// ------------------------------------- streaming rows of any width (2 reads)
+
+// Online merge of (max, sum of exp(x - max)) pairs.
+// The new maximum's own term is exp(x - x): 1, or NaN for x = +inf exactly
+// as exp(inf - inf) in the reference's sum.
+__device__ inline void online_add(float& m, float& s, float x) {
+    if (x > m) {
+        s = s * expf(m - x) + expf(x - x);
+        m = x;
+    } else {
+        s += expf(x - m);
+    }
+}
+
+template <typename T, bool MASK>
+__global__ __launch_bounds__(kThreads) void k_softmax_stream(const T* __restrict__ in,
+                                                             T* __restrict__ out, uint32_t rows,
+                                                             uint32_t width, MaskParams mp) {
+    __shared__ float lds_m[kThreads / kWave];
+    __shared__ float lds_s[kThreads / kWave];
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    __syncthreads();  // the previous row's lds reads are done
+    const uint64_t off = uint64_t(row) * width;
+    const uint32_t kept = MASK ? kept_keys(row, width, mp) : width;
+    auto score = [&](uint32_t i) -> float {
+        if constexpr (MASK) return scaled_score(in[off + i], mp.scale);
+        return to_float(in[off + i]);
+    };
+    // Pass 1: plain max first; the sum uses it, so no rescaling is needed
+    // unless a lane's running max moves (online_add handles that case).
+    float m = -INFINITY, s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < kept; i += kThreads) {
+        float x = score(i);
+        // A -inf score adds exp(-inf - m) = 0 once the row max is finite; if
+        // the max stays -inf the row is handled as a whole below.
+        if (x == -INFINITY) continue;
+        online_add(m, s, x);
+    }
+    // Cross-lane merge of (m, s).
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        float om = __shfl_xor(m, offset, 64);
+        float os = __shfl_xor(s, offset, 64);
+        float nm = fmaxf(m, om);
+        float a = (m == -INFINITY) ? 0.0f : s * expf(m - nm);
+        float b = (om == -INFINITY) ? 0.0f : os * expf(om - nm);
+        m = nm;
+        s = a + b;
+    }
+    if (threadIdx.x % kWave == 0) {
+        lds_m[threadIdx.x / kWave] = m;
+        lds_s[threadIdx.x / kWave] = s;
+    }
+    __syncthreads();
+    float gm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) gm = fmaxf(gm, lds_m[w]);
+    float gs = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w)
+        gs += (lds_m[w] == -INFINITY) ? 0.0f : lds_s[w] * expf(lds_m[w] - gm);
+    if (gm == -INFINITY) {
+        // Every kept score is -inf: f16 writes zeros (softmax.metal:166-173),
+        // f32 yields NaN as exp(-inf - -inf) does in the reference.
+        const T fill = from_float<T>(is_f16<T>() ? 0.0f : __builtin_nanf(""));
+        for (uint32_t i = threadIdx.x; i < width; i += kThreads) out[off + i] = fill;
+        continue;
+    }
+    // NaN scores make gs NaN, and every output NaN, as in the reference.
+    const float inv = 1.0f / gs;
+    for (uint32_t i = threadIdx.x; i < width; i += kThreads) {
+        float e = (i < kept) ? expf(score(i) - gm) : 0.0f;
+        out[off + i] = from_float<T>(e * inv);
+    }
+    }
+}
+
+// ------------------------------------------------------ scale/mask alone
+
+template <typename T, int N>
+__global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ in,
+                                                         T* __restrict__ out, uint32_t rows,
+                                                         uint32_t width, MaskParams mp) {
+    typedef typename VecOf<T, N>::type V;
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const uint32_t w_packs = width / N;
+    const uint64_t row_off = uint64_t(row) * w_packs;
+    const V* src = reinterpret_cast<const V*>(in) + row_off;
+    V* dst = reinterpret_cast<V*>(out) + row_off;
+    const uint32_t kept = kept_keys(row, width, mp);
+    for (uint32_t p = threadIdx.x; p < w_packs; p += kThreads) {
+        V o;
+        if (p * N < kept) {
+            V raw = load_stream(src + p);
+#pragma unroll
+            for (int j = 0; j < N; ++j)
+                o[j] = (p * N + j < kept) ? from_float<T>(to_float(raw[j]) * mp.scale)
+                                          : from_float<T>(-INFINITY);
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) o[j] = from_float<T>(-INFINITY);
+        }
+        store_stream(dst + p, o);
+    }
+    }
+}
+
+// ---------------------------------------------------------------- launch
+
+// Blocks for the one-block-per-row kernels, which loop when rows exceed it.
+inline unsigned row_grid(uint64_t rows) {
+    return unsigned(rows < (uint64_t(1) << 20) ? rows : (uint64_t(1) << 20));
+}
+
+template <typename T, bool MASK>
+rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out, uint64_t rows,
+                         uint64_t width, MaskParams mp) {
+    if (rl_status st = activate(ctx)) return st;
+    constexpr int N = 16 / sizeof(T);
+    const uint32_t r32 = uint32_t(rows), w32 = uint32_t(width);
+    const bool packs_ok = width % N == 0 && aligned_to(in, 16) && aligned_to(out, 16);
+    const uint64_t w_packs = width / N;
+    if (packs_ok && w_packs <= 16 * kWave) {
+        const dim3 grid(unsigned(ceil_div(rows, kRowsPerBlock))), block(kThreads);
+#define RL_SOFTMAX_WAVE(NV)                                                                    \
+    hipLaunchKernelGGL((k_softmax_wave<T, N, NV, MASK>), grid, block, 0, ctx->stream, in, out, \
+                       r32, w32, mp)
+        if (w_packs <= 1 * kWave)
+            RL_SOFTMAX_WAVE(1);
+        else if (w_packs <= 2 * kWave)
+            RL_SOFTMAX_WAVE(2);
+        else if (w_packs <= 4 * kWave)
+            RL_SOFTMAX_WAVE(4);
+        else if (w_packs <= 8 * kWave)
+            RL_SOFTMAX_WAVE(8);
+        else
+            RL_SOFTMAX_WAVE(16);
+#undef RL_SOFTMAX_WAVE
+    } else if (packs_ok && w_packs <= 16 * kThreads) {
+        const dim3 grid(row_grid(rows)), block(kThreads);
+#define RL_SOFTMAX_BLOCK(NV)                                                                    \
+    hipLaunchKernelGGL((k_softmax_block<T, N, NV, MASK>), grid, block, 0, ctx->stream, in, out, \
+                       r32, w32, mp)
+        if (w_packs <= 8 * kThreads)
+            RL_SOFTMAX_BLOCK(8);
+        else
+            RL_SOFTMAX_BLOCK(16);
+#undef RL_SOFTMAX_BLOCK
+    } else {
+        hipLaunchKernelGGL((k_softmax_stream<T, MASK>), dim3(row_grid(rows)), dim3(kThreads), 0,
+                           ctx->stream, in, out, r32, w32, mp);
+    }
+    return after_launch(ctx, name);
+}
+
+template <typename T>
+rl_status launch_scale_mask(rl_context* ctx, const char* name, const T* in, T* out,
+                            uint64_t rows, uint64_t width, MaskParams mp) {
+    if (rl_status st = activate(ctx)) return st;
+    constexpr int N = 16 / sizeof(T);
+    const bool packs_ok = width % N == 0 && aligned_to(in, 16) && aligned_to(out, 16);
+    if (packs_ok)
+        hipLaunchKernelGGL((k_scale_mask<T, N>), dim3(row_grid(rows)), dim3(kThreads), 0,
+                           ctx->stream, in, out, uint32_t(rows), uint32_t(width), mp);
+    else
+        hipLaunchKernelGGL((k_scale_mask<T, 1>), dim3(row_grid(rows)), dim3(kThreads), 0,
+                           ctx->stream, in, out, uint32_t(rows), uint32_t(width), mp);
+    return after_launch(ctx, name);
+}
+
+// src/ops/softmax.rs:91-108 plus the u32 width check of :130-131.
+rl_status validate_softmax(const rl_buffer* input, uint64_t rows, uint64_t width, uint64_t es) {
+    if (rl_status st = check_buffer(input, "input")) return st;
+    if (rows == 0 || width == 0)
+        return fail(RL_ERR_INVALID_SHAPE, "Softmax rows and width must be greater than zero");
+    if (rows > UINT64_MAX / width || input->len != rows * width ||
+        input->byte_len != input->len * es)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "Softmax input has %llu elements (%llu bytes), expected %llu elements of %llu "
+                    "bytes",
+                    (unsigned long long)input->len, (unsigned long long)input->byte_len,
+                    (unsigned long long)(rows > UINT64_MAX / width ? 0 : rows * width),
+                    (unsigned long long)es);
+    if (width > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "Softmax width exceeds u32");
+    if (rows > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "Softmax row count exceeds u32");
+    return RL_OK;
+}
+
+// src/ops/attention_scale_mask.rs:120-161 plus the u32 checks of :349-352.
+rl_status validate_mask(const rl_buffer* input, float scale, uint64_t query_len,
+                        uint64_t key_len, uint64_t start, uint64_t es) {
+    if (rl_status st = check_buffer(input, "input")) return st;
+    if (query_len == 0 || key_len == 0)
+        return fail(RL_ERR_INVALID_SHAPE, "attention query/key length cannot be zero");
+    if (!(scale > 0.0f) || scale == INFINITY)
+        return fail(RL_ERR_INVALID_SHAPE, "attention scale must be positive and finite, got %g",
+                    double(scale));
+    if (start > UINT64_MAX - query_len)
+        return fail(RL_ERR_INVALID_SHAPE, "attention query position overflow");
+    const uint64_t query_end = start + query_len;
+    if (query_end > key_len)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "attention query range [%llu, %llu) exceeds key length %llu",
+                    (unsigned long long)start, (unsigned long long)query_end,
+                    (unsigned long long)key_len);
+    const bool fits = query_len <= UINT64_MAX / key_len;
+    if (!fits || input->len % (query_len * key_len) != 0 || input->byte_len != input->len * es)
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "attention score buffer has %llu elements (%llu bytes), incompatible with "
+                    "query_len=%llu, key_len=%llu and %llu byte elements",
+                    (unsigned long long)input->len, (unsigned long long)input->byte_len,
+                    (unsigned long long)query_len, (unsigned long long)key_len,
+                    (unsigned long long)es);
+    if (query_len > UINT32_MAX || key_len > UINT32_MAX || start > UINT32_MAX ||
+        input->len > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "attention dimension exceeds u32");
+    return RL_OK;
+}
+
+template <typename T>
+rl_status softmax_entry(rl_context* ctx, const char* name, const rl_buffer* input, uint64_t rows,
+                        uint64_t width, const rl_buffer* out) {
+    if (rl_status st = validate_softmax(input, rows, width, sizeof(T))) return st;
+    if (rl_status st = check_output(out, input->len, sizeof(T), "Softmax")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_softmax<T, false>(ctx, name, static_cast<const T*>(input->data),
+                                    static_cast<T*>(out->data), rows, width,
+                                    MaskParams{1.0f, FastDiv(1), 0});
+}
+
+template <typename T>
+rl_status scale_mask_entry(rl_context* ctx, const char* name, const rl_buffer* input,
+                           float scale, uint64_t query_len, uint64_t key_len, uint64_t start,
+                           const rl_buffer* out, bool fused) {
+    if (rl_status st = validate_mask(input, scale, query_len, key_len, start, sizeof(T)))
+        return st;
+    if (rl_status st = check_output(out, input->len, sizeof(T), "attention")) return st;
+    if (rl_status st = require_context(ctx)) return st;
+    if (input->len == 0) return RL_OK;
+    const uint64_t rows = input->len / key_len;
+    const MaskParams mp{scale, FastDiv(uint32_t(query_len)), uint32_t(start)};
+    const T* in = static_cast<const T*>(input->data);
+    T* o = static_cast<T*>(out->data);
+    if (fused) return launch_softmax<T, true>(ctx, name, in, o, rows, key_len, mp);
+    return launch_scale_mask<T>(ctx, name, in, o, rows, key_len, mp);
+}
+
+}  // namespace
+}  // namespace rl
+
+using namespace rl;
+
+extern "C" {
+
+rl_status rl_softmax_f32(rl_context* ctx, const rl_buffer* input, uint64_t rows, uint64_t width,
+                         const rl_buffer* out) {
+    return softmax_entry<float>(ctx, "softmax_f32", input, rows, width, out);
+}
+
+rl_status rl_softmax_f16(rl_context* ctx, const rl_buffer* input, uint64_t rows, uint64_t width,
+                         const rl_buffer* out) {
+    return softmax_entry<half_t>(ctx, "softmax_f16", input, rows, width, out);
+}
+
+rl_status rl_attention_scale_mask_f32(rl_context* ctx, const rl_buffer* input, float scale,
+                                      uint64_t query_len, uint64_t key_len,
+                                      uint64_t query_start_pos, const rl_buffer* out) {
+    return scale_mask_entry<float>(ctx, "attention_scale_mask_f32", input, scale, query_len,
+                                   key_len, query_start_pos, out, false);
+}
+
+rl_status rl_attention_scale_mask_f16(rl_context* ctx, const rl_buffer* input, float scale,
+                                      uint64_t query_len, uint64_t key_len,
+                                      uint64_t query_start_pos, const rl_buffer* out) {
+    return scale_mask_entry<half_t>(ctx, "attention_scale_mask_f16", input, scale, query_len,
+                                    key_len, query_start_pos, out, false);
+}
+
+rl_status rl_attention_softmax_f32(rl_context* ctx, const rl_buffer* input, float scale,
+                                   uint64_t query_len, uint64_t key_len,
+                                   uint64_t query_start_pos, const rl_buffer* out) {
+    return scale_mask_entry<float>(ctx, "attention_softmax_f32", input, scale, query_len,
+                                   key_len, query_start_pos, out, true);
+}
+
+rl_status rl_attention_softmax_f16(rl_context* ctx, const rl_buffer* input, float scale,
+                                   uint64_t query_len, uint64_t key_len,
+                                   uint64_t query_start_pos, const rl_buffer* out) {
+    return scale_mask_entry<half_t>(ctx, "attention_softmax_f16", input, scale, query_len,
+                                    key_len, query_start_pos, out, true);
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+"""Comparison helpers shared by the tests (tolerances as the north star states them)."""
+
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def kats() -> dict:
+    with open(os.path.join(GOLDEN, "reference_kats.json")) as f:
+        data = json.load(f)
+    return {k: v for k, v in data.items() if not k.startswith("_")}
+
+
+def floats(values) -> np.ndarray:
+    """JSON numbers with "inf"/"-inf"/"nan" strings -> float32."""
+    return np.array([float(v) for v in values], dtype=np.float32)
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint16 if a.dtype == np.float16 else np.uint32)
+
+
+def assert_bitexact(got, ref, what=""):
+    """Identical bit patterns; NaNs only need to be NaN on both sides."""
+    got, ref = np.asarray(got), np.asarray(ref)
+    assert got.shape == ref.shape and got.dtype == ref.dtype, (got.shape, ref.shape, got.dtype)
+    gn, rn = np.isnan(got), np.isnan(ref)
+    assert np.array_equal(gn, rn), f"{what}: NaN positions differ"
+    bad = (bits(got) != bits(ref)) & ~gn
+    if bad.any():
+        i = int(np.flatnonzero(bad.ravel())[0])
+        raise AssertionError(f"{what}: {int(bad.sum())} mismatches, first at {i}: "
+                             f"got {got.ravel()[i]!r} ref {ref.ravel()[i]!r}")
+
+
+def max_rel_err(got, ref, floor) -> float:
+    """max |got - ref| / max(|ref|, floor) over finite refs; inf and NaN must match exactly.
+    `floor` may be an array (per-element magnitude floor)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN positions differ"
+    inf = np.isinf(ref)
+    assert np.array_equal(got[inf], ref[inf]), "infinities differ"
+    assert not np.isinf(got[~inf]).any(), "unexpected infinity"
+    fin = np.isfinite(ref)
+    if not fin.any():
+        return 0.0
+    denom = np.maximum(np.abs(ref), floor)
+    if np.ndim(denom):
+        denom = denom[fin]
+    return float(np.max(np.abs(got[fin] - ref[fin]) / denom))
+
+
+def f16_ulp_distance(got, ref) -> int:
+    """Max distance in ordered binary16 encodings; infinities must match exactly."""
+    got = np.ascontiguousarray(got, dtype=np.float16)
+    ref = np.ascontiguousarray(ref, dtype=np.float16)
+    assert got.shape == ref.shape
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN positions differ"
+    inf = np.isinf(ref)
+    assert np.array_equal(got[inf], ref[inf]), "infinities differ"
+
+    def key(a):
+        b = a.view(np.uint16).astype(np.int32)
+        mag = b & 0x7FFF
+        return np.where(b & 0x8000, -mag, mag)
+
+    ok = ~np.isnan(ref)
+    if not ok.any():
+        return 0
+    return int(np.max(np.abs(key(got)[ok] - key(ref)[ok])))

@@ -1,0 +1,261 @@
+"""The C ABI without a GPU: the library loads, exports every declared symbol,
+and validates arguments in the reference's order before touching a device.
+
+With ctx == NULL an op that passes validation reports RL_ERR_DEVICE, so the
+validation result of every path is observable here.  The buffers below carry
+fake device addresses: validation never dereferences them and nothing is
+launched.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from rustllm_amd import abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rustllm_hip.h")
+
+OK, ARG, SHAPE, MISMATCH, DIM, DTYPE, NONCONTIG, POS, FORMAT, DEVICE = range(10)
+
+lib = abi.load()
+NULL = None
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rl_[a-z0-9_]+)\s*\(", text)))
+
+
+def buf(n, es, addr=0x10000):
+    return abi.RlBuffer(addr, n, n * es)
+
+
+def call(name, *args):
+    conv = [ctypes.byref(a) if isinstance(a, abi.RlBuffer) else a for a in args]
+    status = getattr(lib, name)(NULL, *conv)
+    return status, abi.last_error()
+
+
+def u64s(*v):
+    return (ctypes.c_uint64 * len(v))(*v)
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    names = declared_functions()
+    assert len(names) >= 50
+    for name in names:
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in abi.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(abi.SIGNATURES) == set(names)
+
+
+def test_library_is_gfx950_only_and_versioned():
+    assert b"gfx950" in lib.rl_version()
+
+
+def test_context_create_without_gpu_reports_device_error():
+    if abi.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    handle = ctypes.c_void_p()
+    assert lib.rl_context_create(0, ctypes.byref(handle)) == DEVICE
+    assert "no HIP GPU" in abi.last_error()
+    assert not handle
+
+
+def test_null_context_after_valid_arguments_is_a_device_error():
+    st, msg = call("rl_add_f32", buf(8, 4), buf(8, 4), buf(8, 4))
+    assert st == DEVICE and "no HIP context" in msg
+
+
+@pytest.mark.parametrize("name,es", [("rl_add_f32", 4), ("rl_mul_f32", 4), ("rl_mul_f16", 2)])
+def test_binary_length_mismatch(name, es):
+    st, msg = call(name, buf(8, es), buf(9, es), buf(8, es))
+    assert st == SHAPE
+    assert "equal buffer lengths, got 8 and 9" in msg
+
+
+def test_add_f16_checks_element_size_like_the_reference():
+    # src/ops/add.rs:120: a F32-sized buffer is rejected by the F16 add.
+    st, msg = call("rl_add_f16", buf(8, 4), buf(8, 2), buf(8, 2))
+    assert st == SHAPE and "F16 add requires equal F16 buffers" in msg
+    st, msg = call("rl_swiglu_f16", buf(8, 2), buf(7, 2), buf(8, 2))
+    assert st == SHAPE and "SwiGLU requires equal F16 buffers" in msg
+
+
+def test_output_buffer_is_checked():
+    st, msg = call("rl_add_f32", buf(8, 4), buf(8, 4), buf(7, 4))
+    assert st == SHAPE and "output buffer" in msg
+    st, _ = call("rl_cast_f32_to_f16", buf(8, 4), buf(8, 4))  # f16 output must be 2-byte
+    assert st == SHAPE
+
+
+def test_input_smaller_than_its_elements_is_rejected():
+    # An F16 buffer passed to an F32 op would be read past its end.
+    st, msg = call("rl_add_f32", buf(8, 2), buf(8, 2), buf(8, 4))
+    assert st == SHAPE and "fewer than" in msg
+
+
+def test_silu_empty_and_u32():
+    st, msg = call("rl_silu_f32", buf(0, 4), buf(0, 4))
+    assert st == SHAPE and "SiLU input cannot be empty" in msg
+    big = 1 << 32
+    st, msg = call("rl_silu_f32", buf(big, 4), buf(big, 4))
+    assert st == SHAPE and "exceeds u32" in msg
+    st, msg = call("rl_mul_f32", buf(big, 4), buf(big, 4), buf(big, 4))
+    assert st == SHAPE and "multiply input size exceeds u32" in msg
+
+
+def test_rmsnorm_validation_order():
+    # src/ops/rmsnorm.rs:38-116: hidden 0, then input size, then weight size.
+    assert call("rl_rmsnorm_f32", buf(8, 4), buf(4, 4), 2, 0, ctypes.c_float(1e-5),
+                buf(8, 4))[0] == SHAPE
+    st, msg = call("rl_rmsnorm_f32", buf(9, 4), buf(4, 4), 2, 4, ctypes.c_float(1e-5), buf(9, 4))
+    assert st == SHAPE and "RMSNorm input has 9 elements, expected 8" in msg
+    st, msg = call("rl_rmsnorm_f32", buf(8, 4), buf(5, 4), 2, 4, ctypes.c_float(1e-5), buf(8, 4))
+    assert st == SHAPE and "RMSNorm weight has 5 elements, expected 4" in msg
+    for eps in (0.0, -1.0, float("inf"), float("nan")):
+        st, msg = call("rl_rmsnorm_f16", buf(8, 2), buf(4, 2), 2, 4, ctypes.c_float(eps),
+                       buf(8, 2))
+        assert st == SHAPE and "epsilon" in msg
+    assert call("rl_rmsnorm_f16", buf(8, 2), buf(4, 2), 2, 4, ctypes.c_float(1e-5),
+                buf(8, 2))[0] == DEVICE
+
+
+def test_add_rmsnorm_validation():
+    st, _ = call("rl_add_rmsnorm_f32", buf(8, 4), buf(6, 4), buf(4, 4), 2, 4,
+                 ctypes.c_float(1e-5), buf(8, 4), buf(8, 4))
+    assert st == MISMATCH
+    st, _ = call("rl_add_rmsnorm_f32", buf(8, 4), buf(8, 4), buf(4, 4), 2, 4,
+                 ctypes.c_float(1e-5), buf(8, 4), buf(8, 4))
+    assert st == DEVICE
+
+
+def test_softmax_validation():
+    # src/ops/softmax.rs:91-108
+    st, msg = call("rl_softmax_f32", buf(8, 4), 0, 8, buf(8, 4))
+    assert st == SHAPE and "rows and width must be greater than zero" in msg
+    st, msg = call("rl_softmax_f32", buf(8, 4), 3, 3, buf(8, 4))
+    assert st == SHAPE and "Softmax input has 8 elements" in msg
+    st, _ = call("rl_softmax_f16", buf(8, 4), 2, 4, buf(8, 2))  # f32-sized f16 input
+    assert st == SHAPE
+    assert call("rl_softmax_f16", buf(8, 2), 2, 4, buf(8, 2))[0] == DEVICE
+
+
+@pytest.mark.parametrize("name", ["rl_attention_scale_mask_f32", "rl_attention_softmax_f32"])
+def test_scale_mask_validation(name):
+    f = ctypes.c_float
+    # src/ops/attention_scale_mask.rs:120-161, in order
+    st, msg = call(name, buf(9, 4), f(0.5), 0, 3, 0, buf(9, 4))
+    assert st == SHAPE and "query/key length cannot be zero" in msg
+    for bad in (0.0, -0.5, float("inf"), float("nan")):
+        st, msg = call(name, buf(9, 4), f(bad), 3, 3, 0, buf(9, 4))
+        assert st == SHAPE and "scale must be positive and finite" in msg
+    st, msg = call(name, buf(9, 4), f(0.5), 3, 3, 1, buf(9, 4))
+    assert st == SHAPE and "exceeds key length" in msg
+    st, msg = call(name, buf(10, 4), f(0.5), 3, 3, 0, buf(10, 4))
+    assert st == SHAPE and "incompatible with query_len=3" in msg
+    st, _ = call(name, buf(18, 4), f(0.5), 3, 3, 0, buf(18, 4))
+    assert st == DEVICE
+
+
+def test_rope_validation():
+    f = "rl_rope_f32"
+    tab = buf(8 * 2, 4)  # [8, 2] f32 tables for head_dim 4
+    st, msg = call(f, buf(8, 4), tab, tab, 2, 3, 0, buf(8, 4))
+    assert st == SHAPE and "head dimension must be positive and even" in msg
+    st, msg = call(f, buf(8, 4), tab, tab, 0, 4, 0, buf(8, 4))
+    assert st == SHAPE and "sequence length cannot be zero" in msg
+    st, msg = call(f, buf(10, 4), tab, tab, 2, 4, 0, buf(10, 4))
+    assert st == SHAPE and "not divisible by head dimension" in msg
+    st, msg = call(f, buf(12, 4), tab, tab, 2, 4, 0, buf(12, 4))
+    assert st == SHAPE and "incompatible with sequence length" in msg
+    st, msg = call(f, buf(8, 4), tab, tab, 2, 4, 7, buf(8, 4))  # 7 + 2 > 8 table rows
+    assert st == SHAPE and "position range is invalid" in msg
+    st, msg = call(f, buf(8, 4), buf(16, 2), buf(16, 2), 2, 4, 0, buf(8, 4))
+    assert st == DTYPE and "F32 cos/sin tables" in msg
+    assert call(f, buf(8, 4), tab, tab, 2, 4, 6, buf(8, 4))[0] == DEVICE
+
+
+def test_rope_strided_validation():
+    tab = buf(8 * 2, 4)
+    st, _ = call("rl_rope_strided_f16", buf(8, 2), u64s(8), u64s(1), 1, tab, tab, 8, 0,
+                 buf(8, 2))
+    assert st == DIM
+    st, msg = call("rl_rope_strided_f16", buf(8, 2), u64s(2, 4), u64s(1, 2), 2, tab, tab, 8, 0,
+                   buf(8, 2))
+    assert st == NONCONTIG and "unit innermost stride" in msg
+    # [1, 2, 1, 4] permuted to [1, 1, 2, 4]: strides [8, 4, 4, 1] (rope.rs:211-233)
+    assert call("rl_rope_strided_f16", buf(8, 2), u64s(1, 1, 2, 4), u64s(8, 4, 4, 1), 4, tab,
+                tab, 8, 0, buf(8, 2))[0] == DEVICE
+    st, msg = call("rl_rope_strided_f16", buf(8, 2), u64s(1, 1, 2, 4), u64s(8, 4, 8, 1), 4,
+                   tab, tab, 8, 0, buf(8, 2))
+    assert st == SHAPE and "past the end" in msg
+
+
+def test_contiguous_validation():
+    st, msg = call("rl_contiguous_f32", buf(6, 2), u64s(2, 3), u64s(3, 1), 2, buf(6, 4))
+    assert st == SHAPE and "does not match contiguous materialization dtype" in msg
+    st, msg = call("rl_contiguous_f32", buf(4, 4), u64s(2, 3), u64s(3, 1), 2, buf(6, 4))
+    assert st == SHAPE and "reaches element 5 of a 4-element source" in msg
+    st, msg = call("rl_contiguous_f32", buf(6, 4), u64s(2, 3), u64s(1 << 33, 1), 2, buf(6, 4))
+    assert st == SHAPE and "stride exceeds u32" in msg
+    st, msg = call("rl_contiguous_f32", buf(6, 4), u64s(2, 3), u64s(4, 1), 2, buf(6, 4))
+    assert st == SHAPE and "reaches element 6" in msg
+    assert call("rl_contiguous_f32", buf(6, 4), u64s(3, 2), u64s(1, 3), 2,
+                buf(6, 4))[0] == DEVICE
+    assert call("rl_contiguous_f16", buf(5, 2), u64s(4, 5), u64s(0, 1), 2,
+                buf(20, 2))[0] == DEVICE  # stride-0 broadcast is a valid view
+
+
+def test_repeat_kv_validation():
+    st, msg = call("rl_repeat_kv_f32", buf(8, 4), 1, 2, 2, 2, 0, buf(8, 4))
+    assert st == FORMAT and "repeats must be greater than zero" in msg
+    st, _ = call("rl_repeat_kv_f32", buf(9, 4), 1, 2, 2, 2, 3, buf(24, 4))
+    assert st == SHAPE
+    assert call("rl_repeat_kv_f32", buf(8, 4), 1, 2, 2, 2, 3, buf(24, 4))[0] == DEVICE
+
+
+def test_broadcast_validation():
+    st, _ = call("rl_add_broadcast_f32", buf(12, 4), buf(5, 4), 3, 4, buf(12, 4))
+    assert st == MISMATCH
+    assert call("rl_add_broadcast_f32", buf(12, 4), buf(4, 4), 3, 4, buf(12, 4))[0] == DEVICE
+
+
+def test_buffer_calls_without_context():
+    raw = abi.RlBuffer()
+    assert lib.rl_buffer_empty(NULL, 0, 4, ctypes.byref(raw)) == SHAPE  # len must be > 0
+    assert lib.rl_buffer_empty(NULL, 4, 4, ctypes.byref(raw)) == DEVICE
+    assert lib.rl_execution_finish(NULL) == DEVICE
+    assert lib.rl_profile_take(NULL, None) == 0
+
+
+def _fastdiv(d):
+    s = 0
+    while (1 << s) < d:
+        s += 1
+    magic = ((1 << 32) * ((1 << s) - d)) // d + 1
+    assert magic < (1 << 32)
+    return magic, s
+
+
+def test_fastdiv_magic_numbers():
+    """The multiply-high division used by the kernels (FastDiv in common.hpp)
+    against exact integer division, over divisors and numerators at the
+    edges of the 32-bit range."""
+    rng = np.random.default_rng(0)
+    divisors = [1, 2, 3, 5, 7, 9, 15, 64, 576, 1536, 2047, 2048, 4096, 65535, 65537,
+                (1 << 31) - 1, 1 << 31, (1 << 31) + 1, (1 << 32) - 1]
+    divisors += [int(v) for v in rng.integers(1, 1 << 32, 200)]
+    nums = np.concatenate([np.arange(0, 5000, dtype=np.uint64),
+                           (1 << 32) - 1 - np.arange(0, 5000, dtype=np.uint64),
+                           rng.integers(0, 1 << 32, 20000).astype(np.uint64)])
+    for d in divisors:
+        magic, s = _fastdiv(d)
+        hi = (nums * np.uint64(magic)) >> np.uint64(32)
+        q = (hi + nums) >> np.uint64(s)
+        assert np.array_equal(q, nums // np.uint64(d)), d

@@ -1,0 +1,478 @@
+"""HIP library vs the CPU oracle through the C ABI, on seeded inputs.
+
+Bars (stated per test): bit-exact for add, mul, cast, broadcast add,
+contiguous, repeat_kv, scale/mask and RoPE (FMA contraction is off on both
+sides); f32 RMSNorm / softmax / SiLU / SwiGLU within a max relative error of
+1e-5 with a FLT_MIN magnitude floor; every f16 output within 2 ulp.
+Shapes cover the reference's own test vectors, ragged sizes that exercise
+the tail and unaligned paths, and the full benchmark configurations.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from helpers import assert_bitexact, f16_ulp_distance, floats, kats, max_rel_err
+from oracle import oracle as o
+from rustllm_amd import abi, synth
+
+pytestmark = pytest.mark.gpu
+
+K = kats()
+TINY = np.finfo(np.float32).tiny
+F32_REL = 1e-5
+F16_ULP = 2
+
+o.set_threads(min(16, os.cpu_count() or 1))
+
+
+def norm(key, shape, dtype, mu=0.0, sigma=1.0):
+    return synth.normal(synth.seed_for(*key, *shape, np.dtype(dtype).name), shape, mu, sigma,
+                        dtype)
+
+
+def check_float(got, ref, what):
+    if got.dtype == np.float16:
+        d = f16_ulp_distance(got, ref)
+        assert d <= F16_ULP, f"{what}: {d} ulp"
+    else:
+        e = max_rel_err(got, ref, TINY)
+        assert e <= F32_REL, f"{what}: max rel err {e:.3g}"
+
+
+def run(ctx, fn):
+    """Runs one batch (begin .. finish) and returns fn's result."""
+    ctx.begin()
+    out = fn()
+    ctx.finish()
+    return out
+
+
+DT = [np.float32, np.float16]
+SIZES = [1, 3, 7, 8, 9, 1000, 100_003, 4096 * 1536]
+
+
+# ------------------------------------------------------------ element-wise
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("n", SIZES)
+def test_add_mul_bitexact(ctx, dtype, n):
+    a = norm(("add", "a"), (n,), dtype)
+    b = norm(("add", "b"), (n,), dtype)
+    da, db = ctx.upload(a), ctx.upload(b)
+    got_add = run(ctx, lambda: ctx.add(da, db)).numpy()
+    assert_bitexact(got_add, o.add(a, b), f"add {dtype.__name__} n={n}")
+    got_mul = run(ctx, lambda: ctx.mul(da, db)).numpy()
+    assert_bitexact(got_mul, o.mul(a, b), f"mul {dtype.__name__} n={n}")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("n", SIZES)
+def test_silu_swiglu(ctx, dtype, n):
+    g = norm(("silu", "g"), (n,), dtype, 0.0, 3.0)
+    u = norm(("silu", "u"), (n,), dtype)
+    dg, du = ctx.upload(g), ctx.upload(u)
+    check_float(run(ctx, lambda: ctx.silu(dg)).numpy(), o.silu(g), f"silu n={n}")
+    check_float(run(ctx, lambda: ctx.swiglu(dg, du)).numpy(), o.swiglu(g, u), f"swiglu n={n}")
+
+
+def test_silu_extremes(ctx):
+    x = np.array([-1e30, -100, -88.7, -20, -1, -1e-30, -0.0, 0.0, 1e-30, 1, 20, 88.7, 100, 1e30,
+                  np.inf, -np.inf], dtype=np.float32)
+    got = run(ctx, lambda: ctx.silu(ctx.upload(x))).numpy()
+    ref = o.silu(x)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert max_rel_err(got[fin], ref[fin], TINY) <= F32_REL
+    xh = np.array([-65504, -20, -1, -0.0, 0, 1e-7, 1, 20, 65504], dtype=np.float16)
+    got = run(ctx, lambda: ctx.silu(ctx.upload(xh))).numpy()
+    assert f16_ulp_distance(got, o.silu(xh)) <= F16_ULP
+
+
+@pytest.mark.parametrize("n", SIZES)
+def test_cast_bitexact(ctx, n):
+    x = norm(("cast",), (n,), np.float32, 0.0, 2000.0)
+    got = run(ctx, lambda: ctx.cast(ctx.upload(x), np.float16)).numpy()
+    assert_bitexact(got, o.cast(x, np.float16), f"cast f32->f16 n={n}")
+    h = x.astype(np.float16)
+    got = run(ctx, lambda: ctx.cast(ctx.upload(h), np.float32)).numpy()
+    assert_bitexact(got, o.cast(h, np.float32), f"cast f16->f32 n={n}")
+
+
+def test_cast_rounding_probe(ctx):
+    """Every sign/exponent/top-mantissa pattern with the rounding-deciding low
+    bits, including subnormal results, overflow to inf and NaN."""
+    high = np.arange(1 << 19, dtype=np.uint32) << np.uint32(13)
+    lows = np.array([0, 1, 0x0FFF, 0x1000, 0x1001, 0x1FFF], dtype=np.uint32)
+    x = (high[:, None] | lows[None, :]).ravel().view(np.float32)
+    got = run(ctx, lambda: ctx.cast(ctx.upload(x), np.float16)).numpy()
+    assert_bitexact(got, o.cast(x, np.float16), "cast probe")
+    every = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    got = run(ctx, lambda: ctx.cast(ctx.upload(every), np.float32)).numpy()
+    assert_bitexact(got, o.cast(every, np.float32), "f16->f32 exhaustive")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("rows,cols", [(4096, 1536), (3, 5), (17, 24), (1, 8)])
+def test_add_broadcast_bitexact(ctx, dtype, rows, cols):
+    x = norm(("bias", "x"), (rows, cols), dtype)
+    b = norm(("bias", "b"), (cols,), dtype)
+    got = run(ctx, lambda: ctx.add_broadcast(ctx.upload(x), ctx.upload(b))).numpy()
+    assert_bitexact(got, o.add_broadcast(x, b), f"bias add {rows}x{cols}")
+
+
+# ------------------------------------------------------------ reference KATs
+
+def test_reference_kats_elementwise(ctx):
+    kat = K["add_f16"]
+    a = np.array(kat["left"], np.float16).reshape(kat["shape"])
+    b = np.array(kat["right"], np.float16).reshape(kat["shape"])
+    got = run(ctx, lambda: ctx.add(ctx.upload(a), ctx.upload(b))).numpy()
+    assert got.astype(np.float32).ravel().tolist() == kat["expected"]
+
+    # Two ops in one batch, no wait in between (ops/add.rs:113-168, ops/mul.rs:132-203)
+    kat = K["chained_add_f16"]
+    da, db, dc = (ctx.upload(np.array(kat[k], np.float16)) for k in ("a", "b", "c"))
+    got = run(ctx, lambda: ctx.add(ctx.add(da, db), dc)).numpy().astype(np.float32)
+    assert np.all(np.abs(got - kat["expected"]) < kat["tol"])
+    kat = K["add_then_mul_f16"]
+    da, db, dc = (ctx.upload(np.array(kat[k], np.float16)) for k in ("a", "b", "c"))
+    got = run(ctx, lambda: ctx.mul(ctx.add(da, db), dc)).numpy().astype(np.float32)
+    assert np.all(np.abs(got - kat["expected"]) < kat["tol"])
+    kat = K["silu_then_mul_f16"]
+    dg, du = ctx.upload(np.array(kat["gate"], np.float16)), ctx.upload(np.array(kat["up"],
+                                                                                   np.float16))
+    got = run(ctx, lambda: ctx.mul(ctx.silu(dg), du)).numpy().astype(np.float32)
+    assert np.all(np.abs(got - kat["expected"]) < kat["tol"])
+
+
+# ------------------------------------------------------------ data movement
+
+def _view_strides(arr):
+    return [s // arr.itemsize for s in arr.strides]
+
+
+@pytest.mark.parametrize("dtype", DT)
+def test_contiguous_config_transpose(ctx, dtype):
+    # [1, 9, 4096, 64] view of a contiguous [1, 4096, 9, 64] (permute [0, 2, 1, 3])
+    base = norm(("contig",), (1, 4096, 9, 64), dtype)
+    dims, strides = [1, 9, 4096, 64], [4096 * 9 * 64, 64, 9 * 64, 1]
+    d = ctx.upload(base)
+    got = run(ctx, lambda: ctx.contiguous(d, dims, strides)).numpy()
+    assert_bitexact(got, o.contiguous(base.ravel(), dims, strides), "contiguous config")
+    assert_bitexact(got, np.ascontiguousarray(base.transpose(0, 2, 1, 3)), "vs numpy")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("seed", range(12))
+def test_contiguous_random_permutations(ctx, dtype, seed):
+    rng = np.random.default_rng(seed)
+    rank = int(rng.integers(1, 6))
+    shape = [int(v) for v in rng.integers(1, 9, rank)]
+    base = norm(("perm", seed), tuple(shape), dtype)
+    perm = [int(v) for v in rng.permutation(rank)]
+    view = base.transpose(perm)
+    dims, strides = list(view.shape), _view_strides(view)
+    got = run(ctx, lambda: ctx.contiguous(ctx.upload(base), dims, strides)).numpy()
+    assert_bitexact(got, np.ascontiguousarray(view), f"perm {shape} {perm}")
+
+
+def test_contiguous_special_views(ctx):
+    # stride-0 broadcast, transposed inner dims (per-element path), narrowed KV cache
+    bias = norm(("b0",), (24,), np.float32)
+    got = run(ctx, lambda: ctx.contiguous(ctx.upload(bias), [100, 24], [0, 1])).numpy()
+    assert_bitexact(got, np.broadcast_to(bias, (100, 24)).copy())
+    m = norm(("t",), (33, 65), np.float16)
+    got = run(ctx, lambda: ctx.contiguous(ctx.upload(m), [65, 33], [1, 65])).numpy()
+    assert_bitexact(got, m.T.copy())
+    kat = K["kv_cache_narrow_contiguous"]
+    _, heads, max_seq, hd = kat["cache_shape"]
+    cache = np.zeros(kat["cache_shape"], np.float16)
+    for pos, vals in enumerate(kat["appends"]):
+        cache[:, :, pos, :] = np.array(vals, np.float16).reshape(heads, hd)
+    n = kat["narrow_len"]
+    got = run(ctx, lambda: ctx.contiguous(ctx.upload(cache), [1, heads, n, hd],
+                                          [heads * max_seq * hd, max_seq * hd, hd, 1])).numpy()
+    assert got.astype(np.float32).ravel().tolist() == kat["expected"]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("shape,repeats", [((1, 3, 4096, 64), 3), ((1, 5, 4096, 64), 3),
+                                           ((2, 2, 7, 5), 4), ((1, 2, 2, 2), 3),
+                                           ((1, 1, 2, 2), 1)])
+def test_repeat_kv_bitexact(ctx, dtype, shape, repeats):
+    x = norm(("rkv",), shape, dtype)
+    got = run(ctx, lambda: ctx.repeat_kv(ctx.upload(x), repeats)).numpy()
+    assert_bitexact(got, o.repeat_kv(x, repeats), f"repeat_kv {shape} x{repeats}")
+
+
+def test_repeat_kv_kat(ctx):
+    kat = K["repeat_kv_r3"]
+    for dt in (np.float32, np.float16):
+        x = np.array(kat["input"], dt).reshape(kat["shape"])
+        got = run(ctx, lambda: ctx.repeat_kv(ctx.upload(x), kat["repeats"])).numpy()
+        assert list(got.shape) == kat["expected_shape"]
+        assert got.astype(np.float32).ravel().tolist() == kat["expected"]
+
+
+# ---------------------------------------------------------------- RMSNorm
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("hidden", [576, 768, 960])
+@pytest.mark.parametrize("tokens", [1, 16, 256, 4096, 16384])
+def test_rmsnorm_config_grid(ctx, dtype, hidden, tokens):
+    x = norm(("rms", "x"), (tokens, hidden), dtype, 0.0, 2.0)
+    w = synth.uniform_range(synth.seed_for("rms", "w", hidden), (hidden,), 0.5, 1.5, dtype)
+    got = run(ctx, lambda: ctx.rmsnorm(ctx.upload(x), ctx.upload(w), 1e-5)).numpy()
+    check_float(got, o.rmsnorm(x, w, 1e-5), f"rmsnorm {tokens}x{hidden}")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("rows,hidden", [(2, 4), (3, 5), (5, 4097), (2, 20000), (1, 1)])
+def test_rmsnorm_odd_and_large_rows(ctx, dtype, rows, hidden):
+    x = norm(("rms2", "x"), (rows, hidden), dtype, 0.0, 2.0)
+    w = synth.uniform_range(synth.seed_for("rms2", "w", hidden), (hidden,), 0.5, 1.5, dtype)
+    got = run(ctx, lambda: ctx.rmsnorm(ctx.upload(x), ctx.upload(w), 1e-5)).numpy()
+    check_float(got, o.rmsnorm(x, w, 1e-5), f"rmsnorm {rows}x{hidden}")
+
+
+def test_rmsnorm_reference_kats(ctx):
+    kat = K["rmsnorm_2x4"]
+    x = np.array(kat["input"], np.float32)
+    w = np.array(kat["weight"], np.float32)
+    expected = o.cpu_rmsnorm_literal(x, w, kat["eps"])
+    got = run(ctx, lambda: ctx.rmsnorm(ctx.upload(x), ctx.upload(w), kat["eps"])).numpy()
+    assert np.max(np.abs(got - expected)) <= kat["tol_f32"]
+    xh, wh = x.astype(np.float16), w.astype(np.float16)
+    zeros = ctx.upload(np.zeros(8, np.float16))
+    dx, dw = ctx.upload(xh), ctx.upload(wh)
+    got = run(ctx, lambda: ctx.add(ctx.rmsnorm(dx, dw, kat["eps"]), zeros)).numpy()
+    assert np.max(np.abs(got.astype(np.float32) - expected)) <= kat["tol_f16"]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("rows,hidden", [(64, 768), (4096, 960), (3, 5), (2, 9000)])
+def test_add_rmsnorm(ctx, dtype, rows, hidden):
+    # out = RMSNorm(x + r) * w on f32 [64, 768]
+    x = norm(("arms", "x"), (rows, hidden), dtype)
+    r = norm(("arms", "r"), (rows, hidden), dtype)
+    w = synth.uniform_range(synth.seed_for("arms", "w", hidden), (hidden,), 0.5, 1.5, dtype)
+    s, y = run(ctx, lambda: ctx.add_rmsnorm(ctx.upload(x), ctx.upload(r), ctx.upload(w), 1e-5))
+    rs, ry = o.add_rmsnorm(x, r, w, 1e-5)
+    assert_bitexact(s.numpy(), rs, "residual sum")
+    check_float(y.numpy(), ry, f"add_rmsnorm {rows}x{hidden}")
+
+
+# ---------------------------------------------------------------- softmax
+
+def _logits(key, shape, dtype=np.float32):
+    """N(0, 4) logits with 1% of entries set to +20."""
+    x = synth.normal(synth.seed_for(*key, *shape), shape, 0.0, 4.0, np.float32)
+    u = synth.uniform(synth.seed_for("spike", *key, *shape), x.size).reshape(shape)
+    x[u < 0.01] = 20.0
+    return x.astype(dtype)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("rows,width", [(2, 3), (7, 33), (64, 2048), (9, 4096), (5, 5000),
+                                        (3, 9000), (2, 70000), (1, 1)])
+def test_softmax(ctx, dtype, rows, width):
+    x = _logits(("sm",), (rows, width), dtype)
+    got = run(ctx, lambda: ctx.softmax(ctx.upload(x))).numpy()
+    check_float(got, o.softmax(x), f"softmax {rows}x{width}")
+
+
+@pytest.mark.parametrize("width", [8, 3, 5000, 70000])
+def test_softmax_special_rows(ctx, width):
+    # all -inf: f32 NaN (no guard, softmax.metal:7-132), f16 zeros (:166-173);
+    # a NaN score poisons its row; -inf entries get exact zeros.
+    x = np.zeros((4, width), np.float32)
+    x[0] = -np.inf
+    x[1, 0] = np.nan
+    x[2, ::2] = -np.inf
+    x[3] = np.linspace(-3, 3, width, dtype=np.float32)
+    for dt in DT:
+        xi = x.astype(dt)
+        got = run(ctx, lambda: ctx.softmax(ctx.upload(xi))).numpy()
+        ref = o.softmax(xi)
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), dt
+        ok = ~np.isnan(ref)
+        assert np.array_equal(got[ok] == 0, ref[ok] == 0), dt
+        check_float(np.where(ok, got, 0).astype(dt), np.where(ok, ref, 0).astype(dt), "special")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("shape,start", [((9, 2048, 2048), 0), ((9, 1, 2048), 2047),
+                                         ((1, 1, 3, 3), 0), ((2, 5, 40), 11),
+                                         ((3, 4, 6000), 100), ((1, 2, 70000), 3)])
+def test_scale_mask_and_fused_softmax(ctx, dtype, shape, start):
+    x = _logits(("att",), shape, dtype)
+    scale = 1.0 / 8.0
+    d = ctx.upload(x)
+    ref_mask = o.scale_mask(x, scale, start)
+    got_mask = run(ctx, lambda: ctx.scale_mask(d, scale, start)).numpy()
+    assert_bitexact(got_mask, ref_mask, f"scale/mask {shape}")
+    ref = o.softmax(ref_mask)  # the reference's two adjacent calls
+    got = run(ctx, lambda: ctx.attention_softmax(d, scale, start)).numpy()
+    check_float(got, ref, f"fused {shape}")
+    masked = np.isinf(ref_mask)
+    assert np.all(got[masked] == 0), "masked probabilities must be exact zeros"
+    # and the unfused pair on the device agrees with the fused kernel's bar too
+    got2 = run(ctx, lambda: ctx.softmax(ctx.scale_mask(d, scale, start))).numpy()
+    check_float(got2, ref, f"unfused {shape}")
+
+
+def test_scale_mask_reference_kats(ctx):
+    kat = K["scale_mask_prefill"]
+    x = np.array(kat["input"], np.float32).reshape(kat["shape"])
+    got = run(ctx, lambda: ctx.scale_mask(ctx.upload(x), kat["scale"], kat["start"])).numpy()
+    assert_bitexact(got.ravel(), floats(kat["expected_f32"]))
+    for name in ("scale_mask_decode", "scale_mask_intermediate"):
+        kat = K[name]
+        x = np.array(kat["input"], np.float16).reshape(kat["shape"])
+        got = run(ctx, lambda: ctx.scale_mask(ctx.upload(x), kat["scale"], kat["start"]))
+        assert_bitexact(got.numpy().astype(np.float32).ravel(), floats(kat["expected"]))
+    kat = K["mask_softmax"]
+    x = np.array(kat["input"], np.float32).reshape(kat["shape"])
+    ref = o.attention_softmax(x, kat["scale"], kat["start"])
+    for fused in (True, False):
+        d = ctx.upload(x.astype(np.float16))
+        if fused:
+            got = run(ctx, lambda: ctx.attention_softmax(d, kat["scale"], kat["start"]))
+        else:
+            got = run(ctx, lambda: ctx.softmax(ctx.scale_mask(d, kat["scale"], kat["start"])))
+        got = got.numpy().astype(np.float32)
+        assert np.max(np.abs(got - ref)) < kat["tol_f16_vs_f32"]
+        assert all(got.ravel()[i] == 0.0 for i in kat["zero_indices"])
+
+
+def test_fused_softmax_smollm_layer_f16(ctx):
+    """configs[4] step 4: [15, 4096, 4096] f16 causal, scale 1/8."""
+    rng = np.random.default_rng(synth.seed_for("c5", "scores"))
+    x = rng.standard_normal((15, 4096, 4096), dtype=np.float32).astype(np.float16)
+    d = ctx.upload(x)
+    got = run(ctx, lambda: ctx.attention_softmax(d, 0.125, 0)).numpy()
+    del d
+    ref = o.attention_softmax(x, 0.125, 0)
+    check_float(got, ref, "C5 fused softmax")
+    del ref
+    # size-independent invariants: each row sums to 1 and nothing past the diagonal
+    sums = np.add.reduce(got, axis=-1, dtype=np.float32)
+    assert np.all(np.abs(sums - 1.0) < 4e-3)
+    upper = np.triu(np.ones((4096, 4096), bool), 1)
+    for h in range(15):
+        assert not got[h][upper].any()
+
+
+# ------------------------------------------------------------------- RoPE
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("shape,start,table", [((1, 15, 4096, 64), 0, 4096),
+                                               ((1, 5, 4096, 64), 0, 4096),
+                                               ((1, 1, 2, 4), 1, 8), ((2, 3, 7, 6), 5, 16),
+                                               ((1, 2, 1, 64), 4000, 4096)])
+def test_rope_bitexact(ctx, dtype, shape, start, table):
+    head_dim = shape[-1]
+    c, s = o.rope_table(head_dim, table, 10000.0)
+    x = norm(("rope",), shape, dtype)
+    dc, ds = ctx.upload(c), ctx.upload(s)
+    got = run(ctx, lambda: ctx.rope(ctx.upload(x), dc, ds, start)).numpy()
+    assert_bitexact(got, o.rope(x, c, s, start), f"rope {shape} start={start}")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("seq,heads", [(4096, 15), (4096, 5), (3, 2), (1, 1)])
+def test_rope_fused_transpose_gather(ctx, dtype, seq, heads):
+    """ops::rope_encode on the [1, H, S, D] permute of a [1, S, H, D] projection
+    (nn/attention.rs:403-407): gather + rotation in one pass equals
+    contiguous() then rope()."""
+    hd = 64
+    c, s = o.rope_table(hd, max(seq, 8), 10000.0)
+    base = norm(("ropeT",), (1, seq, heads, hd), dtype)
+    dims, strides = [1, heads, seq, hd], [seq * heads * hd, hd, heads * hd, 1]
+    ref = o.rope(o.contiguous(base.ravel(), dims, strides), c, s, 0)
+    dc, ds = ctx.upload(c), ctx.upload(s)
+    got = run(ctx, lambda: ctx.rope_strided(ctx.upload(base), dims, strides, dc, ds, 0)).numpy()
+    assert_bitexact(got, ref, f"fused rope {seq}x{heads}")
+
+
+def test_rope_reference_kats(ctx):
+    kat = K["rope_f16_vs_f32"]
+    c, s = o.rope_table(kat["head_dim"], kat["max_seq_len"], kat["theta"])
+    dc, ds = ctx.upload(c), ctx.upload(s)
+    x = np.array(kat["input"], np.float32).reshape(kat["shape"])
+    ref = run(ctx, lambda: ctx.rope(ctx.upload(x), dc, ds, kat["start"])).numpy()
+    got = run(ctx, lambda: ctx.rope(ctx.upload(x.astype(np.float16)), dc, ds, kat["start"]))
+    assert np.max(np.abs(got.numpy().astype(np.float32) - ref)) <= kat["tol_f16_vs_f32"]
+    kat = K["rope_non_contiguous"]
+    c, s = o.rope_table(kat["head_dim"], kat["max_seq_len"], kat["theta"])
+    base = np.array(kat["input"], np.float16).reshape(kat["shape"])
+    view = base.transpose(kat["permute"])
+    got = run(ctx, lambda: ctx.rope_strided(ctx.upload(base), list(view.shape),
+                                            _view_strides(view), ctx.upload(c), ctx.upload(s),
+                                            kat["start"])).numpy()
+    assert got.dtype == np.float16 and got.flags["C_CONTIGUOUS"]
+    assert_bitexact(got, o.rope(np.ascontiguousarray(view), c, s, kat["start"]))
+
+
+# ------------------------------------------------------- runtime behaviour
+
+def test_one_batch_is_one_submission(ctx):
+    """Submission counters (MetalDecodeProfile semantics): ops enqueued
+    between begin and finish are one command buffer, one commit, one wait."""
+    x = ctx.upload(norm(("prof",), (4, 64), np.float32))
+    w = ctx.upload(np.ones(64, np.float32))
+    ctx.profile_begin()
+    ctx.begin()
+    y = ctx.rmsnorm(x, w, 1e-5)
+    z = ctx.add(y, x)
+    ctx.silu(z)
+    ctx.finish()
+    prof = ctx.profile_take()
+    assert prof["command_buffers"] == 1 and prof["commits"] == 1 and prof["waits"] == 1
+    assert prof["kernel_dispatches"] == 3 and prof["compute_encoders"] == 3
+    assert prof["buffer_allocations"] == 3
+    assert ctx.dispatches("rmsnorm_f32") == 1 and ctx.dispatches("add_f32") == 1
+    assert ctx.profile_take() is None
+
+
+def test_graph_replay_matches_eager(ctx):
+    """A recorded batch replayed several times, with eager work and waits in
+    between, gives the eager result every time."""
+    a = norm(("graph", "a"), (1000, 96), np.float16)
+    b = norm(("graph", "b"), (1000, 96), np.float16)
+    w = synth.uniform_range(7, (96,), 0.5, 1.5, np.float16)
+    da, db, dw = ctx.upload(a), ctx.upload(b), ctx.upload(w)
+    s_out, y_out = ctx.empty(a.shape, np.float16), ctx.empty(a.shape, np.float16)
+    sm_out = ctx.empty(a.shape, np.float16)
+    ctx.capture_begin()
+    ctx.add_rmsnorm(da, db, dw, 1e-5, s_out, y_out)
+    ctx.softmax(y_out, sm_out)
+    graph = ctx.capture_end()
+    rs, ry = o.add_rmsnorm(a, b, w, 1e-5)
+    for i in range(4):
+        ctx.graph_launch(graph)
+        ctx.finish()
+        assert_bitexact(s_out.numpy(), rs, f"replay {i}")
+        check_float(y_out.numpy(), ry, f"replay {i}")
+        check_float(sm_out.numpy(), o.softmax(y_out.numpy()), f"replay {i}")
+        run(ctx, lambda: ctx.mul(da, db))  # unrelated eager work between replays
+    ctx.graph_destroy(graph)
+
+
+def test_device_validation_matches_cpu(ctx):
+    a, b = ctx.upload(np.ones(8, np.float32)), ctx.upload(np.ones(9, np.float32))
+    with pytest.raises(abi.RustLLMError) as err:
+        ctx.add(a, b, out=ctx.empty((8,), np.float32))
+    assert err.value.kind == "InvalidShape"
+    assert "equal buffer lengths, got 8 and 9" in str(err.value)
+
+
+def test_pool_reuses_released_blocks(ctx):
+    n = (1 << 20) + 4097  # a size class no other test uses
+    first = ctx.empty((n,), np.float32)
+    addr = first.ptr
+    first.release()
+    second = ctx.empty((n,), np.float32)
+    assert second.ptr == addr
