@@ -364,6 +364,29 @@ def check_outputs(ctx, dev, outs) -> list[str]:
     return bad
 
 
+def probe(ctx, host, ops):
+    """Hardware-counter probe: each op 3 times, then a plain copy of known
+    size whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters."""
+    s = config2_set(ctx, host)
+    for op in ops:
+        for _ in range(3):
+            ctx.begin()
+            op.launch(ctx, s)
+            ctx.finish()
+        log(f"probe {op.name}: {op.nbytes} algorithmic bytes per launch")
+    # A contiguous "view" of a contiguous buffer is a plain copy kernel.
+    nbytes = 256 << 20
+    n = nbytes // 4
+    src = ctx.upload(np.ones(n, dtype=F32))
+    dst = ctx.empty((n,), F32)
+    for _ in range(3):
+        ctx.begin()
+        ctx.contiguous(src, [n], [1], dst)
+        ctx.finish()
+    log(f"probe copy (contiguous_f32 of a flat view): {nbytes} bytes read and {nbytes} bytes "
+        f"written per launch")
+
+
 # ------------------------------------------------------------------ main
 
 def main():
@@ -377,6 +400,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
     ap.add_argument("--quick", action="store_true", help="fewer extra shapes")
+    ap.add_argument("--probe", action="store_true",
+                    help="no timing: run each configs[1] op 3 times on one buffer set, then a "
+                         "256 MiB device-to-device copy 3 times (for hardware-counter runs)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -388,6 +414,9 @@ def main():
     ctx = abi.Context(0)
     host = config2_inputs("bench")
     ops = config2_ops()
+    if args.probe:
+        probe(ctx, host, ops)
+        return
     log(f"uploading {args.sets} buffer sets")
     sets = [config2_set(ctx, host) for _ in range(args.sets)]
     footprint = sum(set_bytes(s) for s in sets)

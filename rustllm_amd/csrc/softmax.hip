@@ -273,13 +273,15 @@ __global__ __launch_bounds__(kThreads) void k_softmax_stream(const T* __restrict
         if (x == -INFINITY) continue;
         online_add(m, s, x);
     }
-    // Cross-lane merge of (m, s).
+    // Cross-lane merge of (m, s).  A pair whose max is still -inf holds s = 0,
+    // or NaN if it met a NaN score; multiplying by 0 keeps that NaN (the
+    // reference's sum is NaN then) without forming exp(-inf - -inf).
     for (int offset = 32; offset > 0; offset >>= 1) {
         float om = __shfl_xor(m, offset, 64);
         float os = __shfl_xor(s, offset, 64);
         float nm = fmaxf(m, om);
-        float a = (m == -INFINITY) ? 0.0f : s * expf(m - nm);
-        float b = (om == -INFINITY) ? 0.0f : os * expf(om - nm);
+        float a = s * ((m == -INFINITY) ? 0.0f : expf(m - nm));
+        float b = os * ((om == -INFINITY) ? 0.0f : expf(om - nm));
         m = nm;
         s = a + b;
     }
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_stream(const T* __restrict
     float gs = 0.0f;
 #pragma unroll
     for (int w = 0; w < kThreads / kWave; ++w)
-        gs += (lds_m[w] == -INFINITY) ? 0.0f : lds_s[w] * expf(lds_m[w] - gm);
+        gs += lds_s[w] * ((lds_m[w] == -INFINITY) ? 0.0f : expf(lds_m[w] - gm));
     if (gm == -INFINITY) {
         // Every kept score is -inf: f16 writes zeros (softmax.metal:166-173),
         // f32 yields NaN as exp(-inf - -inf) does in the reference.

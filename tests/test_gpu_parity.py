@@ -470,9 +470,13 @@ def test_device_validation_matches_cpu(ctx):
 
 
 def test_pool_reuses_released_blocks(ctx):
-    n = (1 << 20) + 4097  # a size class no other test uses
+    # A released block is handed out again for the same size class: drain the
+    # class first so that the only free block of it is the one released here.
+    n = (1 << 20) + 4097
+    held = [ctx.empty((n,), np.float32) for _ in range(64)]
     first = ctx.empty((n,), np.float32)
     addr = first.ptr
     first.release()
     second = ctx.empty((n,), np.float32)
     assert second.ptr == addr
+    del held
