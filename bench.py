@@ -154,19 +154,41 @@ def capture(ctx, fn):
     return g
 
 
+def kernel_times_us(ctx, launches, reps):
+    """Device time of `reps` launches (cycling through `launches`, one kernel
+    each), every one bracketed by events that the kernel itself stamps at its
+    start and end -- the same per-dispatch duration a kernel trace reports."""
+    for fn in launches:
+        fn()
+    ctx.finish()
+    evs = [(ctx.event(), ctx.event()) for _ in range(reps)]
+    for i, (start, stop) in enumerate(evs):
+        ctx.time_next_kernel(start, stop)
+        launches[i % len(launches)]()
+    ctx.finish()
+    us = [ctx.elapsed_ms(start, stop) * 1e3 for start, stop in evs]
+    for start, stop in evs:
+        ctx.destroy_event(start)
+        ctx.destroy_event(stop)
+    return us
+
+
+def op_row(name, dtype, shape, nbytes, us_list):
+    us = float(np.mean(us_list))
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"  {name:34s} {str(shape):20s} {us:9.2f} us {gbs:8.1f} GB/s ({100 * gbs / PEAK_GBS:5.1f}%)")
+    return {"op": name, "dtype": dtype, "shape": shape, "bytes": nbytes, "us": round(us, 3),
+            "us_min": round(float(np.min(us_list)), 3), "GB/s": round(gbs, 1),
+            "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
+
+
 def per_op_rows(ctx, ops, sets, reps):
-    """Each op alone: a graph of len(sets) launches (one per buffer set) replayed."""
+    """Each op alone, cycling through the buffer sets."""
     rows = []
     for op in ops:
-        graph = capture(ctx, lambda: [op.launch(ctx, s) for s in sets])
-        ms = time_graphs(ctx, [graph], len(sets), reps)
-        ctx.graph_destroy(graph)
-        gbs = op.nbytes / (ms * 1e-3) / 1e9
-        rows.append({"op": op.name, "dtype": op.dtype, "shape": op.shape, "bytes": op.nbytes,
-                     "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                     "pct_peak": round(100 * gbs / PEAK_GBS, 1)})
-        log(f"  {op.name:24s} {str(op.shape):22s} {ms * 1e3:9.2f} us {gbs:8.1f} GB/s "
-            f"({100 * gbs / PEAK_GBS:5.1f}%)")
+        launches = [lambda s=s, op=op: op.launch(ctx, s) for s in sets]
+        rows.append(op_row(op.name, op.dtype, op.shape, op.nbytes,
+                           kernel_times_us(ctx, launches, reps)))
     return rows
 
 
@@ -179,16 +201,9 @@ def extra_rows(ctx, reps, quick):
 
     def measure(name, dtype, shape, nbytes, make_set, launch, nsets):
         sets = [make_set(i) for i in range(nsets)]
-        graph = capture(ctx, lambda: [launch(s) for s in sets])
-        ms = time_graphs(ctx, [graph], nsets, reps)
-        ctx.graph_destroy(graph)
-        del sets
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        rows.append({"op": name, "dtype": dtype, "shape": shape, "bytes": nbytes,
-                     "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                     "pct_peak": round(100 * gbs / PEAK_GBS, 1)})
-        log(f"  {name:24s} {str(shape):22s} {ms * 1e3:9.2f} us {gbs:8.1f} GB/s "
-            f"({100 * gbs / PEAK_GBS:5.1f}%)")
+        launches = [lambda s=s: launch(s) for s in sets]
+        rows.append(op_row(name, dtype, shape, nbytes, kernel_times_us(ctx, launches, reps)))
+        del sets, launches
 
     def nsets_for(footprint):
         return int(min(64, max(4, -(-(1 << 30) // max(footprint, 1)))))
@@ -395,7 +410,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=4, help="buffer sets rotated across steps")
-    ap.add_argument("--op-reps", type=int, default=50, help="graph replays per op line")
+    ap.add_argument("--op-reps", type=int, default=100, help="timed launches per op line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
@@ -463,7 +478,7 @@ def main():
             log(f"MISMATCH against the oracle: {bad}")
         log(f"cpu: {cpu_gbs:.2f} GB/s over {steps} steps")
 
-    extra = [] if args.no_extra else extra_rows(ctx, max(5, args.op_reps // 5), args.quick)
+    extra = [] if args.no_extra else extra_rows(ctx, args.op_reps, args.quick)
     del sets
 
     line = {

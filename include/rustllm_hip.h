@@ -143,6 +143,9 @@ rl_status rl_event_create(rl_context* ctx, rl_event** out);
 rl_status rl_event_record(rl_context* ctx, rl_event* event);
 rl_status rl_event_elapsed_ms(rl_event* start, rl_event* end, float* ms);
 void rl_event_destroy(rl_event* event);
+/* The next kernel this context launches records its own start and end
+ * timestamps in `start` and `stop` (the device time of that one kernel). */
+rl_status rl_event_time_next_kernel(rl_context* ctx, rl_event* start, rl_event* stop);
 
 /* ----------------------------------------------------------- profiling */
 /* MetalContext::begin_decode_submission_profile (src/metal/context.rs:48-50). */

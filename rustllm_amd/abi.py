@@ -87,6 +87,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "rl_event_record": ([_P, _P], _I32),
     "rl_event_elapsed_ms": ([_P, _P, ctypes.POINTER(_F)], _I32),
     "rl_event_destroy": ([_P], None),
+    "rl_event_time_next_kernel": ([_P, _P, _P], _I32),
     "rl_profile_begin": ([_P], None),
     "rl_profile_take": ([_P, ctypes.POINTER(RlProfile)], _I32),
     "rl_profile_dispatches": ([_P, ctypes.c_char_p], _U64),
@@ -273,6 +274,10 @@ class Context:
 
     def destroy_event(self, event) -> None:
         self.lib.rl_event_destroy(event)
+
+    def time_next_kernel(self, start, stop) -> None:
+        """The next kernel launched records its own start/end in these events."""
+        check(self.lib.rl_event_time_next_kernel(self.handle, start, stop))
 
     def capture_begin(self) -> None:
         check(self.lib.rl_graph_capture_begin(self.handle))

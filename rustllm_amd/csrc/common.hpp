@@ -4,6 +4,7 @@
 // 32-bit division by a runtime constant).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -55,7 +56,27 @@ struct rl_context {
     bool profiling = false;
     rl_profile profile{};
     std::map<std::string, uint64_t> dispatches_by_name;
+
+    // Set by rl_event_time_next_kernel: the next launch records its own
+    // start and end in these events.
+    hipEvent_t timed_start = nullptr;
+    hipEvent_t timed_stop = nullptr;
 };
+
+// Every kernel launch of the library: on the context's stream, and, when
+// armed by rl_event_time_next_kernel, with the kernel's own start/end
+// timestamps recorded (hipExtLaunchKernelGGL).
+#define RL_LAUNCH(ctx, kernel, grid, block, ...)                                              \
+    do {                                                                                      \
+        if ((ctx)->timed_start != nullptr) {                                                  \
+            hipExtLaunchKernelGGL(kernel, grid, block, 0, (ctx)->stream, (ctx)->timed_start,  \
+                                  (ctx)->timed_stop, 0, __VA_ARGS__);                         \
+            (ctx)->timed_start = nullptr;                                                     \
+            (ctx)->timed_stop = nullptr;                                                      \
+        } else {                                                                              \
+            hipLaunchKernelGGL(kernel, grid, block, 0, (ctx)->stream, __VA_ARGS__);           \
+        }                                                                                     \
+    } while (0)
 
 namespace rl {
 
@@ -154,6 +175,38 @@ __device__ inline V load_stream(const V* p) {
 template <typename V>
 __device__ inline void store_stream(V* p, V v) {
     __builtin_nontemporal_store(v, p);
+}
+
+// e^x as 2^(x * log2 e) on the hardware exp2 (v_exp_f32), which returns
+// 0 for -inf, inf for +inf and NaN for NaN by itself.  The only error beyond
+// the instruction's own ~1 ulp is the rounding of t = x * log2 e, which
+// scales the result by 2^(dt) with |dt| <= |t| * 2^-24: a relative error of
+// at most |t| * 2^-24 * ln 2, i.e. <= 2.7e-6 over the finite range of e^x
+// (|t| < 128) and <= 3e-7 for |x| < 10.
+// The instruction flushes results below 2^-126 to zero, so arguments whose
+// result would be subnormal are raised by 64 and the result scaled back by
+// an exact power of two.
+__device__ inline float exp_fast(float x) {
+    const float t = x * 1.44269504088896340736f;
+    const bool tiny = t < -126.0f;
+    const float r = __builtin_amdgcn_exp2f(tiny ? t + 64.0f : t);
+    return tiny ? r * 0x1p-64f : r;
+}
+
+// 1 / x on the hardware reciprocal (v_rcp_f32, ~1 ulp; subnormal results
+// flush to zero, so callers keep the result normal).
+__device__ inline float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// SiLU x * (1 / (1 + e^-x)) on the hardware exp2 and reciprocal.  For
+// x < -44 the sigmoid can be subnormal (x < -87.3) although x * sigmoid is
+// not; the denominator is then scaled by 2^-64 so the reciprocal stays
+// normal, and the product is scaled back.  e^-x itself may flush to zero
+// for x > 87.3, where 1 + e^-x rounds to 1 anyway.
+__device__ inline float silu_fast(float x) {
+    const float s = 1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896340736f);
+    const bool big = s > 0x1p64f;
+    const float r = rcp_fast(big ? s * 0x1p-64f : s);
+    return big ? (x * r) * 0x1p-64f : x * r;
 }
 
 // wave64 butterfly reductions (every lane ends with the result).

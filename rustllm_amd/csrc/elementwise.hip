@@ -2,13 +2,17 @@
 // add for gfx950.
 //
 // Every op here is a pure stream: HBM-bound, a few VALU ops per element.
-// Each thread moves UNROLL packs of 16 bytes per operand (float4 / 8 halves;
-// casts use 8-element packs on both sides), issuing all loads of a tile
-// before any arithmetic so each wave keeps UNROLL x 1 KiB per operand in
-// flight.  Tiles are laid out so that one load instruction of a wave covers
-// 1 KiB of contiguous memory.  Loads and stores are non-temporal: nothing
-// is reused, so the data should not displace L2 contents.  The few elements
-// past the last whole pack are handled by block 0.
+// Each thread moves one 16-byte pack per operand (float4 / 8 halves; the
+// casts use 8-element packs when narrowing and 4-element packs when
+// widening, so the wider side is always one contiguous 16-byte access per
+// lane), with a grid-stride loop over packs.  One load or store instruction
+// of a wave covers 1 KiB of contiguous memory.  Loads and stores are
+// non-temporal: nothing is reused, so the data should not displace L2
+// contents.  A sweep over 1-8 packs per thread, 256-1024 threads per block
+// and persistent grids found one pack per thread with 256 threads and a
+// full grid best on gfx950 (about 71% of peak at 75 MB per launch, 80% at
+// 300 MB), and non-temporal accesses worth about 8 points.  The few
+// elements past the last whole pack are handled by block 0.
 #include "common.hpp"
 
 namespace rl {
@@ -25,23 +29,23 @@ struct AddOp {  // vector_add.metal:11,20
 struct MulOp {  // mul.metal:18-19,34-35
     __device__ float operator()(float a, float b) const { return a * b; }
 };
+// SiLU's exp and reciprocal use the hardware instructions (silu_fast in
+// common.hpp): with the IEEE-exact expf and divide (~27 VALU ops per
+// element) the op is ALU-bound below HBM speed.  Error <= 3e-6 relative,
+// within the 1e-5 bar for f32 and 1 ulp of f16.  The f16 kernel's
+// x / (1 + e) and the f32 kernel's x * (1 / (1 + e)) are the same value up
+// to that error, so both use one expression.
 struct SiluF32Op {  // silu.metal:17-23: x * (1 / (1 + exp(-x)))
-    __device__ float operator()(float x, float) const {
-        float sigmoid = 1.0f / (1.0f + expf(-x));
-        return x * sigmoid;
-    }
+    __device__ float operator()(float x, float) const { return silu_fast(x); }
 };
 struct SiluF16Op {  // silu.metal:31-35: x / (1 + exp(-x))
-    __device__ float operator()(float x, float) const { return x / (1.0f + expf(-x)); }
+    __device__ float operator()(float x, float) const { return silu_fast(x); }
 };
 struct SwigluF16Op {  // silu.metal:44-45: (g / (1 + exp(-g))) * u, rounded once
-    __device__ float operator()(float g, float u) const { return (g / (1.0f + expf(-g))) * u; }
+    __device__ float operator()(float g, float u) const { return silu_fast(g) * u; }
 };
 struct SwigluF32Op {  // nn/swiglu.rs:15-37 F32 branch: silu_f32(g) then mul_f32
-    __device__ float operator()(float g, float u) const {
-        float sigmoid = 1.0f / (1.0f + expf(-g));
-        return (g * sigmoid) * u;
-    }
+    __device__ float operator()(float g, float u) const { return SiluF32Op()(g, 0.0f) * u; }
 };
 struct CopyOp {  // cast.metal:10,18: the conversion happens on store/load
     __device__ float operator()(float x, float) const { return x; }
@@ -159,8 +163,11 @@ rl_status launch_map(rl_context* ctx, const char* name, const void* a, const voi
                      uint64_t n, Op op) {
     if (n == 0) return RL_OK;
     if (rl_status st = activate(ctx)) return st;
-    constexpr int N = (sizeof(TIn) == 4 && sizeof(TOut) == 4) ? 4 : 8;
-    constexpr int UNROLL = 4;
+    // 16-byte packs; the widening cast uses 4-element packs so its stores
+    // stay 16 B per lane and contiguous across the wave (8-element f32 packs
+    // would be two strided 16-byte stores, which costs extra HBM writes).
+    constexpr int N = (sizeof(TIn) == 4 && sizeof(TOut) == 4) ? 4 : (sizeof(TOut) == 4 ? 4 : 8);
+    constexpr int UNROLL = 1;
     const bool vec = aligned_to(a, N * sizeof(TIn)) &&
                      (ARITY < 2 || aligned_to(b, N * sizeof(TIn))) &&
                      aligned_to(out, N * sizeof(TOut));
@@ -170,13 +177,9 @@ rl_status launch_map(rl_context* ctx, const char* name, const void* a, const voi
     if (vec) {
         uint64_t n_packs = n / N;
         uint32_t tail = uint32_t(n - n_packs * N);
-        hipLaunchKernelGGL((k_map<TIn, TOut, N, UNROLL, ARITY, Op>),
-                           dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads),
-                           0, ctx->stream, pa, pb, po, n_packs, tail, op);
+        RL_LAUNCH(ctx, (k_map<TIn, TOut, N, UNROLL, ARITY, Op>), dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads), pa, pb, po, n_packs, tail, op);
     } else {
-        hipLaunchKernelGGL((k_map<TIn, TOut, 1, UNROLL, ARITY, Op>),
-                           dim3(grid_for(n, uint64_t(kThreads) * UNROLL)), dim3(kThreads), 0,
-                           ctx->stream, pa, pb, po, n, 0u, op);
+        RL_LAUNCH(ctx, (k_map<TIn, TOut, 1, UNROLL, ARITY, Op>), dim3(grid_for(n, uint64_t(kThreads) * UNROLL)), dim3(kThreads), pa, pb, po, n, 0u, op);
     }
     return after_launch(ctx, name);
 }
@@ -189,7 +192,7 @@ rl_status launch_add_broadcast(rl_context* ctx, const char* name, const rl_buffe
     if (n == 0) return RL_OK;
     if (rl_status st = activate(ctx)) return st;
     constexpr int N = 16 / sizeof(T);
-    constexpr int UNROLL = 4;
+    constexpr int UNROLL = 1;
     const T* px = static_cast<const T*>(x->data);
     const T* pbias = static_cast<const T*>(bias->data);
     T* po = static_cast<T*>(out->data);
@@ -197,12 +200,9 @@ rl_status launch_add_broadcast(rl_context* ctx, const char* name, const rl_buffe
                      aligned_to(po, 16) && n / N <= UINT32_MAX;
     if (vec) {
         uint64_t n_packs = n / N;
-        hipLaunchKernelGGL((k_add_broadcast<T, N, UNROLL>),
-                           dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads),
-                           0, ctx->stream, px, pbias, po, n_packs, FastDiv(uint32_t(cols / N)));
+        RL_LAUNCH(ctx, (k_add_broadcast<T, N, UNROLL>), dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads), px, pbias, po, n_packs, FastDiv(uint32_t(cols / N)));
     } else {
-        hipLaunchKernelGGL((k_add_broadcast_scalar<T>), dim3(grid_for(n, kThreads * 4)),
-                           dim3(kThreads), 0, ctx->stream, px, pbias, po, n, cols);
+        RL_LAUNCH(ctx, (k_add_broadcast_scalar<T>), dim3(grid_for(n, kThreads * 4)), dim3(kThreads), px, pbias, po, n, cols);
     }
     return after_launch(ctx, name);
 }

@@ -183,20 +183,16 @@ rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* 
         const dim3 grid(grid_for(n_packs, uint64_t(kThreads) * U)), block(kThreads);
         switch (n) {
             case 8:
-                hipLaunchKernelGGL((k_gather_rows<T, 8, U>), grid, block, 0, ctx->stream, src, dst,
-                                   uint32_t(n_packs), row_packs, outer);
+                RL_LAUNCH(ctx, (k_gather_rows<T, 8, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
                 break;
             case 4:
-                hipLaunchKernelGGL((k_gather_rows<T, 4, U>), grid, block, 0, ctx->stream, src, dst,
-                                   uint32_t(n_packs), row_packs, outer);
+                RL_LAUNCH(ctx, (k_gather_rows<T, 4, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
                 break;
             case 2:
-                hipLaunchKernelGGL((k_gather_rows<T, 2, U>), grid, block, 0, ctx->stream, src, dst,
-                                   uint32_t(n_packs), row_packs, outer);
+                RL_LAUNCH(ctx, (k_gather_rows<T, 2, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
                 break;
             default:
-                hipLaunchKernelGGL((k_gather_rows<T, 1, U>), grid, block, 0, ctx->stream, src, dst,
-                                   uint32_t(n_packs), row_packs, outer);
+                RL_LAUNCH(ctx, (k_gather_rows<T, 1, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
                 break;
         }
     } else {
@@ -206,8 +202,7 @@ rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* 
             all.dim[d] = FastDiv(uint32_t(v.dims[rank - 1 - d]));
             all.stride[d] = v.strides[rank - 1 - d];
         }
-        hipLaunchKernelGGL((k_gather_elems<T>), dim3(grid_for(numel, kThreads * 4)),
-                           dim3(kThreads), 0, ctx->stream, src, dst, uint32_t(numel), all);
+        RL_LAUNCH(ctx, (k_gather_elems<T>), dim3(grid_for(numel, kThreads * 4)), dim3(kThreads), src, dst, uint32_t(numel), all);
     }
     return after_launch(ctx, name);
 }
@@ -293,10 +288,7 @@ rl_status repeat_kv_impl(rl_context* ctx, const char* name, const rl_buffer* in,
         const uint64_t head_packs = head / N;
         const uint64_t n_packs = in_numel / N;
         const bool small = n_packs <= UINT32_MAX && head_packs <= UINT32_MAX;
-        hipLaunchKernelGGL((k_repeat_kv<T, N, U>), dim3(grid_for(n_packs, kThreads * U)),
-                           dim3(kThreads), 0, ctx->stream, static_cast<const T*>(src),
-                           static_cast<T*>(dst), n_packs, head_packs,
-                           FastDiv(small ? uint32_t(head_packs) : 1u), uint32_t(repeats), small);
+        RL_LAUNCH(ctx, (k_repeat_kv<T, N, U>), dim3(grid_for(n_packs, kThreads * U)), dim3(kThreads), static_cast<const T*>(src), static_cast<T*>(dst), n_packs, head_packs, FastDiv(small ? uint32_t(head_packs) : 1u), uint32_t(repeats), small);
     };
     const bool aligned16 = aligned_to(src, 16) && aligned_to(dst, 16);
     if (es == 4) {

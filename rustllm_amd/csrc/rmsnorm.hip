@@ -135,23 +135,17 @@ rl_status launch_rmsnorm(rl_context* ctx, const char* name, const T* x, const T*
         const uint32_t hp = uint32_t(h_packs);
         const float hf = float(hidden);
         if (h_packs <= 1 * kWave)
-            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 1, ADD>), grid, block, 0, ctx->stream, x,
-                               residual, weight, sum_out, y, r32, hp, hf, eps);
+            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 1, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
         else if (h_packs <= 2 * kWave)
-            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 2, ADD>), grid, block, 0, ctx->stream, x,
-                               residual, weight, sum_out, y, r32, hp, hf, eps);
+            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 2, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
         else if (h_packs <= 4 * kWave)
-            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 4, ADD>), grid, block, 0, ctx->stream, x,
-                               residual, weight, sum_out, y, r32, hp, hf, eps);
+            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 4, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
         else if (h_packs <= 8 * kWave)
-            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 8, ADD>), grid, block, 0, ctx->stream, x,
-                               residual, weight, sum_out, y, r32, hp, hf, eps);
+            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 8, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
         else
-            hipLaunchKernelGGL((k_rmsnorm_wave<T, N, 16, ADD>), grid, block, 0, ctx->stream, x,
-                               residual, weight, sum_out, y, r32, hp, hf, eps);
+            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 16, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
     } else {
-        hipLaunchKernelGGL((k_rmsnorm_block<T, ADD>), dim3(r32), dim3(kThreads), 0, ctx->stream,
-                           x, residual, weight, sum_out, y, r32, uint32_t(hidden), eps);
+        RL_LAUNCH(ctx, (k_rmsnorm_block<T, ADD>), dim3(r32), dim3(kThreads), x, residual, weight, sum_out, y, r32, uint32_t(hidden), eps);
     }
     return after_launch(ctx, name);
 }

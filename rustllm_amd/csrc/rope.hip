@@ -134,20 +134,16 @@ rl_status launch_rope(rl_context* ctx, const char* name, const T* src, const uin
     const uint32_t h32 = uint32_t(half), s32 = uint32_t(start), ni = uint32_t(n_items);
     switch (n) {
         case 8:
-            hipLaunchKernelGGL((k_rope<T, 8, U>), grid, block, 0, ctx->stream, src, cos_table,
-                               sin_table, out, ni, ppr, rd, h32, s32);
+            RL_LAUNCH(ctx, (k_rope<T, 8, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32);
             break;
         case 4:
-            hipLaunchKernelGGL((k_rope<T, 4, U>), grid, block, 0, ctx->stream, src, cos_table,
-                               sin_table, out, ni, ppr, rd, h32, s32);
+            RL_LAUNCH(ctx, (k_rope<T, 4, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32);
             break;
         case 2:
-            hipLaunchKernelGGL((k_rope<T, 2, U>), grid, block, 0, ctx->stream, src, cos_table,
-                               sin_table, out, ni, ppr, rd, h32, s32);
+            RL_LAUNCH(ctx, (k_rope<T, 2, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32);
             break;
         default:
-            hipLaunchKernelGGL((k_rope<T, 1, U>), grid, block, 0, ctx->stream, src, cos_table,
-                               sin_table, out, ni, ppr, rd, h32, s32);
+            RL_LAUNCH(ctx, (k_rope<T, 1, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32);
             break;
     }
     return after_launch(ctx, name);

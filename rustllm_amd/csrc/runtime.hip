@@ -399,6 +399,16 @@ rl_status rl_event_elapsed_ms(rl_event* start, rl_event* end, float* ms) {
     return RL_OK;
 }
 
+rl_status rl_event_time_next_kernel(rl_context* ctx, rl_event* start, rl_event* stop) {
+    if (start == nullptr || stop == nullptr)
+        return fail(RL_ERR_INVALID_ARGUMENT, "null event");
+    if (rl_status st = require_context(ctx)) return st;
+    if (ctx->capturing) return fail(RL_ERR_DEVICE, "cannot time a kernel while recording a graph");
+    ctx->timed_start = start->event;
+    ctx->timed_stop = stop->event;
+    return RL_OK;
+}
+
 void rl_event_destroy(rl_event* event) {
     if (event == nullptr) return;
     if (event->event) (void)hipEventDestroy(event->event);

@@ -18,6 +18,12 @@
 //
 // The standalone scale/mask op also skips reading masked scores: its output
 // there is -inf whatever the input.
+//
+// exp(x - max) runs on the hardware exp2 (exp_fast in common.hpp, subnormal
+// results kept): relative error <= |x - max| * log2(e) * 2^-24 * ln 2 plus
+// ~1 ulp, i.e. <= 2e-6 for scores within 40 of the row max, inside the 1e-5
+// bar; the IEEE expf would make the f16 rows ALU-bound.  The normaliser is
+// one correctly rounded 1 / sum per row.
 #include "common.hpp"
 
 namespace rl {
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_wave(const T* __restrict__
         if (p < w_packs && (!MASK || p * N < kept)) {
 #pragma unroll
             for (int j = 0; j < N; ++j) {
-                float e = expf(v[k][j] - m);
+                float e = exp_fast(v[k][j] - m);
                 v[k][j] = e;
                 s += e;
             }
@@ -211,7 +217,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_block(const T* __restrict_
         if (p < w_packs && (!MASK || p * N < kept)) {
 #pragma unroll
             for (int j = 0; j < N; ++j) {
-                float e = expf(v[k][j] - m);
+                float e = exp_fast(v[k][j] - m);
                 v[k][j] = e;
                 s += e;
             }
@@ -242,10 +248,10 @@ __global__ __launch_bounds__(kThreads) void k_softmax_block(const T* __restrict_
 // as exp(inf - inf) in the reference's sum.
 __device__ inline void online_add(float& m, float& s, float x) {
     if (x > m) {
-        s = s * expf(m - x) + expf(x - x);
+        s = s * exp_fast(m - x) + exp_fast(x - x);
         m = x;
     } else {
-        s += expf(x - m);
+        s += exp_fast(x - m);
     }
 }
 
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_stream(const T* __restrict
     // NaN scores make gs NaN, and every output NaN, as in the reference.
     const float inv = 1.0f / gs;
     for (uint32_t i = threadIdx.x; i < width; i += kThreads) {
-        float e = (i < kept) ? expf(score(i) - gm) : 0.0f;
+        float e = (i < kept) ? exp_fast(score(i) - gm) : 0.0f;
         out[off + i] = from_float<T>(e * inv);
     }
     }
@@ -361,7 +367,7 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
     if (packs_ok && w_packs <= 16 * kWave) {
         const dim3 grid(unsigned(ceil_div(rows, kRowsPerBlock))), block(kThreads);
 #define RL_SOFTMAX_WAVE(NV)                                                                    \
-    hipLaunchKernelGGL((k_softmax_wave<T, N, NV, MASK>), grid, block, 0, ctx->stream, in, out, \
+    RL_LAUNCH(ctx, (k_softmax_wave<T, N, NV, MASK>), grid, block, in, out, \
                        r32, w32, mp)
         if (w_packs <= 1 * kWave)
             RL_SOFTMAX_WAVE(1);
@@ -377,7 +383,7 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
     } else if (packs_ok && w_packs <= 16 * kThreads) {
         const dim3 grid(row_grid(rows)), block(kThreads);
 #define RL_SOFTMAX_BLOCK(NV)                                                                    \
-    hipLaunchKernelGGL((k_softmax_block<T, N, NV, MASK>), grid, block, 0, ctx->stream, in, out, \
+    RL_LAUNCH(ctx, (k_softmax_block<T, N, NV, MASK>), grid, block, in, out, \
                        r32, w32, mp)
         if (w_packs <= 8 * kThreads)
             RL_SOFTMAX_BLOCK(8);
@@ -385,8 +391,7 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
             RL_SOFTMAX_BLOCK(16);
 #undef RL_SOFTMAX_BLOCK
     } else {
-        hipLaunchKernelGGL((k_softmax_stream<T, MASK>), dim3(row_grid(rows)), dim3(kThreads), 0,
-                           ctx->stream, in, out, r32, w32, mp);
+        RL_LAUNCH(ctx, (k_softmax_stream<T, MASK>), dim3(row_grid(rows)), dim3(kThreads), in, out, r32, w32, mp);
     }
     return after_launch(ctx, name);
 }
@@ -398,11 +403,9 @@ rl_status launch_scale_mask(rl_context* ctx, const char* name, const T* in, T* o
     constexpr int N = 16 / sizeof(T);
     const bool packs_ok = width % N == 0 && aligned_to(in, 16) && aligned_to(out, 16);
     if (packs_ok)
-        hipLaunchKernelGGL((k_scale_mask<T, N>), dim3(row_grid(rows)), dim3(kThreads), 0,
-                           ctx->stream, in, out, uint32_t(rows), uint32_t(width), mp);
+        RL_LAUNCH(ctx, (k_scale_mask<T, N>), dim3(row_grid(rows)), dim3(kThreads), in, out, uint32_t(rows), uint32_t(width), mp);
     else
-        hipLaunchKernelGGL((k_scale_mask<T, 1>), dim3(row_grid(rows)), dim3(kThreads), 0,
-                           ctx->stream, in, out, uint32_t(rows), uint32_t(width), mp);
+        RL_LAUNCH(ctx, (k_scale_mask<T, 1>), dim3(row_grid(rows)), dim3(kThreads), in, out, uint32_t(rows), uint32_t(width), mp);
     return after_launch(ctx, name);
 }
 

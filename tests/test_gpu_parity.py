@@ -286,12 +286,14 @@ def test_softmax(ctx, dtype, rows, width):
 @pytest.mark.parametrize("width", [8, 3, 5000, 70000])
 def test_softmax_special_rows(ctx, width):
     # all -inf: f32 NaN (no guard, softmax.metal:7-132), f16 zeros (:166-173);
-    # a NaN score poisons its row; -inf entries get exact zeros.
-    x = np.zeros((4, width), np.float32)
+    # a NaN score poisons its row; -inf entries get exact zeros; scores 85..110
+    # below the max give subnormal probabilities, which must not flush to 0.
+    x = np.zeros((5, width), np.float32)
     x[0] = -np.inf
     x[1, 0] = np.nan
     x[2, ::2] = -np.inf
     x[3] = np.linspace(-3, 3, width, dtype=np.float32)
+    x[4] = -np.linspace(0, 110, width, dtype=np.float32)
     for dt in DT:
         xi = x.astype(dt)
         got = run(ctx, lambda: ctx.softmax(ctx.upload(xi))).numpy()
