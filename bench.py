@@ -154,6 +154,53 @@ def capture(ctx, fn):
     return g
 
 
+def capture_step(ctx, aux, ops, s, events):
+    """One step as a graph.  With aux contexts the independent ops are spread
+    round-robin over their streams, forked from and joined back into ctx's
+    stream, so the recorded graph has parallel branches and one kernel's
+    ramp-down overlaps the next one's ramp-up."""
+    fork, joins = events
+    ctx.capture_begin()
+    try:
+        if aux:
+            ctx.record(fork)
+            for a in aux:
+                a.wait(fork)
+        streams = [ctx] + aux
+        for i, op in enumerate(ops):
+            op.launch(streams[i % len(streams)], s)
+        for a, e in zip(aux, joins):
+            a.record(e)
+            ctx.wait(e)
+    finally:
+        g = ctx.capture_end()
+    return g
+
+
+def time_step(ctx, aux, ops, sets, steps, warmup):
+    """ms per step, replaying one recorded step graph per buffer set."""
+    events = [(ctx.event(), [ctx.event() for _ in aux]) for _ in sets]
+    graphs = [capture_step(ctx, aux, ops, s, ev) for s, ev in zip(sets, events)]
+    for i in range(warmup):
+        ctx.graph_launch(graphs[i % len(graphs)])
+    ctx.finish()
+    start, end = ctx.event(), ctx.event()
+    ctx.record(start)
+    for i in range(steps):
+        ctx.graph_launch(graphs[i % len(graphs)])
+    ctx.record(end)
+    ms = ctx.elapsed_ms(start, end)
+    ctx.finish()
+    for g in graphs:
+        ctx.graph_destroy(g)
+    for fork, joins in events:
+        for e in [fork] + joins:
+            ctx.destroy_event(e)
+    ctx.destroy_event(start)
+    ctx.destroy_event(end)
+    return ms / steps
+
+
 def kernel_times_us(ctx, launches, reps):
     """Device time of `reps` launches (cycling through `launches`, one kernel
     each), every one bracketed by events that the kernel itself stamps at its
@@ -410,6 +457,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=4, help="buffer sets rotated across steps")
+    ap.add_argument("--streams", type=int, default=4,
+                    help="streams the step's independent ops are spread over")
     ap.add_argument("--op-reps", type=int, default=100, help="timed launches per op line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -438,22 +487,17 @@ def main():
     step_bytes = sum(op.nbytes for op in ops)
     log(f"footprint {footprint / 2**30:.2f} GiB, {step_bytes / 1e6:.1f} MB per step")
 
-    graphs = [capture(ctx, lambda s=s: [op.launch(ctx, s) for op in ops]) for s in sets]
-    for i in range(args.warmup):
-        ctx.graph_launch(graphs[i % len(graphs)])
-    ctx.finish()
-    start, end = ctx.event(), ctx.event()
-    ctx.record(start)
-    for i in range(args.steps):
-        ctx.graph_launch(graphs[i % len(graphs)])
-    ctx.record(end)
-    ms_total = ctx.elapsed_ms(start, end)
-    ctx.finish()
-    ms_step = ms_total / args.steps
+    aux = [abi.Context(0) for _ in range(max(0, args.streams - 1))]
+    ms_step = time_step(ctx, aux, ops, sets, args.steps, args.warmup)
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"step: {ms_step * 1e3:.1f} us, {value:.1f} GB/s ({100 * value / PEAK_GBS:.1f}% of peak)")
-    for g in graphs:
-        ctx.graph_destroy(g)
+    log(f"step on {args.streams} streams: {ms_step * 1e3:.1f} us, {value:.1f} GB/s "
+        f"({100 * value / PEAK_GBS:.1f}% of peak)")
+    ms_seq = time_step(ctx, [], ops, sets, args.steps, args.warmup)
+    seq_value = step_bytes / (ms_seq * 1e-3) / 1e9
+    log(f"step on 1 stream: {ms_seq * 1e3:.1f} us, {seq_value:.1f} GB/s "
+        f"({100 * seq_value / PEAK_GBS:.1f}% of peak)")
+    for a in aux:
+        a.close()
 
     log("per op (configs[1]):")
     rows = per_op_rows(ctx, ops, sets, args.op_reps)
@@ -498,7 +542,10 @@ def main():
                                "f16 storage (add, mul, silu, swiglu, bias add, casts, "
                                "contiguous [1,9,4096,64] view, repeat_kv 3->9)",
                    "ops_per_step": len(ops), "bytes_per_step": step_bytes,
-                   "buffer_sets": args.sets, "footprint_gib": round(footprint / 2**30, 2)},
+                   "buffer_sets": args.sets, "footprint_gib": round(footprint / 2**30, 2),
+                   "streams": args.streams,
+                   "one_stream_GBps": round(seq_value, 1),
+                   "one_stream_ms_per_step": round(ms_seq, 5)},
         "pct_of_peak": round(100 * value / PEAK_GBS, 1),
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -138,9 +138,13 @@ rl_status rl_graph_capture_end(rl_context* ctx, rl_graph** out);
 rl_status rl_graph_launch(rl_context* ctx, rl_graph* graph);
 void rl_graph_destroy(rl_graph* graph);
 
-/* Stream timestamps for measuring device time. */
+/* Stream timestamps for measuring device time, and cross-stream ordering:
+ * rl_event_wait makes later work of `ctx` wait for `event` (recorded on
+ * another context's stream), which also forks and joins a graph recording
+ * across contexts so that independent ops become parallel branches. */
 rl_status rl_event_create(rl_context* ctx, rl_event** out);
 rl_status rl_event_record(rl_context* ctx, rl_event* event);
+rl_status rl_event_wait(rl_context* ctx, rl_event* event);
 rl_status rl_event_elapsed_ms(rl_event* start, rl_event* end, float* ms);
 void rl_event_destroy(rl_event* event);
 /* The next kernel this context launches records its own start and end

@@ -85,6 +85,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "rl_graph_destroy": ([_P], None),
     "rl_event_create": ([_P, ctypes.POINTER(_P)], _I32),
     "rl_event_record": ([_P, _P], _I32),
+    "rl_event_wait": ([_P, _P], _I32),
     "rl_event_elapsed_ms": ([_P, _P, ctypes.POINTER(_F)], _I32),
     "rl_event_destroy": ([_P], None),
     "rl_event_time_next_kernel": ([_P, _P, _P], _I32),
@@ -266,6 +267,10 @@ class Context:
 
     def record(self, event) -> None:
         check(self.lib.rl_event_record(self.handle, event))
+
+    def wait(self, event) -> None:
+        """Later work on this context waits for `event`."""
+        check(self.lib.rl_event_wait(self.handle, event))
 
     def elapsed_ms(self, start, end) -> float:
         ms = ctypes.c_float()

@@ -391,6 +391,14 @@ rl_status rl_event_record(rl_context* ctx, rl_event* event) {
     return RL_OK;
 }
 
+rl_status rl_event_wait(rl_context* ctx, rl_event* event) {
+    if (event == nullptr) return fail(RL_ERR_INVALID_ARGUMENT, "event is null");
+    if (rl_status st = require_context(ctx)) return st;
+    if (rl_status st = activate(ctx)) return st;
+    RL_HIP(hipStreamWaitEvent(ctx->stream, event->event, 0), "hipStreamWaitEvent");
+    return RL_OK;
+}
+
 rl_status rl_event_elapsed_ms(rl_event* start, rl_event* end, float* ms) {
     if (start == nullptr || end == nullptr || ms == nullptr)
         return fail(RL_ERR_INVALID_ARGUMENT, "null event or result pointer");

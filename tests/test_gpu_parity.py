@@ -463,6 +463,54 @@ def test_graph_replay_matches_eager(ctx):
     ctx.graph_destroy(graph)
 
 
+def test_forked_graph_over_two_streams_matches_eager(ctx):
+    """Independent ops recorded on two contexts' streams (fork/join by events)
+    replay correctly, every time, with eager work in between."""
+    aux = abi.Context(0)
+    try:
+        a = norm(("fork", "a"), (2048, 256), np.float32)
+        b = norm(("fork", "b"), (2048, 256), np.float32)
+        h = norm(("fork", "h"), (2048, 256), np.float16)
+        da, db, dh = ctx.upload(a), ctx.upload(b), ctx.upload(h)
+        o1, o2, o3 = (ctx.empty(a.shape, np.float32), ctx.empty(a.shape, np.float32),
+                      ctx.empty(a.shape, np.float16))
+        fork, join = ctx.event(), ctx.event()
+        ctx.capture_begin()
+        ctx.record(fork)
+        aux.wait(fork)
+        ctx.add(da, db, o1)
+        aux.swiglu(da, db, o2)
+        aux.silu(dh, o3)
+        aux.record(join)
+        ctx.wait(join)
+        graph = ctx.capture_end()
+        for i in range(3):
+            ctx.graph_launch(graph)
+            ctx.finish()
+            assert_bitexact(o1.numpy(), o.add(a, b), f"replay {i}")
+            check_float(o2.numpy(), o.swiglu(a, b), f"replay {i}")
+            check_float(o3.numpy(), o.silu(h), f"replay {i}")
+            run(ctx, lambda: ctx.mul(da, db))
+        ctx.graph_destroy(graph)
+        ctx.destroy_event(fork)
+        ctx.destroy_event(join)
+    finally:
+        aux.close()
+
+
+def test_kernel_stamped_events_time_one_kernel(ctx):
+    a = ctx.upload(norm(("evt",), (1 << 22,), np.float32))
+    start, stop = ctx.event(), ctx.event()
+    ctx.time_next_kernel(start, stop)
+    out = ctx.silu(a)
+    ctx.finish()
+    us = ctx.elapsed_ms(start, stop) * 1e3
+    assert 0.5 < us < 5000
+    check_float(out.numpy(), o.silu(a.numpy()), "timed launch")
+    ctx.destroy_event(start)
+    ctx.destroy_event(stop)
+
+
 def test_device_validation_matches_cpu(ctx):
     a, b = ctx.upload(np.ones(8, np.float32)), ctx.upload(np.ones(9, np.float32))
     with pytest.raises(abi.RustLLMError) as err:
