@@ -436,6 +436,28 @@ def probe(ctx, host, ops):
             op.launch(ctx, s)
             ctx.finish()
         log(f"probe {op.name}: {op.nbytes} algorithmic bytes per launch")
+    # The row ops at their benchmark shapes.
+    hid, tok = 960, 4096
+    x = ctx.upload(synth.normal(1, (tok, hid), 0, 2.0, F16))
+    w = ctx.upload(synth.uniform_range(2, (hid,), 0.5, 1.5, F16))
+    y = ctx.empty((tok, hid), F16)
+    c, s_ = _rope_table(64, tok)
+    dc, ds = ctx.upload(c), ctx.upload(s_)
+    q = ctx.upload(synth.normal(3, (1, 15, tok, 64), 0, 1, F16))
+    qo = ctx.empty((1, 15, tok, 64), F16)
+    sc = ctx.upload(synth.normal(4, (9, 2048, 2048), 0, 4.0, F32))
+    so = ctx.empty((9, 2048, 2048), F32)
+    for name, nbytes, fn in [
+        ("rmsnorm_f16 [4096,960]", tok * hid * 4 + hid * 2, lambda: ctx.rmsnorm(x, w, 1e-5, y)),
+        ("rope_f16 [1,15,4096,64]", 2 * 15 * tok * 64 * 2, lambda: ctx.rope(q, dc, ds, 0, qo)),
+        ("attention_softmax_f32 [9,2048,2048]", 9 * (2048 * 2049 // 2) * 4 + 9 * 2048 * 2048 * 4,
+         lambda: ctx.attention_softmax(sc, 0.125, 0, so)),
+    ]:
+        for _ in range(3):
+            ctx.begin()
+            fn()
+            ctx.finish()
+        log(f"probe {name}: {nbytes} algorithmic bytes per launch")
     # A contiguous "view" of a contiguous buffer is a plain copy kernel.
     nbytes = 256 << 20
     n = nbytes // 4
