@@ -479,7 +479,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=4, help="buffer sets rotated across steps")
-    ap.add_argument("--streams", type=int, default=4,
+    ap.add_argument("--streams", type=int, default=1,
                     help="streams the step's independent ops are spread over")
     ap.add_argument("--op-reps", type=int, default=100, help="timed launches per op line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -514,10 +514,11 @@ def main():
     value = step_bytes / (ms_step * 1e-3) / 1e9
     log(f"step on {args.streams} streams: {ms_step * 1e3:.1f} us, {value:.1f} GB/s "
         f"({100 * value / PEAK_GBS:.1f}% of peak)")
-    ms_seq = time_step(ctx, [], ops, sets, args.steps, args.warmup)
+    ms_seq = ms_step if not aux else time_step(ctx, [], ops, sets, args.steps, args.warmup)
     seq_value = step_bytes / (ms_seq * 1e-3) / 1e9
-    log(f"step on 1 stream: {ms_seq * 1e3:.1f} us, {seq_value:.1f} GB/s "
-        f"({100 * seq_value / PEAK_GBS:.1f}% of peak)")
+    if aux:
+        log(f"step on 1 stream: {ms_seq * 1e3:.1f} us, {seq_value:.1f} GB/s "
+            f"({100 * seq_value / PEAK_GBS:.1f}% of peak)")
     for a in aux:
         a.close()
 
