@@ -2,12 +2,17 @@
 // gfx950.
 //
 // Softmax (kernels/softmax.metal) reads each row three times through a
-// 256-thread group with two 8-barrier shared-memory trees.  Here a row of up
-// to 64 x 16 packs (4096 f32 / 8192 f16) is owned by one wave64 and held in
-// VGPRs: one HBM read, a butterfly max, exp in registers, a butterfly sum,
-// one write.  Longer rows use a whole 256-thread block per row (LDS only for
-// the cross-wave step) while they fit its registers, and beyond that a
-// streaming kernel with an online max/sum (m, s) merge and a second read.
+// 256-thread group with two 8-barrier shared-memory trees.  Here a row is
+// held in VGPRs by a group of TPR = 64, 128 or 256 threads (one to four
+// waves) with up to NV 16-byte packs per thread: one HBM read, a max
+// reduction, exp in registers, a sum reduction, one write.  Reductions are
+// wave64 butterflies of cross-lane shuffles; LDS is used only to combine the
+// waves of a group.  A sweep of 64/128/256 threads per row on the causal
+// configurations ([9, 2048, 2048] f32, [15, 4096, 4096] f16) found two waves
+// per row with four packs per thread best: 73% / 76% of HBM peak, against
+// 66% / 71% for one wave per row with eight packs.  Rows longer than
+// 256 x 16 packs use a streaming kernel with an online (max, sum) merge and
+// a second read.
 //
 // Scale/mask + softmax fused (the adjacent calls at nn/attention.rs:233-240):
 // for query row q the keys past start + q are masked, so their scores are
@@ -31,7 +36,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
-constexpr int kRowsPerBlock = kThreads / kWave;
 
 struct MaskParams {
     float scale;
@@ -58,186 +62,120 @@ __device__ inline uint32_t kept_keys(uint32_t row, uint32_t width, const MaskPar
     return kept < width ? uint32_t(kept) : width;
 }
 
-// ------------------------------------------------ one wave per row, in VGPRs
-
-template <typename T, int N, int NV, bool MASK>
-__global__ __launch_bounds__(kThreads) void k_softmax_wave(const T* __restrict__ in,
-                                                           T* __restrict__ out, uint32_t rows,
-                                                           uint32_t width, MaskParams mp) {
-    typedef typename VecOf<T, N>::type V;
-    const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t row = blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
-    if (row >= rows) return;  // whole wave leaves together
-    const uint32_t w_packs = width / N;
-    const uint64_t row_off = uint64_t(row) * w_packs;
-    const V* src = reinterpret_cast<const V*>(in) + row_off;
-    V* dst = reinterpret_cast<V*>(out) + row_off;
-    const uint32_t kept = MASK ? kept_keys(row, width, mp) : width;
-
-    float v[NV][N];
-    float m = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const uint32_t p = lane + k * kWave;
-        if (p < w_packs && (!MASK || p * N < kept)) {
-            V raw = load_stream(src + p);
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                float f;
-                if constexpr (MASK)
-                    f = (p * N + j < kept) ? scaled_score(raw[j], mp.scale) : -INFINITY;
-                else
-                    f = to_float(raw[j]);
-                v[k][j] = f;
-                m = fmaxf(m, f);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < N; ++j) v[k][j] = -INFINITY;
-        }
-    }
-    m = wave_max(m);
-    if (is_f16<T>() && m == -INFINITY) {  // softmax.metal:166-173
-        V z;
-#pragma unroll
-        for (int j = 0; j < N; ++j) z[j] = from_float<T>(0.0f);
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const uint32_t p = lane + k * kWave;
-            if (p < w_packs) store_stream(dst + p, z);
-        }
-        return;
-    }
-    float s = 0.0f;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const uint32_t p = lane + k * kWave;
-        if (p < w_packs && (!MASK || p * N < kept)) {
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                float e = exp_fast(v[k][j] - m);
-                v[k][j] = e;
-                s += e;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < N; ++j) v[k][j] = 0.0f;
-        }
-    }
-    s = wave_sum(s);
-    const float inv = 1.0f / s;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const uint32_t p = lane + k * kWave;
-        if (p < w_packs) {
-            V o;
-#pragma unroll
-            for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
-            store_stream(dst + p, o);
-        }
-    }
-}
-
-// --------------------------------------- 256 threads per row, in VGPRs + LDS
-
-__device__ inline float block_max(float v, float* lds) {
+// Max / sum over the TPR threads of a row group (the waves of a group are
+// consecutive).  `lds` holds one slot per wave of the block and is written
+// once per call; callers separate consecutive uses by a barrier.
+template <int TPR>
+__device__ inline float group_max(float v, float* lds) {
     v = wave_max(v);
-    __syncthreads();  // lds may still be read from a previous reduction
-    if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
-    __syncthreads();
-    float r = lds[0];
+    if constexpr (TPR > kWave) {
+        constexpr int WPR = TPR / kWave;
+        if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
+        __syncthreads();
+        const int first = (threadIdx.x / TPR) * WPR;
+        float r = lds[first];
 #pragma unroll
-    for (int w = 1; w < kThreads / kWave; ++w) r = fmaxf(r, lds[w]);
-    return r;
-}
-
-__device__ inline float block_sum(float v, float* lds) {
-    v = wave_sum(v);
-    __syncthreads();
-    if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
-    __syncthreads();
-    float r = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kThreads / kWave; ++w) r += lds[w];
-    return r;
-}
-
-template <typename T, int N, int NV, bool MASK>
-__global__ __launch_bounds__(kThreads) void k_softmax_block(const T* __restrict__ in,
-                                                            T* __restrict__ out, uint32_t rows,
-                                                            uint32_t width, MaskParams mp) {
-    typedef typename VecOf<T, N>::type V;
-    __shared__ float lds[kThreads / kWave];
-    // Rows are uniform per block, so the barriers inside stay uniform too.
-    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    const uint32_t w_packs = width / N;
-    const uint64_t row_off = uint64_t(row) * w_packs;
-    const V* src = reinterpret_cast<const V*>(in) + row_off;
-    V* dst = reinterpret_cast<V*>(out) + row_off;
-    const uint32_t kept = MASK ? kept_keys(row, width, mp) : width;
-
-    float v[NV][N];
-    float m = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const uint32_t p = threadIdx.x + k * kThreads;
-        if (p < w_packs && (!MASK || p * N < kept)) {
-            V raw = load_stream(src + p);
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                float f;
-                if constexpr (MASK)
-                    f = (p * N + j < kept) ? scaled_score(raw[j], mp.scale) : -INFINITY;
-                else
-                    f = to_float(raw[j]);
-                v[k][j] = f;
-                m = fmaxf(m, f);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < N; ++j) v[k][j] = -INFINITY;
-        }
+        for (int w = 1; w < WPR; ++w) r = fmaxf(r, lds[first + w]);
+        v = r;
     }
-    m = block_max(m, lds);
-    if (is_f16<T>() && m == -INFINITY) {
-        V z;
+    return v;
+}
+
+template <int TPR>
+__device__ inline float group_sum(float v, float* lds) {
+    v = wave_sum(v);
+    if constexpr (TPR > kWave) {
+        constexpr int WPR = TPR / kWave;
+        if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
+        __syncthreads();
+        const int first = (threadIdx.x / TPR) * WPR;
+        float r = 0.0f;
 #pragma unroll
-        for (int j = 0; j < N; ++j) z[j] = from_float<T>(0.0f);
+        for (int w = 0; w < WPR; ++w) r += lds[first + w];
+        v = r;
+    }
+    return v;
+}
+
+// ------------------------------------------ a row per TPR threads, in VGPRs
+
+// Block b takes rows row_base + b * RPB ... + RPB - 1 (RPB = kThreads / TPR).
+// Threads of a group past the last row take part in the barriers with no
+// memory accesses.  (One group per block, no grid-stride loop: the loop
+// doubled the VGPR count of the masked f16 variant.)
+template <typename T, int N, int NV, int TPR, bool MASK>
+__global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__ in,
+                                                           T* __restrict__ out, uint32_t row_base,
+                                                           uint32_t rows, uint32_t width,
+                                                           MaskParams mp) {
+    typedef typename VecOf<T, N>::type V;
+    constexpr int RPB = kThreads / TPR;
+    __shared__ float lds_m[kThreads / kWave];
+    __shared__ float lds_s[kThreads / kWave];
+    const uint32_t lane = threadIdx.x % TPR;
+    const uint32_t w_packs = width / N;
+    {
+        const uint64_t row64 = uint64_t(row_base) + uint64_t(blockIdx.x) * RPB + threadIdx.x / TPR;
+        const bool active = row64 < rows;
+        const uint32_t row = uint32_t(row64);
+        const uint64_t row_off = uint64_t(active ? row : 0) * w_packs;
+        const V* src = reinterpret_cast<const V*>(in) + row_off;
+        V* dst = reinterpret_cast<V*>(out) + row_off;
+        const uint32_t kept = !active ? 0u : MASK ? kept_keys(row, width, mp) : width;
+
+        float v[NV][N];
+        float m = -INFINITY;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const uint32_t p = threadIdx.x + k * kThreads;
-            if (p < w_packs) store_stream(dst + p, z);
-        }
-        continue;  // uniform across the block: every thread saw the same m
-    }
-    float s = 0.0f;
+            const uint32_t p = lane + k * TPR;
+            if (p < w_packs && p * N < kept) {
+                V raw = load_stream(src + p);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const uint32_t p = threadIdx.x + k * kThreads;
-        if (p < w_packs && (!MASK || p * N < kept)) {
+                for (int j = 0; j < N; ++j) {
+                    float f;
+                    if constexpr (MASK)
+                        f = (p * N + j < kept) ? scaled_score(raw[j], mp.scale) : -INFINITY;
+                    else
+                        f = to_float(raw[j]);
+                    v[k][j] = f;
+                    m = fmaxf(m, f);
+                }
+            } else {
 #pragma unroll
-            for (int j = 0; j < N; ++j) {
-                float e = exp_fast(v[k][j] - m);
-                v[k][j] = e;
-                s += e;
+                for (int j = 0; j < N; ++j) v[k][j] = -INFINITY;
             }
-        } else {
-#pragma unroll
-            for (int j = 0; j < N; ++j) v[k][j] = 0.0f;
         }
-    }
-    s = block_sum(s, lds);
-    const float inv = 1.0f / s;
+        m = group_max<TPR>(m, lds_m);
+        // softmax.metal:166-173: an f16 row whose max is -inf is all zeros.
+        const bool zero_row = is_f16<T>() && m == -INFINITY;
+        float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const uint32_t p = threadIdx.x + k * kThreads;
-        if (p < w_packs) {
-            V o;
+        for (int k = 0; k < NV; ++k) {
+            const uint32_t p = lane + k * TPR;
+            if (!zero_row && p < w_packs && p * N < kept) {
 #pragma unroll
-            for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
-            store_stream(dst + p, o);
+                for (int j = 0; j < N; ++j) {
+                    float e = exp_fast(v[k][j] - m);
+                    v[k][j] = e;
+                    s += e;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < N; ++j) v[k][j] = 0.0f;
+            }
         }
-    }
+        s = group_sum<TPR>(s, lds_s);
+        const float inv = zero_row ? 0.0f : 1.0f / s;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const uint32_t p = lane + k * TPR;
+            if (active && p < w_packs) {
+                V o;
+#pragma unroll
+                for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
+                store_stream(dst + p, o);
+            }
+        }
     }
 }
 
@@ -255,6 +193,13 @@ __device__ inline void online_add(float& m, float& s, float x) {
     }
 }
 
+// A pair whose max is still -inf holds s = 0, or NaN if it met a NaN score;
+// multiplying by 0 keeps that NaN (the reference's sum is NaN then) without
+// forming exp(-inf - -inf).
+__device__ inline float rescale(float s, float m, float new_m) {
+    return s * ((m == -INFINITY) ? 0.0f : expf(m - new_m));
+}
+
 template <typename T, bool MASK>
 __global__ __launch_bounds__(kThreads) void k_softmax_stream(const T* __restrict__ in,
                                                              T* __restrict__ out, uint32_t rows,
@@ -262,60 +207,52 @@ __global__ __launch_bounds__(kThreads) void k_softmax_stream(const T* __restrict
     __shared__ float lds_m[kThreads / kWave];
     __shared__ float lds_s[kThreads / kWave];
     for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    __syncthreads();  // the previous row's lds reads are done
-    const uint64_t off = uint64_t(row) * width;
-    const uint32_t kept = MASK ? kept_keys(row, width, mp) : width;
-    auto score = [&](uint32_t i) -> float {
-        if constexpr (MASK) return scaled_score(in[off + i], mp.scale);
-        return to_float(in[off + i]);
-    };
-    // Pass 1: plain max first; the sum uses it, so no rescaling is needed
-    // unless a lane's running max moves (online_add handles that case).
-    float m = -INFINITY, s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < kept; i += kThreads) {
-        float x = score(i);
-        // A -inf score adds exp(-inf - m) = 0 once the row max is finite; if
-        // the max stays -inf the row is handled as a whole below.
-        if (x == -INFINITY) continue;
-        online_add(m, s, x);
-    }
-    // Cross-lane merge of (m, s).  A pair whose max is still -inf holds s = 0,
-    // or NaN if it met a NaN score; multiplying by 0 keeps that NaN (the
-    // reference's sum is NaN then) without forming exp(-inf - -inf).
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        float om = __shfl_xor(m, offset, 64);
-        float os = __shfl_xor(s, offset, 64);
-        float nm = fmaxf(m, om);
-        float a = s * ((m == -INFINITY) ? 0.0f : expf(m - nm));
-        float b = os * ((om == -INFINITY) ? 0.0f : expf(om - nm));
-        m = nm;
-        s = a + b;
-    }
-    if (threadIdx.x % kWave == 0) {
-        lds_m[threadIdx.x / kWave] = m;
-        lds_s[threadIdx.x / kWave] = s;
-    }
-    __syncthreads();
-    float gm = -INFINITY;
+        __syncthreads();  // the previous row's lds reads are done
+        const uint64_t off = uint64_t(row) * width;
+        const uint32_t kept = MASK ? kept_keys(row, width, mp) : width;
+        auto score = [&](uint32_t i) -> float {
+            if constexpr (MASK) return scaled_score(in[off + i], mp.scale);
+            return to_float(in[off + i]);
+        };
+        float m = -INFINITY, s = 0.0f;
+        for (uint32_t i = threadIdx.x; i < kept; i += kThreads) {
+            float x = score(i);
+            // A -inf score adds exp(-inf - m) = 0 once the row max is finite;
+            // if the max stays -inf the row is handled as a whole below.
+            if (x == -INFINITY) continue;
+            online_add(m, s, x);
+        }
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            float om = __shfl_xor(m, offset, 64);
+            float os = __shfl_xor(s, offset, 64);
+            float nm = fmaxf(m, om);
+            s = rescale(s, m, nm) + rescale(os, om, nm);
+            m = nm;
+        }
+        if (threadIdx.x % kWave == 0) {
+            lds_m[threadIdx.x / kWave] = m;
+            lds_s[threadIdx.x / kWave] = s;
+        }
+        __syncthreads();
+        float gm = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kThreads / kWave; ++w) gm = fmaxf(gm, lds_m[w]);
-    float gs = 0.0f;
+        for (int w = 0; w < kThreads / kWave; ++w) gm = fmaxf(gm, lds_m[w]);
+        float gs = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kThreads / kWave; ++w)
-        gs += lds_s[w] * ((lds_m[w] == -INFINITY) ? 0.0f : expf(lds_m[w] - gm));
-    if (gm == -INFINITY) {
-        // Every kept score is -inf: f16 writes zeros (softmax.metal:166-173),
-        // f32 yields NaN as exp(-inf - -inf) does in the reference.
-        const T fill = from_float<T>(is_f16<T>() ? 0.0f : __builtin_nanf(""));
-        for (uint32_t i = threadIdx.x; i < width; i += kThreads) out[off + i] = fill;
-        continue;
-    }
-    // NaN scores make gs NaN, and every output NaN, as in the reference.
-    const float inv = 1.0f / gs;
-    for (uint32_t i = threadIdx.x; i < width; i += kThreads) {
-        float e = (i < kept) ? exp_fast(score(i) - gm) : 0.0f;
-        out[off + i] = from_float<T>(e * inv);
-    }
+        for (int w = 0; w < kThreads / kWave; ++w) gs += rescale(lds_s[w], lds_m[w], gm);
+        if (gm == -INFINITY) {
+            // Every kept score is -inf: f16 writes zeros (softmax.metal:166-173),
+            // f32 yields NaN as exp(-inf - -inf) does in the reference.
+            const T fill = from_float<T>(is_f16<T>() ? 0.0f : __builtin_nanf(""));
+            for (uint32_t i = threadIdx.x; i < width; i += kThreads) out[off + i] = fill;
+            continue;
+        }
+        // NaN scores make gs NaN, and every output NaN, as in the reference.
+        const float inv = 1.0f / gs;
+        for (uint32_t i = threadIdx.x; i < width; i += kThreads) {
+            float e = (i < kept) ? exp_fast(score(i) - gm) : 0.0f;
+            out[off + i] = from_float<T>(e * inv);
+        }
     }
 }
 
@@ -326,34 +263,34 @@ __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ i
                                                          T* __restrict__ out, uint32_t rows,
                                                          uint32_t width, MaskParams mp) {
     typedef typename VecOf<T, N>::type V;
-    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const uint32_t w_packs = width / N;
-    const uint64_t row_off = uint64_t(row) * w_packs;
-    const V* src = reinterpret_cast<const V*>(in) + row_off;
-    V* dst = reinterpret_cast<V*>(out) + row_off;
-    const uint32_t kept = kept_keys(row, width, mp);
-    for (uint32_t p = threadIdx.x; p < w_packs; p += kThreads) {
-        V o;
-        if (p * N < kept) {
-            V raw = load_stream(src + p);
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const uint64_t row_off = uint64_t(row) * w_packs;
+        const V* src = reinterpret_cast<const V*>(in) + row_off;
+        V* dst = reinterpret_cast<V*>(out) + row_off;
+        const uint32_t kept = kept_keys(row, width, mp);
+        for (uint32_t p = threadIdx.x; p < w_packs; p += kThreads) {
+            V o;
+            if (p * N < kept) {
+                V raw = load_stream(src + p);
 #pragma unroll
-            for (int j = 0; j < N; ++j)
-                o[j] = (p * N + j < kept) ? from_float<T>(to_float(raw[j]) * mp.scale)
-                                          : from_float<T>(-INFINITY);
-        } else {
+                for (int j = 0; j < N; ++j)
+                    o[j] = (p * N + j < kept) ? from_float<T>(to_float(raw[j]) * mp.scale)
+                                              : from_float<T>(-INFINITY);
+            } else {
 #pragma unroll
-            for (int j = 0; j < N; ++j) o[j] = from_float<T>(-INFINITY);
+                for (int j = 0; j < N; ++j) o[j] = from_float<T>(-INFINITY);
+            }
+            store_stream(dst + p, o);
         }
-        store_stream(dst + p, o);
-    }
     }
 }
 
 // ---------------------------------------------------------------- launch
 
-// Blocks for the one-block-per-row kernels, which loop when rows exceed it.
-inline unsigned row_grid(uint64_t rows) {
-    return unsigned(rows < (uint64_t(1) << 20) ? rows : (uint64_t(1) << 20));
+// Blocks for a grid-stride loop over `items` (rows or row groups).
+inline unsigned row_grid(uint64_t items) {
+    return unsigned(items < (uint64_t(1) << 20) ? items : (uint64_t(1) << 20));
 }
 
 template <typename T, bool MASK>
@@ -364,35 +301,35 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
     const uint32_t r32 = uint32_t(rows), w32 = uint32_t(width);
     const bool packs_ok = width % N == 0 && aligned_to(in, 16) && aligned_to(out, 16);
     const uint64_t w_packs = width / N;
-    if (packs_ok && w_packs <= 16 * kWave) {
-        const dim3 grid(unsigned(ceil_div(rows, kRowsPerBlock))), block(kThreads);
-#define RL_SOFTMAX_WAVE(NV)                                                                    \
-    RL_LAUNCH(ctx, (k_softmax_wave<T, N, NV, MASK>), grid, block, in, out, \
-                       r32, w32, mp)
-        if (w_packs <= 1 * kWave)
-            RL_SOFTMAX_WAVE(1);
-        else if (w_packs <= 2 * kWave)
-            RL_SOFTMAX_WAVE(2);
-        else if (w_packs <= 4 * kWave)
-            RL_SOFTMAX_WAVE(4);
-        else if (w_packs <= 8 * kWave)
-            RL_SOFTMAX_WAVE(8);
-        else
-            RL_SOFTMAX_WAVE(16);
-#undef RL_SOFTMAX_WAVE
-    } else if (packs_ok && w_packs <= 16 * kThreads) {
-        const dim3 grid(row_grid(rows)), block(kThreads);
-#define RL_SOFTMAX_BLOCK(NV)                                                                    \
-    RL_LAUNCH(ctx, (k_softmax_block<T, N, NV, MASK>), grid, block, in, out, \
-                       r32, w32, mp)
-        if (w_packs <= 8 * kThreads)
-            RL_SOFTMAX_BLOCK(8);
-        else
-            RL_SOFTMAX_BLOCK(16);
-#undef RL_SOFTMAX_BLOCK
-    } else {
-        RL_LAUNCH(ctx, (k_softmax_stream<T, MASK>), dim3(row_grid(rows)), dim3(kThreads), in, out, r32, w32, mp);
-    }
+    const dim3 block(kThreads);
+    // Row chunks of at most 2^30 blocks each (one launch for any real shape).
+#define RL_SOFTMAX_ROWS(NV, TPR)                                                                 \
+    do {                                                                                         \
+        for (uint64_t base = 0; base < rows; base += (uint64_t(1) << 30) * (kThreads / TPR)) { \
+            const uint64_t left = ceil_div(rows - base, kThreads / TPR);                         \
+            RL_LAUNCH(ctx, (k_softmax_rows<T, N, NV, TPR, MASK>),                                \
+                      dim3(unsigned(left < (uint64_t(1) << 30) ? left : (uint64_t(1) << 30))),   \
+                      block, in, out, uint32_t(base), r32, w32, mp);                             \
+        }                                                                                        \
+    } while (0)
+    if (packs_ok && w_packs <= 64)
+        RL_SOFTMAX_ROWS(1, 64);
+    else if (packs_ok && w_packs <= 128)
+        RL_SOFTMAX_ROWS(2, 64);
+    else if (packs_ok && w_packs <= 256)
+        RL_SOFTMAX_ROWS(4, 64);
+    else if (packs_ok && w_packs <= 512)
+        RL_SOFTMAX_ROWS(4, 128);
+    else if (packs_ok && w_packs <= 1024)
+        RL_SOFTMAX_ROWS(4, 256);
+    else if (packs_ok && w_packs <= 2048)
+        RL_SOFTMAX_ROWS(8, 256);
+    else if (packs_ok && w_packs <= 4096)
+        RL_SOFTMAX_ROWS(16, 256);
+    else
+        RL_LAUNCH(ctx, (k_softmax_stream<T, MASK>), dim3(row_grid(rows)), block, in, out, r32,
+                  w32, mp);
+#undef RL_SOFTMAX_ROWS
     return after_launch(ctx, name);
 }
 
@@ -403,9 +340,11 @@ rl_status launch_scale_mask(rl_context* ctx, const char* name, const T* in, T* o
     constexpr int N = 16 / sizeof(T);
     const bool packs_ok = width % N == 0 && aligned_to(in, 16) && aligned_to(out, 16);
     if (packs_ok)
-        RL_LAUNCH(ctx, (k_scale_mask<T, N>), dim3(row_grid(rows)), dim3(kThreads), in, out, uint32_t(rows), uint32_t(width), mp);
+        RL_LAUNCH(ctx, (k_scale_mask<T, N>), dim3(row_grid(rows)), dim3(kThreads), in, out,
+                  uint32_t(rows), uint32_t(width), mp);
     else
-        RL_LAUNCH(ctx, (k_scale_mask<T, 1>), dim3(row_grid(rows)), dim3(kThreads), in, out, uint32_t(rows), uint32_t(width), mp);
+        RL_LAUNCH(ctx, (k_scale_mask<T, 1>), dim3(row_grid(rows)), dim3(kThreads), in, out,
+                  uint32_t(rows), uint32_t(width), mp);
     return after_launch(ctx, name);
 }
 
