@@ -309,7 +309,7 @@ def extra_rows(ctx, reps, quick):
     for heads, label in ((qh, "Q"), (kvh, "K")):
         proj = synth.normal(synth.seed_for("c5", label), (1, tok, heads, hd), 0, 1, F16)
         dims, strides = [1, heads, tok, hd], [tok * heads * hd, hd, heads * hd, 1]
-        nbytes = 2 * proj.size * 2
+        nbytes = 2 * proj.size * 2 + 2 * tok * (hd // 2) * 4  # + cos/sin tables, once
         measure(f"c5.2 rope_{label}_f16 (fused gather)", "f16", dims, nbytes,
                 lambda i, proj=proj, dims=dims: (ctx.upload(proj), ctx.empty(dims, F16)),
                 lambda s, dims=dims, strides=strides: ctx.rope_strided(s[0], dims, strides, dc,
@@ -449,7 +449,8 @@ def probe(ctx, host, ops):
     so = ctx.empty((9, 2048, 2048), F32)
     for name, nbytes, fn in [
         ("rmsnorm_f16 [4096,960]", tok * hid * 4 + hid * 2, lambda: ctx.rmsnorm(x, w, 1e-5, y)),
-        ("rope_f16 [1,15,4096,64]", 2 * 15 * tok * 64 * 2, lambda: ctx.rope(q, dc, ds, 0, qo)),
+        ("rope_f16 [1,15,4096,64]", 2 * 15 * tok * 64 * 2 + 2 * tok * 32 * 4,
+         lambda: ctx.rope(q, dc, ds, 0, qo)),
         ("attention_softmax_f32 [9,2048,2048]", 9 * (2048 * 2049 // 2) * 4 + 9 * 2048 * 2048 * 4,
          lambda: ctx.attention_softmax(sc, 0.125, 0, so)),
     ]:
