@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Per-op HBM bandwidth of the gfx950 tensor-op library on one MI355X.
 
-A step is one pass of the elementwise/broadcast batch on [4096, 1536]
-(configs[1]): add, mul, SiLU, fused SwiGLU, stride-0 bias add and cast, in
+A step is one pass of the elementwise/broadcast batch on [4096, 1536]:
+add, mul, SiLU, fused SwiGLU, stride-0 bias add and cast, in
 f32 and f16, plus contiguous of a [1, 9, 4096, 64] transposed view and
 repeat_kv 3 -> 9 heads -- 16 kernel launches.  Inputs are resident in HBM
 before timing.  Each step uses the next of several buffer sets (>= 1 GiB in
@@ -12,8 +12,9 @@ stream events.
 
 GB/s = algorithmic bytes (inputs read once + outputs written once) / time.
 The JSON line's `value` is the whole step's aggregate; `per_op` lists each
-op, and the RMSNorm, softmax and decoder-layer shapes of the other configs
-are timed the same way as extra lines in `per_op`.
+op, and the RMSNorm grid, the attention-score softmax shapes and the
+SmolLM2-360M decoder-layer chain are timed the same way as extra lines in
+`per_op`.
 
     python bench.py [--steps K] [--warmup W] [--sets R] [--no-cpu] [--quick]
 """
@@ -51,8 +52,8 @@ class Op:
                                                                        launch)
 
 
-def config2_inputs(seed_tag: str):
-    """Host arrays of configs[1] (N(0,1) values)."""
+def batch_inputs(seed_tag: str):
+    """Host arrays of the [4096, 1536] elementwise batch (N(0,1) values)."""
     arrs = {}
     for dt in (F32, F16):
         tag = np.dtype(dt).name
@@ -71,7 +72,7 @@ VIEW_DIMS = [1, 9, 4096, 64]
 VIEW_STRIDES = [4096 * 9 * 64, 64, 9 * 64, 1]
 
 
-def config2_ops():
+def batch_ops():
     ops = []
     n = T * H
     for dt in (F32, F16):
@@ -111,7 +112,7 @@ def config2_ops():
     return ops
 
 
-def config2_set(ctx, host):
+def batch_set(ctx, host):
     """Device buffers of one set: the inputs plus one output per op."""
     b = {k: ctx.upload(v) for k, v in host.items()}
     for dt in (F32, F16):
@@ -239,11 +240,12 @@ def per_op_rows(ctx, ops, sets, reps):
     return rows
 
 
-# ----------------------------------------------------- other configs' shapes
+# ------------------------------------------------------- the other shapes
 
 def extra_rows(ctx, reps, quick):
-    """RMSNorm, scale/mask + softmax and the decoder
-    layer chain -- same method, rotated buffer sets."""
+    """RMSNorm over hidden {576, 768, 960} x tokens, scale/mask + softmax on
+    [9, 2048, 2048] scores and the SmolLM2-360M decoder-layer chain -- same
+    method, rotated buffer sets."""
     rows = []
 
     def measure(name, dtype, shape, nbytes, make_set, launch, nsets):
@@ -272,7 +274,7 @@ def extra_rows(ctx, reps, quick):
                         lambda s, w=w: ctx.rmsnorm(s[0], w, 1e-5, s[1]),
                         nsets_for(x.nbytes * 2))
 
-    # prefill [9, 2048, 2048] causal, scale 1/8; decode [9, 1, 2048]
+    # attention scores: prefill [9, 2048, 2048] causal, scale 1/8; decode [9, 1, 2048]
     def logits(shape, dt=F32):
         x = synth.normal(synth.seed_for("logits", *shape), shape, 0, 4.0, F32)
         u = synth.uniform(synth.seed_for("spike", *shape), x.size).reshape(shape)
@@ -297,29 +299,29 @@ def extra_rows(ctx, reps, quick):
             lambda i: (ctx.upload(dec), ctx.empty(dec.shape, F32)),
             lambda s: ctx.attention_softmax(s[0], 0.125, 2047, s[1]), 16)
 
-    # SmolLM2-360M layer, f16, 4096 tokens
+    # SmolLM2-360M decoder layer, f16, 4096 tokens
     hid, qh, kvh, hd, ffn, tok = 960, 15, 5, 64, 2560, 4096
     c, s_ = _rope_table(hd, tok)
     dc, ds = ctx.upload(c), ctx.upload(s_)
     wn = ctx.upload(synth.uniform_range(1, (hid,), 0.5, 1.5, F16))
     x = synth.normal(synth.seed_for("c5", "x"), (tok, hid), 0, 1, F16)
-    measure("c5.1 rmsnorm_f16", "f16", [tok, hid], tok * hid * 4 + hid * 2,
+    measure("layer.1 rmsnorm_f16", "f16", [tok, hid], tok * hid * 4 + hid * 2,
             lambda i: (ctx.upload(x), ctx.empty((tok, hid), F16)),
             lambda s: ctx.rmsnorm(s[0], wn, 1e-5, s[1]), 16)
     for heads, label in ((qh, "Q"), (kvh, "K")):
         proj = synth.normal(synth.seed_for("c5", label), (1, tok, heads, hd), 0, 1, F16)
         dims, strides = [1, heads, tok, hd], [tok * heads * hd, hd, heads * hd, 1]
         nbytes = 2 * proj.size * 2 + 2 * tok * (hd // 2) * 4  # + cos/sin tables, once
-        measure(f"c5.2 rope_{label}_f16 (fused gather)", "f16", dims, nbytes,
+        measure(f"layer.2 rope_{label}_f16 (fused gather)", "f16", dims, nbytes,
                 lambda i, proj=proj, dims=dims: (ctx.upload(proj), ctx.empty(dims, F16)),
                 lambda s, dims=dims, strides=strides: ctx.rope_strided(s[0], dims, strides, dc,
                                                                         ds, 0, s[1]), 16)
         cont = np.ascontiguousarray(proj.transpose(0, 2, 1, 3))
-        measure(f"c5.2 rope_{label}_f16", "f16", list(cont.shape), nbytes,
+        measure(f"layer.2 rope_{label}_f16", "f16", list(cont.shape), nbytes,
                 lambda i, cont=cont: (ctx.upload(cont), ctx.empty(cont.shape, F16)),
                 lambda s: ctx.rope(s[0], dc, ds, 0, s[1]), 16)
     kv = synth.normal(synth.seed_for("c5", "kv"), (1, kvh, tok, hd), 0, 1, F16)
-    measure("c5.3 repeat_kv_f16", "f16", [1, kvh, tok, hd], (kv.size + 3 * kv.size) * 2,
+    measure("layer.3 repeat_kv_f16", "f16", [1, kvh, tok, hd], (kv.size + 3 * kv.size) * 2,
             lambda i: (ctx.upload(kv), ctx.empty((1, qh, tok, hd), F16)),
             lambda s: ctx.repeat_kv(s[0], 3, s[1]), 16)
     if not quick:
@@ -327,20 +329,21 @@ def extra_rows(ctx, reps, quick):
         sc = rng.standard_normal((qh, tok, tok), dtype=np.float32).astype(F16)
         n = sc.size
         unm = qh * (tok * (tok + 1) // 2)
-        measure("c5.4 attention_softmax_f16", "f16", [qh, tok, tok], unm * 2 + n * 2,
+        measure("layer.4 attention_softmax_f16", "f16", [qh, tok, tok], unm * 2 + n * 2,
                 lambda i: (ctx.upload(sc), ctx.empty(sc.shape, F16)),
                 lambda s: ctx.attention_softmax(s[0], 0.125, 0, s[1]), 3)
         del sc
     g = synth.normal(synth.seed_for("c5", "g"), (tok, ffn), 0, 1, F16)
     u = synth.normal(synth.seed_for("c5", "u"), (tok, ffn), 0, 1, F16)
-    measure("c5.5 swiglu_f16", "f16", [tok, ffn], 3 * g.size * 2,
+    measure("layer.5 swiglu_f16", "f16", [tok, ffn], 3 * g.size * 2,
             lambda i: (ctx.upload(g), ctx.upload(u), ctx.empty(g.shape, F16)),
             lambda s: ctx.swiglu(s[0], s[1], s[2]), 8)
     r = synth.normal(synth.seed_for("c5", "r"), (tok, hid), 0, 1, F16)
-    measure("c5.6 residual add_f16", "f16", [tok, hid], 3 * r.size * 2,
+    measure("layer.6 residual add_f16", "f16", [tok, hid], 3 * r.size * 2,
             lambda i: (ctx.upload(x), ctx.upload(r), ctx.empty(r.shape, F16)),
             lambda s: ctx.add(s[0], s[1], s[2]), 16)
-    # configs[0] shape, fused add + RMSNorm (writes the sum and the norm)
+    # [64, 768] f32 (the reference's CPU-runnable case), fused add + RMSNorm
+    # (writes the sum and the norm)
     x0 = synth.normal(1, (64, 768), 0, 1, F32)
     w0 = ctx.upload(synth.uniform_range(2, (768,), 0.5, 1.5, F32))
     measure("add_rmsnorm_f32", "f32", [64, 768], 64 * 768 * 4 * 4 + 768 * 4,
@@ -364,7 +367,7 @@ def _rope_table(head_dim, max_seq, theta=10000.0):
 
 def cpu_baseline(host, budget_s: float):
     """The oracle (scalar C restatement of the reference ops, 1 thread) on
-    whole configs[1] steps until `budget_s` seconds of CPU work have run."""
+    whole batch steps until `budget_s` seconds of CPU work have run."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as o
 
@@ -429,7 +432,7 @@ def check_outputs(ctx, dev, outs) -> list[str]:
 def probe(ctx, host, ops):
     """Hardware-counter probe: each op 3 times, then a plain copy of known
     size whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters."""
-    s = config2_set(ctx, host)
+    s = batch_set(ctx, host)
     for op in ops:
         for _ in range(3):
             ctx.begin()
@@ -472,6 +475,23 @@ def probe(ctx, host, ops):
         f"written per launch")
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_batch.json")
+
+
+def measured_traffic(op_name):
+    """HBM bytes per launch of `op_name` as the hardware counters read it:
+    FETCH_SIZE and WRITE_SIZE per dispatch from two `rocprofv3 --pmc` runs of
+    `bench.py --probe`, each scaled by its reading on a copy of known size.
+    The summary is committed text; None if it has no entry for the op."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = data.get("ops", {}).get(op_name)
+    return None if entry is None else entry["hbm_bytes"]
+
+
 # ------------------------------------------------------------------ main
 
 def main():
@@ -488,7 +508,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
     ap.add_argument("--quick", action="store_true", help="fewer extra shapes")
     ap.add_argument("--probe", action="store_true",
-                    help="no timing: run each configs[1] op 3 times on one buffer set, then a "
+                    help="no timing: run each batch op 3 times on one buffer set, then a "
                          "256 MiB device-to-device copy 3 times (for hardware-counter runs)")
     args = ap.parse_args()
 
@@ -499,13 +519,13 @@ def main():
         sys.exit(2)
 
     ctx = abi.Context(0)
-    host = config2_inputs("bench")
-    ops = config2_ops()
+    host = batch_inputs("bench")
+    ops = batch_ops()
     if args.probe:
         probe(ctx, host, ops)
         return
     log(f"uploading {args.sets} buffer sets")
-    sets = [config2_set(ctx, host) for _ in range(args.sets)]
+    sets = [batch_set(ctx, host) for _ in range(args.sets)]
     footprint = sum(set_bytes(s) for s in sets)
     step_bytes = sum(op.nbytes for op in ops)
     log(f"footprint {footprint / 2**30:.2f} GiB, {step_bytes / 1e6:.1f} MB per step")
@@ -523,14 +543,16 @@ def main():
     for a in aux:
         a.close()
 
-    log("per op (configs[1]):")
+    log("per op ([4096, 1536] batch):")
     rows = per_op_rows(ctx, ops, sets, args.op_reps)
-    dominant = max(rows, key=lambda r: r["us"])
+    # The step's dominant kernel: the largest launch (add, mul and SwiGLU f32 tie
+    # on bytes and, within noise, on time; the first in step order is taken).
+    dominant = max(rows, key=lambda r: r["bytes"])
     roofline = {"bound": "hbm", "kernel": dominant["op"], "achieved": dominant["GB/s"],
                 "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(dominant["GB/s"] / PEAK_GBS, 4),
                 "bytes_per_launch": dominant["bytes"], "us_per_launch": dominant["us"],
-                "traffic": None}
+                "traffic": measured_traffic(dominant["op"])}
 
     cpu = None
     if not args.no_cpu:
@@ -539,7 +561,7 @@ def main():
         bad = check_outputs(ctx, sets[0], outs)
         cpu_gbs = step_bytes * steps / elapsed / 1e9
         cpu = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{steps} whole configs[1] steps (16 ops on [4096,1536] and the "
+               "sample": f"{steps} whole batch steps (16 ops on [4096,1536] and the "
                          f"view/KV shapes) in {elapsed:.1f} s",
                "gpu_outputs_match_oracle": not bad}
         if bad:
@@ -562,7 +584,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "configs[1]: elementwise+broadcast batch [4096,1536], f32 and "
+        "config": {"workload": "elementwise+broadcast batch [4096,1536], f32 and "
                                "f16 storage (add, mul, silu, swiglu, bias add, casts, "
                                "contiguous [1,9,4096,64] view, repeat_kv 3->9)",
                    "ops_per_step": len(ops), "bytes_per_step": step_bytes,

@@ -254,7 +254,7 @@ def test_rmsnorm_reference_kats(ctx):
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("rows,hidden", [(64, 768), (4096, 960), (3, 5), (2, 9000)])
 def test_add_rmsnorm(ctx, dtype, rows, hidden):
-    # out = RMSNorm(x + r) * w on f32 [64, 768]
+    # the reference's CPU-runnable case: out = RMSNorm(x + r) * w on f32 [64, 768]
     x = norm(("arms", "x"), (rows, hidden), dtype)
     r = norm(("arms", "r"), (rows, hidden), dtype)
     w = synth.uniform_range(synth.seed_for("arms", "w", hidden), (hidden,), 0.5, 1.5, dtype)
@@ -267,7 +267,7 @@ def test_add_rmsnorm(ctx, dtype, rows, hidden):
 # ---------------------------------------------------------------- softmax
 
 def _logits(key, shape, dtype=np.float32):
-    """N(0, 4) logits with 1% of entries set to +20."""
+    """N(0, 4) logits with 1% of entries set to +20 (spiky attention scores)."""
     x = synth.normal(synth.seed_for(*key, *shape), shape, 0.0, 4.0, np.float32)
     u = synth.uniform(synth.seed_for("spike", *key, *shape), x.size).reshape(shape)
     x[u < 0.01] = 20.0
@@ -350,14 +350,15 @@ def test_scale_mask_reference_kats(ctx):
 
 
 def test_fused_softmax_smollm_layer_f16(ctx):
-    """configs[4] step 4: [15, 4096, 4096] f16 causal, scale 1/8."""
+    """SmolLM2-360M layer at 4096 tokens: [15, 4096, 4096] f16 causal scores,
+    scale 1/8."""
     rng = np.random.default_rng(synth.seed_for("c5", "scores"))
     x = rng.standard_normal((15, 4096, 4096), dtype=np.float32).astype(np.float16)
     d = ctx.upload(x)
     got = run(ctx, lambda: ctx.attention_softmax(d, 0.125, 0)).numpy()
     del d
     ref = o.attention_softmax(x, 0.125, 0)
-    check_float(got, ref, "C5 fused softmax")
+    check_float(got, ref, "SmolLM2 layer fused softmax")
     del ref
     # size-independent invariants: each row sums to 1 and nothing past the diagonal
     sums = np.add.reduce(got, axis=-1, dtype=np.float32)
