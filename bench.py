@@ -202,32 +202,110 @@ def time_step(ctx, aux, ops, sets, steps, warmup):
     return ms / steps
 
 
+def split_by_bytes(ops, n):
+    """Greedy split of the ops over n streams, largest first, balancing bytes;
+    each stream keeps the step's op order."""
+    load = [0] * n
+    owner = {}
+    for i in sorted(range(len(ops)), key=lambda i: -ops[i].nbytes):
+        k = load.index(min(load))
+        owner[i] = k
+        load[k] += ops[i].nbytes
+    return [[op for i, op in enumerate(ops) if owner[i] == k] for k in range(n)]
+
+
+def time_step_streams(ctx, aux, ops, sets, steps, warmup):
+    """ms per step with the step's independent ops spread over several
+    streams: each stream replays its own recorded graph (its share of the
+    ops), forked from and joined back into ctx's stream with events every
+    step.  Kernels on different streams may run concurrently, so one
+    kernel's ramp-down overlaps another's ramp-up."""
+    streams = [ctx] + aux
+    shares = split_by_bytes(ops, len(streams))
+    graphs = []
+    for s in sets:
+        row = []
+        for c, share in zip(streams, shares):
+            c.capture_begin()
+            try:
+                for op in share:
+                    op.launch(c, s)
+            finally:
+                row.append(c.capture_end())
+        graphs.append(row)
+    fork = [ctx.event() for _ in range(2)]
+    joins = [[a.event() for a in aux] for _ in range(2)]
+
+    def one_step(i):
+        f, js = fork[i % 2], joins[i % 2]
+        ctx.record(f)
+        for a in aux:
+            a.wait(f)
+        row = graphs[i % len(graphs)]
+        for c, g in zip(streams, row):
+            c.graph_launch(g)
+        for a, e in zip(aux, js):
+            a.record(e)
+            ctx.wait(e)
+
+    for i in range(warmup):
+        one_step(i)
+    ctx.finish()
+    for a in aux:
+        a.finish()
+    start, end = ctx.event(), ctx.event()
+    ctx.record(start)
+    for i in range(steps):
+        one_step(i)
+    ctx.record(end)
+    ms = ctx.elapsed_ms(start, end)
+    ctx.finish()
+    for a in aux:
+        a.finish()
+    for row in graphs:
+        for c, g in zip(streams, row):
+            c.graph_destroy(g)
+    for e in fork + [e for js in joins for e in js]:
+        ctx.destroy_event(e)
+    ctx.destroy_event(start)
+    ctx.destroy_event(end)
+    return ms / steps
+
+
 def kernel_times_us(ctx, launches, reps):
     """Device time of `reps` launches (cycling through `launches`, one kernel
     each), every one bracketed by events that the kernel itself stamps at its
-    start and end -- the same per-dispatch duration a kernel trace reports."""
+    start and end -- the same per-dispatch duration a kernel trace reports.
+    Also returns the whole batch's time per launch (events recorded on the
+    stream before the first and after the last launch; includes the gaps
+    between back-to-back kernels)."""
     for fn in launches:
         fn()
     ctx.finish()
     evs = [(ctx.event(), ctx.event()) for _ in range(reps)]
+    b0, b1 = ctx.event(), ctx.event()
+    ctx.record(b0)
     for i, (start, stop) in enumerate(evs):
         ctx.time_next_kernel(start, stop)
         launches[i % len(launches)]()
+    ctx.record(b1)
     ctx.finish()
     us = [ctx.elapsed_ms(start, stop) * 1e3 for start, stop in evs]
-    for start, stop in evs:
-        ctx.destroy_event(start)
-        ctx.destroy_event(stop)
-    return us
+    batch_us = ctx.elapsed_ms(b0, b1) * 1e3 / reps
+    for e in [b0, b1] + [e for pair in evs for e in pair]:
+        ctx.destroy_event(e)
+    return us, batch_us
 
 
-def op_row(name, dtype, shape, nbytes, us_list):
+def op_row(name, dtype, shape, nbytes, timing):
+    us_list, batch_us = timing
     us = float(np.mean(us_list))
     gbs = nbytes / (us * 1e-6) / 1e9
-    log(f"  {name:34s} {str(shape):20s} {us:9.2f} us {gbs:8.1f} GB/s ({100 * gbs / PEAK_GBS:5.1f}%)")
+    log(f"  {name:34s} {str(shape):20s} {us:9.2f} us {gbs:8.1f} GB/s ({100 * gbs / PEAK_GBS:5.1f}%)"
+        f"  batch {batch_us:7.2f} us/launch")
     return {"op": name, "dtype": dtype, "shape": shape, "bytes": nbytes, "us": round(us, 3),
-            "us_min": round(float(np.min(us_list)), 3), "GB/s": round(gbs, 1),
-            "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
+            "us_min": round(float(np.min(us_list)), 3), "us_batch": round(batch_us, 3),
+            "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
 
 
 def per_op_rows(ctx, ops, sets, reps):
@@ -502,6 +580,9 @@ def main():
     ap.add_argument("--sets", type=int, default=4, help="buffer sets rotated across steps")
     ap.add_argument("--streams", type=int, default=1,
                     help="streams the step's independent ops are spread over")
+    ap.add_argument("--forked-graph", action="store_true",
+                    help="with --streams > 1: one recorded graph with parallel branches "
+                         "instead of one graph per stream")
     ap.add_argument("--op-reps", type=int, default=100, help="timed launches per op line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -531,7 +612,12 @@ def main():
     log(f"footprint {footprint / 2**30:.2f} GiB, {step_bytes / 1e6:.1f} MB per step")
 
     aux = [abi.Context(0) for _ in range(max(0, args.streams - 1))]
-    ms_step = time_step(ctx, aux, ops, sets, args.steps, args.warmup)
+    if aux and args.forked_graph:
+        ms_step = time_step(ctx, aux, ops, sets, args.steps, args.warmup)
+    elif aux:
+        ms_step = time_step_streams(ctx, aux, ops, sets, args.steps, args.warmup)
+    else:
+        ms_step = time_step(ctx, [], ops, sets, args.steps, args.warmup)
     value = step_bytes / (ms_step * 1e-3) / 1e9
     log(f"step on {args.streams} streams: {ms_step * 1e3:.1f} us, {value:.1f} GB/s "
         f"({100 * value / PEAK_GBS:.1f}% of peak)")

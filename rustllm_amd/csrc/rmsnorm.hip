@@ -2,13 +2,18 @@
 //
 // y = x * rsqrt(sum(x^2) / h + eps) * w per row of h elements
 // (kernels/rmsnorm.metal:7-126).  The reference gives each row a 256-thread
-// group with an 8-barrier shared-memory tree and reads x twice.  Here one
-// wave64 owns one row: it loads the row once into VGPRs as 16-byte packs
-// (h <= 64 * 16 packs), reduces the sum of squares with a butterfly of
-// cross-lane shuffles (no LDS, no barrier), and writes y from registers, so
-// x is read from HBM exactly once.  Four rows share a 256-thread block.
-// Rows longer than the register budget fall back to a block per row with
-// an LDS step across its four waves and a second (L2-resident) read.
+// group with an 8-barrier shared-memory tree and reads x twice.  Here a
+// group of TPR lanes (16, 32 or 64: a quarter, half or whole wave64) owns
+// one row: it loads the row once into VGPRs as 16-byte packs, NV packs per
+// lane, loads the weight packs alongside (they stay L2-resident), reduces
+// the sum of squares with a butterfly of cross-lane shuffles inside the
+// group (no LDS, no barrier) and writes y from registers, so x is read from
+// HBM exactly once.  TPR is picked per row length so that every lane holds
+// 3-12 packs with few idle lanes: 2-5 packs per lane left the loads too
+// short to cover HBM latency (f16 rows of 576-960 reached 50-63% of peak
+// with a wave per row, 63-73% with 16-32 lanes per row).  Rows longer than
+// 64 x 16 packs fall back to a block per row with an LDS step across its
+// four waves and a second (L2-resident) read.
 //
 // The fused variant first forms s = x + r rounded to the dtype (the add
 // kernel's result), writes s and normalises it: the two adjacent calls of
@@ -20,24 +25,40 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
-constexpr int kRowsPerBlock = kThreads / kWave;
+// Rows per launch chunk: keeps blocks x threads far below 2^32.
+constexpr uint32_t kRowChunk = 1u << 22;
 
-template <typename T, int N, int NV, bool ADD>
-__global__ __launch_bounds__(kThreads) void k_rmsnorm_wave(
+// Sum over the TPR lanes of an aligned lane group (TPR <= 64 divides the
+// wave; xor offsets below TPR stay inside the group).
+template <int TPR>
+__device__ inline float lane_group_sum(float v) {
+#pragma unroll
+    for (int offset = TPR / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+    return v;
+}
+
+// Rows [row_base, row_base + rows) of the launch chunk; TPR lanes per row,
+// kThreads / TPR rows per block.  Lanes of a group stride over the row's
+// packs (pack p = lane + k * TPR), so each load instruction covers TPR
+// consecutive packs of every row in the wave.
+template <typename T, int N, int NV, int TPR, bool ADD>
+__global__ __launch_bounds__(kThreads) void k_rmsnorm_rows(
     const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ weight,
-    T* __restrict__ sum_out, T* __restrict__ y, uint32_t rows, uint32_t h_packs, float hidden,
-    float eps) {
+    T* __restrict__ sum_out, T* __restrict__ y, uint32_t row_base, uint32_t rows,
+    uint32_t h_packs, float hidden, float eps) {
     typedef typename VecOf<T, N>::type V;
-    const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t row = blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
-    if (row >= rows) return;  // whole wave leaves together; no block barrier below
+    constexpr int kRowsPerBlock = kThreads / TPR;
+    const uint32_t lane = threadIdx.x % TPR;
+    const uint32_t row = row_base + blockIdx.x * kRowsPerBlock + threadIdx.x / TPR;
+    if (row >= rows) return;  // the whole lane group leaves; no block barrier below
     const uint64_t row_off = uint64_t(row) * h_packs;
     const V* xr = reinterpret_cast<const V*>(x) + row_off;
+    const V* wr = reinterpret_cast<const V*>(weight);
     V v[NV];
-    float ss = 0.0f;
+    V w[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const uint32_t p = lane + k * kWave;
+        const uint32_t p = lane + k * TPR;
         if (p < h_packs) v[k] = load_stream(xr + p);
     }
     if constexpr (ADD) {
@@ -45,7 +66,7 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_wave(
         V* sr = reinterpret_cast<V*>(sum_out) + row_off;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const uint32_t p = lane + k * kWave;
+            const uint32_t p = lane + k * TPR;
             if (p < h_packs) {
                 V r = load_stream(rr + p);
                 V s;
@@ -56,9 +77,17 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_wave(
             }
         }
     }
+    // The weight (h elements shared by every row) comes from L2; issuing its
+    // loads before the reduction hides their latency behind the shuffles.
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const uint32_t p = lane + k * kWave;
+        const uint32_t p = lane + k * TPR;
+        if (p < h_packs) w[k] = wr[p];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = lane + k * TPR;
         if (p < h_packs) {
 #pragma unroll
             for (int j = 0; j < N; ++j) {
@@ -67,19 +96,17 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_wave(
             }
         }
     }
-    ss = wave_sum(ss);
+    ss = lane_group_sum<TPR>(ss);
     const float inverse_rms = rsqrtf(ss / hidden + eps);  // rmsnorm.metal:55-60
-    const V* wr = reinterpret_cast<const V*>(weight);
     V* yr = reinterpret_cast<V*>(y) + row_off;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const uint32_t p = lane + k * kWave;
+        const uint32_t p = lane + k * TPR;
         if (p < h_packs) {
-            V w = wr[p];  // h elements, shared by every row: L2-resident
             V o;
 #pragma unroll
             for (int j = 0; j < N; ++j)
-                o[j] = from_float<T>(to_float(v[k][j]) * inverse_rms * to_float(w[j]));
+                o[j] = from_float<T>(to_float(v[k][j]) * inverse_rms * to_float(w[k][j]));
             store_stream(yr + p, o);
         }
     }
@@ -90,9 +117,9 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_wave(
 template <typename T, bool ADD>
 __global__ __launch_bounds__(kThreads) void k_rmsnorm_block(
     const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ weight,
-    T* __restrict__ sum_out, T* __restrict__ y, uint32_t rows, uint32_t h, float eps) {
+    T* __restrict__ sum_out, T* __restrict__ y, uint32_t row_base, uint32_t h, float eps) {
     __shared__ float partial[kThreads / kWave];
-    const uint32_t row = blockIdx.x;
+    const uint32_t row = row_base + blockIdx.x;
     const uint64_t off = uint64_t(row) * h;
     const T* src = ADD ? sum_out : x;
     float ss = 0.0f;
@@ -119,6 +146,79 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_block(
         y[off + i] = from_float<T>(to_float(src[off + i]) * inverse_rms * to_float(weight[i]));
 }
 
+// Packs per lane instantiated for each lane-group width.
+constexpr int kNv64[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
+constexpr int kNv32[] = {3, 4, 5, 8, 10, 12};
+constexpr int kNv16[] = {3, 4, 5, 8, 9, 12};
+
+template <size_t K>
+int smallest_at_least(const int (&set)[K], uint64_t need) {
+    for (int v : set)
+        if (uint64_t(v) >= need) return v;
+    return 0;
+}
+
+struct RowPlan {
+    int tpr;  // lanes per row
+    int nv;   // packs per lane (instantiated, >= ceil(h_packs / tpr))
+};
+
+// Lane-group width for `rows` rows of h_packs packs (1 <= h_packs <= 1024):
+// prefer 3..12 packs per lane, then the fewest idle lanes, then the wider
+// group; then widen the group while the launch would have fewer than 4096
+// waves (4 per SIMD), where more, shorter waves hide latency better
+// ([4096, 960] f16: 4.4 us with 64 lanes per row, 4.9 us with 32).
+RowPlan plan_by_length(uint64_t h_packs);
+
+RowPlan plan_rows(uint64_t h_packs, uint64_t rows) {
+    RowPlan plan = plan_by_length(h_packs);
+    while (plan.tpr < 64 && rows * uint64_t(plan.tpr) < 4096ull * kWave) {
+        const int tpr = plan.tpr * 2;
+        const uint64_t need = ceil_div(h_packs, uint64_t(tpr));
+        const int nv = tpr == 64 ? smallest_at_least(kNv64, need) : smallest_at_least(kNv32, need);
+        if (nv == 0) break;
+        plan = {tpr, nv};
+    }
+    return plan;
+}
+
+RowPlan plan_by_length(uint64_t h_packs) {
+    RowPlan best{0, 0};
+    bool best_ok = false;
+    uint64_t best_num = 0, best_den = 1;  // lane use = num / den
+    for (int tpr : {64, 32, 16}) {
+        const uint64_t need = ceil_div(h_packs, uint64_t(tpr));
+        const int nv = tpr == 64   ? smallest_at_least(kNv64, need)
+                       : tpr == 32 ? smallest_at_least(kNv32, need)
+                                   : smallest_at_least(kNv16, need);
+        if (nv == 0) continue;
+        const bool ok = need >= 3 && need <= 12;
+        const uint64_t num = h_packs, den = uint64_t(tpr) * need;
+        const bool better_use = num * best_den > best_num * den;
+        if (best.tpr == 0 || (ok && !best_ok) || (ok == best_ok && better_use)) {
+            best = {tpr, nv};
+            best_ok = ok;
+            best_num = num;
+            best_den = den;
+        }
+    }
+    return best;
+}
+
+template <typename T, int N, int NV, int TPR, bool ADD>
+void launch_rows(rl_context* ctx, const T* x, const T* residual, const T* weight, T* sum_out,
+                 T* y, uint32_t rows, uint32_t h_packs, float hidden, float eps) {
+    constexpr uint32_t kRowsPerBlock = kThreads / TPR;
+    static_assert(kRowChunk % kRowsPerBlock == 0, "chunks must hold whole blocks");
+    for (uint32_t base = 0; base < rows; base += kRowChunk) {
+        const uint32_t n = rows - base < kRowChunk ? rows - base : kRowChunk;
+        const dim3 grid(unsigned(ceil_div(n, kRowsPerBlock))), block(kThreads);
+        RL_LAUNCH(ctx, (k_rmsnorm_rows<T, N, NV, TPR, ADD>), grid, block, x, residual, weight,
+                  sum_out, y, base, rows, h_packs, hidden, eps);
+        if (rows - base <= kRowChunk) break;
+    }
+}
+
 template <typename T, bool ADD>
 rl_status launch_rmsnorm(rl_context* ctx, const char* name, const T* x, const T* residual,
                          const T* weight, T* sum_out, T* y, uint64_t rows, uint64_t hidden,
@@ -131,21 +231,31 @@ rl_status launch_rmsnorm(rl_context* ctx, const char* name, const T* x, const T*
     const uint64_t h_packs = hidden / N;
     const uint32_t r32 = uint32_t(rows);
     if (packs_ok && h_packs <= 16 * kWave) {
-        const dim3 grid(unsigned(ceil_div(rows, kRowsPerBlock))), block(kThreads);
+        const RowPlan plan = plan_rows(h_packs, rows);
         const uint32_t hp = uint32_t(h_packs);
         const float hf = float(hidden);
-        if (h_packs <= 1 * kWave)
-            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 1, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
-        else if (h_packs <= 2 * kWave)
-            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 2, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
-        else if (h_packs <= 4 * kWave)
-            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 4, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
-        else if (h_packs <= 8 * kWave)
-            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 8, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
-        else
-            RL_LAUNCH(ctx, (k_rmsnorm_wave<T, N, 16, ADD>), grid, block, x, residual, weight, sum_out, y, r32, hp, hf, eps);
-    } else {
-        RL_LAUNCH(ctx, (k_rmsnorm_block<T, ADD>), dim3(r32), dim3(kThreads), x, residual, weight, sum_out, y, r32, uint32_t(hidden), eps);
+#define RL_RMS_PLAN(TPR_, NV_)                                                                \
+    if (plan.tpr == TPR_ && plan.nv == NV_) {                                                 \
+        launch_rows<T, N, NV_, TPR_, ADD>(ctx, x, residual, weight, sum_out, y, r32, hp, hf,  \
+                                          eps);                                               \
+        return after_launch(ctx, name);                                                       \
+    }
+        RL_RMS_PLAN(64, 1) RL_RMS_PLAN(64, 2)
+        RL_RMS_PLAN(64, 3) RL_RMS_PLAN(64, 4) RL_RMS_PLAN(64, 5) RL_RMS_PLAN(64, 6)
+        RL_RMS_PLAN(64, 8) RL_RMS_PLAN(64, 10) RL_RMS_PLAN(64, 12) RL_RMS_PLAN(64, 16)
+        RL_RMS_PLAN(32, 3) RL_RMS_PLAN(32, 4) RL_RMS_PLAN(32, 5) RL_RMS_PLAN(32, 8)
+        RL_RMS_PLAN(32, 10) RL_RMS_PLAN(32, 12)
+        RL_RMS_PLAN(16, 3) RL_RMS_PLAN(16, 4) RL_RMS_PLAN(16, 5) RL_RMS_PLAN(16, 8)
+        RL_RMS_PLAN(16, 9) RL_RMS_PLAN(16, 12)
+#undef RL_RMS_PLAN
+        return fail(RL_ERR_DEVICE, "RMSNorm: no kernel for %d lanes x %d packs per row",
+                    plan.tpr, plan.nv);
+    }
+    for (uint32_t base = 0; base < r32; base += kRowChunk) {
+        const uint32_t n = r32 - base < kRowChunk ? r32 - base : kRowChunk;
+        RL_LAUNCH(ctx, (k_rmsnorm_block<T, ADD>), dim3(n), dim3(kThreads), x, residual, weight,
+                  sum_out, y, base, uint32_t(hidden), eps);
+        if (r32 - base <= kRowChunk) break;
     }
     return after_launch(ctx, name);
 }

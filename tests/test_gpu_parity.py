@@ -90,6 +90,26 @@ def test_silu_extremes(ctx):
     assert f16_ulp_distance(got, o.silu(xh)) <= F16_ULP
 
 
+def test_silu_swiglu_f16_every_half(ctx):
+    """SiLU over all 65,536 halves (incl. +-inf, NaN, subnormals and the range
+    where the sigmoid's reciprocal is subnormal), and SwiGLU with every half as
+    the gate against a few up values."""
+    xh = np.arange(65536, dtype=np.uint16).view(np.float16)
+    ref = o.silu(xh)
+    got = run(ctx, lambda: ctx.silu(ctx.upload(xh))).numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert f16_ulp_distance(got[~nan], ref[~nan]) <= F16_ULP
+    dg = ctx.upload(xh)
+    for u in (1.0, -3.5, 65504.0, 1e-3):
+        uh = np.full(xh.shape, u, dtype=np.float16)
+        ref = o.swiglu(xh, uh)
+        got = run(ctx, lambda: ctx.swiglu(dg, ctx.upload(uh))).numpy()
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(got), nan), u
+        assert f16_ulp_distance(got[~nan], ref[~nan]) <= F16_ULP, u
+
+
 @pytest.mark.parametrize("n", SIZES)
 def test_cast_bitexact(ctx, n):
     x = norm(("cast",), (n,), np.float32, 0.0, 2000.0)
@@ -235,6 +255,31 @@ def test_rmsnorm_odd_and_large_rows(ctx, dtype, rows, hidden):
     w = synth.uniform_range(synth.seed_for("rms2", "w", hidden), (hidden,), 0.5, 1.5, dtype)
     got = run(ctx, lambda: ctx.rmsnorm(ctx.upload(x), ctx.upload(w), 1e-5)).numpy()
     check_float(got, o.rmsnorm(x, w, 1e-5), f"rmsnorm {rows}x{hidden}")
+
+
+# Row lengths in 16-byte packs that select each lane-group width x packs-per-
+# lane kernel of the row planner (16/32/64 lanes per row, 1..16 packs each).
+# Narrow groups are only chosen for launches of >= 4096 waves, hence the
+# second row count; neither count is a multiple of a rows-per-block count.
+RMS_PACKS = [2, 20, 48, 50, 70, 100, 120, 130, 150, 170, 180, 200, 240, 270, 300, 330, 360,
+             400, 600, 700, 1000, 1024]
+RMS_PLAN_CASES = [(p, 37) for p in RMS_PACKS] + [(p, 16411) for p in RMS_PACKS if p <= 352]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("packs,rows", RMS_PLAN_CASES)
+def test_rmsnorm_row_plans(ctx, dtype, packs, rows):
+    hidden = packs * (16 // np.dtype(dtype).itemsize)
+    x = norm(("rmsplan", "x"), (rows, hidden), dtype, 0.0, 2.0)
+    r = norm(("rmsplan", "r"), (rows, hidden), dtype)
+    w = synth.uniform_range(synth.seed_for("rmsplan", "w", hidden), (hidden,), 0.5, 1.5, dtype)
+    dx, dr, dw = ctx.upload(x), ctx.upload(r), ctx.upload(w)
+    got = run(ctx, lambda: ctx.rmsnorm(dx, dw, 1e-5)).numpy()
+    check_float(got, o.rmsnorm(x, w, 1e-5), f"rmsnorm {rows}x{hidden}")
+    s, y = run(ctx, lambda: ctx.add_rmsnorm(dx, dr, dw, 1e-5))
+    rs, ry = o.add_rmsnorm(x, r, w, 1e-5)
+    assert_bitexact(s.numpy(), rs, "residual sum")
+    check_float(y.numpy(), ry, f"add_rmsnorm {rows}x{hidden}")
 
 
 def test_rmsnorm_reference_kats(ctx):
