@@ -398,6 +398,23 @@ def extra_rows(ctx, reps, quick):
         measure(f"layer.2 rope_{label}_f16", "f16", list(cont.shape), nbytes,
                 lambda i, cont=cont: (ctx.upload(cont), ctx.empty(cont.shape, F16)),
                 lambda s: ctx.rope(s[0], dc, ds, 0, s[1]), 16)
+    # K rotated straight into a [1, 5, 4096, 64] cache, V gathered into one
+    proj_k = synth.normal(synth.seed_for("c5", "Kc"), (1, tok, kvh, hd), 0, 1, F16)
+    kdims, kstrides = [1, kvh, tok, hd], [tok * kvh * hd, hd, kvh * hd, 1]
+    measure("layer.2 rope_K_f16 -> KV cache (fused)", "f16", kdims,
+            2 * proj_k.size * 2 + 2 * tok * (hd // 2) * 4,
+            lambda i: (ctx.upload(proj_k), ctx.empty(kdims, F16)),
+            lambda s: ctx.rope_kv_cache_write(s[0], kdims, kstrides, dc, ds, 0, s[1]), 16)
+    measure("layer.2 V_f16 -> KV cache (fused gather)", "f16", kdims, 2 * proj_k.size * 2,
+            lambda i: (ctx.upload(proj_k), ctx.empty(kdims, F16)),
+            lambda s: ctx.kv_cache_write_strided(s[0], kdims, kstrides, s[1], 0), 16)
+    # token embedding gather: 4096 ids into a [49152, 960] f16 table
+    vocab = 49152
+    emb = ctx.upload(synth.normal(synth.seed_for("c5", "emb"), (vocab, hid), 0, 1, F16))
+    ids = (synth.uniform(synth.seed_for("c5", "ids"), tok) * vocab).astype(np.uint32)
+    measure("layer.0 embedding_f16", "f16", [tok, hid], 2 * tok * hid * 2 + tok * 4,
+            lambda i: (ctx.empty((tok, hid), F16),),
+            lambda s: ctx.embedding(emb, ids, s[0]), 16)
     kv = synth.normal(synth.seed_for("c5", "kv"), (1, kvh, tok, hd), 0, 1, F16)
     measure("layer.3 repeat_kv_f16", "f16", [1, kvh, tok, hd], (kv.size + 3 * kv.size) * 2,
             lambda i: (ctx.upload(kv), ctx.empty((1, qh, tok, hd), F16)),

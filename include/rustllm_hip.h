@@ -55,6 +55,7 @@ typedef int32_t rl_status;
 #define RL_ERR_POSITION_OUT_OF_RANGE 7 /* TinyError::PositionOutOfRange   src/error.rs:20-24 */
 #define RL_ERR_MODEL_FORMAT 8          /* TinyError::ModelFormat          src/error.rs:32  */
 #define RL_ERR_DEVICE 9                /* TinyError::Metal                src/error.rs:38  */
+#define RL_ERR_INVALID_TOKEN_ID 10     /* TinyError::InvalidTokenId       src/error.rs:13-16 */
 
 /* --------------------------------------------------------------- handles */
 typedef struct rl_context rl_context; /* MetalContext   src/metal/context.rs:10-18 */
@@ -288,6 +289,63 @@ rl_status rl_rope_strided_f16(rl_context* ctx, const rl_buffer* src, const uint6
                               const uint64_t* strides, uint32_t rank, const rl_buffer* cos_table,
                               const rl_buffer* sin_table, uint64_t table_rows,
                               uint64_t start_pos, const rl_buffer* out);
+
+/* ======================================================== KV cache writes */
+/* ops::kv_cache_write_f32_encode (src/ops/kv_cache_write.rs:24-41,71-141):
+ * a contiguous [1, kv_heads, seq_len, head_dim] source into rows
+ * start .. start + seq_len of each head of the [1, kv_heads, max_seq, head_dim]
+ * cache (written in place).  start + seq_len > max_seq is
+ * RL_ERR_POSITION_OUT_OF_RANGE. */
+rl_status rl_kv_cache_write_f32(rl_context* ctx, const rl_buffer* cache, uint64_t kv_heads,
+                                uint64_t max_seq, uint64_t head_dim, const rl_buffer* source,
+                                uint64_t seq_len, uint64_t start);
+/* ops::kv_cache_write_f16_encode (src/ops/kv_cache_write.rs:54-69). */
+rl_status rl_kv_cache_write_f16(rl_context* ctx, const rl_buffer* cache, uint64_t kv_heads,
+                                uint64_t max_seq, uint64_t head_dim, const rl_buffer* source,
+                                uint64_t seq_len, uint64_t start);
+/* LayerKvCache::append_encode's contiguous_encode + kv_cache_write of one
+ * tensor (src/model/kv_cache.rs:123-137) in one pass: `src` is a rank-4
+ * [1, kv_heads, seq_len, head_dim] view (dims/strides, any strides) written
+ * into the cache as above. */
+rl_status rl_kv_cache_write_strided_f32(rl_context* ctx, const rl_buffer* src,
+                                        const uint64_t* dims, const uint64_t* strides,
+                                        uint32_t rank, const rl_buffer* cache, uint64_t max_seq,
+                                        uint64_t start);
+rl_status rl_kv_cache_write_strided_f16(rl_context* ctx, const rl_buffer* src,
+                                        const uint64_t* dims, const uint64_t* strides,
+                                        uint32_t rank, const rl_buffer* cache, uint64_t max_seq,
+                                        uint64_t start);
+/* RotaryEmbedding::forward_encode of the key view then its append into the
+ * cache (src/nn/attention.rs:202-207, src/model/kv_cache.rs:112-142) in one
+ * pass: the [1, kv_heads, seq_len, head_dim] view (unit innermost stride) is
+ * rotated at positions start_pos .. start_pos + seq_len and written to the
+ * same rows of the [1, kv_heads, max_seq, head_dim] cache.  RoPE's checks
+ * come first, then the cache write's. */
+rl_status rl_rope_kv_cache_write_f32(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                                     const uint64_t* strides, uint32_t rank,
+                                     const rl_buffer* cos_table, const rl_buffer* sin_table,
+                                     uint64_t table_rows, uint64_t start_pos,
+                                     const rl_buffer* cache, uint64_t max_seq);
+rl_status rl_rope_kv_cache_write_f16(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                                     const uint64_t* strides, uint32_t rank,
+                                     const rl_buffer* cos_table, const rl_buffer* sin_table,
+                                     uint64_t table_rows, uint64_t start_pos,
+                                     const rl_buffer* cache, uint64_t max_seq);
+
+/* ============================================================= embedding */
+/* ops::embedding_f32_encode (src/ops/embedding.rs:32-57,119-193):
+ * out[t, :] = weight[token_ids[t], :] for a [vocab_size, hidden_size] weight.
+ * token_ids is host memory (n_tokens values), checked against vocab_size
+ * (RL_ERR_INVALID_TOKEN_ID) and copied to the device in stream order; it may
+ * be reused as soon as the call returns.  Not allowed while recording a
+ * graph. */
+rl_status rl_embedding_f32(rl_context* ctx, const rl_buffer* weight, uint64_t vocab_size,
+                           uint64_t hidden_size, const uint32_t* token_ids, uint64_t n_tokens,
+                           const rl_buffer* out);
+/* ops::embedding_f16_encode (src/ops/embedding.rs:81-106). */
+rl_status rl_embedding_f16(rl_context* ctx, const rl_buffer* weight, uint64_t vocab_size,
+                           uint64_t hidden_size, const uint32_t* token_ids, uint64_t n_tokens,
+                           const rl_buffer* out);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,7 @@ STATUS_NAMES = {
     7: "PositionOutOfRange",
     8: "ModelFormat",
     9: "Device",
+    10: "InvalidTokenId",
 }
 
 
@@ -122,6 +123,18 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "rl_rope_f16": ([_P, _BUF, _BUF, _BUF, _U64, _U64, _U64, _BUF], _I32),
     "rl_rope_strided_f32": ([_P, _BUF, _U64P, _U64P, _U32, _BUF, _BUF, _U64, _U64, _BUF], _I32),
     "rl_rope_strided_f16": ([_P, _BUF, _U64P, _U64P, _U32, _BUF, _BUF, _U64, _U64, _BUF], _I32),
+    "rl_kv_cache_write_f32": ([_P, _BUF, _U64, _U64, _U64, _BUF, _U64, _U64], _I32),
+    "rl_kv_cache_write_f16": ([_P, _BUF, _U64, _U64, _U64, _BUF, _U64, _U64], _I32),
+    "rl_kv_cache_write_strided_f32": ([_P, _BUF, _U64P, _U64P, _U32, _BUF, _U64, _U64], _I32),
+    "rl_kv_cache_write_strided_f16": ([_P, _BUF, _U64P, _U64P, _U32, _BUF, _U64, _U64], _I32),
+    "rl_rope_kv_cache_write_f32": ([_P, _BUF, _U64P, _U64P, _U32, _BUF, _BUF, _U64, _U64, _BUF,
+                                    _U64], _I32),
+    "rl_rope_kv_cache_write_f16": ([_P, _BUF, _U64P, _U64P, _U32, _BUF, _BUF, _U64, _U64, _BUF,
+                                    _U64], _I32),
+    "rl_embedding_f32": ([_P, _BUF, _U64, _U64, ctypes.POINTER(ctypes.c_uint32), _U64, _BUF],
+                         _I32),
+    "rl_embedding_f16": ([_P, _BUF, _U64, _U64, ctypes.POINTER(ctypes.c_uint32), _U64, _BUF],
+                         _I32),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -399,4 +412,31 @@ class Context:
         table_rows = cos.shape[0]
         self._call(f"rl_rope_strided_{self._sfx(src)}", src, d, s, len(dims), cos, sin,
                    table_rows, start, out)
+        return out
+
+    # ------------------------------------------------ KV cache, embedding
+    def kv_cache_write(self, cache, source, start: int) -> None:
+        """Writes a contiguous [1, H, S, D] `source` into rows start.. of the
+        [1, H, max, D] `cache` (in place)."""
+        _, heads, max_seq, head_dim = cache.shape
+        seq = source.shape[2]
+        self._call(f"rl_kv_cache_write_{self._sfx(cache)}", cache, heads, max_seq, head_dim,
+                   source, seq, start)
+
+    def kv_cache_write_strided(self, src, dims, strides, cache, start: int) -> None:
+        d, s = _u64_array(dims), _u64_array(strides)
+        self._call(f"rl_kv_cache_write_strided_{self._sfx(cache)}", src, d, s, len(dims), cache,
+                   cache.shape[2], start)
+
+    def rope_kv_cache_write(self, src, dims, strides, cos, sin, start: int, cache) -> None:
+        d, s = _u64_array(dims), _u64_array(strides)
+        self._call(f"rl_rope_kv_cache_write_{self._sfx(cache)}", src, d, s, len(dims), cos, sin,
+                   cos.shape[0], start, cache, cache.shape[2])
+
+    def embedding(self, weight, token_ids, out=None):
+        ids = np.ascontiguousarray(token_ids, dtype=np.uint32)
+        vocab, hidden = weight.shape
+        out = out or self.empty((ids.size, hidden), weight.dtype)
+        self._call(f"rl_embedding_{self._sfx(weight)}", weight, vocab, hidden,
+                   ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), ids.size, out)
         return out

@@ -61,6 +61,14 @@ struct rl_context {
     // start and end in these events.
     hipEvent_t timed_start = nullptr;
     hipEvent_t timed_stop = nullptr;
+
+    // Pinned host staging for small host arrays an op takes by value (the
+    // embedding's token ids): copied here, then to device memory in stream
+    // order; `staging_done` marks when the last such copy has read it.
+    void* staging = nullptr;
+    uint64_t staging_bytes = 0;
+    hipEvent_t staging_done = nullptr;
+    bool staging_pending = false;
 };
 
 // Every kernel launch of the library: on the context's stream, and, when
@@ -93,6 +101,19 @@ rl_status activate(rl_context* ctx);
 // Bookkeeping after a kernel launch: launch errors become RL_ERR_DEVICE and
 // the dispatch is counted in an active profile.
 rl_status after_launch(rl_context* ctx, const char* kernel_name);
+
+// Copies `bytes` of host memory to a pool block in the context's stream
+// order (through the pinned staging area) and returns the block in *dev.
+// The caller enqueues its readers and then releases the block to the pool.
+// Not allowed while recording a graph (the copy would replay stale data).
+rl_status stage_to_device(rl_context* ctx, const void* host, uint64_t bytes, void** dev);
+
+// Checks of a KV-cache write of a [1, H, S, D] source view (dims/strides,
+// rank 4) into a [1, H, max_seq, D] cache of `es`-byte elements; with
+// `exact_source` the source buffer must hold exactly H*S*D elements.
+rl_status validate_kv_write(const char* name, const rl_buffer* cache, uint64_t max_seq,
+                            const rl_buffer* src, const uint64_t* dims, const uint64_t* strides,
+                            uint32_t rank, uint64_t start, uint64_t es, bool exact_source);
 
 inline bool aligned_to(const void* p, uint64_t bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
@@ -135,6 +156,16 @@ struct FastDiv {
         q = div(n);
         r = n - q * divisor;
     }
+};
+
+// The row dims of a strided view (every dim but the innermost), innermost
+// first: dim[0] is the sequence dim of a [..., S, D] view.  Passed by value
+// to kernels that decode a row index into an element offset.
+constexpr int kMaxRowRank = 16;
+struct RowDims {
+    uint32_t rank;
+    FastDiv dim[kMaxRowRank];
+    uint64_t stride[kMaxRowRank];
 };
 
 }  // namespace rl

@@ -22,14 +22,16 @@ namespace rl {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxRank = 16;
+constexpr int kMaxRank = kMaxRowRank;
 
-// Row dims of the view (all but the innermost), innermost first; dim[0] is
-// the sequence dim.
-struct RowDims {
-    uint32_t rank;
-    FastDiv dim[kMaxRank];
-    uint64_t stride[kMaxRank];
+// Output row of input row (g, p) -- g the index over all dims outside the
+// sequence dim, p the position -- is g * group_rows + first_row + p: the
+// contiguous [..., S, D] result for group_rows = S, first_row = 0, or the
+// rows of a [1, H, max_seq, D] KV cache from `start` on for
+// group_rows = max_seq, first_row = start.
+struct DstRows {
+    uint32_t group_rows;
+    uint32_t first_row;
 };
 
 template <typename T, int N, int UNROLL>
@@ -38,7 +40,8 @@ __global__ __launch_bounds__(kThreads) void k_rope(const T* __restrict__ src,
                                                    const float* __restrict__ sin_table,
                                                    T* __restrict__ out, uint32_t n_items,
                                                    FastDiv packs_per_row, RowDims rd,
-                                                   uint32_t half_dim, uint32_t start) {
+                                                   uint32_t half_dim, uint32_t start,
+                                                   DstRows dst) {
     typedef typename VecOf<T, N>::type V;
     typedef typename VecOf<float, N>::type VF;
     const uint64_t tile = uint64_t(kThreads) * UNROLL;
@@ -56,12 +59,15 @@ __global__ __launch_bounds__(kThreads) void k_rope(const T* __restrict__ src,
                 packs_per_row.divmod(uint32_t(i), row, pp);
                 // Decode the row: the innermost row dim is the sequence position.
                 uint64_t src_off = 0;
-                uint32_t position = 0;
+                uint32_t position = 0, group = 0;
                 uint32_t rest = row;
                 for (uint32_t d = 0; d < rd.rank; ++d) {
                     uint32_t q, r;
                     rd.dim[d].divmod(rest, q, r);
-                    if (d == 0) position = r;
+                    if (d == 0) {
+                        position = r;
+                        group = q;
+                    }
                     src_off += uint64_t(r) * rd.stride[d];
                     rest = q;
                 }
@@ -71,7 +77,9 @@ __global__ __launch_bounds__(kThreads) void k_rope(const T* __restrict__ src,
                 b[u] = *reinterpret_cast<const V*>(src + src_off + half_dim + pair);
                 c[u] = *reinterpret_cast<const VF*>(cos_table + t);
                 s[u] = *reinterpret_cast<const VF*>(sin_table + t);
-                dst_off[u] = uint64_t(row) * (2 * half_dim) + pair;
+                const uint64_t dst_row =
+                    uint64_t(group) * dst.group_rows + dst.first_row + position;
+                dst_off[u] = dst_row * (2 * half_dim) + pair;
             }
         }
 #pragma unroll
@@ -101,10 +109,12 @@ inline unsigned grid_for(uint64_t items, uint64_t per_block) {
 }
 
 // dims/strides: the view, outermost first, rank >= 2, strides[rank-1] == 1.
+// dst.group_rows == 0 means the contiguous [dims] output.
 template <typename T>
 rl_status launch_rope(rl_context* ctx, const char* name, const T* src, const uint64_t* dims,
                       const uint64_t* strides, uint32_t rank, const float* cos_table,
-                      const float* sin_table, uint64_t start, T* out) {
+                      const float* sin_table, uint64_t start, T* out,
+                      DstRows dst = DstRows{0, 0}) {
     if (rl_status st = activate(ctx)) return st;
     const uint64_t head_dim = dims[rank - 1];
     const uint64_t half = head_dim / 2;
@@ -132,18 +142,19 @@ rl_status launch_rope(rl_context* ctx, const char* name, const T* src, const uin
     constexpr int U = 2;
     const dim3 grid(grid_for(n_items, uint64_t(kThreads) * U)), block(kThreads);
     const uint32_t h32 = uint32_t(half), s32 = uint32_t(start), ni = uint32_t(n_items);
+    if (dst.group_rows == 0) dst = DstRows{uint32_t(dims[rank - 2]), 0};
     switch (n) {
         case 8:
-            RL_LAUNCH(ctx, (k_rope<T, 8, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32);
+            RL_LAUNCH(ctx, (k_rope<T, 8, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32, dst);
             break;
         case 4:
-            RL_LAUNCH(ctx, (k_rope<T, 4, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32);
+            RL_LAUNCH(ctx, (k_rope<T, 4, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32, dst);
             break;
         case 2:
-            RL_LAUNCH(ctx, (k_rope<T, 2, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32);
+            RL_LAUNCH(ctx, (k_rope<T, 2, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32, dst);
             break;
         default:
-            RL_LAUNCH(ctx, (k_rope<T, 1, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32);
+            RL_LAUNCH(ctx, (k_rope<T, 1, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32, dst);
             break;
     }
     return after_launch(ctx, name);
@@ -255,12 +266,76 @@ rl_status rope_strided_entry(rl_context* ctx, const char* name, const rl_buffer*
                           static_cast<T*>(out->data));
 }
 
+// RotaryEmbedding::forward_encode on the [1, H, S, D] key view followed by
+// LayerKvCache::append_encode's write of the result into the cache
+// (src/nn/attention.rs:202-207 then src/model/kv_cache.rs:112-142): the
+// gather, the rotation and the cache write in one pass.  The rotation uses
+// positions start .. start + S, the cache rows the same range, as both
+// calls take the cache's current length.
+template <typename T>
+rl_status rope_kv_entry(rl_context* ctx, const char* name, const char* write_name,
+                        const rl_buffer* src, const uint64_t* dims, const uint64_t* strides,
+                        uint32_t rank, const rl_buffer* cos_table, const rl_buffer* sin_table,
+                        uint64_t table_rows, uint64_t start, const rl_buffer* cache,
+                        uint64_t max_seq) {
+    // The rotation's checks come first, as forward_encode runs before the
+    // append; its output would be a contiguous tensor of the view's dims.
+    if (rl_status st = check_buffer(src, "input")) return st;
+    if (dims == nullptr || strides == nullptr)
+        return fail(RL_ERR_INVALID_ARGUMENT, "dims or strides is null");
+    if (rank < 2)
+        return fail(RL_ERR_INVALID_DIMENSION,
+                    "RoPE expects [..., sequence, head_dim], got rank %u", rank);
+    if (rank > kMaxRank + 1) return fail(RL_ERR_INVALID_SHAPE, "tensor rank exceeds %d", kMaxRank + 1);
+    const uint64_t seq_len = dims[rank - 2], head_dim = dims[rank - 1];
+    if (head_dim == 0 || head_dim % 2 != 0)
+        return fail(RL_ERR_INVALID_SHAPE, "RoPE head dimension must be positive and even, got %llu",
+                    (unsigned long long)head_dim);
+    for (uint32_t d = 0; d < rank; ++d)
+        if (dims[d] == 0)
+            return fail(RL_ERR_INVALID_SHAPE, "shape dimensions must be greater than zero");
+    if (rl_status st = check_tables(cos_table, sin_table, table_rows, head_dim / 2, start, seq_len))
+        return st;
+    if (strides[rank - 1] != 1)
+        return fail(RL_ERR_NON_CONTIGUOUS, "RoPE view must have a unit innermost stride");
+    // Then the cache write's.
+    if (rl_status st = validate_kv_write(write_name, cache, max_seq, src, dims, strides, rank,
+                                         start, sizeof(T), false))
+        return st;
+    if (rl_status st = require_context(ctx)) return st;
+    return launch_rope<T>(ctx, name, static_cast<const T*>(src->data), dims, strides, rank,
+                          static_cast<const float*>(cos_table->data),
+                          static_cast<const float*>(sin_table->data), start,
+                          static_cast<T*>(cache->data),
+                          DstRows{uint32_t(max_seq), uint32_t(start)});
+}
+
 }  // namespace
 }  // namespace rl
 
 using namespace rl;
 
 extern "C" {
+
+rl_status rl_rope_kv_cache_write_f32(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                                     const uint64_t* strides, uint32_t rank,
+                                     const rl_buffer* cos_table, const rl_buffer* sin_table,
+                                     uint64_t table_rows, uint64_t start_pos,
+                                     const rl_buffer* cache, uint64_t max_seq) {
+    return rope_kv_entry<float>(ctx, "rope_kv_cache_write_f32", "kv_cache_write_f32", src, dims,
+                                strides, rank, cos_table, sin_table, table_rows, start_pos, cache,
+                                max_seq);
+}
+
+rl_status rl_rope_kv_cache_write_f16(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
+                                     const uint64_t* strides, uint32_t rank,
+                                     const rl_buffer* cos_table, const rl_buffer* sin_table,
+                                     uint64_t table_rows, uint64_t start_pos,
+                                     const rl_buffer* cache, uint64_t max_seq) {
+    return rope_kv_entry<half_t>(ctx, "rope_kv_cache_write_f16", "kv_cache_write_f16", src, dims,
+                                 strides, rank, cos_table, sin_table, table_rows, start_pos,
+                                 cache, max_seq);
+}
 
 rl_status rl_rope_f32(rl_context* ctx, const rl_buffer* input, const rl_buffer* cos_table,
                       const rl_buffer* sin_table, uint64_t seq_len, uint64_t head_dim,

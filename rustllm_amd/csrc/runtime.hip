@@ -105,6 +105,44 @@ rl_status after_launch(rl_context* ctx, const char* kernel_name) {
     return RL_OK;
 }
 
+rl_status stage_to_device(rl_context* ctx, const void* host, uint64_t bytes, void** dev) {
+    *dev = nullptr;
+    if (ctx->capturing)
+        return fail(RL_ERR_DEVICE, "host arrays cannot be recorded into a graph");
+    // The previous staged copy must have read the staging area before it is
+    // overwritten (or freed to grow it).
+    if (ctx->staging_pending) {
+        RL_HIP(hipEventSynchronize(ctx->staging_done), "hipEventSynchronize");
+        ctx->staging_pending = false;
+    }
+    if (bytes > ctx->staging_bytes) {
+        uint64_t cap = 4096;
+        while (cap < bytes) cap *= 2;
+        if (ctx->staging != nullptr) {
+            (void)hipHostFree(ctx->staging);
+            ctx->staging = nullptr;
+            ctx->staging_bytes = 0;
+        }
+        RL_HIP(hipHostMalloc(&ctx->staging, cap, hipHostMallocDefault), "hipHostMalloc");
+        ctx->staging_bytes = cap;
+    }
+    if (ctx->staging_done == nullptr)
+        RL_HIP(hipEventCreateWithFlags(&ctx->staging_done, hipEventDisableTiming),
+               "hipEventCreateWithFlags");
+    std::memcpy(ctx->staging, host, bytes);
+    void* p = nullptr;
+    if (rl_status st = ctx->pool.allocate(bytes, &p)) return st;
+    hipError_t err = hipMemcpyAsync(p, ctx->staging, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (err == hipSuccess) err = hipEventRecord(ctx->staging_done, ctx->stream);
+    if (err != hipSuccess) {
+        ctx->pool.release(p);
+        return hip_fail(err, "staging copy");
+    }
+    ctx->staging_pending = true;
+    *dev = p;
+    return RL_OK;
+}
+
 rl_status check_buffer(const rl_buffer* b, const char* what) {
     if (b == nullptr) return fail(RL_ERR_INVALID_ARGUMENT, "%s buffer is null", what);
     if (b->len > 0 && b->data == nullptr)
@@ -197,6 +235,8 @@ void rl_context_destroy(rl_context* ctx) {
     if (ctx == nullptr) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->staging != nullptr) (void)hipHostFree(ctx->staging);
+    if (ctx->staging_done != nullptr) (void)hipEventDestroy(ctx->staging_done);
     if (ctx->owns_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;  // the pool frees its blocks
 }

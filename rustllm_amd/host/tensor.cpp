@@ -12,7 +12,7 @@ namespace rustllm {
 
 static const char* const kKindNames[] = {
     "InvalidArgument", "InvalidShape", "ShapeMismatch",      "InvalidDimension", "UnsupportedDType",
-    "NonContiguousTensor", "PositionOutOfRange", "ModelFormat", "Device",
+    "NonContiguousTensor", "PositionOutOfRange", "ModelFormat", "Device", "InvalidTokenId",
 };
 
 const char* kind_name(TinyError::Kind kind) { return kKindNames[int(kind)]; }
@@ -21,7 +21,7 @@ TinyError::TinyError(Kind kind, const std::string& message)
     : std::runtime_error(std::string(kind_name(kind)) + ": " + message), kind_(kind) {}
 
 TinyError TinyError::from_status(rl_status status) {
-    Kind kind = (status >= 1 && status <= 9) ? Kind(status - 1) : Kind::Device;
+    Kind kind = (status >= 1 && status <= 10) ? Kind(status - 1) : Kind::Device;
     return TinyError(kind, rl_last_error_message());
 }
 
@@ -895,8 +895,8 @@ Tensor rope(const Context& ctx, const Tensor& input, const Tensor& cos, const Te
 
 // src/ops/rope.rs:303-370.  A strided input with a unit innermost stride is
 // gathered and rotated by one kernel instead of contiguous_encode + rope.
-Tensor rope_encode(const Context& ctx, const Tensor& input, const Tensor& cos, const Tensor& sin,
-                   size_t start_pos) {
+// ops::rope_encode's checks (src/ops/rope.rs:303-343) in order.
+void validate_rope(const Tensor& input, const Tensor& cos, const Tensor& sin, size_t start_pos) {
     if (cos.dtype() != DType::F32 || sin.dtype() != DType::F32)
         throw TinyError(TinyError::Kind::UnsupportedDType, "RoPE requires F32 cos/sin tables");
     if (input.rank() < 2)
@@ -916,6 +916,13 @@ Tensor rope_encode(const Context& ctx, const Tensor& input, const Tensor& cos, c
         start_pos + seq_len > table_rows)
         throw TinyError(TinyError::Kind::InvalidShape,
                         "RoPE cos/sin table shape or position range is invalid");
+}
+
+Tensor rope_encode(const Context& ctx, const Tensor& input, const Tensor& cos, const Tensor& sin,
+                   size_t start_pos) {
+    validate_rope(input, cos, sin, start_pos);
+    const size_t seq_len = input.dim(input.rank() - 2), head_dim = input.dim(input.rank() - 1);
+    const size_t table_rows = cos.dim(0);
     const size_t es = size_in_bytes(input.dtype());
     if (!input.is_contiguous() && input.strides().values().back() == 1) {
         Buffer out = Buffer::empty_with_element_size(ctx, input.numel(), es);
@@ -956,6 +963,115 @@ std::pair<Tensor, Tensor> add_rmsnorm_encode(const Context& ctx, const Tensor& x
                                        norm.raw()));
     return {Tensor::from_buffer(std::move(sum), x.shape().dims(), x.dtype()),
             Tensor::from_buffer(std::move(norm), x.shape().dims(), x.dtype())};
+}
+
+// src/ops/embedding.rs:10-193.  The library validates the ids and copies
+// them to the device in stream order.
+static Buffer embedding_encode(const Context& ctx, const Buffer& weight,
+                               const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                               size_t hidden_size, DType dtype) {
+    const size_t es = size_in_bytes(dtype);
+    Buffer out;
+    if (token_ids.empty()) {  // the library reports the reference's error
+        const rl_buffer none{nullptr, 0, 0};
+        check(dtype == DType::F32
+                  ? rl_embedding_f32(ctx.raw(), weight.raw(), vocab_size, hidden_size,
+                                     token_ids.data(), 0, &none)
+                  : rl_embedding_f16(ctx.raw(), weight.raw(), vocab_size, hidden_size,
+                                     token_ids.data(), 0, &none));
+    }
+    out = Buffer::empty_with_element_size(ctx, token_ids.size() * hidden_size, es);
+    check(dtype == DType::F32
+              ? rl_embedding_f32(ctx.raw(), weight.raw(), vocab_size, hidden_size,
+                                 token_ids.data(), token_ids.size(), out.raw())
+              : rl_embedding_f16(ctx.raw(), weight.raw(), vocab_size, hidden_size,
+                                 token_ids.data(), token_ids.size(), out.raw()));
+    return out;
+}
+
+Buffer embedding_f32_encode(const Context& ctx, const Buffer& weight,
+                            const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                            size_t hidden_size) {
+    return embedding_encode(ctx, weight, token_ids, vocab_size, hidden_size, DType::F32);
+}
+
+Buffer embedding_f16_encode(const Context& ctx, const Buffer& weight,
+                            const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                            size_t hidden_size) {
+    return embedding_encode(ctx, weight, token_ids, vocab_size, hidden_size, DType::F16);
+}
+
+Buffer embedding_f32(const Context& ctx, const Buffer& weight,
+                     const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                     size_t hidden_size) {
+    Execution exe(ctx);
+    Buffer out = embedding_f32_encode(ctx, weight, token_ids, vocab_size, hidden_size);
+    exe.finish();
+    return out;
+}
+
+Buffer embedding_f16(const Context& ctx, const Buffer& weight,
+                     const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                     size_t hidden_size) {
+    Execution exe(ctx);
+    Buffer out = embedding_f16_encode(ctx, weight, token_ids, vocab_size, hidden_size);
+    exe.finish();
+    return out;
+}
+
+// kv_cache_write_encode (src/ops/kv_cache_write.rs:71-141), Tensor-level
+// checks in order; the buffer-level ones are repeated by the library.
+static void kv_cache_write_tensor_encode(const Context& ctx, const Tensor& cache,
+                                         const Tensor& source, size_t start, DType dtype,
+                                         const char* kernel_name) {
+    if (cache.dtype() != dtype || source.dtype() != dtype)
+        throw TinyError(TinyError::Kind::UnsupportedDType,
+                        std::string(kernel_name) + " expects " + dtype_name(dtype) +
+                            " cache and source, got " + dtype_name(cache.dtype()) + " and " +
+                            dtype_name(source.dtype()));
+    if (cache.rank() != 4 || source.rank() != 4 || cache.dim(0) != 1 || source.dim(0) != 1 ||
+        cache.dim(1) != source.dim(1) || cache.dim(3) != source.dim(3))
+        throw TinyError(TinyError::Kind::InvalidShape, "invalid KV cache write shape");
+    const size_t seq = source.dim(2), max_seq = cache.dim(2);
+    if (start + seq < start || start + seq > max_seq)
+        throw TinyError(TinyError::Kind::PositionOutOfRange,
+                        "position range [" + std::to_string(start) + ", " +
+                            std::to_string(start + seq) + ") exceeds max sequence length " +
+                            std::to_string(max_seq));
+    if (!source.is_contiguous())
+        throw TinyError(TinyError::Kind::NonContiguousTensor,
+                        "batched KV cache write requires a contiguous source");
+    check(dtype == DType::F32
+              ? rl_kv_cache_write_f32(ctx.raw(), cache.buffer().raw(), cache.dim(1), max_seq,
+                                      cache.dim(3), source.buffer().raw(), seq, start)
+              : rl_kv_cache_write_f16(ctx.raw(), cache.buffer().raw(), cache.dim(1), max_seq,
+                                      cache.dim(3), source.buffer().raw(), seq, start));
+}
+
+void kv_cache_write_f32_encode(const Context& ctx, const Tensor& cache, const Tensor& source,
+                               size_t start) {
+    kv_cache_write_tensor_encode(ctx, cache, source, start, DType::F32, "kv_cache_write_f32");
+}
+
+void kv_cache_write_f16_encode(const Context& ctx, const Tensor& cache, const Tensor& source,
+                               size_t start) {
+    kv_cache_write_tensor_encode(ctx, cache, source, start, DType::F16, "kv_cache_write_f16");
+}
+
+void kv_cache_write_f32(const Context& ctx, const Tensor& cache, const Tensor& source,
+                        size_t start) {  // kv_cache_write.rs:9-20
+    Execution exe(ctx);
+    Tensor src = source.contiguous_encode(ctx);
+    kv_cache_write_f32_encode(ctx, cache, src, start);
+    exe.finish();
+}
+
+void kv_cache_write_f16(const Context& ctx, const Tensor& cache, const Tensor& source,
+                        size_t start) {  // kv_cache_write.rs:43-54
+    Execution exe(ctx);
+    Tensor src = source.contiguous_encode(ctx);
+    kv_cache_write_f16_encode(ctx, cache, src, start);
+    exe.finish();
 }
 
 }  // namespace ops
@@ -1084,4 +1200,111 @@ Tensor SwiGlu::forward_encode(const Context& ctx, const Tensor& gate, const Tens
 }
 
 }  // namespace nn
+// ------------------------------------------------------------------ model
+
+namespace model {
+
+// LayerKvCache::new (src/model/kv_cache.rs:53-74)
+LayerKvCache::LayerKvCache(const Context& ctx, size_t num_kv_heads, size_t max, size_t dim,
+                           DType dtype)
+    : key_(Tensor::empty(ctx, {1, num_kv_heads ? num_kv_heads : 1, max ? max : 1, dim ? dim : 1},
+                         dtype)),
+      value_(Tensor::empty(ctx, {1, num_kv_heads ? num_kv_heads : 1, max ? max : 1, dim ? dim : 1},
+                           dtype)),
+      max_seq_len_(max),
+      num_kv_heads_(num_kv_heads),
+      head_dim_(dim) {
+    if (num_kv_heads == 0 || max == 0 || dim == 0)
+        throw TinyError(TinyError::Kind::InvalidShape, "KV cache dimensions must be positive");
+}
+
+size_t LayerKvCache::storage_bytes() const {  // kv_cache.rs:86-89
+    return 2 * num_kv_heads_ * max_seq_len_ * head_dim_ * size_in_bytes(dtype());
+}
+
+Tensor LayerKvCache::key() const { return key_.narrow(2, 0, len_); }
+Tensor LayerKvCache::value() const { return value_.narrow(2, 0, len_); }
+
+// kv_cache.rs:18-52
+void LayerKvCache::validate_append(const Tensor& key, const Tensor& value) const {
+    if (key.dtype() != key_.dtype() || value.dtype() != value_.dtype())
+        throw TinyError(TinyError::Kind::UnsupportedDType,
+                        std::string("KV cache dtype mismatch: cache=") + dtype_name(key_.dtype()) +
+                            "/" + dtype_name(value_.dtype()) + ", input=" +
+                            dtype_name(key.dtype()) + "/" + dtype_name(value.dtype()));
+    if (key.shape() != value.shape() || key.rank() != 4 || key.dim(0) != 1 ||
+        key.dim(1) != num_kv_heads_ || key.dim(3) != head_dim_)
+        throw TinyError(TinyError::Kind::ModelFormat,
+                        "KV cache write shape does not match this layer: cache has " +
+                            std::to_string(num_kv_heads_) + " KV heads, input has " +
+                            std::to_string(key.dim(1)) + " heads");
+    const size_t seq = key.dim(2);
+    if (len_ + seq < len_ || len_ + seq > max_seq_len_)
+        throw TinyError(TinyError::Kind::PositionOutOfRange,
+                        "position range [" + std::to_string(len_) + ", " +
+                            std::to_string(len_ + seq) + ") exceeds max sequence length " +
+                            std::to_string(max_seq_len_));
+}
+
+// One tensor of append_encode (kv_cache.rs:123-137): contiguous_encode then
+// kv_cache_write, or both at once for a strided view.
+static void write_into(const Context& ctx, const Tensor& cache, const Tensor& src, size_t start) {
+    if (src.is_contiguous()) {
+        if (cache.dtype() == DType::F32)
+            ops::kv_cache_write_f32_encode(ctx, cache, src, start);
+        else
+            ops::kv_cache_write_f16_encode(ctx, cache, src, start);
+        return;
+    }
+    std::vector<uint64_t> d(src.shape().dims().begin(), src.shape().dims().end());
+    std::vector<uint64_t> s(src.strides().values().begin(), src.strides().values().end());
+    check(cache.dtype() == DType::F32
+              ? rl_kv_cache_write_strided_f32(ctx.raw(), src.buffer().raw(), d.data(), s.data(),
+                                              uint32_t(d.size()), cache.buffer().raw(),
+                                              cache.dim(2), start)
+              : rl_kv_cache_write_strided_f16(ctx.raw(), src.buffer().raw(), d.data(), s.data(),
+                                              uint32_t(d.size()), cache.buffer().raw(),
+                                              cache.dim(2), start));
+}
+
+void LayerKvCache::append_encode(const Context& ctx, const Tensor& key, const Tensor& value) {
+    validate_append(key, value);
+    const size_t start = len_, seq = key.dim(2);
+    write_into(ctx, key_, key, start);
+    write_into(ctx, value_, value, start);
+    len_ = start + seq;
+}
+
+void LayerKvCache::append(const Context& ctx, const Tensor& key, const Tensor& value) {
+    Execution exe(ctx);  // kv_cache.rs:104-111
+    append_encode(ctx, key, value);
+    exe.finish();
+}
+
+void LayerKvCache::append_rotated_encode(const Context& ctx, const nn::RotaryEmbedding& rope,
+                                         const Tensor& key, const Tensor& value) {
+    if (key.rank() == 4 && key.strides().values().back() == 1 && key.dtype() == key_.dtype()) {
+        ops::validate_rope(key, rope.cos_table(), rope.sin_table(), len_);  // forward_encode first
+        validate_append(key, value);
+        const size_t start = len_, seq = key.dim(2);
+        std::vector<uint64_t> d(key.shape().dims().begin(), key.shape().dims().end());
+        std::vector<uint64_t> s(key.strides().values().begin(), key.strides().values().end());
+        const Tensor& c = rope.cos_table();
+        const Tensor& sn = rope.sin_table();
+        check(key_.dtype() == DType::F32
+                  ? rl_rope_kv_cache_write_f32(ctx.raw(), key.buffer().raw(), d.data(), s.data(),
+                                               4, c.buffer().raw(), sn.buffer().raw(), c.dim(0),
+                                               start, key_.buffer().raw(), max_seq_len_)
+                  : rl_rope_kv_cache_write_f16(ctx.raw(), key.buffer().raw(), d.data(), s.data(),
+                                               4, c.buffer().raw(), sn.buffer().raw(), c.dim(0),
+                                               start, key_.buffer().raw(), max_seq_len_));
+        write_into(ctx, value_, value, start);
+        len_ = start + seq;
+        return;
+    }
+    // Anything else takes the two-step path (and raises its errors).
+    append_encode(ctx, rope.forward_encode(ctx, key, len_), value);
+}
+
+}  // namespace model
 }  // namespace rustllm

@@ -41,6 +41,7 @@ class TinyError : public std::runtime_error {
         PositionOutOfRange,
         ModelFormat,
         Device,
+        InvalidTokenId,
     };
     TinyError(Kind kind, const std::string& message);
     Kind kind() const { return kind_; }
@@ -286,10 +287,33 @@ Tensor rope(const Context& ctx, const Tensor& input, const Tensor& cos, const Te
             size_t start_pos);
 Tensor rope_encode(const Context& ctx, const Tensor& input, const Tensor& cos, const Tensor& sin,
                    size_t start_pos);
+void validate_rope(const Tensor& input, const Tensor& cos, const Tensor& sin, size_t start_pos);
 // Residual add + RMSNorm fused (nn/transformer_block.rs:148-152); returns {sum, norm}.
 std::pair<Tensor, Tensor> add_rmsnorm_encode(const Context& ctx, const Tensor& x,
                                              const Tensor& residual, const Tensor& weight,
                                              float epsilon);
+// src/ops/embedding.rs:10-193: rows of a [vocab_size, hidden_size] weight.
+Buffer embedding_f32(const Context& ctx, const Buffer& weight,
+                     const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                     size_t hidden_size);
+Buffer embedding_f16(const Context& ctx, const Buffer& weight,
+                     const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                     size_t hidden_size);
+Buffer embedding_f32_encode(const Context& ctx, const Buffer& weight,
+                            const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                            size_t hidden_size);
+Buffer embedding_f16_encode(const Context& ctx, const Buffer& weight,
+                            const std::vector<uint32_t>& token_ids, size_t vocab_size,
+                            size_t hidden_size);
+// src/ops/kv_cache_write.rs:9-141: source [1, H, S, D] into cache [1, H, max, D] at start.
+void kv_cache_write_f32(const Context& ctx, const Tensor& cache, const Tensor& source,
+                        size_t start);
+void kv_cache_write_f16(const Context& ctx, const Tensor& cache, const Tensor& source,
+                        size_t start);
+void kv_cache_write_f32_encode(const Context& ctx, const Tensor& cache, const Tensor& source,
+                               size_t start);
+void kv_cache_write_f16_encode(const Context& ctx, const Tensor& cache, const Tensor& source,
+                               size_t start);
 }  // namespace ops
 
 // --------------------------------------------------------------------- nn
@@ -339,4 +363,38 @@ struct SwiGlu {
 };
 
 }  // namespace nn
+
+// ------------------------------------------------------------------ model
+
+namespace model {
+
+// src/model/kv_cache.rs:9-142: one layer's [1, kv_heads, max, dim] key and
+// value caches and the logical length.
+class LayerKvCache {
+   public:
+    LayerKvCache(const Context& ctx, size_t num_kv_heads, size_t max, size_t dim, DType dtype);
+    size_t len() const { return len_; }
+    bool is_empty() const { return len_ == 0; }
+    size_t capacity() const { return max_seq_len_; }
+    size_t storage_bytes() const;
+    void reset() { len_ = 0; }
+    DType dtype() const { return key_.dtype(); }
+    Tensor key() const;    // narrow(2, 0, len)
+    Tensor value() const;  // narrow(2, 0, len)
+    void append(const Context& ctx, const Tensor& key, const Tensor& value);
+    // Gathers strided key/value views straight into the cache (the
+    // contiguous_encode + kv_cache_write of the reference in one pass each).
+    void append_encode(const Context& ctx, const Tensor& key, const Tensor& value);
+    // RotaryEmbedding::forward_encode(key, len()) then append_encode, with the
+    // rotated key written straight into the cache (nn/attention.rs:202-207,306-307).
+    void append_rotated_encode(const Context& ctx, const nn::RotaryEmbedding& rope,
+                               const Tensor& key, const Tensor& value);
+
+   private:
+    void validate_append(const Tensor& key, const Tensor& value) const;
+    Tensor key_, value_;
+    size_t len_ = 0, max_seq_len_, num_kv_heads_, head_dim_;
+};
+
+}  // namespace model
 }  // namespace rustllm

@@ -368,6 +368,146 @@ TEST(f16_cache_narrow_view_materialises_in_order) {
            std::vector<float>{1, 2, 3, 4, 9, 10, 11, 12, 5, 6, 7, 8, 13, 14, 15, 16}));
 }
 
+// ------------------------------------------------- src/model/kv_cache.rs
+
+Tensor f16_tensor(const Context& context, const std::vector<float>& data,
+                  const std::vector<size_t>& dims) {
+    return Tensor::from_f32_slice(context, data, dims).to_dtype(context, DType::F16);
+}
+
+// kv_cache.rs:213-258
+TEST(f16_cache_appends_decode_tokens_and_returns_f16_prefix) {
+    model::LayerKvCache cache(context, 2, 8, 4, DType::F16);
+    CHECK(cache.dtype() == DType::F16);
+    CHECK(cache.len() == 0);
+    cache.append(context, f16_tensor(context, {1, 2, 3, 4, 5, 6, 7, 8}, {1, 2, 1, 4}),
+                 f16_tensor(context, {10, 20, 30, 40, 50, 60, 70, 80}, {1, 2, 1, 4}));
+    cache.append(context, f16_tensor(context, {9, 10, 11, 12, 13, 14, 15, 16}, {1, 2, 1, 4}),
+                 f16_tensor(context, {90, 100, 110, 120, 130, 140, 150, 160}, {1, 2, 1, 4}));
+    CHECK(cache.len() == 2);
+    auto cached_key = cache.key();
+    auto cached_value = cache.value();
+    CHECK((cached_key.shape().dims() == std::vector<size_t>{1, 2, 2, 4}));
+    CHECK(cached_key.dtype() == DType::F16);
+    CHECK(cached_value.dtype() == DType::F16);
+    CHECK((cached_key.contiguous(context).to_f32_vec() ==
+           std::vector<float>{1, 2, 3, 4, 9, 10, 11, 12, 5, 6, 7, 8, 13, 14, 15, 16}));
+    CHECK((cached_value.contiguous(context).to_f32_vec() ==
+           std::vector<float>{10, 20, 30, 40, 90, 100, 110, 120, 50, 60, 70, 80, 130, 140, 150,
+                              160}));
+}
+
+// kv_cache.rs:260-273
+TEST(f16_cache_appends_prefill_sequence) {
+    model::LayerKvCache cache(context, 2, 8, 4, DType::F16);
+    cache.append(context, f16_tensor(context, std::vector<float>(24, 1.0f), {1, 2, 3, 4}),
+                 f16_tensor(context, std::vector<float>(24, 2.0f), {1, 2, 3, 4}));
+    CHECK(cache.len() == 3);
+    CHECK((cache.key().shape().dims() == std::vector<size_t>{1, 2, 3, 4}));
+}
+
+// kv_cache.rs:275-295
+TEST(append_encode_updates_the_logical_prefix_after_submission) {
+    model::LayerKvCache cache(context, 2, 8, 2, DType::F16);
+    auto key = f16_tensor(context, std::vector<float>(4, 1.0f), {1, 2, 1, 2});
+    auto value = f16_tensor(context, std::vector<float>(4, 2.0f), {1, 2, 1, 2});
+    Execution execution(context);
+    cache.append_encode(context, key, value);
+    execution.finish();
+    CHECK(cache.len() == 1);
+    CHECK((cache.key().shape().dims() == std::vector<size_t>{1, 2, 1, 2}));
+    CHECK((cache.value().shape().dims() == std::vector<size_t>{1, 2, 1, 2}));
+}
+
+// kv_cache.rs:297-309
+TEST(f16_cache_rejects_f32_inputs_without_casting) {
+    model::LayerKvCache cache(context, 2, 8, 4, DType::F16);
+    auto key = Tensor::from_f32_slice(context, std::vector<float>(8, 1.0f), {1, 2, 1, 4});
+    auto value = Tensor::from_f32_slice(context, std::vector<float>(8, 2.0f), {1, 2, 1, 4});
+    CHECK(expect_error([&] { cache.append(context, key, value); }) ==
+          TinyError::Kind::UnsupportedDType);
+    CHECK(cache.len() == 0);
+}
+
+// kv_cache.rs:31-50: wrong head count, then a write past max_seq_len.
+TEST(cache_rejects_foreign_shapes_and_overflow) {
+    model::LayerKvCache cache(context, 2, 4, 4, DType::F32);
+    auto three_heads = Tensor::from_f32_slice(context, std::vector<float>(12, 1.0f), {1, 3, 1, 4});
+    CHECK(expect_error([&] { cache.append(context, three_heads, three_heads); }) ==
+          TinyError::Kind::ModelFormat);
+    auto five = Tensor::from_f32_slice(context, std::vector<float>(40, 1.0f), {1, 2, 5, 4});
+    CHECK(expect_error([&] { cache.append(context, five, five); }) ==
+          TinyError::Kind::PositionOutOfRange);
+    CHECK(expect_error([&] { model::LayerKvCache(context, 0, 4, 4, DType::F32); }) ==
+          TinyError::Kind::InvalidShape);
+    CHECK(cache.storage_bytes() == 2 * 2 * 4 * 4 * 4);
+}
+
+// The attention path (nn/attention.rs:196-207, 306-307): K and V come as
+// [1, H, S, D] permutes of the [1, S, H*D] projections; K is rotated at the
+// cache's length.  Appending the views (gather + write in one pass) and the
+// rotated key (rotation + write in one pass) equals contiguous -> rope ->
+// append of the materialised tensors, bit for bit.
+TEST(fused_append_of_projection_views_equals_the_unfused_path) {
+    const size_t seq = 3, heads = 2, hd = 8, max = 8;
+    nn::RotaryEmbedding rope(context, hd, max, 10000.0f);
+    std::vector<float> kd(seq * heads * hd), vd(seq * heads * hd);
+    for (size_t i = 0; i < kd.size(); ++i) {
+        kd[i] = std::sin(0.37f * float(i)) * 3.0f;
+        vd[i] = std::cos(0.11f * float(i)) * 2.0f;
+    }
+    for (DType dtype : {DType::F32, DType::F16}) {
+        auto k = Tensor::from_f32_slice(context, kd, {1, seq, heads, hd}).to_dtype(context, dtype);
+        auto v = Tensor::from_f32_slice(context, vd, {1, seq, heads, hd}).to_dtype(context, dtype);
+        auto k_view = k.permute({0, 2, 1, 3});
+        auto v_view = v.permute({0, 2, 1, 3});
+        CHECK(!k_view.is_contiguous());
+        model::LayerKvCache fused(context, heads, max, hd, dtype);
+        model::LayerKvCache plain(context, heads, max, hd, dtype);
+        for (size_t round = 0; round < 2; ++round) {  // second append at start = 3
+            Execution a(context);
+            fused.append_rotated_encode(context, rope, k_view, v_view);
+            a.finish();
+            Execution b(context);
+            auto k_rot = rope.forward_encode(context, k_view.contiguous_encode(context),
+                                             plain.len());
+            plain.append_encode(context, k_rot, v_view.contiguous_encode(context));
+            b.finish();
+        }
+        CHECK(fused.len() == 2 * seq && plain.len() == 2 * seq);
+        CHECK(fused.key().contiguous(context).to_f32_vec() ==
+              plain.key().contiguous(context).to_f32_vec());
+        CHECK(fused.value().contiguous(context).to_f32_vec() ==
+              plain.value().contiguous(context).to_f32_vec());
+    }
+}
+
+// ---------------------------------------------------- src/ops/embedding.rs
+
+// ops/embedding.rs:119-149: rows of the weight, token ids checked against the vocabulary.
+TEST(embedding_gathers_rows_and_rejects_bad_ids) {
+    const size_t vocab = 5, hidden = 3;
+    std::vector<float> w(vocab * hidden);
+    for (size_t i = 0; i < w.size(); ++i) w[i] = float(i) * 0.5f;
+    auto weight = Buffer::from_slice(context, w);
+    auto out = ops::embedding_f32(context, weight, {4, 0, 4, 2}, vocab, hidden);
+    std::vector<float> expected;
+    for (uint32_t id : {4u, 0u, 4u, 2u})
+        for (size_t h = 0; h < hidden; ++h) expected.push_back(w[id * hidden + h]);
+    CHECK(out.as_slice() == expected);
+    auto weight16 = Buffer::from_f16_slice(context, to_f16(w));
+    auto out16 = ops::embedding_f16(context, weight16, {1, 3}, vocab, hidden);
+    CHECK((out16.as_f16_slice() ==
+           std::vector<uint16_t>{to_f16(w)[3], to_f16(w)[4], to_f16(w)[5], to_f16(w)[9],
+                                 to_f16(w)[10], to_f16(w)[11]}));
+    CHECK(expect_error([&] { ops::embedding_f32(context, weight, {1, 5}, vocab, hidden); }) ==
+          TinyError::Kind::InvalidTokenId);
+    CHECK(expect_error([&] { ops::embedding_f32(context, weight, {}, vocab, hidden); }) ==
+          TinyError::Kind::InvalidShape);
+    CHECK(expect_error([&] { ops::embedding_f32(context, weight, {1}, vocab, hidden + 1); }) ==
+          TinyError::Kind::InvalidShape);
+}
+
 // Submission counters (nn/attention.rs:562-588 style): a batch of encoded
 // ops is one command buffer, one commit and one wait.
 TEST(one_execution_is_one_submission) {

@@ -259,3 +259,83 @@ def test_fastdiv_magic_numbers():
         hi = (nums * np.uint64(magic)) >> np.uint64(32)
         q = (hi + nums) >> np.uint64(s)
         assert np.array_equal(q, nums // np.uint64(d)), d
+
+
+TOKEN = 10  # RL_ERR_INVALID_TOKEN_ID
+
+
+def test_kv_cache_write_validation():
+    # src/ops/kv_cache_write.rs:79-135: dtype, shape, position range, u32 limits
+    f = "rl_kv_cache_write_f16"
+    cache = buf(2 * 8 * 4, 2)  # [1, 2, 8, 4]
+    st, msg = call(f, buf(64, 4), 2, 8, 4, buf(8, 2), 1, 0)
+    assert st == DTYPE and "kv_cache_write_f16 expects F16 cache and source" in msg
+    st, msg = call(f, buf(63, 2), 2, 8, 4, buf(8, 2), 1, 0)
+    assert st == SHAPE and "invalid KV cache write shape" in msg
+    st, msg = call(f, cache, 2, 8, 4, buf(12, 2), 1, 0)  # source is not [1, 2, 1, 4]
+    assert st == SHAPE and "invalid KV cache write shape" in msg
+    st, msg = call(f, cache, 2, 8, 4, buf(0, 2), 0, 0)
+    assert st == SHAPE and "greater than zero" in msg
+    st, msg = call(f, cache, 2, 8, 4, buf(16, 2), 2, 7)
+    assert st == POS and "position range [7, 9) exceeds max sequence length 8" in msg
+    assert call(f, cache, 2, 8, 4, buf(16, 2), 2, 6)[0] == DEVICE
+
+
+def test_kv_cache_write_strided_validation():
+    f = "rl_kv_cache_write_strided_f32"
+    cache = buf(2 * 8 * 4, 4)
+    # [1, 2, 3, 4] permute of a [1, 3, 2, 4] projection: strides [24, 4, 8, 1]
+    dims, strides = u64s(1, 2, 3, 4), u64s(24, 4, 8, 1)
+    st, msg = call(f, buf(24, 4), u64s(2, 3, 4), u64s(12, 4, 1), 3, cache, 8, 0)
+    assert st == SHAPE and "invalid KV cache write shape" in msg
+    st, _ = call(f, buf(48, 4), u64s(2, 1, 3, 4), u64s(24, 24, 8, 1), 4, buf(8 * 4, 4), 8, 0)
+    assert st == SHAPE  # batch 2
+    st, msg = call(f, buf(23, 4), dims, strides, 4, cache, 8, 0)
+    assert st == SHAPE and "past the end" in msg
+    st, _ = call(f, buf(24, 4), dims, strides, 4, cache, 8, 6)
+    assert st == POS
+    assert call(f, buf(24, 4), dims, strides, 4, cache, 8, 5)[0] == DEVICE
+    # any innermost stride is accepted (the gather handles it)
+    assert call(f, buf(24, 4), u64s(1, 2, 3, 4), u64s(24, 1, 2, 6), 4, cache, 8, 0)[0] == DEVICE
+
+
+def test_rope_kv_cache_write_validation():
+    f = "rl_rope_kv_cache_write_f16"
+    tab = buf(8 * 2, 4)  # [8, 2] tables, head_dim 4
+    cache = buf(2 * 8 * 4, 2)
+    dims, strides = u64s(1, 2, 3, 4), u64s(24, 4, 8, 1)
+    # RoPE's checks first ...
+    assert call(f, buf(24, 2), u64s(4), u64s(1), 1, tab, tab, 8, 0, cache, 8)[0] == DIM
+    st, msg = call(f, buf(24, 2), u64s(1, 2, 4, 3), u64s(24, 12, 3, 1), 4, tab, tab, 8, 0,
+                   cache, 8)
+    assert st == SHAPE and "head dimension must be positive and even" in msg
+    st, _ = call(f, buf(24, 2), dims, strides, 4, buf(16, 2), buf(16, 2), 8, 0, cache, 8)
+    assert st == DTYPE
+    st, msg = call(f, buf(24, 2), dims, u64s(24, 1, 2, 6), 4, tab, tab, 8, 0, cache, 8)
+    assert st == NONCONTIG
+    st, msg = call(f, buf(24, 2), dims, strides, 4, tab, tab, 8, 6, cache, 8)
+    assert st == SHAPE and "position range is invalid" in msg  # 6 + 3 > 8 table rows
+    # ... then the cache write's
+    st, msg = call(f, buf(24, 2), dims, strides, 4, tab, tab, 8, 0, buf(2 * 8 * 4, 4), 8)
+    assert st == DTYPE and "kv_cache_write_f16" in msg
+    st, _ = call(f, buf(24, 2), dims, strides, 4, tab, tab, 8, 5, buf(2 * 6 * 4, 2), 6)
+    assert st == POS
+    assert call(f, buf(24, 2), dims, strides, 4, tab, tab, 8, 5, cache, 8)[0] == DEVICE
+
+
+def test_embedding_validation():
+    # src/ops/embedding.rs:119-149, then the u32 limits of :171-183
+    ids = (ctypes.c_uint32 * 3)(0, 5, 9)
+    f = "rl_embedding_f32"
+    st, msg = call(f, buf(40, 4), 10, 4, ids, 0, buf(0, 4))
+    assert st == SHAPE and "at least one token" in msg
+    st, msg = call(f, buf(39, 4), 10, 4, ids, 3, buf(12, 4))
+    assert st == SHAPE and "embedding weight has 39 elements" in msg
+    st, msg = call("rl_embedding_f16", buf(40, 4), 10, 4, ids, 3, buf(12, 2))
+    assert st == SHAPE and "of 2 bytes" in msg
+    bad = (ctypes.c_uint32 * 3)(0, 10, 2)
+    st, msg = call(f, buf(40, 4), 10, 4, bad, 3, buf(12, 4))
+    assert st == TOKEN and "invalid token id 10: vocabulary size is 10" in msg
+    st, msg = call(f, buf(40, 4), 10, 4, ids, 3, buf(11, 4))
+    assert st == SHAPE and "output buffer" in msg
+    assert call(f, buf(40, 4), 10, 4, ids, 3, buf(12, 4))[0] == DEVICE

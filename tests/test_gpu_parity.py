@@ -464,6 +464,105 @@ def test_rope_reference_kats(ctx):
     assert_bitexact(got, o.rope(np.ascontiguousarray(view), c, s, kat["start"]))
 
 
+# ------------------------------------------------------ KV cache, embedding
+
+# (kv_heads, max_seq, head_dim, seq_len, start)
+KV_CASES = [(5, 4096, 64, 4096, 0), (5, 4096, 64, 1, 4095), (5, 4096, 64, 7, 100),
+            (2, 8, 4, 1, 3), (3, 17, 6, 5, 12), (2, 9, 5, 4, 2)]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("heads,max_seq,hd,seq,start", KV_CASES)
+def test_kv_cache_write_bitexact(ctx, dtype, heads, max_seq, hd, seq, start):
+    """ops::kv_cache_write_*: rows start.. of each head are replaced, every
+    other row of the cache keeps its contents."""
+    cache0 = norm(("kvc",), (1, heads, max_seq, hd), dtype)
+    src = norm(("kvs",), (1, heads, seq, hd), dtype)
+    dc = ctx.upload(cache0)
+    run(ctx, lambda: ctx.kv_cache_write(dc, ctx.upload(src), start))
+    assert_bitexact(dc.numpy(), o.kv_cache_write(cache0, src, start), "kv_cache_write")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("heads,max_seq,hd,seq,start", KV_CASES)
+def test_kv_cache_write_from_projection_view(ctx, dtype, heads, max_seq, hd, seq, start):
+    """append_encode's contiguous + kv_cache_write in one pass, from the
+    [1, H, S, D] permute of a [1, S, H, D] projection."""
+    cache0 = norm(("kvc2",), (1, heads, max_seq, hd), dtype)
+    proj = norm(("kvp",), (1, seq, heads, hd), dtype)
+    dims, strides = [1, heads, seq, hd], [seq * heads * hd, hd, heads * hd, 1]
+    dc = ctx.upload(cache0)
+    run(ctx, lambda: ctx.kv_cache_write_strided(ctx.upload(proj), dims, strides, dc, start))
+    ref = o.kv_cache_write(cache0, o.contiguous(proj.ravel(), dims, strides), start)
+    assert_bitexact(dc.numpy(), ref, "strided kv_cache_write")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("heads,max_seq,hd,seq,start",
+                         [c for c in KV_CASES if c[2] % 2 == 0])
+def test_rope_kv_cache_write_bitexact(ctx, dtype, heads, max_seq, hd, seq, start):
+    """RoPE of the key view at positions start.. written straight into the
+    cache equals contiguous -> rope -> kv_cache_write."""
+    c, s = o.rope_table(hd, max_seq, 10000.0)
+    cache0 = norm(("kvc3",), (1, heads, max_seq, hd), dtype)
+    proj = norm(("kvr",), (1, seq, heads, hd), dtype)
+    dims, strides = [1, heads, seq, hd], [seq * heads * hd, hd, heads * hd, 1]
+    dc, dcos, dsin = ctx.upload(cache0), ctx.upload(c), ctx.upload(s)
+    run(ctx, lambda: ctx.rope_kv_cache_write(ctx.upload(proj), dims, strides, dcos, dsin,
+                                             start, dc))
+    rotated = o.rope(o.contiguous(proj.ravel(), dims, strides), c, s, start)
+    assert_bitexact(dc.numpy(), o.kv_cache_write(cache0, rotated, start), "rope+kv write")
+
+
+def test_kv_cache_appends_reference_kat(ctx):
+    """src/model/kv_cache.rs:213-258: two one-token f16 appends into a
+    [1, 2, 8, 4] cache, then the narrowed [1, 2, 2, 4] prefix made
+    contiguous."""
+    kat = K["kv_cache_narrow_contiguous"]
+    _, heads, max_seq, hd = kat["cache_shape"]
+    cache = ctx.upload(np.zeros(kat["cache_shape"], np.float16))
+    ctx.begin()
+    for pos, vals in enumerate(kat["appends"]):
+        key = np.array(vals, np.float16).reshape(kat["append_shape"])
+        ctx.kv_cache_write(cache, ctx.upload(key), pos)
+    n = kat["narrow_len"]
+    got = ctx.contiguous(cache, [1, heads, n, hd], [heads * max_seq * hd, max_seq * hd, hd, 1])
+    ctx.finish()
+    assert got.numpy().astype(np.float32).ravel().tolist() == kat["expected"]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("vocab,hidden,tokens", [(49152, 960, 4096), (1000, 576, 1),
+                                                 (300, 7, 33), (64, 12, 5)])
+def test_embedding_bitexact(ctx, dtype, vocab, hidden, tokens):
+    w = norm(("emb",), (vocab, hidden), dtype)
+    ids = (synth.uniform(synth.seed_for("ids", vocab, tokens), tokens) * vocab).astype(np.uint32)
+    ids[0] = vocab - 1
+    dw = ctx.upload(w)
+    got = run(ctx, lambda: ctx.embedding(dw, ids)).numpy()
+    assert_bitexact(got, o.embedding(w, ids), f"embedding {vocab}x{hidden} [{tokens}]")
+
+
+def test_embedding_staging_reuse(ctx):
+    """Token ids are copied in stream order: several gathers enqueued in one
+    batch, with the host array overwritten between calls and growing past
+    the staging size, each see their own ids."""
+    vocab, hidden = 512, 64
+    w = norm(("emb2",), (vocab, hidden), np.float32)
+    dw = ctx.upload(w)
+    ids = np.zeros(1, np.uint32)
+    outs, expected = [], []
+    ctx.begin()
+    for k, n in enumerate([1, 3, 2000, 5, 9000]):
+        ids = ((np.arange(n, dtype=np.uint64) * 7919 + k) % vocab).astype(np.uint32)
+        outs.append(ctx.embedding(dw, ids))
+        expected.append(w[ids])
+        ids[:] = 0  # the library must not read the host array after the call
+    ctx.finish()
+    for got, ref in zip(outs, expected):
+        assert_bitexact(got.numpy(), ref, "embedding batch")
+
+
 # ------------------------------------------------------- runtime behaviour
 
 def test_one_batch_is_one_submission(ctx):
