@@ -276,35 +276,54 @@ def kernel_times_us(ctx, launches, reps):
     """Device time of `reps` launches (cycling through `launches`, one kernel
     each), every one bracketed by events that the kernel itself stamps at its
     start and end -- the same per-dispatch duration a kernel trace reports.
-    Also returns the whole batch's time per launch (events recorded on the
-    stream before the first and after the last launch; includes the gaps
-    between back-to-back kernels)."""
+    Also returns the time per launch of a batch of back-to-back launches
+    (recorded once as a graph and replayed, so host launch cost is out of
+    it and the gaps between kernels are in), or None for ops that cannot be
+    recorded."""
     for fn in launches:
         fn()
     ctx.finish()
     evs = [(ctx.event(), ctx.event()) for _ in range(reps)]
-    b0, b1 = ctx.event(), ctx.event()
-    ctx.record(b0)
     for i, (start, stop) in enumerate(evs):
         ctx.time_next_kernel(start, stop)
         launches[i % len(launches)]()
-    ctx.record(b1)
     ctx.finish()
     us = [ctx.elapsed_ms(start, stop) * 1e3 for start, stop in evs]
-    batch_us = ctx.elapsed_ms(b0, b1) * 1e3 / reps
-    for e in [b0, b1] + [e for pair in evs for e in pair]:
+    for e in [e for pair in evs for e in pair]:
         ctx.destroy_event(e)
-    return us, batch_us
+    return us, graph_batch_us(ctx, launches)
+
+
+def graph_batch_us(ctx, launches, per_graph=32, replays=8):
+    """us per launch of `per_graph` back-to-back launches replayed as a graph."""
+    ctx.capture_begin()
+    failed = False
+    try:
+        for i in range(per_graph):
+            launches[i % len(launches)]()
+    except abi.RustLLMError:
+        failed = True
+    finally:
+        graph = ctx.capture_end()
+    if failed:
+        ctx.graph_destroy(graph)
+        return None
+    ms = time_graphs(ctx, [graph], per_graph, replays)
+    ctx.finish()
+    ctx.graph_destroy(graph)
+    return ms * 1e3
 
 
 def op_row(name, dtype, shape, nbytes, timing):
     us_list, batch_us = timing
     us = float(np.mean(us_list))
     gbs = nbytes / (us * 1e-6) / 1e9
+    batch = "   n/a" if batch_us is None else f"{batch_us:7.2f}"
     log(f"  {name:34s} {str(shape):20s} {us:9.2f} us {gbs:8.1f} GB/s ({100 * gbs / PEAK_GBS:5.1f}%)"
-        f"  batch {batch_us:7.2f} us/launch")
+        f"  graph batch {batch} us/launch")
     return {"op": name, "dtype": dtype, "shape": shape, "bytes": nbytes, "us": round(us, 3),
-            "us_min": round(float(np.min(us_list)), 3), "us_batch": round(batch_us, 3),
+            "us_min": round(float(np.min(us_list)), 3),
+            "us_graph_batch": None if batch_us is None else round(batch_us, 3),
             "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
 
 
@@ -326,14 +345,15 @@ def extra_rows(ctx, reps, quick):
     method, rotated buffer sets."""
     rows = []
 
-    def measure(name, dtype, shape, nbytes, make_set, launch, nsets):
-        sets = [make_set(i) for i in range(nsets)]
+    def measure(name, dtype, shape, nbytes, make_set, launch):
+        # As many buffer sets as make >= 1 GiB in total (4 .. 256 sets).
+        first = make_set(0)
+        footprint = sum(b.byte_len for b in first)
+        nsets = int(min(256, max(4, -(-(1 << 30) // max(footprint, 1)))))
+        sets = [first] + [make_set(i) for i in range(1, nsets)]
         launches = [lambda s=s: launch(s) for s in sets]
         rows.append(op_row(name, dtype, shape, nbytes, kernel_times_us(ctx, launches, reps)))
-        del sets, launches
-
-    def nsets_for(footprint):
-        return int(min(64, max(4, -(-(1 << 30) // max(footprint, 1)))))
+        del sets, launches, first
 
     tokens_list = [4096, 16384] if quick else [1, 16, 256, 4096, 16384]
     for dt in (F32, F16):
@@ -349,8 +369,7 @@ def extra_rows(ctx, reps, quick):
                 measure(f"rmsnorm_{sfx}", sfx, [tokens, hidden], nbytes,
                         lambda i, x=x, tokens=tokens, hidden=hidden, dt=dt:
                         (ctx.upload(x), ctx.empty((tokens, hidden), dt)),
-                        lambda s, w=w: ctx.rmsnorm(s[0], w, 1e-5, s[1]),
-                        nsets_for(x.nbytes * 2))
+                        lambda s, w=w: ctx.rmsnorm(s[0], w, 1e-5, s[1]))
 
     # attention scores: prefill [9, 2048, 2048] causal, scale 1/8; decode [9, 1, 2048]
     def logits(shape, dt=F32):
@@ -370,12 +389,11 @@ def extra_rows(ctx, reps, quick):
         ("softmax_f32", 2 * n * 4, lambda s: ctx.softmax(s[0], s[1])),
     ]:
         measure(name, "f32", [9, 2048, 2048], nbytes,
-                lambda i: (ctx.upload(pre), ctx.empty(pre.shape, F32)), fn,
-                nsets_for(2 * pre.nbytes))
+                lambda i: (ctx.upload(pre), ctx.empty(pre.shape, F32)), fn)
     dec = logits((9, 1, 2048))
     measure("attention_softmax_f32", "f32", [9, 1, 2048], 2 * dec.size * 4,
             lambda i: (ctx.upload(dec), ctx.empty(dec.shape, F32)),
-            lambda s: ctx.attention_softmax(s[0], 0.125, 2047, s[1]), 16)
+            lambda s: ctx.attention_softmax(s[0], 0.125, 2047, s[1]))
 
     # SmolLM2-360M decoder layer, f16, 4096 tokens
     hid, qh, kvh, hd, ffn, tok = 960, 15, 5, 64, 2560, 4096
@@ -385,7 +403,7 @@ def extra_rows(ctx, reps, quick):
     x = synth.normal(synth.seed_for("c5", "x"), (tok, hid), 0, 1, F16)
     measure("layer.1 rmsnorm_f16", "f16", [tok, hid], tok * hid * 4 + hid * 2,
             lambda i: (ctx.upload(x), ctx.empty((tok, hid), F16)),
-            lambda s: ctx.rmsnorm(s[0], wn, 1e-5, s[1]), 16)
+            lambda s: ctx.rmsnorm(s[0], wn, 1e-5, s[1]))
     for heads, label in ((qh, "Q"), (kvh, "K")):
         proj = synth.normal(synth.seed_for("c5", label), (1, tok, heads, hd), 0, 1, F16)
         dims, strides = [1, heads, tok, hd], [tok * heads * hd, hd, heads * hd, 1]
@@ -393,32 +411,33 @@ def extra_rows(ctx, reps, quick):
         measure(f"layer.2 rope_{label}_f16 (fused gather)", "f16", dims, nbytes,
                 lambda i, proj=proj, dims=dims: (ctx.upload(proj), ctx.empty(dims, F16)),
                 lambda s, dims=dims, strides=strides: ctx.rope_strided(s[0], dims, strides, dc,
-                                                                        ds, 0, s[1]), 16)
+                                                                        ds, 0, s[1]))
         cont = np.ascontiguousarray(proj.transpose(0, 2, 1, 3))
         measure(f"layer.2 rope_{label}_f16", "f16", list(cont.shape), nbytes,
                 lambda i, cont=cont: (ctx.upload(cont), ctx.empty(cont.shape, F16)),
-                lambda s: ctx.rope(s[0], dc, ds, 0, s[1]), 16)
+                lambda s: ctx.rope(s[0], dc, ds, 0, s[1]))
     # K rotated straight into a [1, 5, 4096, 64] cache, V gathered into one
     proj_k = synth.normal(synth.seed_for("c5", "Kc"), (1, tok, kvh, hd), 0, 1, F16)
     kdims, kstrides = [1, kvh, tok, hd], [tok * kvh * hd, hd, kvh * hd, 1]
     measure("layer.2 rope_K_f16 -> KV cache (fused)", "f16", kdims,
             2 * proj_k.size * 2 + 2 * tok * (hd // 2) * 4,
             lambda i: (ctx.upload(proj_k), ctx.empty(kdims, F16)),
-            lambda s: ctx.rope_kv_cache_write(s[0], kdims, kstrides, dc, ds, 0, s[1]), 16)
+            lambda s: ctx.rope_kv_cache_write(s[0], kdims, kstrides, dc, ds, 0, s[1]))
     measure("layer.2 V_f16 -> KV cache (fused gather)", "f16", kdims, 2 * proj_k.size * 2,
             lambda i: (ctx.upload(proj_k), ctx.empty(kdims, F16)),
-            lambda s: ctx.kv_cache_write_strided(s[0], kdims, kstrides, s[1], 0), 16)
+            lambda s: ctx.kv_cache_write_strided(s[0], kdims, kstrides, s[1], 0))
     # token embedding gather: 4096 ids into a [49152, 960] f16 table
+    # (each set has its own 94 MB table, so the gathered rows come from HBM)
     vocab = 49152
-    emb = ctx.upload(synth.normal(synth.seed_for("c5", "emb"), (vocab, hid), 0, 1, F16))
+    emb = synth.normal(synth.seed_for("c5", "emb"), (vocab, hid), 0, 1, F16)
     ids = (synth.uniform(synth.seed_for("c5", "ids"), tok) * vocab).astype(np.uint32)
     measure("layer.0 embedding_f16", "f16", [tok, hid], 2 * tok * hid * 2 + tok * 4,
-            lambda i: (ctx.empty((tok, hid), F16),),
-            lambda s: ctx.embedding(emb, ids, s[0]), 16)
+            lambda i: (ctx.upload(emb), ctx.empty((tok, hid), F16)),
+            lambda s: ctx.embedding(s[0], ids, s[1]))
     kv = synth.normal(synth.seed_for("c5", "kv"), (1, kvh, tok, hd), 0, 1, F16)
     measure("layer.3 repeat_kv_f16", "f16", [1, kvh, tok, hd], (kv.size + 3 * kv.size) * 2,
             lambda i: (ctx.upload(kv), ctx.empty((1, qh, tok, hd), F16)),
-            lambda s: ctx.repeat_kv(s[0], 3, s[1]), 16)
+            lambda s: ctx.repeat_kv(s[0], 3, s[1]))
     if not quick:
         rng = np.random.default_rng(5)
         sc = rng.standard_normal((qh, tok, tok), dtype=np.float32).astype(F16)
@@ -426,17 +445,17 @@ def extra_rows(ctx, reps, quick):
         unm = qh * (tok * (tok + 1) // 2)
         measure("layer.4 attention_softmax_f16", "f16", [qh, tok, tok], unm * 2 + n * 2,
                 lambda i: (ctx.upload(sc), ctx.empty(sc.shape, F16)),
-                lambda s: ctx.attention_softmax(s[0], 0.125, 0, s[1]), 3)
+                lambda s: ctx.attention_softmax(s[0], 0.125, 0, s[1]))
         del sc
     g = synth.normal(synth.seed_for("c5", "g"), (tok, ffn), 0, 1, F16)
     u = synth.normal(synth.seed_for("c5", "u"), (tok, ffn), 0, 1, F16)
     measure("layer.5 swiglu_f16", "f16", [tok, ffn], 3 * g.size * 2,
             lambda i: (ctx.upload(g), ctx.upload(u), ctx.empty(g.shape, F16)),
-            lambda s: ctx.swiglu(s[0], s[1], s[2]), 8)
+            lambda s: ctx.swiglu(s[0], s[1], s[2]))
     r = synth.normal(synth.seed_for("c5", "r"), (tok, hid), 0, 1, F16)
     measure("layer.6 residual add_f16", "f16", [tok, hid], 3 * r.size * 2,
             lambda i: (ctx.upload(x), ctx.upload(r), ctx.empty(r.shape, F16)),
-            lambda s: ctx.add(s[0], s[1], s[2]), 16)
+            lambda s: ctx.add(s[0], s[1], s[2]))
     # [64, 768] f32 (the reference's CPU-runnable case), fused add + RMSNorm
     # (writes the sum and the norm)
     x0 = synth.normal(1, (64, 768), 0, 1, F32)
@@ -444,7 +463,7 @@ def extra_rows(ctx, reps, quick):
     measure("add_rmsnorm_f32", "f32", [64, 768], 64 * 768 * 4 * 4 + 768 * 4,
             lambda i: (ctx.upload(x0), ctx.upload(x0), ctx.empty(x0.shape, F32),
                        ctx.empty(x0.shape, F32)),
-            lambda s: ctx.add_rmsnorm(s[0], s[1], w0, 1e-5, s[2], s[3]), 16)
+            lambda s: ctx.add_rmsnorm(s[0], s[1], w0, 1e-5, s[2], s[3]))
     return rows
 
 
@@ -545,8 +564,22 @@ def probe(ctx, host, ops):
     qo = ctx.empty((1, 15, tok, 64), F16)
     sc = ctx.upload(synth.normal(4, (9, 2048, 2048), 0, 4.0, F32))
     so = ctx.empty((9, 2048, 2048), F32)
+    xl = ctx.upload(synth.normal(5, (16384, hid), 0, 2.0, F16))
+    yl = ctx.empty((16384, hid), F16)
+    kproj = ctx.upload(synth.normal(6, (1, tok, 5, 64), 0, 1, F16))
+    kcache = ctx.empty((1, 5, tok, 64), F16)
+    kdims, kstrides = [1, 5, tok, 64], [tok * 5 * 64, 64, 5 * 64, 1]
+    vocab = 49152
+    emb = ctx.upload(synth.normal(7, (vocab, hid), 0, 1, F16))
+    ids = (synth.uniform(8, tok) * vocab).astype(np.uint32)
     for name, nbytes, fn in [
         ("rmsnorm_f16 [4096,960]", tok * hid * 4 + hid * 2, lambda: ctx.rmsnorm(x, w, 1e-5, y)),
+        ("rmsnorm_f16 [16384,960]", 16384 * hid * 4 + hid * 2,
+         lambda: ctx.rmsnorm(xl, w, 1e-5, yl)),
+        ("rope_K_f16 -> KV cache [1,5,4096,64]", 2 * 5 * tok * 64 * 2 + 2 * tok * 32 * 4,
+         lambda: ctx.rope_kv_cache_write(kproj, kdims, kstrides, dc, ds, 0, kcache)),
+        ("embedding_f16 [4096 of 49152,960]", 2 * tok * hid * 2 + tok * 4,
+         lambda: ctx.embedding(emb, ids, y)),
         ("rope_f16 [1,15,4096,64]", 2 * 15 * tok * 64 * 2 + 2 * tok * 32 * 4,
          lambda: ctx.rope(q, dc, ds, 0, qo)),
         ("attention_softmax_f32 [9,2048,2048]", 9 * (2048 * 2049 // 2) * 4 + 9 * 2048 * 2048 * 4,
