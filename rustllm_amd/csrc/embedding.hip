@@ -2,19 +2,33 @@
 //
 // out[t, :] = weight[ids[t], :] (kernels/embedding.metal:5-54).  The ids
 // are validated on the host against the vocabulary (src/ops/embedding.rs:
-// 119-149), staged to device memory in stream order, and each thread then
-// copies one 16-byte pack of a row: the row's id is read once per pack from
-// L2, the weight row and the output row move as whole packs.
+// 119-149).  Up to 256 of them (decode steps, short prompts) travel in the
+// kernel arguments, so the gather is one launch with no copy and no
+// dependent id load from memory; more are staged to device memory in
+// stream order.  Each thread copies one 16-byte pack of a row; the weight
+// row and the output row move as whole packs.
 #include "common.hpp"
 
 namespace rl {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr uint32_t kInlineIds = 256;
 
-template <typename T, int N, int UNROLL>
-__global__ __launch_bounds__(kThreads) void k_embedding(const T* __restrict__ weight,
-                                                        const uint32_t* __restrict__ ids,
+// Token ids in device memory.
+struct DeviceIds {
+    const uint32_t* p;
+    __device__ uint32_t operator[](uint32_t t) const { return p[t]; }
+};
+
+// Token ids in the kernel arguments.
+struct InlineIds {
+    uint32_t id[kInlineIds];
+    __device__ uint32_t operator[](uint32_t t) const { return id[t]; }
+};
+
+template <typename T, int N, int UNROLL, typename Ids>
+__global__ __launch_bounds__(kThreads) void k_embedding(const T* __restrict__ weight, Ids ids,
                                                         T* __restrict__ out, uint32_t n_items,
                                                         FastDiv packs_per_row) {
     typedef typename VecOf<T, N>::type V;
@@ -49,6 +63,34 @@ inline unsigned grid_for(uint64_t items, uint64_t per_block) {
     return unsigned(blocks);
 }
 
+template <typename T, typename Ids>
+void launch_gather(rl_context* ctx, const T* w, const Ids& ids, T* o, uint64_t hidden_size,
+                   uint64_t out_elements) {
+    constexpr int U = 2;
+    int n = 16 / int(sizeof(T));
+    while (n > 1 && !(hidden_size % n == 0 && aligned_to(w, n * sizeof(T)) &&
+                      aligned_to(o, n * sizeof(T))))
+        n >>= 1;
+    const uint64_t n_items = out_elements / n;
+    const FastDiv ppr(uint32_t(hidden_size / n));
+    const dim3 grid(grid_for(n_items, uint64_t(kThreads) * U)), block(kThreads);
+    const uint32_t ni = uint32_t(n_items);
+    switch (n) {
+        case 8:
+            RL_LAUNCH(ctx, (k_embedding<T, 8, U, Ids>), grid, block, w, ids, o, ni, ppr);
+            break;
+        case 4:
+            RL_LAUNCH(ctx, (k_embedding<T, 4, U, Ids>), grid, block, w, ids, o, ni, ppr);
+            break;
+        case 2:
+            RL_LAUNCH(ctx, (k_embedding<T, 2, U, Ids>), grid, block, w, ids, o, ni, ppr);
+            break;
+        default:
+            RL_LAUNCH(ctx, (k_embedding<T, 1, U, Ids>), grid, block, w, ids, o, ni, ppr);
+            break;
+    }
+}
+
 // src/ops/embedding.rs:119-149 (validate) and :171-183 (u32 limits), in order.
 template <typename T>
 rl_status embedding_entry(rl_context* ctx, const char* name, const rl_buffer* weight,
@@ -80,35 +122,19 @@ rl_status embedding_entry(rl_context* ctx, const char* name, const rl_buffer* we
     if (rl_status st = require_context(ctx)) return st;
     if (rl_status st = activate(ctx)) return st;
 
+    const T* w = static_cast<const T*>(weight->data);
+    T* o = static_cast<T*>(out->data);
+    if (n_tokens <= kInlineIds) {
+        InlineIds ids{};
+        for (uint64_t t = 0; t < n_tokens; ++t) ids.id[t] = token_ids[t];
+        launch_gather<T>(ctx, w, ids, o, hidden_size, out_elements);
+        return after_launch(ctx, name);
+    }
     void* dev_ids = nullptr;
     if (rl_status st = stage_to_device(ctx, token_ids, n_tokens * sizeof(uint32_t), &dev_ids))
         return st;
-    const T* w = static_cast<const T*>(weight->data);
-    T* o = static_cast<T*>(out->data);
-    const uint32_t* ids = static_cast<const uint32_t*>(dev_ids);
-    constexpr int U = 2;
-    int n = 16 / int(sizeof(T));
-    while (n > 1 && !(hidden_size % n == 0 && aligned_to(w, n * sizeof(T)) &&
-                      aligned_to(o, n * sizeof(T))))
-        n >>= 1;
-    const uint64_t n_items = out_elements / n;
-    const FastDiv ppr(uint32_t(hidden_size / n));
-    const dim3 grid(grid_for(n_items, uint64_t(kThreads) * U)), block(kThreads);
-    const uint32_t ni = uint32_t(n_items);
-    switch (n) {
-        case 8:
-            RL_LAUNCH(ctx, (k_embedding<T, 8, U>), grid, block, w, ids, o, ni, ppr);
-            break;
-        case 4:
-            RL_LAUNCH(ctx, (k_embedding<T, 4, U>), grid, block, w, ids, o, ni, ppr);
-            break;
-        case 2:
-            RL_LAUNCH(ctx, (k_embedding<T, 2, U>), grid, block, w, ids, o, ni, ppr);
-            break;
-        default:
-            RL_LAUNCH(ctx, (k_embedding<T, 1, U>), grid, block, w, ids, o, ni, ppr);
-            break;
-    }
+    launch_gather<T>(ctx, w, DeviceIds{static_cast<const uint32_t*>(dev_ids)}, o, hidden_size,
+                     out_elements);
     const rl_status st = after_launch(ctx, name);
     ctx->pool.release(dev_ids);  // stream-ordered: later users run after the gather
     return st;

@@ -54,6 +54,19 @@ __device__ inline bool is_f16() {
     return sizeof(T) == 2;
 }
 
+// exp(d), d = x - max <= 0, for a row of T outputs p = e * (1 / sum), sum >= 1.
+// f32 keeps subnormal e (exp_fast).  For f16 the bare v_exp_f32 suffices:
+// where it flushes (e < 2^-126) p < 2^-126 rounds to 0 in f16 either way and
+// the sum is unchanged; three VALU operations instead of eight matter here,
+// as the f16 rows carry twice the elements per byte.
+template <typename T>
+__device__ inline float exp_row(float d) {
+    if constexpr (sizeof(T) == 2)
+        return __builtin_amdgcn_exp2f(d * 1.44269504088896340736f);
+    else
+        return exp_fast(d);
+}
+
 // Number of unmasked keys of a row: keys 0 ..= start + q are kept.
 __device__ inline uint32_t kept_keys(uint32_t row, uint32_t width, const MaskParams& mp) {
     uint32_t q, qi;
@@ -130,15 +143,21 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
             const uint32_t p = lane + k * TPR;
             if (p < w_packs && p * N < kept) {
                 V raw = load_stream(src + p);
+                if (!MASK || (p + 1) * N <= kept) {  // the whole pack is kept
 #pragma unroll
-                for (int j = 0; j < N; ++j) {
-                    float f;
-                    if constexpr (MASK)
-                        f = (p * N + j < kept) ? scaled_score(raw[j], mp.scale) : -INFINITY;
-                    else
-                        f = to_float(raw[j]);
-                    v[k][j] = f;
-                    m = fmaxf(m, f);
+                    for (int j = 0; j < N; ++j) {
+                        const float f = MASK ? scaled_score(raw[j], mp.scale) : to_float(raw[j]);
+                        v[k][j] = f;
+                        m = fmaxf(m, f);
+                    }
+                } else {  // the pack holding the row's last kept key
+#pragma unroll
+                    for (int j = 0; j < N; ++j) {
+                        const float f =
+                            (p * N + j < kept) ? scaled_score(raw[j], mp.scale) : -INFINITY;
+                        v[k][j] = f;
+                        m = fmaxf(m, f);
+                    }
                 }
             } else {
 #pragma unroll
@@ -155,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
             if (!zero_row && p < w_packs && p * N < kept) {
 #pragma unroll
                 for (int j = 0; j < N; ++j) {
-                    float e = exp_fast(v[k][j] - m);
+                    float e = exp_row<T>(v[k][j] - m);
                     v[k][j] = e;
                     s += e;
                 }

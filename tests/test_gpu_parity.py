@@ -563,6 +563,37 @@ def test_embedding_staging_reuse(ctx):
         assert_bitexact(got.numpy(), ref, "embedding batch")
 
 
+def test_embedding_in_a_graph(ctx):
+    """Up to 256 ids travel in the kernel arguments, so such a gather can be
+    recorded and replayed; more ids would need a host copy, which a graph
+    cannot hold, and are refused while recording."""
+    vocab, hidden = 300, 96
+    w = norm(("emb3",), (vocab, hidden), np.float16)
+    dw = ctx.upload(w)
+    ids = np.array([7, 299, 0, 7, 150], np.uint32)
+    out = ctx.empty((ids.size, hidden), np.float16)
+    ctx.capture_begin()
+    try:
+        ctx.embedding(dw, ids, out)
+    finally:
+        graph = ctx.capture_end()
+    ids[:] = 1  # the recorded launch keeps the ids it was given
+    for _ in range(3):
+        ctx.begin()
+        ctx.graph_launch(graph)
+        ctx.finish()
+        assert_bitexact(out.numpy(), w[[7, 299, 0, 7, 150]], "replayed embedding")
+    ctx.graph_destroy(graph)
+    big = np.zeros(257, np.uint32)
+    big_out = ctx.empty((big.size, hidden), np.float16)
+    ctx.capture_begin()
+    try:
+        with pytest.raises(abi.RustLLMError, match="graph"):
+            ctx.embedding(dw, big, big_out)
+    finally:
+        ctx.graph_destroy(ctx.capture_end())
+
+
 # ------------------------------------------------------- runtime behaviour
 
 def test_one_batch_is_one_submission(ctx):
