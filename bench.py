@@ -321,19 +321,51 @@ def op_row(name, dtype, shape, nbytes, timing):
     batch = "   n/a" if batch_us is None else f"{batch_us:7.2f}"
     log(f"  {name:34s} {str(shape):20s} {us:9.2f} us {gbs:8.1f} GB/s ({100 * gbs / PEAK_GBS:5.1f}%)"
         f"  graph batch {batch} us/launch")
-    return {"op": name, "dtype": dtype, "shape": shape, "bytes": nbytes, "us": round(us, 3),
-            "us_min": round(float(np.min(us_list)), 3),
-            "us_graph_batch": None if batch_us is None else round(batch_us, 3),
-            "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
+    row = {"op": name, "dtype": dtype, "shape": shape, "bytes": nbytes, "us": round(us, 3),
+           "us_min": round(float(np.min(us_list)), 3),
+           "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+           "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None}
+    if batch_us is not None:
+        gb = nbytes / (batch_us * 1e-6) / 1e9
+        row.update({"us_graph_batch": round(batch_us, 3), "GB/s_graph_batch": round(gb, 1),
+                    "pct_peak_graph_batch": round(100 * gb / PEAK_GBS, 1)})
+    return row
+
+
+class _KeyProbe(dict):
+    """A buffer set that records which buffers an op reads or writes."""
+
+    def __init__(self, base):
+        super().__init__(base)
+        self.used = set()
+
+    def __getitem__(self, key):
+        self.used.add(key)
+        return super().__getitem__(key)
+
+
+class _NullContext:
+    """Accepts any op call and does nothing (for _KeyProbe runs)."""
+
+    def __getattr__(self, name):
+        return lambda *args, **kwargs: None
 
 
 def per_op_rows(ctx, ops, sets, reps):
-    """Each op alone, cycling through the buffer sets."""
+    """Each op alone, cycling through copies of its own buffers: as many
+    copies as make >= 1 GiB (4 .. 256), so its reads come from HBM."""
     rows = []
     for op in ops:
-        launches = [lambda s=s, op=op: op.launch(ctx, s) for s in sets]
+        probe = _KeyProbe(sets[0])
+        op.launch(_NullContext(), probe)
+        footprint = sum(sets[0][k].byte_len for k in probe.used)
+        n = int(min(256, max(4, -(-(1 << 30) // footprint))))
+        op_sets = [{k: (s[k] if i < len(sets) else ctx.clone(s[k])) for k in probe.used}
+                   for i, s in ((i, sets[i % len(sets)]) for i in range(n))]
+        launches = [lambda s=s, op=op: op.launch(ctx, s) for s in op_sets]
         rows.append(op_row(op.name, op.dtype, op.shape, op.nbytes,
                            kernel_times_us(ctx, launches, reps)))
+        del launches, op_sets
     return rows
 
 

@@ -244,6 +244,13 @@ class Context:
         check(self.lib.rl_buffer_empty(self.handle, n, dtype.itemsize, ctypes.byref(raw)))
         return DeviceBuffer(self, raw, dtype, shape)
 
+    def clone(self, buf: DeviceBuffer) -> DeviceBuffer:
+        """A new buffer with a stream-ordered device copy of `buf`."""
+        out = self.empty(buf.shape, buf.dtype)
+        check(self.lib.rl_buffer_copy(self.handle, ctypes.byref(buf.raw), ctypes.byref(out.raw),
+                                      buf.byte_len))
+        return out
+
     def upload(self, array) -> DeviceBuffer:
         a = np.ascontiguousarray(array)
         if a.dtype not in _DTYPES and a.dtype != np.uint32:

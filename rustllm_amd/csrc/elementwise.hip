@@ -5,14 +5,13 @@
 // Each thread moves one 16-byte pack per operand (float4 / 8 halves; the
 // casts use 8-element packs when narrowing and 4-element packs when
 // widening, so the wider side is always one contiguous 16-byte access per
-// lane), with a grid-stride loop over packs.  One load or store instruction
-// of a wave covers 1 KiB of contiguous memory.  Loads and stores are
+// lane), 256 threads per block over a full grid.  One load or store
+// instruction of a wave covers 1 KiB of contiguous memory.  Loads are
 // non-temporal: nothing is reused, so the data should not displace L2
-// contents.  A sweep over 1-8 packs per thread, 256-1024 threads per block
-// and persistent grids found one pack per thread with 256 threads and a
-// full grid best on gfx950 (about 71% of peak at 75 MB per launch, 80% at
-// 300 MB), and non-temporal accesses worth about 8 points.  The few
-// elements past the last whole pack are handled by block 0.
+// contents.  Packs per thread and the store kind are set per op (MapShape
+// below); with one pack per thread a 75 MB launch reaches about 71% of peak
+// and a 300 MB one 80%, non-temporal loads being worth about 8 points.  The
+// few elements past the last whole pack are handled by block 0.
 #include "common.hpp"
 
 namespace rl {
@@ -59,8 +58,58 @@ struct CopyOp {  // cast.metal:10,18: the conversion happens on store/load
     __device__ float operator()(float x, float) const { return x; }
 };
 
-// out[i] = op(a[i], b[i]) for ARITY 2, op(a[i]) for ARITY 1.
-template <typename TIn, typename TOut, int N, int UNROLL, int ARITY, typename Op>
+// Launch shape of each op: 16-byte packs per thread and the store kind.
+// Measured on [4096, 1536] ([4096, 2560] for f16 SwiGLU) over 128-1024
+// threads per block x 1, 2, 4 packs per thread x non-temporal / plain
+// stores, two boxes agreeing within 1.5 points: about four loads in flight
+// per thread pays where the math is light (f16 add 62% -> 69% of HBM peak,
+// f16 -> f32 cast 62% -> 71%, f32 SiLU 67% -> 72%), while the exp/rcp-heavy
+// f16 SwiGLU is best at one pack per thread.
+template <typename Op, typename TIn, typename TOut>
+struct MapShape {
+    static constexpr int unroll = 1;
+    static constexpr bool nt_store = true;
+};
+template <typename TIn, typename TOut>
+struct MapShape<AddOp, TIn, TOut> {  // f32: 72% -> 74%, f16: 62% -> 66-69%
+    static constexpr int unroll = sizeof(TIn) == 4 ? 4 : 2;
+    static constexpr bool nt_store = false;
+};
+template <typename TIn, typename TOut>
+struct MapShape<MulOp, TIn, TOut> {
+    static constexpr int unroll = sizeof(TIn) == 4 ? 4 : 2;
+    static constexpr bool nt_store = false;
+};
+template <typename TIn, typename TOut>
+struct MapShape<SwigluF32Op, TIn, TOut> {  // 70% -> 73%
+    static constexpr int unroll = 4;
+    static constexpr bool nt_store = false;
+};
+template <typename TIn, typename TOut>
+struct MapShape<SiluF32Op, TIn, TOut> {
+    static constexpr int unroll = 4;
+    static constexpr bool nt_store = true;
+};
+template <typename TIn, typename TOut>
+struct MapShape<SiluF16Op, TIn, TOut> {
+    static constexpr int unroll = 2;
+    static constexpr bool nt_store = true;
+};
+template <>
+struct MapShape<CopyOp, half_t, float> {  // widening cast: 8-byte loads
+    static constexpr int unroll = 4;
+    static constexpr bool nt_store = true;
+};
+template <>
+struct MapShape<CopyOp, float, half_t> {
+    static constexpr int unroll = 2;
+    static constexpr bool nt_store = false;
+};
+
+// out[i] = op(a[i], b[i]) for ARITY 2, op(a[i]) for ARITY 1.  Block b covers
+// packs [b * 256 * UNROLL, (b + 1) * 256 * UNROLL): the grid spans the whole
+// array (at most 2^32 elements, so at most 2^22 blocks), with no loop.
+template <typename TIn, typename TOut, int N, int UNROLL, int ARITY, bool NTS, typename Op>
 __global__ __launch_bounds__(kThreads) void k_map(const TIn* __restrict__ a,
                                                   const TIn* __restrict__ b,
                                                   TOut* __restrict__ out, uint64_t n_packs,
@@ -70,33 +119,32 @@ __global__ __launch_bounds__(kThreads) void k_map(const TIn* __restrict__ a,
     const VI* va = reinterpret_cast<const VI*>(a);
     const VI* vb = reinterpret_cast<const VI*>(b);
     VO* vo = reinterpret_cast<VO*>(out);
-    const uint64_t tile = uint64_t(kThreads) * UNROLL;
-    const uint64_t step = uint64_t(gridDim.x) * tile;
-    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_packs;
-         base += step) {
-        VI ra[UNROLL], rb[UNROLL];
+    const uint64_t base = uint64_t(blockIdx.x) * kThreads * UNROLL + threadIdx.x;
+    VI ra[UNROLL], rb[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            uint64_t i = base + uint64_t(u) * kThreads;
-            if (i < n_packs) {
-                ra[u] = load_stream(va + i);
-                if constexpr (ARITY == 2) rb[u] = load_stream(vb + i);
-            }
+    for (int u = 0; u < UNROLL; ++u) {
+        const uint64_t i = base + uint64_t(u) * kThreads;
+        if (i < n_packs) {
+            ra[u] = load_stream(va + i);
+            if constexpr (ARITY == 2) rb[u] = load_stream(vb + i);
         }
+    }
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            uint64_t i = base + uint64_t(u) * kThreads;
-            if (i < n_packs) {
-                VO r;
+    for (int u = 0; u < UNROLL; ++u) {
+        const uint64_t i = base + uint64_t(u) * kThreads;
+        if (i < n_packs) {
+            VO r;
 #pragma unroll
-                for (int k = 0; k < N; ++k) {
-                    float x = to_float(ra[u][k]);
-                    float y = 0.0f;
-                    if constexpr (ARITY == 2) y = to_float(rb[u][k]);
-                    r[k] = from_float<TOut>(op(x, y));
-                }
-                store_stream(vo + i, r);
+            for (int k = 0; k < N; ++k) {
+                float x = to_float(ra[u][k]);
+                float y = 0.0f;
+                if constexpr (ARITY == 2) y = to_float(rb[u][k]);
+                r[k] = from_float<TOut>(op(x, y));
             }
+            if constexpr (NTS)
+                store_stream(vo + i, r);
+            else
+                vo[i] = r;
         }
     }
     if (blockIdx.x == 0 && threadIdx.x < tail) {
@@ -175,19 +223,24 @@ rl_status launch_map(rl_context* ctx, const char* name, const void* a, const voi
     // stay 16 B per lane and contiguous across the wave (8-element f32 packs
     // would be two strided 16-byte stores, which costs extra HBM writes).
     constexpr int N = (sizeof(TIn) == 4 && sizeof(TOut) == 4) ? 4 : (sizeof(TOut) == 4 ? 4 : 8);
-    constexpr int UNROLL = 1;
+    constexpr int UNROLL = MapShape<Op, TIn, TOut>::unroll;
+    constexpr bool NTS = MapShape<Op, TIn, TOut>::nt_store;
     const bool vec = aligned_to(a, N * sizeof(TIn)) &&
                      (ARITY < 2 || aligned_to(b, N * sizeof(TIn))) &&
                      aligned_to(out, N * sizeof(TOut));
     const TIn* pa = static_cast<const TIn*>(a);
     const TIn* pb = static_cast<const TIn*>(b);
     TOut* po = static_cast<TOut*>(out);
+    // The kernel has no grid-stride loop: the grid must cover every pack.
+    if (ceil_div(n, uint64_t(kThreads) * UNROLL) > (1u << 30))
+        return fail(RL_ERR_INVALID_SHAPE, "%s: %llu elements exceed one launch", name,
+                    (unsigned long long)n);
     if (vec) {
         uint64_t n_packs = n / N;
         uint32_t tail = uint32_t(n - n_packs * N);
-        RL_LAUNCH(ctx, (k_map<TIn, TOut, N, UNROLL, ARITY, Op>), dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads), pa, pb, po, n_packs, tail, op);
+        RL_LAUNCH(ctx, (k_map<TIn, TOut, N, UNROLL, ARITY, NTS, Op>), dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads), pa, pb, po, n_packs, tail, op);
     } else {
-        RL_LAUNCH(ctx, (k_map<TIn, TOut, 1, UNROLL, ARITY, Op>), dim3(grid_for(n, uint64_t(kThreads) * UNROLL)), dim3(kThreads), pa, pb, po, n, 0u, op);
+        RL_LAUNCH(ctx, (k_map<TIn, TOut, 1, UNROLL, ARITY, NTS, Op>), dim3(grid_for(n, uint64_t(kThreads) * UNROLL)), dim3(kThreads), pa, pb, po, n, 0u, op);
     }
     return after_launch(ctx, name);
 }
@@ -200,7 +253,9 @@ rl_status launch_add_broadcast(rl_context* ctx, const char* name, const rl_buffe
     if (n == 0) return RL_OK;
     if (rl_status st = activate(ctx)) return st;
     constexpr int N = 16 / sizeof(T);
-    constexpr int UNROLL = 1;
+    // Four packs per thread: f32 65% -> 69%, f16 53% -> 56% of peak on
+    // [4096, 1536] (same sweep as MapShape).
+    constexpr int UNROLL = 4;
     const T* px = static_cast<const T*>(x->data);
     const T* pbias = static_cast<const T*>(bias->data);
     T* po = static_cast<T*>(out->data);
