@@ -291,7 +291,15 @@ def kernel_times_us(ctx, launches, reps):
     us = [ctx.elapsed_ms(start, stop) * 1e3 for start, stop in evs]
     for e in [e for pair in evs for e in pair]:
         ctx.destroy_event(e)
-    return us, graph_batch_us(ctx, launches)
+    return us, (graph_batch_us(ctx, launches) if GRAPH_BATCH else None)
+
+
+# --graph-batch: also time each op as 32 back-to-back launches recorded in a
+# graph.  Off by default: under `rocprofv3 --kernel-trace` the replay of
+# these short-lived graphs crashed the traced process inside hipGraphLaunch
+# (a host read of a device-memory address in the tracer's launch hook),
+# while the long-lived step graphs trace cleanly.
+GRAPH_BATCH = False
 
 
 def graph_batch_us(ctx, launches, per_graph=32, replays=8):
@@ -670,10 +678,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
     ap.add_argument("--quick", action="store_true", help="fewer extra shapes")
+    ap.add_argument("--graph-batch", action="store_true",
+                    help="also time every op as back-to-back launches replayed from a graph")
     ap.add_argument("--probe", action="store_true",
                     help="no timing: run each batch op 3 times on one buffer set, then a "
                          "256 MiB device-to-device copy 3 times (for hardware-counter runs)")
     args = ap.parse_args()
+    global GRAPH_BATCH
+    GRAPH_BATCH = args.graph_batch
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every op runs on one MI355X and shards across GPUs "

@@ -179,7 +179,10 @@ rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* 
         }
         const uint64_t n_packs = numel / n;
         const FastDiv row_packs(uint32_t(inner / n));
-        constexpr int U = 4;
+        // Two packs per thread: on the [1, 4096, H, 64] -> [1, H, 4096, 64]
+        // transpose (9.4-18.9 MB) back-to-back launches take 10-15% less
+        // time than with four (fewer, longer waves) and match one.
+        constexpr int U = 2;
         const dim3 grid(grid_for(n_packs, uint64_t(kThreads) * U)), block(kThreads);
         switch (n) {
             case 8:
