@@ -466,6 +466,16 @@ def extra_rows(ctx, reps, quick):
     measure("layer.2 V_f16 -> KV cache (fused gather)", "f16", kdims, 2 * proj_k.size * 2,
             lambda i: (ctx.upload(proj_k), ctx.empty(kdims, F16)),
             lambda s: ctx.kv_cache_write_strided(s[0], kdims, kstrides, s[1], 0))
+    # Q and K rotated, K and V appended, as one launch
+    proj_q = synth.normal(synth.seed_for("c5", "Qc"), (1, tok, qh, hd), 0, 1, F16)
+    qdims, qstrides = [1, qh, tok, hd], [tok * qh * hd, hd, qh * hd, 1]
+    measure("layer.2 QKV rotate + KV append (one launch)", "f16", [1, qh + 2 * kvh, tok, hd],
+            2 * (proj_q.size + 2 * proj_k.size) * 2 + 2 * tok * (hd // 2) * 4,
+            lambda i: (ctx.upload(proj_q), ctx.upload(proj_k), ctx.upload(proj_k),
+                       ctx.empty(qdims, F16), ctx.empty(kdims, F16), ctx.empty(kdims, F16)),
+            lambda s: ctx.qkv_rope_kv_append((s[0], qdims, qstrides), (s[1], kdims, kstrides),
+                                             (s[2], kdims, kstrides), dc, ds, 0, s[4], s[5],
+                                             s[3]))
     # token embedding gather: 4096 ids into a [49152, 960] f16 table
     # (each set has its own 94 MB table, so the gathered rows come from HBM)
     vocab = 49152

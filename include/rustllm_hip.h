@@ -332,6 +332,36 @@ rl_status rl_rope_kv_cache_write_f16(rl_context* ctx, const rl_buffer* src, cons
                                      uint64_t table_rows, uint64_t start_pos,
                                      const rl_buffer* cache, uint64_t max_seq);
 
+/* The non-GEMM part of the attention's projection step as one launch:
+ * RotaryEmbedding::forward_encode of Q and of K at start_pos
+ * (src/nn/attention.rs:202-207) and LayerKvCache::append_encode of K and V at
+ * the same position (src/model/kv_cache.rs:112-142, called with
+ * cache.len() == start_pos at src/nn/attention.rs:304-307).  q/k/v are rank-4
+ * [1, H, S, D] views with unit innermost strides (the permutes of the
+ * [1, S, H*D] projections); Q (QH heads) is written rotated to the contiguous
+ * q_out, K rotated and V as is to rows start_pos .. start_pos + S of the
+ * [1, KVH, max_seq, D] caches.  Checks in the reference's order (RoPE on Q,
+ * RoPE on K, the append's K/V shape check as RL_ERR_MODEL_FORMAT, the two
+ * cache writes). */
+rl_status rl_qkv_rope_kv_append_f32(rl_context* ctx, const rl_buffer* q_src,
+                                    const uint64_t* q_dims, const uint64_t* q_strides,
+                                    const rl_buffer* k_src, const uint64_t* k_dims,
+                                    const uint64_t* k_strides, const rl_buffer* v_src,
+                                    const uint64_t* v_dims, const uint64_t* v_strides,
+                                    const rl_buffer* cos_table, const rl_buffer* sin_table,
+                                    uint64_t table_rows, uint64_t start_pos,
+                                    const rl_buffer* q_out, const rl_buffer* k_cache,
+                                    const rl_buffer* v_cache, uint64_t max_seq);
+rl_status rl_qkv_rope_kv_append_f16(rl_context* ctx, const rl_buffer* q_src,
+                                    const uint64_t* q_dims, const uint64_t* q_strides,
+                                    const rl_buffer* k_src, const uint64_t* k_dims,
+                                    const uint64_t* k_strides, const rl_buffer* v_src,
+                                    const uint64_t* v_dims, const uint64_t* v_strides,
+                                    const rl_buffer* cos_table, const rl_buffer* sin_table,
+                                    uint64_t table_rows, uint64_t start_pos,
+                                    const rl_buffer* q_out, const rl_buffer* k_cache,
+                                    const rl_buffer* v_cache, uint64_t max_seq);
+
 /* ============================================================= embedding */
 /* ops::embedding_f32_encode (src/ops/embedding.rs:32-57,119-193):
  * out[t, :] = weight[token_ids[t], :] for a [vocab_size, hidden_size] weight.

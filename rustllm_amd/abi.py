@@ -131,6 +131,10 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                                     _U64], _I32),
     "rl_rope_kv_cache_write_f16": ([_P, _BUF, _U64P, _U64P, _U32, _BUF, _BUF, _U64, _U64, _BUF,
                                     _U64], _I32),
+    "rl_qkv_rope_kv_append_f32": ([_P, _BUF, _U64P, _U64P, _BUF, _U64P, _U64P, _BUF, _U64P,
+                                   _U64P, _BUF, _BUF, _U64, _U64, _BUF, _BUF, _BUF, _U64], _I32),
+    "rl_qkv_rope_kv_append_f16": ([_P, _BUF, _U64P, _U64P, _BUF, _U64P, _U64P, _BUF, _U64P,
+                                   _U64P, _BUF, _BUF, _U64, _U64, _BUF, _BUF, _BUF, _U64], _I32),
     "rl_embedding_f32": ([_P, _BUF, _U64, _U64, ctypes.POINTER(ctypes.c_uint32), _U64, _BUF],
                          _I32),
     "rl_embedding_f16": ([_P, _BUF, _U64, _U64, ctypes.POINTER(ctypes.c_uint32), _U64, _BUF],
@@ -439,6 +443,16 @@ class Context:
         d, s = _u64_array(dims), _u64_array(strides)
         self._call(f"rl_rope_kv_cache_write_{self._sfx(cache)}", src, d, s, len(dims), cos, sin,
                    cos.shape[0], start, cache, cache.shape[2])
+
+    def qkv_rope_kv_append(self, q, k, v, cos, sin, start: int, k_cache, v_cache, q_out=None):
+        """q/k/v: (buffer, dims, strides) of [1, H, S, D] views.  Returns the
+        rotated contiguous Q; K (rotated) and V land in the caches at start."""
+        (qb, qd, qs), (kb, kd, ks), (vb, vd, vs) = q, k, v
+        q_out = q_out or self.empty(qd, qb.dtype)
+        self._call(f"rl_qkv_rope_kv_append_{self._sfx(qb)}", qb, _u64_array(qd), _u64_array(qs),
+                   kb, _u64_array(kd), _u64_array(ks), vb, _u64_array(vd), _u64_array(vs), cos,
+                   sin, cos.shape[0], start, q_out, k_cache, v_cache, k_cache.shape[2])
+        return q_out
 
     def embedding(self, weight, token_ids, out=None):
         ids = np.ascontiguousarray(token_ids, dtype=np.uint32)

@@ -310,12 +310,268 @@ rl_status rope_kv_entry(rl_context* ctx, const char* name, const char* write_nam
                           DstRows{uint32_t(max_seq), uint32_t(start)});
 }
 
+// ------------------------------------------- Q, K and V of a layer, one launch
+
+// One [1, H, S, D] view moved to its destination rows, rotated or copied.
+struct RowTask {
+    const void* src;
+    void* dst;
+    RowDims rd;
+    FastDiv packs_per_row;  // packs of pairs per row (half_dim / N)
+    DstRows dst_rows;
+    uint32_t n_items;       // rows * packs_per_row
+    uint32_t first_block;   // blocks [first_block, next task's first_block)
+    uint32_t rotate;
+};
+
+struct RowTasks {
+    RowTask task[3];
+};
+
+// Blocks are split between the three tasks; each block serves one task
+// (a uniform branch), each thread UNROLL packs of pairs of it.
+template <typename T, int N, int UNROLL>
+__global__ __launch_bounds__(kThreads) void k_rope_tasks(RowTasks tasks,
+                                                         const float* __restrict__ cos_table,
+                                                         const float* __restrict__ sin_table,
+                                                         uint32_t half_dim, uint32_t start) {
+    typedef typename VecOf<T, N>::type V;
+    typedef typename VecOf<float, N>::type VF;
+    const uint32_t k = (blockIdx.x >= tasks.task[1].first_block ? 1u : 0u) +
+                       (blockIdx.x >= tasks.task[2].first_block ? 1u : 0u);
+    const RowTask& task = tasks.task[k];
+    const T* src = static_cast<const T*>(task.src);
+    T* out = static_cast<T*>(task.dst);
+    const uint64_t base =
+        uint64_t(blockIdx.x - task.first_block) * kThreads * UNROLL + threadIdx.x;
+    V a[UNROLL], b[UNROLL];
+    VF c[UNROLL], s[UNROLL];
+    uint64_t dst_off[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+        const uint64_t i = base + uint64_t(u) * kThreads;
+        if (i < task.n_items) {
+            uint32_t row, pp;
+            task.packs_per_row.divmod(uint32_t(i), row, pp);
+            uint64_t src_off = 0;
+            uint32_t position = 0, group = 0;
+            uint32_t rest = row;
+            for (uint32_t d = 0; d < task.rd.rank; ++d) {
+                uint32_t q, r;
+                task.rd.dim[d].divmod(rest, q, r);
+                if (d == 0) {
+                    position = r;
+                    group = q;
+                }
+                src_off += uint64_t(r) * task.rd.stride[d];
+                rest = q;
+            }
+            const uint32_t pair = pp * N;
+            a[u] = *reinterpret_cast<const V*>(src + src_off + pair);
+            b[u] = *reinterpret_cast<const V*>(src + src_off + half_dim + pair);
+            if (task.rotate) {
+                const uint64_t t = uint64_t(start + position) * half_dim + pair;
+                c[u] = *reinterpret_cast<const VF*>(cos_table + t);
+                s[u] = *reinterpret_cast<const VF*>(sin_table + t);
+            }
+            const uint64_t dst_row =
+                uint64_t(group) * task.dst_rows.group_rows + task.dst_rows.first_row + position;
+            dst_off[u] = dst_row * (2 * half_dim) + pair;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+        const uint64_t i = base + uint64_t(u) * kThreads;
+        if (i < task.n_items) {
+            V o1 = a[u], o2 = b[u];
+            if (task.rotate) {
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    const float first = to_float(a[u][j]);
+                    const float second = to_float(b[u][j]);
+                    o1[j] = from_float<T>(first * c[u][j] - second * s[u][j]);
+                    o2[j] = from_float<T>(second * c[u][j] + first * s[u][j]);
+                }
+            }
+            store_stream(reinterpret_cast<V*>(out + dst_off[u]), o1);
+            store_stream(reinterpret_cast<V*>(out + dst_off[u] + half_dim), o2);
+        }
+    }
+}
+
+// A view's checks as an input of this launch: rank 4 [1, H, S, D] with a
+// unit innermost stride, within its buffer, u32 sizes.
+rl_status check_head_view(const rl_buffer* src, const uint64_t* dims, const uint64_t* strides,
+                          uint64_t es, const char* what) {
+    if (rl_status st = check_buffer(src, what)) return st;
+    if (dims == nullptr || strides == nullptr)
+        return fail(RL_ERR_INVALID_ARGUMENT, "%s dims or strides is null", what);
+    uint64_t numel = 1;
+    for (uint32_t d = 0; d < 4; ++d) {
+        if (dims[d] == 0)
+            return fail(RL_ERR_INVALID_SHAPE, "shape dimensions must be greater than zero");
+        if (dims[d] > UINT32_MAX || strides[d] > UINT32_MAX || numel > UINT64_MAX / dims[d])
+            return fail(RL_ERR_INVALID_SHAPE, "shape dimension exceeds u32");
+        numel *= dims[d];
+    }
+    if (numel > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "%s size exceeds u32", what);
+    if (strides[3] != 1)
+        return fail(RL_ERR_NON_CONTIGUOUS, "%s view must have a unit innermost stride", what);
+    if (src->byte_len < src->len * es)
+        return fail(RL_ERR_INVALID_SHAPE, "%s does not hold %llu-byte elements", what,
+                    (unsigned long long)es);
+    unsigned __int128 last = 0;
+    for (uint32_t d = 0; d < 4; ++d) last += (unsigned __int128)(dims[d] - 1) * strides[d];
+    if (last >= src->len)
+        return fail(RL_ERR_INVALID_SHAPE, "%s view reaches past the end of its %llu-element buffer",
+                    what, (unsigned long long)src->len);
+    return RL_OK;
+}
+
+// RotaryEmbedding::forward_encode of Q and of K at start_pos
+// (src/nn/attention.rs:202-207), then LayerKvCache::append_encode of K and V
+// at the same position (src/model/kv_cache.rs:112-142; the attention calls it
+// with cache.len() == start_pos, :304-307), as one launch: Q rotated into a
+// contiguous [1, QH, S, D] output, K rotated and V copied into rows start ..
+// start + S of their caches.  Checks in the reference's order: RoPE on Q,
+// RoPE on K, the append's shape check (ModelFormat), the two cache writes.
+template <typename T>
+rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
+                    const uint64_t* q_dims, const uint64_t* q_strides, const rl_buffer* k_src,
+                    const uint64_t* k_dims, const uint64_t* k_strides, const rl_buffer* v_src,
+                    const uint64_t* v_dims, const uint64_t* v_strides,
+                    const rl_buffer* cos_table, const rl_buffer* sin_table, uint64_t table_rows,
+                    uint64_t start, const rl_buffer* q_out, const rl_buffer* k_cache,
+                    const rl_buffer* v_cache, uint64_t max_seq) {
+    const char* write_name = sizeof(T) == 4 ? "kv_cache_write_f32" : "kv_cache_write_f16";
+    for (int v = 0; v < 2; ++v) {  // Q, then K: RotaryEmbedding::forward_encode
+        const rl_buffer* src = v == 0 ? q_src : k_src;
+        const uint64_t* dims = v == 0 ? q_dims : k_dims;
+        const uint64_t* strides = v == 0 ? q_strides : k_strides;
+        if (rl_status st = check_head_view(src, dims, strides, sizeof(T), v == 0 ? "Q" : "K"))
+            return st;
+        const uint64_t head_dim = dims[3];
+        if (head_dim % 2 != 0)
+            return fail(RL_ERR_INVALID_SHAPE,
+                        "RoPE head dimension must be positive and even, got %llu",
+                        (unsigned long long)head_dim);
+        if (rl_status st = check_tables(cos_table, sin_table, table_rows, head_dim / 2, start,
+                                        dims[2]))
+            return st;
+    }
+    if (rl_status st = check_output(q_out, q_dims[0] * q_dims[1] * q_dims[2] * q_dims[3],
+                                    sizeof(T), "RoPE"))
+        return st;
+    if (rl_status st = check_head_view(v_src, v_dims, v_strides, sizeof(T), "V")) return st;
+    // LayerKvCache::validate_append (kv_cache.rs:31-40): K and V of one shape.
+    for (uint32_t d = 0; d < 4; ++d)
+        if (k_dims[d] != v_dims[d])
+            return fail(RL_ERR_MODEL_FORMAT,
+                        "KV cache write shape does not match this layer: key and value differ");
+    // Q and K of one layout apart from the head count (one sequence, one head_dim).
+    if (q_dims[0] != k_dims[0] || q_dims[2] != k_dims[2] || q_dims[3] != k_dims[3])
+        return fail(RL_ERR_INVALID_SHAPE, "Q and K must share batch, sequence and head_dim");
+    if (rl_status st = validate_kv_write(write_name, k_cache, max_seq, k_src, k_dims, k_strides,
+                                         4, start, sizeof(T), false))
+        return st;
+    if (rl_status st = validate_kv_write(write_name, v_cache, max_seq, v_src, v_dims, v_strides,
+                                         4, start, sizeof(T), false))
+        return st;
+    if (rl_status st = require_context(ctx)) return st;
+    if (rl_status st = activate(ctx)) return st;
+
+    const uint64_t half = q_dims[3] / 2;
+    const float* cs = static_cast<const float*>(cos_table->data);
+    const float* sn = static_cast<const float*>(sin_table->data);
+    const void* srcs[3] = {q_src->data, k_src->data, v_src->data};
+    void* dsts[3] = {q_out->data, k_cache->data, v_cache->data};
+    const uint64_t* dims[3] = {q_dims, k_dims, v_dims};
+    const uint64_t* strides[3] = {q_strides, k_strides, v_strides};
+    int n = 16 / int(sizeof(T));
+    while (n > 1) {
+        bool ok = half % n == 0 && aligned_to(cs, n * 4) && aligned_to(sn, n * 4);
+        for (int t = 0; t < 3 && ok; ++t) {
+            ok = aligned_to(srcs[t], n * sizeof(T)) && aligned_to(dsts[t], n * sizeof(T));
+            for (uint32_t d = 0; d < 3 && ok; ++d) ok = strides[t][d] % n == 0;
+        }
+        if (ok) break;
+        n >>= 1;
+    }
+    constexpr int U = 2;
+    RowTasks tasks{};
+    uint64_t blocks = 0;
+    for (int t = 0; t < 3; ++t) {
+        RowTask& task = tasks.task[t];
+        task.src = srcs[t];
+        task.dst = dsts[t];
+        task.rd.rank = 3;
+        for (uint32_t d = 0; d < 3; ++d) {
+            task.rd.dim[d] = FastDiv(uint32_t(dims[t][2 - d]));
+            task.rd.stride[d] = strides[t][2 - d];
+        }
+        task.packs_per_row = FastDiv(uint32_t(half / n));
+        task.dst_rows = t == 0 ? DstRows{uint32_t(dims[t][2]), 0}
+                               : DstRows{uint32_t(max_seq), uint32_t(start)};
+        const uint64_t rows = dims[t][0] * dims[t][1] * dims[t][2];
+        task.n_items = uint32_t(rows * (half / n));
+        task.first_block = uint32_t(blocks);
+        task.rotate = t < 2 ? 1u : 0u;
+        blocks += ceil_div(task.n_items, uint64_t(kThreads) * U);
+    }
+    if (blocks > (1u << 30)) return fail(RL_ERR_INVALID_SHAPE, "%s: work exceeds one launch", name);
+    const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+    const uint32_t h32 = uint32_t(half), s32 = uint32_t(start);
+    switch (n) {
+        case 8:
+            RL_LAUNCH(ctx, (k_rope_tasks<T, 8, U>), grid, block, tasks, cs, sn, h32, s32);
+            break;
+        case 4:
+            RL_LAUNCH(ctx, (k_rope_tasks<T, 4, U>), grid, block, tasks, cs, sn, h32, s32);
+            break;
+        case 2:
+            RL_LAUNCH(ctx, (k_rope_tasks<T, 2, U>), grid, block, tasks, cs, sn, h32, s32);
+            break;
+        default:
+            RL_LAUNCH(ctx, (k_rope_tasks<T, 1, U>), grid, block, tasks, cs, sn, h32, s32);
+            break;
+    }
+    return after_launch(ctx, name);
+}
+
 }  // namespace
 }  // namespace rl
 
 using namespace rl;
 
 extern "C" {
+
+rl_status rl_qkv_rope_kv_append_f32(rl_context* ctx, const rl_buffer* q_src,
+                                    const uint64_t* q_dims, const uint64_t* q_strides,
+                                    const rl_buffer* k_src, const uint64_t* k_dims,
+                                    const uint64_t* k_strides, const rl_buffer* v_src,
+                                    const uint64_t* v_dims, const uint64_t* v_strides,
+                                    const rl_buffer* cos_table, const rl_buffer* sin_table,
+                                    uint64_t table_rows, uint64_t start_pos,
+                                    const rl_buffer* q_out, const rl_buffer* k_cache,
+                                    const rl_buffer* v_cache, uint64_t max_seq) {
+    return qkv_entry<float>(ctx, "qkv_rope_kv_append_f32", q_src, q_dims, q_strides, k_src,
+                            k_dims, k_strides, v_src, v_dims, v_strides, cos_table, sin_table,
+                            table_rows, start_pos, q_out, k_cache, v_cache, max_seq);
+}
+
+rl_status rl_qkv_rope_kv_append_f16(rl_context* ctx, const rl_buffer* q_src,
+                                    const uint64_t* q_dims, const uint64_t* q_strides,
+                                    const rl_buffer* k_src, const uint64_t* k_dims,
+                                    const uint64_t* k_strides, const rl_buffer* v_src,
+                                    const uint64_t* v_dims, const uint64_t* v_strides,
+                                    const rl_buffer* cos_table, const rl_buffer* sin_table,
+                                    uint64_t table_rows, uint64_t start_pos,
+                                    const rl_buffer* q_out, const rl_buffer* k_cache,
+                                    const rl_buffer* v_cache, uint64_t max_seq) {
+    return qkv_entry<half_t>(ctx, "qkv_rope_kv_append_f16", q_src, q_dims, q_strides, k_src,
+                             k_dims, k_strides, v_src, v_dims, v_strides, cos_table, sin_table,
+                             table_rows, start_pos, q_out, k_cache, v_cache, max_seq);
+}
 
 rl_status rl_rope_kv_cache_write_f32(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,
                                      const uint64_t* strides, uint32_t rank,

@@ -339,3 +339,37 @@ def test_embedding_validation():
     st, msg = call(f, buf(40, 4), 10, 4, ids, 3, buf(11, 4))
     assert st == SHAPE and "output buffer" in msg
     assert call(f, buf(40, 4), 10, 4, ids, 3, buf(12, 4))[0] == DEVICE
+
+
+def test_qkv_rope_kv_append_validation():
+    f = "rl_qkv_rope_kv_append_f16"
+    tab = buf(8 * 2, 4)  # [8, 2] tables, head_dim 4
+    # Q: [1, 3, 2, 4] permute of [1, 2, 3, 4]; K, V: [1, 1, 2, 4] permutes of [1, 2, 1, 4]
+    qd, qs = u64s(1, 3, 2, 4), u64s(24, 4, 12, 1)
+    kd, ks = u64s(1, 1, 2, 4), u64s(8, 4, 4, 1)
+    kc, vc = buf(1 * 8 * 4, 2), buf(1 * 8 * 4, 2)
+
+    def go(q=None, k=None, v=None, start=0, tables=(tab, tab), q_out=None, kcache=None,
+           vcache=None, max_seq=8):
+        qb, qdd, qss = q or (buf(24, 2), qd, qs)
+        kb, kdd, kss = k or (buf(8, 2), kd, ks)
+        vb, vdd, vss = v or (buf(8, 2), kd, ks)
+        return call(f, qb, qdd, qss, kb, kdd, kss, vb, vdd, vss, tables[0], tables[1], 8, start,
+                    q_out or buf(24, 2), kcache or kc, vcache or vc, max_seq)
+
+    assert go()[0] == DEVICE
+    st, msg = go(q=(buf(24, 2), u64s(1, 3, 2, 4), u64s(24, 4, 12, 2)))
+    assert st == NONCONTIG and "Q view" in msg
+    st, msg = go(k=(buf(6, 2), u64s(1, 1, 2, 3), u64s(6, 3, 3, 1)))
+    assert st == SHAPE and "head dimension" in msg
+    assert go(tables=(buf(16, 2), buf(16, 2)))[0] == DTYPE
+    st, msg = go(start=7)  # 7 + 2 > 8 table rows
+    assert st == SHAPE and "position range is invalid" in msg
+    st, _ = go(q_out=buf(23, 2))
+    assert st == SHAPE
+    st, msg = go(v=(buf(16, 2), u64s(1, 2, 2, 4), u64s(16, 8, 4, 1)))
+    assert st == FORMAT and "key and value differ" in msg
+    st, msg = go(kcache=buf(32, 4))
+    assert st == DTYPE and "kv_cache_write_f16" in msg
+    st, _ = go(start=5, max_seq=6, kcache=buf(24, 2), vcache=buf(24, 2))
+    assert st == POS

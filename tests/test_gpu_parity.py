@@ -514,6 +514,39 @@ def test_rope_kv_cache_write_bitexact(ctx, dtype, heads, max_seq, hd, seq, start
     assert_bitexact(dc.numpy(), o.kv_cache_write(cache0, rotated, start), "rope+kv write")
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("qh,kvh,seq,hd,start,max_seq", [(15, 5, 4096, 64, 0, 4096),
+                                                         (15, 5, 1, 64, 100, 4096),
+                                                         (4, 2, 7, 6, 3, 12),
+                                                         (2, 2, 5, 2, 0, 5)])
+def test_qkv_rope_kv_append_one_launch(ctx, dtype, qh, kvh, seq, hd, start, max_seq):
+    """Q and K rotated, K and V appended to the caches, in one launch, equals
+    contiguous -> rope (Q, K) and contiguous -> kv_cache_write (K, V)."""
+    c, s = o.rope_table(hd, max_seq, 10000.0)
+    qp = norm(("qkv", "q"), (1, seq, qh, hd), dtype)
+    kp = norm(("qkv", "k"), (1, seq, kvh, hd), dtype)
+    vp = norm(("qkv", "v"), (1, seq, kvh, hd), dtype)
+    kc0 = norm(("qkv", "kc"), (1, kvh, max_seq, hd), dtype)
+    vc0 = norm(("qkv", "vc"), (1, kvh, max_seq, hd), dtype)
+
+    def view(h):
+        return [1, h, seq, hd], [seq * h * hd, hd, h * hd, 1]
+
+    qd, qs = view(qh)
+    kd, ks = view(kvh)
+    dkc, dvc = ctx.upload(kc0), ctx.upload(vc0)
+    dcos, dsin = ctx.upload(c), ctx.upload(s)
+    q_out = run(ctx, lambda: ctx.qkv_rope_kv_append(
+        (ctx.upload(qp), qd, qs), (ctx.upload(kp), kd, ks), (ctx.upload(vp), kd, ks),
+        dcos, dsin, start, dkc, dvc)).numpy()
+    q_ref = o.rope(o.contiguous(qp.ravel(), qd, qs), c, s, start)
+    k_ref = o.kv_cache_write(kc0, o.rope(o.contiguous(kp.ravel(), kd, ks), c, s, start), start)
+    v_ref = o.kv_cache_write(vc0, o.contiguous(vp.ravel(), kd, ks), start)
+    assert_bitexact(q_out, q_ref, "Q")
+    assert_bitexact(dkc.numpy(), k_ref, "K cache")
+    assert_bitexact(dvc.numpy(), v_ref, "V cache")
+
+
 def test_kv_cache_appends_reference_kat(ctx):
     """src/model/kv_cache.rs:213-258: two one-token f16 appends into a
     [1, 2, 8, 4] cache, then the narrowed [1, 2, 2, 4] prefix made
