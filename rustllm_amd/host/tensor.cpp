@@ -1306,5 +1306,49 @@ void LayerKvCache::append_rotated_encode(const Context& ctx, const nn::RotaryEmb
     append_encode(ctx, rope.forward_encode(ctx, key, len_), value);
 }
 
+Tensor LayerKvCache::rotate_query_and_append_encode(const Context& ctx,
+                                                    const nn::RotaryEmbedding& rope,
+                                                    const Tensor& query, const Tensor& key,
+                                                    const Tensor& value) {
+    auto fusable = [&](const Tensor& t) {
+        return t.rank() == 4 && t.strides().values().back() == 1 && t.dtype() == key_.dtype();
+    };
+    if (!(fusable(query) && fusable(key) && fusable(value) && query.dim(2) == key.dim(2))) {
+        Tensor q = rope.forward_encode(ctx, query, len_);  // the unfused order and errors
+        append_rotated_encode(ctx, rope, key, value);
+        return q;
+    }
+    ops::validate_rope(query, rope.cos_table(), rope.sin_table(), len_);
+    ops::validate_rope(key, rope.cos_table(), rope.sin_table(), len_);
+    validate_append(key, value);
+    const size_t start = len_, seq = key.dim(2);
+    auto dims = [](const Tensor& t) {
+        return std::vector<uint64_t>(t.shape().dims().begin(), t.shape().dims().end());
+    };
+    auto strides = [](const Tensor& t) {
+        return std::vector<uint64_t>(t.strides().values().begin(), t.strides().values().end());
+    };
+    const auto qd = dims(query), kd = dims(key), vd = dims(value);
+    const auto qs = strides(query), ks = strides(key), vs = strides(value);
+    Buffer out = Buffer::empty_with_element_size(ctx, query.numel(), size_in_bytes(key_.dtype()));
+    const Tensor& c = rope.cos_table();
+    const Tensor& sn = rope.sin_table();
+    check(key_.dtype() == DType::F32
+              ? rl_qkv_rope_kv_append_f32(ctx.raw(), query.buffer().raw(), qd.data(), qs.data(),
+                                          key.buffer().raw(), kd.data(), ks.data(),
+                                          value.buffer().raw(), vd.data(), vs.data(),
+                                          c.buffer().raw(), sn.buffer().raw(), c.dim(0), start,
+                                          out.raw(), key_.buffer().raw(), value_.buffer().raw(),
+                                          max_seq_len_)
+              : rl_qkv_rope_kv_append_f16(ctx.raw(), query.buffer().raw(), qd.data(), qs.data(),
+                                          key.buffer().raw(), kd.data(), ks.data(),
+                                          value.buffer().raw(), vd.data(), vs.data(),
+                                          c.buffer().raw(), sn.buffer().raw(), c.dim(0), start,
+                                          out.raw(), key_.buffer().raw(), value_.buffer().raw(),
+                                          max_seq_len_));
+    len_ = start + seq;
+    return Tensor::from_buffer(std::move(out), query.shape().dims(), key_.dtype());
+}
+
 }  // namespace model
 }  // namespace rustllm

@@ -389,6 +389,12 @@ class LayerKvCache {
     // rotated key written straight into the cache (nn/attention.rs:202-207,306-307).
     void append_rotated_encode(const Context& ctx, const nn::RotaryEmbedding& rope,
                                const Tensor& key, const Tensor& value);
+    // The attention step's Q and K rotation at len() and the K/V append
+    // (nn/attention.rs:196-207, 304-307) in one launch; returns the rotated,
+    // contiguous Q.
+    Tensor rotate_query_and_append_encode(const Context& ctx, const nn::RotaryEmbedding& rope,
+                                          const Tensor& query, const Tensor& key,
+                                          const Tensor& value);
 
    private:
     void validate_append(const Tensor& key, const Tensor& value) const;

@@ -482,6 +482,46 @@ TEST(fused_append_of_projection_views_equals_the_unfused_path) {
     }
 }
 
+// The same with Q: its rotation and the K/V append in one launch equals
+// rope(Q), rope(K), append of the materialised tensors.
+TEST(one_launch_query_rotation_and_append_equals_the_unfused_path) {
+    const size_t seq = 3, qheads = 4, heads = 2, hd = 8, max = 8;
+    nn::RotaryEmbedding rope(context, hd, max, 10000.0f);
+    std::vector<float> qd(seq * qheads * hd), kd(seq * heads * hd), vd(seq * heads * hd);
+    for (size_t i = 0; i < qd.size(); ++i) qd[i] = std::cos(0.23f * float(i)) * 2.5f;
+    for (size_t i = 0; i < kd.size(); ++i) {
+        kd[i] = std::sin(0.37f * float(i)) * 3.0f;
+        vd[i] = std::cos(0.11f * float(i)) * 2.0f;
+    }
+    for (DType dtype : {DType::F32, DType::F16}) {
+        auto q = Tensor::from_f32_slice(context, qd, {1, seq, qheads, hd}).to_dtype(context, dtype)
+                     .permute({0, 2, 1, 3});
+        auto k = Tensor::from_f32_slice(context, kd, {1, seq, heads, hd}).to_dtype(context, dtype)
+                     .permute({0, 2, 1, 3});
+        auto v = Tensor::from_f32_slice(context, vd, {1, seq, heads, hd}).to_dtype(context, dtype)
+                     .permute({0, 2, 1, 3});
+        model::LayerKvCache fused(context, heads, max, hd, dtype);
+        model::LayerKvCache plain(context, heads, max, hd, dtype);
+        for (size_t round = 0; round < 2; ++round) {
+            Execution a(context);
+            auto q_fused = fused.rotate_query_and_append_encode(context, rope, q, k, v);
+            a.finish();
+            Execution b(context);
+            auto q_plain = rope.forward_encode(context, q, plain.len());
+            auto k_rot = rope.forward_encode(context, k, plain.len());
+            plain.append_encode(context, k_rot, v);
+            b.finish();
+            CHECK(q_fused.is_contiguous());
+            CHECK(q_fused.to_f32_vec() == q_plain.to_f32_vec());
+        }
+        CHECK(fused.len() == 2 * seq);
+        CHECK(fused.key().contiguous(context).to_f32_vec() ==
+              plain.key().contiguous(context).to_f32_vec());
+        CHECK(fused.value().contiguous(context).to_f32_vec() ==
+              plain.value().contiguous(context).to_f32_vec());
+    }
+}
+
 // ---------------------------------------------------- src/ops/embedding.rs
 
 // ops/embedding.rs:119-149: rows of the weight, token ids checked against the vocabulary.
