@@ -158,15 +158,74 @@ struct FastDiv {
     }
 };
 
-// The row dims of a strided view (every dim but the innermost), innermost
-// first: dim[0] is the sequence dim of a [..., S, D] view.  Passed by value
-// to kernels that decode a row index into an element offset.
+// The row dims of a strided [..., S, D] view (every dim but the innermost D)
+// in the order rows are enumerated, fastest first.  Decoding row index r
+// gives the source element offset, the sequence position (the coordinate of
+// dim `seq_dim`) and the group: the flat index of the other row dims in the
+// view's own row-major order (e.g. the head of a [1, H, S, D] view), which
+// places the row in a contiguous or cache-shaped destination.
 constexpr int kMaxRowRank = 16;
 struct RowDims {
     uint32_t rank;
+    uint32_t seq_dim;
     FastDiv dim[kMaxRowRank];
     uint64_t stride[kMaxRowRank];
+    uint32_t group_mult[kMaxRowRank];
 };
+
+// Rows enumerated in the view's memory order (row dims sorted by source
+// stride, smallest first), so consecutive rows read consecutive memory where
+// the view allows: for the [1, H, S, D] permute of a [1, S, H, D] projection
+// the heads of one position come together, reading the projection straight
+// through and sharing that position's table row.  dims/strides: outermost
+// first, `rank` >= 2 including the innermost dim.
+inline RowDims make_row_dims(const uint64_t* dims, const uint64_t* strides, uint32_t rank) {
+    RowDims rd{};
+    const uint32_t n = rank - 1;  // row dims: 0 .. rank - 2; the sequence dim is rank - 2
+    uint32_t order[kMaxRowRank];
+    for (uint32_t i = 0; i < n; ++i) order[i] = n - 1 - i;  // innermost first
+    for (uint32_t i = 1; i < n; ++i) {  // stable insertion sort by stride
+        const uint32_t v = order[i];
+        uint32_t j = i;
+        while (j > 0 && strides[order[j - 1]] > strides[v]) {
+            order[j] = order[j - 1];
+            --j;
+        }
+        order[j] = v;
+    }
+    rd.rank = n;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t d = order[i];
+        rd.dim[i] = FastDiv(uint32_t(dims[d]));
+        rd.stride[i] = strides[d];
+        if (d == n - 1) {
+            rd.seq_dim = i;
+            rd.group_mult[i] = 0;
+        } else {
+            uint64_t mult = 1;  // row-major over the row dims other than the sequence dim
+            for (uint32_t e = d + 1; e < n - 1; ++e) mult *= dims[e];
+            rd.group_mult[i] = uint32_t(mult);
+        }
+    }
+    return rd;
+}
+
+__device__ inline void decode_row(const RowDims& rd, uint32_t row, uint64_t& src_off,
+                                  uint32_t& position, uint32_t& group) {
+    src_off = 0;
+    position = 0;
+    group = 0;
+    for (uint32_t d = 0; d < rd.rank; ++d) {
+        uint32_t q, r;
+        rd.dim[d].divmod(row, q, r);
+        src_off += uint64_t(r) * rd.stride[d];
+        if (d == rd.seq_dim)
+            position = r;
+        else
+            group += r * rd.group_mult[d];
+        row = q;
+    }
+}
 
 }  // namespace rl
 

@@ -35,19 +35,9 @@ __global__ __launch_bounds__(kThreads) void k_kv_write(const T* __restrict__ src
             if (i < n_items) {
                 uint32_t row, pp;
                 packs_per_row.divmod(uint32_t(i), row, pp);
-                uint64_t src_off = 0;
-                uint32_t position = 0, head = 0;
-                uint32_t rest = row;
-                for (uint32_t d = 0; d < rd.rank; ++d) {
-                    uint32_t q, r;
-                    rd.dim[d].divmod(rest, q, r);
-                    if (d == 0) {
-                        position = r;
-                        head = q;
-                    }
-                    src_off += uint64_t(r) * rd.stride[d];
-                    rest = q;
-                }
+                uint64_t src_off;
+                uint32_t position, head;
+                decode_row(rd, row, src_off, position, head);
                 const uint32_t col = pp * N;
                 if constexpr (N == 1) {
                     v[u][0] = src[src_off + uint64_t(col) * inner_stride];
@@ -86,12 +76,7 @@ rl_status launch_kv_write(rl_context* ctx, const char* name, const T* src, const
         if (ok) break;
         n >>= 1;
     }
-    RowDims rd{};
-    rd.rank = 2;
-    rd.dim[0] = FastDiv(uint32_t(seq));
-    rd.stride[0] = strides[2];
-    rd.dim[1] = FastDiv(uint32_t(heads));
-    rd.stride[1] = strides[1];
+    const RowDims rd = make_row_dims(dims, strides, 4);
     const uint64_t n_items = heads * seq * (head_dim / n);
     const FastDiv ppr(uint32_t(head_dim / n));
     constexpr int U = 2;

@@ -13,7 +13,10 @@
 // [1, H, S, D] permute of [1, S, H, D] the attention path rotates): the
 // gather that ops::rope_encode does first with contiguous_encode
 // (src/ops/rope.rs:345) happens in the same pass, rows being decoded with
-// 32-bit multiply-high division.
+// 32-bit multiply-high division.  Rows are taken in the view's memory order:
+// for that permute the heads of one position come together, so the
+// projection is read straight through and the position's cos/sin row is
+// fetched once per wave instead of once per head.
 #include "common.hpp"
 
 #pragma clang fp contract(off)
@@ -57,20 +60,10 @@ __global__ __launch_bounds__(kThreads) void k_rope(const T* __restrict__ src,
             if (i < n_items) {
                 uint32_t row, pp;
                 packs_per_row.divmod(uint32_t(i), row, pp);
-                // Decode the row: the innermost row dim is the sequence position.
-                uint64_t src_off = 0;
-                uint32_t position = 0, group = 0;
-                uint32_t rest = row;
-                for (uint32_t d = 0; d < rd.rank; ++d) {
-                    uint32_t q, r;
-                    rd.dim[d].divmod(rest, q, r);
-                    if (d == 0) {
-                        position = r;
-                        group = q;
-                    }
-                    src_off += uint64_t(r) * rd.stride[d];
-                    rest = q;
-                }
+                // Rows run in the view's memory order (make_row_dims).
+                uint64_t src_off;
+                uint32_t position, group;
+                decode_row(rd, row, src_off, position, group);
                 const uint32_t pair = pp * N;
                 const uint64_t t = uint64_t(start + position) * half_dim + pair;
                 a[u] = *reinterpret_cast<const V*>(src + src_off + pair);
@@ -131,12 +124,7 @@ rl_status launch_rope(rl_context* ctx, const char* name, const T* src, const uin
         if (ok) break;
         n >>= 1;
     }
-    RowDims rd{};
-    rd.rank = rank - 1;
-    for (uint32_t d = 0; d + 1 < rank; ++d) {
-        rd.dim[d] = FastDiv(uint32_t(dims[rank - 2 - d]));
-        rd.stride[d] = strides[rank - 2 - d];
-    }
+    const RowDims rd = make_row_dims(dims, strides, rank);
     const uint64_t n_items = rows * (half / n);
     const FastDiv ppr(uint32_t(half / n));
     constexpr int U = 2;
@@ -353,19 +341,9 @@ __global__ __launch_bounds__(kThreads) void k_rope_tasks(RowTasks tasks,
         if (i < task.n_items) {
             uint32_t row, pp;
             task.packs_per_row.divmod(uint32_t(i), row, pp);
-            uint64_t src_off = 0;
-            uint32_t position = 0, group = 0;
-            uint32_t rest = row;
-            for (uint32_t d = 0; d < task.rd.rank; ++d) {
-                uint32_t q, r;
-                task.rd.dim[d].divmod(rest, q, r);
-                if (d == 0) {
-                    position = r;
-                    group = q;
-                }
-                src_off += uint64_t(r) * task.rd.stride[d];
-                rest = q;
-            }
+            uint64_t src_off;
+            uint32_t position, group;
+            decode_row(task.rd, row, src_off, position, group);
             const uint32_t pair = pp * N;
             a[u] = *reinterpret_cast<const V*>(src + src_off + pair);
             b[u] = *reinterpret_cast<const V*>(src + src_off + half_dim + pair);
@@ -504,11 +482,7 @@ rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
         RowTask& task = tasks.task[t];
         task.src = srcs[t];
         task.dst = dsts[t];
-        task.rd.rank = 3;
-        for (uint32_t d = 0; d < 3; ++d) {
-            task.rd.dim[d] = FastDiv(uint32_t(dims[t][2 - d]));
-            task.rd.stride[d] = strides[t][2 - d];
-        }
+        task.rd = make_row_dims(dims[t], strides[t], 4);
         task.packs_per_row = FastDiv(uint32_t(half / n));
         task.dst_rows = t == 0 ? DstRows{uint32_t(dims[t][2]), 0}
                                : DstRows{uint32_t(max_seq), uint32_t(start)};
