@@ -79,7 +79,7 @@ rl_status launch_kv_write(rl_context* ctx, const char* name, const T* src, const
     const RowDims rd = make_row_dims(dims, strides, 4);
     const uint64_t n_items = heads * seq * (head_dim / n);
     const FastDiv ppr(uint32_t(head_dim / n));
-    constexpr int U = 2;
+    constexpr int U = 1;
     const dim3 grid(grid_for(n_items, uint64_t(kThreads) * U)), block(kThreads);
     const uint32_t ni = uint32_t(n_items), is = uint32_t(strides[3]), hd = uint32_t(head_dim),
                    ms = uint32_t(max_seq), st = uint32_t(start);

@@ -127,7 +127,7 @@ rl_status launch_rope(rl_context* ctx, const char* name, const T* src, const uin
     const RowDims rd = make_row_dims(dims, strides, rank);
     const uint64_t n_items = rows * (half / n);
     const FastDiv ppr(uint32_t(half / n));
-    constexpr int U = 2;
+    constexpr int U = 1;
     const dim3 grid(grid_for(n_items, uint64_t(kThreads) * U)), block(kThreads);
     const uint32_t h32 = uint32_t(half), s32 = uint32_t(start), ni = uint32_t(n_items);
     if (dst.group_rows == 0) dst = DstRows{uint32_t(dims[rank - 2]), 0};
@@ -475,7 +475,7 @@ rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
         if (ok) break;
         n >>= 1;
     }
-    constexpr int U = 2;
+    constexpr int U = 1;
     RowTasks tasks{};
     uint64_t blocks = 0;
     for (int t = 0; t < 3; ++t) {
