@@ -506,6 +506,8 @@ def extra_rows(ctx, reps, quick):
     measure("layer.6 residual add_f16", "f16", [tok, hid], 3 * r.size * 2,
             lambda i: (ctx.upload(x), ctx.upload(r), ctx.empty(r.shape, F16)),
             lambda s: ctx.add(s[0], s[1], s[2]))
+    if not quick:
+        rows.append(layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds))
     # [64, 768] f32 (the reference's CPU-runnable case), fused add + RMSNorm
     # (writes the sum and the norm)
     x0 = synth.normal(1, (64, 768), 0, 1, F32)
@@ -515,6 +517,71 @@ def extra_rows(ctx, reps, quick):
                        ctx.empty(x0.shape, F32)),
             lambda s: ctx.add_rmsnorm(s[0], s[1], w0, 1e-5, s[2], s[3]))
     return rows
+
+
+def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20):
+    """The whole non-GEMM chain of one SmolLM2-360M layer in order -- RMSNorm,
+    RoPE of Q and K (from the projections' [1, H, S, D] views), repeat_kv of K
+    and V, causal scale/mask + softmax, SwiGLU, residual add: 8 launches
+    recorded as one graph per buffer set and replayed; bytes are the sum of
+    the launches' algorithmic bytes."""
+    rng_key = ("chain",)
+    qdims, qstrides = [1, qh, tok, hd], [tok * qh * hd, hd, qh * hd, 1]
+    kdims, kstrides = [1, kvh, tok, hd], [tok * kvh * hd, hd, kvh * hd, 1]
+    unmasked = qh * (tok * (tok + 1) // 2)
+    nbytes = (tok * hid * 4 + hid * 2                                   # RMSNorm
+              + 2 * (qh + kvh) * tok * hd * 2 + 2 * 2 * tok * (hd // 2) * 4  # RoPE Q, K
+              + 2 * (kvh + qh) * tok * hd * 2                           # repeat_kv K, V
+              + unmasked * 2 + qh * tok * tok * 2                       # scale/mask + softmax
+              + 3 * tok * ffn * 2                                       # SwiGLU
+              + 3 * tok * hid * 2)                                      # residual add
+
+    scores = np.random.default_rng(7).standard_normal((qh, tok, tok), dtype=np.float32)
+    scores = scores.astype(F16)
+
+    def make(i):
+        b = {"x": ctx.upload(synth.normal(synth.seed_for(*rng_key, "x", i), (tok, hid), 0, 1, F16)),
+             "q": ctx.upload(synth.normal(synth.seed_for(*rng_key, "q", i), (1, tok, qh, hd), 0, 1,
+                                          F16)),
+             "k": ctx.upload(synth.normal(synth.seed_for(*rng_key, "k", i), (1, tok, kvh, hd), 0,
+                                          1, F16)),
+             "v": ctx.upload(synth.normal(synth.seed_for(*rng_key, "v", i), (1, kvh, tok, hd), 0,
+                                          1, F16)),
+             "s": ctx.upload(scores),
+             "g": ctx.upload(synth.normal(synth.seed_for(*rng_key, "g", i), (tok, ffn), 0, 1, F16)),
+             "u": ctx.upload(synth.normal(synth.seed_for(*rng_key, "u", i), (tok, ffn), 0, 1, F16)),
+             "r": ctx.upload(synth.normal(synth.seed_for(*rng_key, "r", i), (tok, hid), 0, 1, F16))}
+        b.update({"xn": ctx.empty((tok, hid), F16), "qr": ctx.empty(qdims, F16),
+                  "kr": ctx.empty(kdims, F16), "kq": ctx.empty(qdims, F16),
+                  "vq": ctx.empty(qdims, F16), "p": ctx.empty((qh, tok, tok), F16),
+                  "h": ctx.empty((tok, ffn), F16), "o": ctx.empty((tok, hid), F16)})
+        return b
+
+    def chain(b):
+        ctx.rmsnorm(b["x"], wn, 1e-5, b["xn"])
+        ctx.rope_strided(b["q"], qdims, qstrides, dc, ds, 0, b["qr"])
+        ctx.rope_strided(b["k"], kdims, kstrides, dc, ds, 0, b["kr"])
+        ctx.repeat_kv(b["kr"], qh // kvh, b["kq"])
+        ctx.repeat_kv(b["v"], qh // kvh, b["vq"])
+        ctx.attention_softmax(b["s"], 0.125, 0, b["p"])
+        ctx.swiglu(b["g"], b["u"], b["h"])
+        ctx.add(b["xn"], b["r"], b["o"])
+
+    bufs = [make(i) for i in range(sets)]
+    graphs = [capture(ctx, lambda b=b: chain(b)) for b in bufs]
+    ms = time_graphs(ctx, graphs, 1, reps)
+    ctx.finish()
+    for g in graphs:
+        ctx.graph_destroy(g)
+    us = ms * 1e3
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"  {'layer chain (8 launches, one graph)':34s} {us:9.2f} us {gbs:8.1f} GB/s "
+        f"({100 * gbs / PEAK_GBS:5.1f}%)")
+    return {"op": "layer chain (8 launches, one graph)", "dtype": "f16",
+            "shape": [tok, hid], "bytes": nbytes, "us": round(us, 3), "us_min": None,
+            "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+            "us_graph_batch": round(us, 3), "GB/s_graph_batch": round(gbs, 1),
+            "pct_peak_graph_batch": round(100 * gbs / PEAK_GBS, 1)}
 
 
 def _rope_table(head_dim, max_seq, theta=10000.0):
