@@ -437,3 +437,90 @@ void oracle_rope_table(size_t head_dim, size_t max_seq_len, float theta, float* 
         }
     }
 }
+
+/* ------------------------------------------------------ GQA attention core */
+
+/* gqa_matmul.metal:7-161 (f32) and :163-322 (f16): one thread per score;
+ * kv_head = q_head / (q_heads / kv_heads) (:25-38); K rows of a head are
+ * kv_capacity apart (:59-65); the dot product runs over d in order (16-wide
+ * tiles, each summed in order, :75-140) in float32, f16 products widened first
+ * (:287-295), and the f16 score is rounded once at the store (:319). */
+void oracle_gqa_qk_f32(const float* q, const float* k, float* out, size_t batch,
+                       size_t q_heads, size_t kv_heads, size_t q_len, size_t kv_len,
+                       size_t head_dim, size_t kv_capacity) {
+    size_t groups = q_heads / kv_heads;
+    size_t rows = batch * q_heads * q_len;
+    PAR_FOR
+    for (size_t row = 0; row < rows; ++row) {
+        size_t flat_head = row / q_len, query = row % q_len;
+        size_t b = flat_head / q_heads, kv_head = (flat_head % q_heads) / groups;
+        const float* qr = q + (flat_head * q_len + query) * head_dim;
+        const float* kh = k + (b * kv_heads + kv_head) * kv_capacity * head_dim;
+        for (size_t key = 0; key < kv_len; ++key) {
+            float sum = 0.0f;
+            for (size_t d = 0; d < head_dim; ++d) sum += qr[d] * kh[key * head_dim + d];
+            out[row * kv_len + key] = sum;
+        }
+    }
+}
+
+void oracle_gqa_qk_f16(const uint16_t* q, const uint16_t* k, uint16_t* out, size_t batch,
+                       size_t q_heads, size_t kv_heads, size_t q_len, size_t kv_len,
+                       size_t head_dim, size_t kv_capacity) {
+    size_t groups = q_heads / kv_heads;
+    size_t rows = batch * q_heads * q_len;
+    PAR_FOR
+    for (size_t row = 0; row < rows; ++row) {
+        size_t flat_head = row / q_len, query = row % q_len;
+        size_t b = flat_head / q_heads, kv_head = (flat_head % q_heads) / groups;
+        const uint16_t* qr = q + (flat_head * q_len + query) * head_dim;
+        const uint16_t* kh = k + (b * kv_heads + kv_head) * kv_capacity * head_dim;
+        for (size_t key = 0; key < kv_len; ++key) {
+            float sum = 0.0f;
+            for (size_t d = 0; d < head_dim; ++d) sum += H2F(qr[d]) * H2F(kh[key * head_dim + d]);
+            out[row * kv_len + key] = F2H(sum);
+        }
+    }
+}
+
+/* gqa_matmul.metal:323-474 (f32) and :475-629 (f16): out[b,h,i,d] =
+ * sum over keys j in order of p[b,h,i,j] * v[b,h/g,j,d] in float32, V rows
+ * kv_capacity apart per head (:372-378); f16 rounded once at the store. */
+void oracle_gqa_pv_f32(const float* probs, const float* v, float* out, size_t batch,
+                       size_t q_heads, size_t kv_heads, size_t q_len, size_t kv_len,
+                       size_t head_dim, size_t kv_capacity) {
+    size_t groups = q_heads / kv_heads;
+    size_t rows = batch * q_heads * q_len;
+    PAR_FOR
+    for (size_t row = 0; row < rows; ++row) {
+        size_t flat_head = row / q_len;
+        size_t b = flat_head / q_heads, kv_head = (flat_head % q_heads) / groups;
+        const float* pr = probs + row * kv_len;
+        const float* vh = v + (b * kv_heads + kv_head) * kv_capacity * head_dim;
+        for (size_t d = 0; d < head_dim; ++d) {
+            float sum = 0.0f;
+            for (size_t key = 0; key < kv_len; ++key) sum += pr[key] * vh[key * head_dim + d];
+            out[row * head_dim + d] = sum;
+        }
+    }
+}
+
+void oracle_gqa_pv_f16(const uint16_t* probs, const uint16_t* v, uint16_t* out, size_t batch,
+                       size_t q_heads, size_t kv_heads, size_t q_len, size_t kv_len,
+                       size_t head_dim, size_t kv_capacity) {
+    size_t groups = q_heads / kv_heads;
+    size_t rows = batch * q_heads * q_len;
+    PAR_FOR
+    for (size_t row = 0; row < rows; ++row) {
+        size_t flat_head = row / q_len;
+        size_t b = flat_head / q_heads, kv_head = (flat_head % q_heads) / groups;
+        const uint16_t* pr = probs + row * kv_len;
+        const uint16_t* vh = v + (b * kv_heads + kv_head) * kv_capacity * head_dim;
+        for (size_t d = 0; d < head_dim; ++d) {
+            float sum = 0.0f;
+            for (size_t key = 0; key < kv_len; ++key)
+                sum += H2F(pr[key]) * H2F(vh[key * head_dim + d]);
+            out[row * head_dim + d] = F2H(sum);
+        }
+    }
+}

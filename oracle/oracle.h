@@ -94,6 +94,23 @@ void oracle_embedding(const void* weight, const uint32_t* ids, void* out, size_t
 void oracle_kv_cache_write(void* cache, const void* src, size_t heads, size_t src_seq,
                            size_t max_seq, size_t head_dim, size_t start, size_t element_size);
 
+/* Grouped-query matmuls of the attention core.  q and probs are contiguous
+ * [B, QH, Q, D] / [B, QH, Q, K]; k and v hold kv_capacity rows per KV head
+ * ([B, KVH, kv_capacity, D], the first kv_len used); query head h reads KV
+ * head h / (QH / KVH).  Sums run in float32 in index order. */
+void oracle_gqa_qk_f32(const float* q, const float* k, float* out, size_t batch,
+                       size_t q_heads, size_t kv_heads, size_t q_len, size_t kv_len,
+                       size_t head_dim, size_t kv_capacity);
+void oracle_gqa_qk_f16(const uint16_t* q, const uint16_t* k, uint16_t* out, size_t batch,
+                       size_t q_heads, size_t kv_heads, size_t q_len, size_t kv_len,
+                       size_t head_dim, size_t kv_capacity);
+void oracle_gqa_pv_f32(const float* probs, const float* v, float* out, size_t batch,
+                       size_t q_heads, size_t kv_heads, size_t q_len, size_t kv_len,
+                       size_t head_dim, size_t kv_capacity);
+void oracle_gqa_pv_f16(const uint16_t* probs, const uint16_t* v, uint16_t* out, size_t batch,
+                       size_t q_heads, size_t kv_heads, size_t q_len, size_t kv_len,
+                       size_t head_dim, size_t kv_capacity);
+
 #ifdef __cplusplus
 }
 #endif

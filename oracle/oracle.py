@@ -73,6 +73,10 @@ def _load() -> ctypes.CDLL:
         "oracle_rope_table": ([_S, _S, _F, _P, _P], None),
         "oracle_embedding": ([_P, _P, _P, _S, _S, _S], None),
         "oracle_kv_cache_write": ([_P, _P, _S, _S, _S, _S, _S, _S], None),
+        "oracle_gqa_qk_f32": ([_P, _P, _P] + [_S] * 7, None),
+        "oracle_gqa_qk_f16": ([_P, _P, _P] + [_S] * 7, None),
+        "oracle_gqa_pv_f32": ([_P, _P, _P] + [_S] * 7, None),
+        "oracle_gqa_pv_f16": ([_P, _P, _P] + [_S] * 7, None),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -319,3 +323,47 @@ def rope_table(head_dim: int, max_seq_len: int, theta: float):
     s = np.empty((max_seq_len, half), dtype=np.float32)
     _lib.oracle_rope_table(head_dim, max_seq_len, theta, _ptr(c), _ptr(s))
     return c, s
+
+
+def _gqa_shapes(left, right, kv_len):
+    batch, q_heads, q_len = left.shape[:3]
+    r_batch, kv_heads, capacity, head_dim = right.shape
+    kv_len = capacity if kv_len is None else kv_len
+    assert r_batch == batch and q_heads % kv_heads == 0 and kv_len <= capacity
+    return batch, q_heads, kv_heads, q_len, kv_len, head_dim, capacity
+
+
+def gqa_qk(q, k, kv_len=None):
+    """Q [B, QH, Q, D] x K^T with K [B, KVH, capacity, D], its first kv_len
+    rows per head used: scores [B, QH, Q, kv_len] (gqa_matmul.metal:7-322)."""
+    q = np.asarray(q)
+    conv = _f16 if q.dtype == np.float16 else _f32
+    q, k = conv(q), conv(k)
+    b, qh, kvh, ql, kl, hd, cap = _gqa_shapes(q, k, kv_len)
+    assert q.shape[3] == hd
+    out = np.empty((b, qh, ql, kl), dtype=q.dtype)
+    name = "oracle_gqa_qk_f16" if q.dtype == np.float16 else "oracle_gqa_qk_f32"
+    getattr(_lib, name)(_ptr(q), _ptr(k), _ptr(out), b, qh, kvh, ql, kl, hd, cap)
+    return out
+
+
+def gqa_pv(probs, v, kv_len=None):
+    """P [B, QH, Q, kv_len] x V with V [B, KVH, capacity, D]: [B, QH, Q, D]
+    (gqa_matmul.metal:323-629)."""
+    probs = np.asarray(probs)
+    conv = _f16 if probs.dtype == np.float16 else _f32
+    probs, v = conv(probs), conv(v)
+    b, qh, kvh, ql, kl, hd, cap = _gqa_shapes(probs, v, kv_len)
+    assert probs.shape[3] == kl
+    out = np.empty((b, qh, ql, hd), dtype=probs.dtype)
+    name = "oracle_gqa_pv_f16" if probs.dtype == np.float16 else "oracle_gqa_pv_f32"
+    getattr(_lib, name)(_ptr(probs), _ptr(v), _ptr(out), b, qh, kvh, ql, kl, hd, cap)
+    return out
+
+
+def attention(q, k, v, scale: float, start: int, kv_len=None):
+    """The reference's attention core (nn/attention.rs:216-247) as its four
+    calls with their rounding points: QK^T, scale/mask, softmax, PV."""
+    scores = gqa_qk(q, k, kv_len)
+    probs = softmax(scale_mask(scores, scale, start))
+    return gqa_pv(probs, v, scores.shape[-1])

@@ -76,3 +76,32 @@ def f16_ulp_distance(got, ref) -> int:
     if not ok.any():
         return 0
     return int(np.max(np.abs(key(got)[ok] - key(ref)[ok])))
+
+
+def gqa_expand(kv, q_heads: int, kv_len: int) -> np.ndarray:
+    """[B, KVH, capacity, D] -> float64 [B, QH, kv_len, D]: query head h reads
+    KV head h // (QH / KVH) (np.repeat, the textbook grouped-query layout)."""
+    kv = np.asarray(kv, dtype=np.float64)[:, :, :kv_len]
+    return np.repeat(kv, q_heads // kv.shape[1], axis=1)
+
+
+def attention_exact(q, k, v, scale: float, start: int, kv_len=None):
+    """Float64 causal attention, softmax(mask(scale * Q K^T)) V, computed with
+    numpy matrix products.  Returns (out, weight, dot_abs): weight[..., i, d] =
+    sum_j p_ij |v_jd| (the magnitude an error bound of the output scales with)
+    and dot_abs[..., i] = max_j sum_d |q_id k_jd| (that of the scores)."""
+    q = np.asarray(q, dtype=np.float64)
+    kv_len = k.shape[2] if kv_len is None else kv_len
+    ke = gqa_expand(k, q.shape[1], kv_len)
+    ve = gqa_expand(v, q.shape[1], kv_len)
+    s = np.matmul(q, np.swapaxes(ke, -1, -2)) * float(scale)
+    q_len = q.shape[2]
+    masked = np.arange(kv_len)[None, :] > (start + np.arange(q_len))[:, None]
+    s = np.where(masked, -np.inf, s)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    out = np.matmul(p, ve)
+    weight = np.matmul(p, np.abs(ve))
+    dot_abs = np.max(np.where(masked, 0.0, np.matmul(np.abs(q), np.swapaxes(np.abs(ke), -1, -2))),
+                     axis=-1)
+    return out, weight, dot_abs

@@ -10,7 +10,8 @@ planted-mistake tests at the end show that these checks catch plausible bugs.
 import numpy as np
 import pytest
 
-from helpers import assert_bitexact, f16_ulp_distance, floats, kats, max_rel_err
+from helpers import (assert_bitexact, attention_exact, f16_ulp_distance, floats, gqa_expand, kats,
+                     max_rel_err)
 from oracle import oracle as o
 from rustllm_amd import synth
 
@@ -382,6 +383,127 @@ def test_rope_kat_f16_vs_f32():
 
 # ------------------------------------------------- planted mistakes are caught
 
+# ------------------------------------------------------------ attention core
+
+U32 = 2.0 ** -24
+
+
+def _ulp16(x):
+    """Spacing of binary16 at |x| (2^-24 below the normal range)."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def _cache(seed, batch, heads, capacity, head_dim, kv_len, dtype=np.float32):
+    """A [B, H, capacity, D] cache whose rows past kv_len hold NaN, so a read
+    of an unused row shows up in every result."""
+    kv = synth.normal(seed, (batch, heads, capacity, head_dim)).astype(dtype)
+    kv[:, :, kv_len:] = np.nan
+    return kv
+
+
+GQA_CASES = [  # batch, q_heads, kv_heads, q_len, kv_len, capacity, head_dim
+    (1, 6, 2, 5, 7, 9, 16),
+    (2, 3, 3, 4, 4, 4, 8),
+    (1, 15, 5, 3, 33, 40, 64),
+]
+
+
+@pytest.mark.parametrize("case", GQA_CASES)
+def test_gqa_qk_against_float64(case):
+    b, qh, kvh, ql, kl, cap, hd = case
+    q = synth.normal(61, (b, qh, ql, hd))
+    k = _cache(62, b, kvh, cap, hd, kl)
+    exact = np.matmul(q.astype(np.float64), np.swapaxes(gqa_expand(k, qh, kl), -1, -2))
+    dot_abs = np.matmul(np.abs(q.astype(np.float64)), np.swapaxes(np.abs(gqa_expand(k, qh, kl)), -1, -2))
+    got = o.gqa_qk(q, k, kl)
+    assert got.shape == (b, qh, ql, kl)
+    assert np.all(np.abs(got - exact) <= hd * U32 * dot_abs + 1e-30)
+    qh16, kh16 = q.astype(np.float16), k.astype(np.float16)
+    exact16 = np.matmul(qh16.astype(np.float64), np.swapaxes(gqa_expand(kh16, qh, kl), -1, -2))
+    got16 = o.gqa_qk(qh16, kh16, kl)
+    dot16 = np.matmul(np.abs(qh16.astype(np.float64)),
+                      np.swapaxes(np.abs(gqa_expand(kh16, qh, kl)), -1, -2))
+    assert np.all(np.abs(got16 - exact16) <= hd * U32 * dot16 + _ulp16(exact16) / 2 * 1.0001)
+
+
+@pytest.mark.parametrize("case", GQA_CASES)
+def test_gqa_pv_against_float64(case):
+    b, qh, kvh, ql, kl, cap, hd = case
+    p = synth.uniform_range(63, (b, qh, ql, kl), 0.0, 1.0)
+    v = _cache(64, b, kvh, cap, hd, kl)
+    ve = gqa_expand(v, qh, kl)
+    exact = np.matmul(p.astype(np.float64), ve)
+    weight = np.matmul(p.astype(np.float64), np.abs(ve))
+    got = o.gqa_pv(p, v, kl)
+    assert got.shape == (b, qh, ql, hd)
+    assert np.all(np.abs(got - exact) <= kl * U32 * weight + 1e-30)
+    p16, v16 = p.astype(np.float16), v.astype(np.float16)
+    exact16 = np.matmul(p16.astype(np.float64), gqa_expand(v16, qh, kl))
+    weight16 = np.matmul(p16.astype(np.float64), np.abs(gqa_expand(v16, qh, kl)))
+    got16 = o.gqa_pv(p16, v16, kl)
+    assert np.all(np.abs(got16 - exact16) <= kl * U32 * weight16 + _ulp16(exact16) / 2 * 1.0001)
+
+
+def test_gqa_small_integers_are_exact():
+    """Small-integer operands: every product and partial sum is exact in
+    float32 and in the f16 result, so any order gives the float64 value."""
+    q = (np.arange(2 * 6 * 3 * 8) % 7 - 3).reshape(2, 6, 3, 8).astype(np.float32)
+    k = (np.arange(2 * 2 * 5 * 8) % 5 - 2).reshape(2, 2, 5, 8).astype(np.float32)
+    exact = np.matmul(q.astype(np.float64), np.swapaxes(gqa_expand(k, 6, 5), -1, -2))
+    for dt in (np.float32, np.float16):
+        assert np.array_equal(o.gqa_qk(q.astype(dt), k.astype(dt)).astype(np.float64), exact)
+        assert np.array_equal(o.gqa_pv(exact.astype(dt) / 8, k.astype(dt)).astype(np.float64),
+                              np.matmul(exact / 8, gqa_expand(k, 6, 5)))
+
+
+def _composition_bounds(q, k, v, scale, start, kv_len, f16):
+    exact, weight, dot_abs = attention_exact(q, k, v, scale, start, kv_len)
+    hd = q.shape[-1]
+    tmax = float(scale * np.max(dot_abs)) * 2 + 1
+    vmax = float(np.nanmax(np.abs(np.asarray(v, np.float64)[:, :, :kv_len])))
+    if f16:
+        rel = 2.0 ** -8 * scale * dot_abs[..., None] + 2.0 ** -9 + 8 * U32 * tmax + kv_len * U32
+        bound = rel * weight + kv_len * 2.0 ** -25 * vmax + _ulp16(exact)
+    else:
+        rel = 2 * scale * (hd + 1) * U32 * dot_abs[..., None] + 8 * U32 * tmax + (kv_len + 2) * U32
+        bound = rel * weight
+    return exact, bound
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+@pytest.mark.parametrize("case", [(1, 6, 2, 5, 7, 9, 16, 2), (1, 15, 5, 17, 17, 24, 64, 0),
+                                  (2, 4, 4, 1, 12, 12, 32, 11)])
+def test_attention_composition_against_float64(case, dtype):
+    """QK^T -> scale/mask -> softmax -> PV with the reference's rounding points
+    stays within the forward error bound of those roundings."""
+    b, qh, kvh, ql, kl, cap, hd, start = case
+    q = synth.normal(65, (b, qh, ql, hd)).astype(dtype)
+    k = _cache(66, b, kvh, cap, hd, kl, dtype)
+    v = _cache(67, b, kvh, cap, hd, kl, dtype)
+    scale = 1.0 / np.sqrt(hd)
+    got = o.attention(q, k, v, scale, start, kl)
+    exact, bound = _composition_bounds(q, k, v, scale, start, kl, dtype == np.float16)
+    assert got.shape == exact.shape and np.isfinite(got).all()
+    assert np.all(np.abs(got.astype(np.float64) - exact) <= bound)
+
+
+def test_attention_core_kat():
+    """nn/attention.rs:590-668: attention_core_encode == the op-by-op calls,
+    (2, 2) and (3, 1) heads, D 4, 3 new positions after 2 cached, values
+    (i % 5) - 2 and (i % 3) - 1, tolerance 1e-5."""
+    kat = K["attention_core"]
+    for case in kat["cases"]:
+        qh, kvh = case["heads"]
+        d, sl, start = kat["head_dim"], kat["seq_len"], kat["start_pos"]
+        q = (np.arange(qh * sl * d) % 5 - 2).astype(np.float32).reshape(1, qh, sl, d)
+        kv = (np.arange(kvh * (start + sl) * d) % 3 - 1).astype(np.float32)
+        kv = kv.reshape(1, kvh, start + sl, d)
+        got = o.attention(q, kv, kv, 1.0 / np.sqrt(d), start)
+        expected = np.array(case["expected"], dtype=np.float64).reshape(got.shape)
+        assert np.max(np.abs(got - expected)) < kat["tol"]
+
+
 def test_planted_mistakes_fail_the_pins():
     """Plausible slips (a transposed operand, a dropped term, an off-by-one in
     the mask, double rounding) must fail the independent checks above."""
@@ -408,3 +530,14 @@ def test_planted_mistakes_fail_the_pins():
     assert np.array_equal(o.contiguous(base, [3, 2, 4], [4, 12, 1]), good)
     kv = synth.normal(55, (1, 2, 3, 4))
     assert not np.array_equal(o.repeat_kv(kv, 2), np.tile(kv, (1, 2, 1, 1)))
+    # attention: KV head h % KVH instead of h // (QH / KVH), and a mask start one too
+    # late, both leave the float64 bound
+    q = synth.normal(56, (1, 6, 4, 16))
+    kc, vc = synth.normal(57, (1, 2, 8, 16)), synth.normal(58, (1, 2, 8, 16))
+    exact, bound = _composition_bounds(q, kc, vc, 0.25, 3, 8, False)
+    wrong_heads = np.concatenate([o.attention(q[:, h:h + 1], kc[:, h % 2:h % 2 + 1],
+                                              vc[:, h % 2:h % 2 + 1], 0.25, 3)
+                                  for h in range(6)], axis=1)
+    assert np.all(np.abs(o.attention(q, kc, vc, 0.25, 3) - exact) <= bound)
+    assert not np.all(np.abs(wrong_heads - exact) <= bound)
+    assert not np.all(np.abs(o.attention(q, kc, vc, 0.25, 4) - exact) <= bound)
