@@ -377,6 +377,36 @@ rl_status rl_embedding_f16(rl_context* ctx, const rl_buffer* weight, uint64_t vo
                            uint64_t hidden_size, const uint32_t* token_ids, uint64_t n_tokens,
                            const rl_buffer* out);
 
+/* ============================================================= attention */
+/* SelfAttention::attention_core_encode (src/nn/attention.rs:216-247) as one
+ * pass: scores = Q K^T (Tensor::gqa_qk_matmul_encode,
+ * src/tensor/gqa_matmul.rs:23-61, or batched_matmul when q_heads ==
+ * kv_heads), attention_scale_mask(scale, query_start_pos), softmax over the
+ * keys, then P V (gqa_pv_matmul_encode, :72-110); the [B, QH, Q, K] scores
+ * are never written.
+ *   q:    contiguous [batch, q_heads, q_len, head_dim]
+ *   k, v: [batch, kv_heads, kv_capacity, head_dim]; the first kv_len rows of
+ *         each head are used (a LayerKvCache's buffers with kv_capacity =
+ *         max_seq, or contiguous tensors with kv_capacity = kv_len); query
+ *         head h reads KV head h / (q_heads / kv_heads)
+ *   out:  contiguous [batch, q_heads, q_len, head_dim]
+ * Key j is masked for query i when j > query_start_pos + i.  Checks in the
+ * reference's order (head groups as RL_ERR_MODEL_FORMAT, the u32 limits,
+ * the scale/mask checks); also rejected: kv_capacity < kv_len and
+ * head_dim > 512 when the matrix-core path (f16, head_dim 32/64/96/128)
+ * does not apply.  Results differ from the four separate calls by their
+ * intermediate roundings: scores and probabilities stay in f32 here. */
+rl_status rl_attention_f32(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
+                           const rl_buffer* v, uint64_t batch, uint64_t q_heads,
+                           uint64_t kv_heads, uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                           uint64_t kv_capacity, float scale, uint64_t query_start_pos,
+                           const rl_buffer* out);
+rl_status rl_attention_f16(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
+                           const rl_buffer* v, uint64_t batch, uint64_t q_heads,
+                           uint64_t kv_heads, uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                           uint64_t kv_capacity, float scale, uint64_t query_start_pos,
+                           const rl_buffer* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -139,6 +139,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                          _I32),
     "rl_embedding_f16": ([_P, _BUF, _U64, _U64, ctypes.POINTER(ctypes.c_uint32), _U64, _BUF],
                          _I32),
+    "rl_attention_f32": ([_P, _BUF, _BUF, _BUF] + [_U64] * 7 + [_F, _U64, _BUF], _I32),
+    "rl_attention_f16": ([_P, _BUF, _BUF, _BUF] + [_U64] * 7 + [_F, _U64, _BUF], _I32),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -453,6 +455,17 @@ class Context:
                    kb, _u64_array(kd), _u64_array(ks), vb, _u64_array(vd), _u64_array(vs), cos,
                    sin, cos.shape[0], start, q_out, k_cache, v_cache, k_cache.shape[2])
         return q_out
+
+    def attention(self, q, k, v, scale: float, start: int, kv_len=None, out=None):
+        """Fused attention core: q [B, QH, Q, D]; k, v [B, KVH, capacity, D]
+        buffers of which the first kv_len rows per head are used."""
+        b, qh, ql, hd = q.shape
+        kvh, cap = k.shape[1], k.shape[2]
+        kv_len = cap if kv_len is None else kv_len
+        out = out or self.empty(q.shape, q.dtype)
+        self._call(f"rl_attention_{self._sfx(q)}", q, k, v, b, qh, kvh, ql, kv_len, hd, cap,
+                   ctypes.c_float(scale), start, out)
+        return out
 
     def embedding(self, weight, token_ids, out=None):
         ids = np.ascontiguousarray(token_ids, dtype=np.uint32)

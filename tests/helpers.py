@@ -105,3 +105,48 @@ def attention_exact(q, k, v, scale: float, start: int, kv_len=None):
     dot_abs = np.max(np.where(masked, 0.0, np.matmul(np.abs(q), np.swapaxes(np.abs(ke), -1, -2))),
                      axis=-1)
     return out, weight, dot_abs
+
+
+U32 = 2.0 ** -24
+
+
+def ulp16(x):
+    """Spacing of binary16 at |x| (2^-24 below the normal range)."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def attention_bound(q, k, v, scale: float, start: int, kv_len=None, kind="f32"):
+    """(exact, bound): float64 attention and a forward error bound per output
+    element, from the roundings each evaluation makes.
+
+    u = 2^-24, w = sum_j p_j |v_j| (the output's magnitude scale), S = max_j
+    sum_d |q_d k_jd|, T = a bound on |logit - max|:
+      f32           scores in f32 (D u S each, times scale, on two logits),
+                    exp / subtraction (8 u (1 + T)), sums over kv_len keys:
+                    (2 scale (D + 1) u S + 8 u (1 + T) + (kv_len + 2) u) w
+      f16_fused     the same plus probabilities fed to the P V product as
+                    f16 (2^-11, twice with the normaliser: 2^-10), f16
+                    subnormal probabilities (kv_len 2^-25 max|v|) and the
+                    final rounding (1 ulp)
+      f16_reference the reference's four calls: scores and scaled scores
+                    rounded to f16 (2^-11 |x| each on two logits: 2^-8
+                    scale S), probabilities rounded (2^-9 with the sum),
+                    then as f16_fused."""
+    exact, weight, dot_abs = attention_exact(q, k, v, scale, start, kv_len)
+    kv_len = k.shape[2] if kv_len is None else kv_len
+    hd = q.shape[-1]
+    s_term = dot_abs[..., None]
+    tmax = 2.0 * scale * float(np.max(dot_abs)) + 1.0
+    rel = (2.0 * scale * (hd + 1) * U32 * s_term + 8.0 * U32 * (1.0 + tmax)
+           + (kv_len + 2) * U32)
+    if kind == "f32":
+        return exact, rel * weight + 1e-30
+    vmax = float(np.max(np.abs(np.asarray(v, np.float64)[:, :, :kv_len])))
+    if kind == "f16_fused":
+        rel = rel + 2.0 ** -10
+    elif kind == "f16_reference":
+        rel = rel + 2.0 ** -8 * scale * s_term + 2.0 ** -9
+    else:
+        raise ValueError(kind)
+    return exact, rel * weight + kv_len * 2.0 ** -25 * vmax + ulp16(exact)

@@ -373,3 +373,45 @@ def test_qkv_rope_kv_append_validation():
     assert st == DTYPE and "kv_cache_write_f16" in msg
     st, _ = go(start=5, max_seq=6, kcache=buf(24, 2), vcache=buf(24, 2))
     assert st == POS
+
+
+@pytest.mark.parametrize("dt,es", [("f32", 4), ("f16", 2)])
+def test_attention_validation(dt, es):
+    # nn/attention.rs:216-247: gqa_matmul.rs head groups and u32 limits, then the
+    # scale/mask checks of attention_scale_mask.rs:120-161, then the buffers
+    f = f"rl_attention_{dt}"
+
+    def go(b=1, qh=6, kvh=2, ql=3, kl=5, hd=64, cap=8, scale=0.125, start=2, qn=None, kn=None,
+           vn=None, on=None):
+        qn = b * qh * ql * hd if qn is None else qn
+        kvn = b * kvh * cap * hd
+        return call(f, buf(qn, es), buf(kvn if kn is None else kn, es),
+                    buf(kvn if vn is None else vn, es), b, qh, kvh, ql, kl, hd, cap,
+                    ctypes.c_float(scale), start, buf(b * qh * ql * hd if on is None else on, es))
+
+    assert go()[0] == DEVICE
+    assert go(hd=48)[0] == DEVICE and go(hd=512)[0] == DEVICE
+    st, msg = go(ql=0)
+    assert st == SHAPE and "greater than zero" in msg
+    st, msg = go(kvh=4)
+    assert st == FORMAT and "Q heads 6 must be divisible by non-zero KV heads 4" in msg
+    assert go(kvh=0)[0] == FORMAT
+    st, msg = go(kl=9)
+    assert st == SHAPE and "KV capacity 8 is smaller than the key length 9" in msg
+    st, msg = go(scale=0.0)
+    assert st == SHAPE and "scale must be positive and finite" in msg
+    assert go(scale=float("inf"))[0] == SHAPE
+    st, msg = go(start=3)  # 3 + 3 > 5
+    assert st == SHAPE and "query range [3, 6) exceeds key length 5" in msg
+    st, msg = go(qn=6 * 3 * 64 - 1)
+    assert st == SHAPE and "query buffer" in msg
+    st, msg = go(kn=2 * 5 * 64)  # capacity rows, not kv_len rows
+    assert st == SHAPE and "key buffer" in msg
+    st, msg = go(vn=1)
+    assert st == SHAPE and "value buffer" in msg
+    st, msg = go(on=5)
+    assert st == SHAPE and "attention output buffer" in msg
+    st, msg = go(hd=520)
+    assert st == SHAPE and "head size 520 exceeds 512" in msg
+    st, msg = go(kl=1 << 33, cap=1 << 33, hd=1)
+    assert st == SHAPE and "exceeds u32" in msg

@@ -1,0 +1,128 @@
+"""The fused attention core (rl_attention_*) on the GPU against float64.
+
+SelfAttention::attention_core_encode (nn/attention.rs:216-247) is QK^T,
+scale/mask, softmax and PV; the fused pass keeps scores and probabilities in
+f32, so it is compared with float64 attention under the forward error bound
+of its own roundings (helpers.attention_bound, "f32" / "f16_fused"), and the
+reference's four calls (the oracle) are held to the bound of theirs.  Shapes
+cover both kernels (the f16 matrix-core path for head sizes 32..128 in steps
+of 32, the row kernel for f32 and other head sizes), grouped and plain heads,
+batches, ragged query/key counts, a start offset (chunked prefill and decode)
+and KV caches whose rows past kv_len hold NaN (never read).
+"""
+
+import numpy as np
+import pytest
+
+from helpers import attention_bound, attention_exact, kats
+from oracle import oracle as o
+from rustllm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+K = kats()
+
+
+def cache(seed, batch, heads, capacity, head_dim, kv_len, dtype):
+    kv = synth.normal(seed, (batch, heads, capacity, head_dim)).astype(dtype)
+    kv[:, :, kv_len:] = np.nan
+    return kv
+
+
+def run_attention(ctx, q, k, v, scale, start, kv_len):
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    ctx.begin()
+    out = ctx.attention(dq, dk, dv, scale, start, kv_len)
+    ctx.finish()
+    return out.numpy()
+
+
+def check(got, q, k, v, scale, start, kv_len, what):
+    kind = "f16_fused" if got.dtype == np.float16 else "f32"
+    exact, bound = attention_bound(q, k, v, scale, start, kv_len, kind)
+    err = np.abs(got.astype(np.float64) - exact)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    worst = np.unravel_index(np.argmax(err / bound), err.shape)
+    assert np.all(err <= bound), (f"{what}: error {err[worst]:.3g} > bound {bound[worst]:.3g} "
+                                  f"at {worst}")
+    return float(err.max())
+
+
+# batch, q_heads, kv_heads, q_len, kv_len, capacity, head_dim, start
+SHAPES = [
+    (1, 6, 2, 5, 7, 9, 64, 2),          # grouped, tiny, cache with spare rows
+    (1, 15, 5, 130, 130, 160, 64, 0),   # SmolLM2 heads, two ragged query tiles
+    (2, 4, 4, 100, 357, 400, 64, 257),  # batch 2, plain heads, chunked prefill
+    (1, 3, 1, 257, 257, 257, 32, 0),    # three query tiles (paired 0/2, 1 alone)
+    (1, 2, 1, 64, 64, 64, 96, 0),
+    (1, 2, 2, 200, 300, 300, 128, 100),
+    (1, 6, 2, 1, 2048, 4096, 64, 2047),  # decode step from a half-full cache
+    (1, 2, 1, 33, 40, 40, 48, 7),        # head size off the matrix-core path
+    (1, 2, 2, 17, 17, 20, 80, 0),
+    (1, 2, 1, 9, 300, 300, 256, 291),
+]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_attention_within_float64_bound(ctx, dtype, shape):
+    b, qh, kvh, ql, kl, cap, hd, start = shape
+    q = synth.normal(synth.seed_for("attn-q", *shape), (b, qh, ql, hd)).astype(dtype)
+    k = cache(synth.seed_for("attn-k", *shape), b, kvh, cap, hd, kl, dtype)
+    v = cache(synth.seed_for("attn-v", *shape), b, kvh, cap, hd, kl, dtype)
+    scale = 1.0 / np.sqrt(hd)
+    got = run_attention(ctx, q, k, v, scale, start, kl)
+    check(got, q, k, v, scale, start, kl, f"attention {np.dtype(dtype).name} {shape}")
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_attention_core_reference_kat(ctx, dtype):
+    """nn/attention.rs:590-668 (fused core == op-by-op calls within 1e-5):
+    (2, 2) and (3, 1) heads, D 4, 3 new positions after 2 cached."""
+    kat = K["attention_core"]
+    d, sl, start = kat["head_dim"], kat["seq_len"], kat["start_pos"]
+    for case in kat["cases"]:
+        qh, kvh = case["heads"]
+        q = (np.arange(qh * sl * d) % 5 - 2).astype(dtype).reshape(1, qh, sl, d)
+        kv = (np.arange(kvh * (start + sl) * d) % 3 - 1).astype(dtype).reshape(1, kvh, start + sl, d)
+        got = run_attention(ctx, q, kv, kv, 1.0 / np.sqrt(d), start, start + sl)
+        expected = np.array(case["expected"]).reshape(got.shape)
+        tol = kat["tol"] if dtype == np.float32 else 2.0 ** -10  # f16: the output's rounding
+        assert np.max(np.abs(got.astype(np.float64) - expected)) < tol, case["heads"]
+
+
+def test_attention_f16_is_closer_than_the_reference_composition(ctx):
+    """Both within their bounds; the fused pass (no f16 scores in between) is
+    the more accurate of the two on a SmolLM2-shaped block."""
+    shape = (1, 15, 5, 256, 256, 256, 64, 0)
+    b, qh, kvh, ql, kl, cap, hd, start = shape
+    q = synth.normal(101, (b, qh, ql, hd)).astype(np.float16)
+    k = synth.normal(102, (b, kvh, cap, hd)).astype(np.float16)
+    v = synth.normal(103, (b, kvh, cap, hd)).astype(np.float16)
+    got = run_attention(ctx, q, k, v, 0.125, start, kl)
+    fused_err = check(got, q, k, v, 0.125, start, kl, "fused")
+    ref = o.attention(q, k, v, 0.125, start)
+    exact, bound = attention_bound(q, k, v, 0.125, start, kl, "f16_reference")
+    ref_err = np.abs(ref.astype(np.float64) - exact)
+    assert np.all(ref_err <= bound)
+    assert fused_err <= float(ref_err.max())
+
+
+def test_attention_smollm_layer_f16(ctx):
+    """SmolLM2-360M layer at 4096 tokens: Q [1, 15, 4096, 64], K/V
+    [1, 5, 4096, 64] f16, causal, scale 1/8.  Every output is finite and
+    sampled query rows of every head (first, last, tile edges, random) are
+    within the float64 bound."""
+    q = synth.normal(201, (1, 15, 4096, 64)).astype(np.float16)
+    k = synth.normal(202, (1, 5, 4096, 64)).astype(np.float16)
+    v = synth.normal(203, (1, 5, 4096, 64)).astype(np.float16)
+    got = run_attention(ctx, q, k, v, 0.125, 0, 4096)
+    assert np.isfinite(got).all()
+    rows = sorted({0, 1, 31, 32, 127, 128, 2047, 2048, 4094, 4095} |
+                  set(np.random.default_rng(204).integers(0, 4096, 12).tolist()))
+    for r in rows:
+        exact, bound = attention_bound(q[:, :, r:r + 1], k, v, 0.125, r, 4096, "f16_fused")
+        err = np.abs(got[:, :, r:r + 1].astype(np.float64) - exact)
+        assert np.all(err <= bound), f"row {r}: max error {err.max():.3g}"
+    # row 0 attends to key 0 only: its output is V's first row of its KV head
+    assert np.array_equal(got[0, :, 0], np.repeat(v[0, :, 0], 3, axis=0))

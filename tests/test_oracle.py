@@ -10,8 +10,8 @@ planted-mistake tests at the end show that these checks catch plausible bugs.
 import numpy as np
 import pytest
 
-from helpers import (assert_bitexact, attention_exact, f16_ulp_distance, floats, gqa_expand, kats,
-                     max_rel_err)
+from helpers import (U32, assert_bitexact, attention_bound, f16_ulp_distance, floats, gqa_expand,
+                     kats, max_rel_err, ulp16)
 from oracle import oracle as o
 from rustllm_amd import synth
 
@@ -385,15 +385,6 @@ def test_rope_kat_f16_vs_f32():
 
 # ------------------------------------------------------------ attention core
 
-U32 = 2.0 ** -24
-
-
-def _ulp16(x):
-    """Spacing of binary16 at |x| (2^-24 below the normal range)."""
-    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -14)))
-    return 2.0 ** (e - 10)
-
-
 def _cache(seed, batch, heads, capacity, head_dim, kv_len, dtype=np.float32):
     """A [B, H, capacity, D] cache whose rows past kv_len hold NaN, so a read
     of an unused row shows up in every result."""
@@ -424,7 +415,7 @@ def test_gqa_qk_against_float64(case):
     got16 = o.gqa_qk(qh16, kh16, kl)
     dot16 = np.matmul(np.abs(qh16.astype(np.float64)),
                       np.swapaxes(np.abs(gqa_expand(kh16, qh, kl)), -1, -2))
-    assert np.all(np.abs(got16 - exact16) <= hd * U32 * dot16 + _ulp16(exact16) / 2 * 1.0001)
+    assert np.all(np.abs(got16 - exact16) <= hd * U32 * dot16 + ulp16(exact16) / 2 * 1.0001)
 
 
 @pytest.mark.parametrize("case", GQA_CASES)
@@ -442,7 +433,7 @@ def test_gqa_pv_against_float64(case):
     exact16 = np.matmul(p16.astype(np.float64), gqa_expand(v16, qh, kl))
     weight16 = np.matmul(p16.astype(np.float64), np.abs(gqa_expand(v16, qh, kl)))
     got16 = o.gqa_pv(p16, v16, kl)
-    assert np.all(np.abs(got16 - exact16) <= kl * U32 * weight16 + _ulp16(exact16) / 2 * 1.0001)
+    assert np.all(np.abs(got16 - exact16) <= kl * U32 * weight16 + ulp16(exact16) / 2 * 1.0001)
 
 
 def test_gqa_small_integers_are_exact():
@@ -458,17 +449,7 @@ def test_gqa_small_integers_are_exact():
 
 
 def _composition_bounds(q, k, v, scale, start, kv_len, f16):
-    exact, weight, dot_abs = attention_exact(q, k, v, scale, start, kv_len)
-    hd = q.shape[-1]
-    tmax = float(scale * np.max(dot_abs)) * 2 + 1
-    vmax = float(np.nanmax(np.abs(np.asarray(v, np.float64)[:, :, :kv_len])))
-    if f16:
-        rel = 2.0 ** -8 * scale * dot_abs[..., None] + 2.0 ** -9 + 8 * U32 * tmax + kv_len * U32
-        bound = rel * weight + kv_len * 2.0 ** -25 * vmax + _ulp16(exact)
-    else:
-        rel = 2 * scale * (hd + 1) * U32 * dot_abs[..., None] + 8 * U32 * tmax + (kv_len + 2) * U32
-        bound = rel * weight
-    return exact, bound
+    return attention_bound(q, k, v, scale, start, kv_len, "f16_reference" if f16 else "f32")
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
