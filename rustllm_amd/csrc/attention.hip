@@ -31,6 +31,7 @@
 // (relative error 2^-11 per probability, inside the same bound).
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 
@@ -39,6 +40,7 @@ namespace {
 
 typedef half_t h8 __attribute__((ext_vector_type(8)));
 typedef half_t h4 __attribute__((ext_vector_type(4)));
+typedef half_t h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.44269504088896340736f;
@@ -59,14 +61,20 @@ struct AttnParams {
 
 // ------------------------------------------------------------- MFMA kernel
 
-constexpr int kBlockKeys = 64;
-
 // Key order inside a 32-key tile: row i of the S^T tile holds key
 // perm32(i), bits 2 and 3 of i swapped.  With the 32x32 result layout (lane
 // l holds column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4 in register
 // r) register r of lane l then holds key 16 * (r / 8) + 8 * (l / 32) + r % 8.
 __device__ inline uint32_t perm32(uint32_t i) {
     return (i & ~12u) | ((i & 4u) << 1) | ((i & 8u) >> 1);
+}
+
+// max(a, b, c) in one v_max3_f32.  (fmaxf on a value the compiler cannot
+// prove canonical, such as an MFMA result, costs an extra v_max_f32 x, x.)
+__device__ inline float max3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
 }
 
 // ds_read_b64_tr_b16: in each group of 16 lanes, lanes 4j .. 4j + 3 read 8
@@ -89,13 +97,12 @@ constexpr float kRescaleSlack = 3.0f;
 // blocks of the tile between them (group g takes blocks g, g + KSPLIT, ...)
 // and merge their partial (max, sum, output) through LDS at the end, so a
 // tile keeps KSPLIT x QW waves busy.
-template <int NT, int QW, int KSPLIT>
+template <int NT, int QW, int KSPLIT, int BN, int STAGES, int PRIO>
 __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
     half_t* __restrict__ out, AttnParams p) {
     constexpr int D = 32 * NT;          // head size
     constexpr int DC = D / 16;          // 16-wide slices of a head (MFMA depth)
-    constexpr int BN = kBlockKeys;
     // LDS rows: K at a stride of D + 8 halves (a 16-byte read of 8
     // consecutive rows hits 8 distinct bank quads), V at D + 16 (the four
     // rows a transpose read of 16 lanes touches hit 32 distinct banks).
@@ -107,8 +114,8 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     constexpr int ROW_CHUNKS = D / 8;
     constexpr int KV_HALVES = BN * KS + BN * VS;       // one block of K and V
     constexpr int MERGE = NT * 16 + 2;                 // floats a lane hands over
-    constexpr int LDS_BYTES = KSPLIT * KV_HALVES * 2 > (KSPLIT - 1) * QW * 64 * MERGE * 4
-                                  ? KSPLIT * KV_HALVES * 2
+    constexpr int LDS_BYTES = STAGES * KSPLIT * KV_HALVES * 2 > (KSPLIT - 1) * QW * 64 * MERGE * 4
+                                  ? STAGES * KSPLIT * KV_HALVES * 2
                                   : (KSPLIT - 1) * QW * 64 * MERGE * 4;
     static_assert((BLOCK_CHUNKS * KSPLIT) % THREADS == 0, "blocks must split evenly");
     __shared__ __align__(16) unsigned char lds[LDS_BYTES];
@@ -127,8 +134,6 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t col = lane % 32;     // query column of this lane
     const uint32_t hs = lane / 32;      // which 8 of 16 in an MFMA slice
-    const half_t* ks = kv_lds + sub * KV_HALVES;
-    const half_t* vs = ks + BN * KS;
     // Transpose reads of V for the A operand of O^T += V^T P^T: lane
     // 16g + 4j + a reads row 8(g / 2) + j (+ 16c + 4e2 for slice c, half e2)
     // at columns 16(g % 2) + 4a (+ 32t for head tile t); the hardware then
@@ -181,6 +186,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
         float l = 0.0f;       // this lane's share of the running sum
 
         h8 kreg[LOADS], vreg[LOADS];
+        bool vlive[LOADS];
         auto load_step = [&](uint32_t step) {
 #pragma unroll
             for (int li = 0; li < LOADS; ++li) {
@@ -189,48 +195,56 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                 const uint32_t c = chunk % BLOCK_CHUNKS;
                 const uint32_t key = blk * BN + c / ROW_CHUNKS;
                 const uint32_t d0 = (c % ROW_CHUNKS) * 8;
-                if (key < p.kv_len) {
-                    kreg[li] = *reinterpret_cast<const h8*>(kh + uint64_t(key) * D + d0);
-                    vreg[li] = *reinterpret_cast<const h8*>(vh + uint64_t(key) * D + d0);
-                } else {
-                    // rows past kv_len are never read (they may hold anything)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        kreg[li][e] = half_t(0.0f);
-                        vreg[li][e] = half_t(0.0f);
-                    }
-                }
+                // Rows past kv_len are never read (they may hold anything): a
+                // key past the end loads row kv_len - 1 instead; its score is
+                // masked (selected to -inf) and its value row zeroed, so it
+                // adds nothing even if that row is not finite.
+                // (The zeroing happens at the LDS store, after the compute:
+                // a select here would make the wave wait for the load now.)
+                const uint32_t row = min(key, p.kv_len - 1);
+                kreg[li] = *reinterpret_cast<const h8*>(kh + uint64_t(row) * D + d0);
+                vreg[li] = *reinterpret_cast<const h8*>(vh + uint64_t(row) * D + d0);
+                vlive[li] = key < p.kv_len;
             }
         };
-        auto store_step = [&]() {
+        auto store_step = [&](uint32_t stage) {
 #pragma unroll
             for (int li = 0; li < LOADS; ++li) {
                 const uint32_t chunk = threadIdx.x + THREADS * li;
                 const uint32_t c = chunk % BLOCK_CHUNKS;
-                half_t* kdst = kv_lds + (chunk / BLOCK_CHUNKS) * KV_HALVES;
+                half_t* kdst = kv_lds + (stage * KSPLIT + chunk / BLOCK_CHUNKS) * KV_HALVES;
                 half_t* vdst = kdst + BN * KS;
                 const uint32_t key = c / ROW_CHUNKS;
                 const uint32_t d0 = (c % ROW_CHUNKS) * 8;
                 // K row `key` goes to LDS row perm32(key): the S^T operand of
                 // lane i is then LDS row i.
                 *reinterpret_cast<h8*>(kdst + perm32(key) * KS + d0) = kreg[li];
-                *reinterpret_cast<h8*>(vdst + key * VS + d0) = vreg[li];
+                const h8 zero = {};
+                *reinterpret_cast<h8*>(vdst + key * VS + d0) = vlive[li] ? vreg[li] : zero;
             }
         };
 
         load_step(0);
         __syncthreads();  // the previous tile's LDS use is over
-        store_step();
+        store_step(0);
         __syncthreads();
 
+        // With two stages the next block is stored into the other stage
+        // while this one is read: one barrier per step.
         for (uint32_t step = 0; step < steps; ++step) {
             if (step + 1 < steps) load_step(step + 1);
             const uint32_t blk = step * KSPLIT + sub;
+            const half_t* ks = kv_lds + ((step % STAGES) * KSPLIT + sub) * KV_HALVES;
+            const half_t* vs = ks + BN * KS;
             if (blk < blocks && blk * BN < wave_keys) {
-                // S^T = K Q^T for two 32-key tiles.
-                f32x16 s[2];
+                // S^T = K Q^T for BN / 32 tiles of 32 keys.
+                constexpr int KT = BN / 32;
+                f32x16 s[KT];
+                // A wave issuing matrix work goes first, so the other wave of
+                // the SIMD fills the vector ALU meanwhile (wave priority only).
+                if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(PRIO);
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt) {
+                for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
                     const half_t* krow = ks + (kt * 32 + col) * KS + 8 * hs;
@@ -239,23 +253,28 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                         s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                             *reinterpret_cast<const h8*>(krow + 16 * c), qf[c], s[kt], 0, 0, 0);
                 }
+                if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(0);
                 // mask; the block's max raw score of each query
                 const uint32_t kbase = blk * BN;
                 if (kbase + BN - 1 > p.start + q0 || kbase + BN > p.kv_len) {
 #pragma unroll
-                    for (int kt = 0; kt < 2; ++kt)
+                    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const uint32_t key = kbase + kt * 32 + 16 * (r >> 3) + 8 * hs + (r & 7);
                             if (key > key_limit) s[kt][r] = -INFINITY;
                         }
                 }
-                float mx = -INFINITY;
+                // two independent max chains, joined at the end
+                float mx = -INFINITY, my = -INFINITY;
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
+                for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 16; r += 2)
-                        mx = fmaxf(mx, fmaxf(s[kt][r], s[kt][r + 1]));
+                    for (int r = 0; r < 16; r += 4) {
+                        mx = max3(mx, s[kt][r], s[kt][r + 1]);
+                        my = max3(my, s[kt][r + 2], s[kt][r + 3]);
+                    }
+                mx = fmaxf(mx, my);
                 mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
                 const float mx_log2 = mx * p.scale_log2;
                 if (__any(mx_log2 > m + kRescaleSlack)) {
@@ -271,25 +290,26 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                 // p = 2^(s * scale * log2 e - m); a query that has seen no key
                 // yet (m = -inf) has only -inf scores here, and p = 0.
                 const float neg_m = m == -INFINITY ? 0.0f : -m;
-                float rs = 0.0f;
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt) {
+                for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float e =
+                    for (int r = 0; r < 16; ++r)
+                        s[kt][r] =
                             __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], p.scale_log2, neg_m));
-                        s[kt][r] = e;
-                        rs += e;
-                    }
-                }
-                l += rs;
                 // O^T += V^T P^T, 16 keys per MFMA: lane half hs supplies keys
                 // 16c + 8hs .. +7, which it holds in registers 8(c%2) .. +7 of tile c/2.
+                // The running sum adds the same f16 probabilities the product
+                // uses (v_dot2_f32_f16 against ones, f32 accumulation).
+                const h2 ones = {half_t(1.0f), half_t(1.0f)};
+                if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(PRIO);
 #pragma unroll
                 for (int c = 0; c < BN / 16; ++c) {
                     h8 pb;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) pb[e] = half_t(s[c >> 1][8 * (c & 1) + e]);
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2)
+                        l = __builtin_amdgcn_fdot2(h2{pb[e], pb[e + 1]}, ones, l, false);
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         const half_t* vsrc = vs + tr_off + 16 * c * VS + 32 * t;
@@ -299,9 +319,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[t], 0, 0, 0);
                     }
                 }
+                if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(0);
             }
-            __syncthreads();
-            if (step + 1 < steps) store_step();
+            if constexpr (STAGES == 1) __syncthreads();
+            if (step + 1 < steps) store_step((step + 1) % STAGES);
             __syncthreads();
         }
 
@@ -443,6 +464,231 @@ __global__ __launch_bounds__(64) void k_attention_rows(const T* __restrict__ q,
     }
 }
 
+// ------------------------------------------------- split keys (decode)
+
+// Few query rows per KV head (a decode step: R = group * q_len rows): the
+// rows of one KV head share every K and V row read.  Workgroup (kv head,
+// split) takes 64 keys per wave and writes one partial (max, sum, output
+// row) per query row; k_attention_combine merges the splits.  A wave's loads
+// are issued together -- its 64 value rows (contiguous in the cache) go
+// straight to LDS (global_load_lds), its key rows to registers -- so a split
+// costs one memory round trip.  RM bounds the rows, DPL the head elements
+// per lane (D <= 64 DPL).
+constexpr int kSplitWaves = 4;
+constexpr int kSplitKeys = 64 * kSplitWaves;   // keys per workgroup
+constexpr int kStageBytes = 64 * 256;          // LDS per wave for staged value rows
+
+template <typename T, int RM, int DPL>
+__global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    float* __restrict__ part, AttnParams p, uint32_t splits, bool vec_rows) {
+    constexpr int DMAX = 64 * DPL;
+    typedef typename Pack16<T>::type V;
+    constexpr int N = Pack16<T>::N;
+    __shared__ __align__(16) float qs[RM * DMAX];
+    __shared__ float ps[kSplitWaves][RM][64];
+    __shared__ __align__(16) unsigned char vstage[kSplitWaves][kStageBytes];
+    __shared__ float merge_m[kSplitWaves][RM];
+    __shared__ float merge_l[kSplitWaves][RM];
+    __shared__ float merge_o[kSplitWaves][RM][DMAX];
+    const uint32_t wave = threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t kvb = blockIdx.x / splits;  // b * kv_heads + kv head
+    const uint32_t split = blockIdx.x % splits;
+    const uint32_t kv_heads = p.q_heads / p.group;
+    const uint32_t b = kvb / kv_heads;
+    const uint32_t first_head = (kvb % kv_heads) * p.group;
+    const uint32_t R = p.group * p.q_len;
+    const uint32_t D = p.head_dim;
+    const T* kh = k + uint64_t(kvb) * p.kv_head_stride;
+    const T* vh = v + uint64_t(kvb) * p.kv_head_stride;
+    const uint32_t base = split * kSplitKeys + wave * 64;
+    const uint32_t n = p.kv_len > base ? min(64u, p.kv_len - base) : 0u;  // this wave's keys
+    const uint32_t key = base + lane;
+    // value rows to LDS when 64 of them fit the stage, else read in place
+    const bool staged = vec_rows && 64 * D * sizeof(T) <= kStageBytes;
+    if (staged) {
+        const uint32_t chunks = n * D * sizeof(T) / 16;  // 16-byte pieces of the n rows
+        const unsigned char* src = reinterpret_cast<const unsigned char*>(vh + uint64_t(base) * D);
+        for (uint32_t c0 = 0; c0 < chunks; c0 += 64) {
+            if (c0 + lane < chunks)
+                __builtin_amdgcn_global_load_lds(
+                    src + uint64_t(c0 + lane) * 16,
+                    (__attribute__((address_space(3))) void*)(vstage[wave] + c0 * 16), 16, 0, 0);
+        }
+    }
+    // key rows (lane = key), every load before the first use
+    constexpr int PACKS = DMAX / N;
+    V kv[PACKS];
+    if (vec_rows && lane < n) {
+        const T* krow = kh + uint64_t(key) * D;
+#pragma unroll
+        for (int i = 0; i < PACKS; ++i)
+            if (uint32_t(i * N) < D) kv[i] = *reinterpret_cast<const V*>(krow + i * N);
+    }
+    // row r = g * q_len + qi is query qi of head first_head + g
+    for (uint32_t i = threadIdx.x; i < RM * DMAX; i += 64 * kSplitWaves) {
+        const uint32_t r = i / DMAX, d = i % DMAX;
+        float x = 0.0f;
+        if (r < R && d < D) {
+            const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
+                                 r % p.q_len;
+            x = to_float(q[row * D + d]);
+        }
+        qs[i] = x;
+    }
+    __syncthreads();
+
+    float sc[RM];
+#pragma unroll
+    for (int r = 0; r < RM; ++r) sc[r] = 0.0f;
+    if (lane < n) {
+        if (vec_rows) {
+#pragma unroll
+            for (int i = 0; i < PACKS; ++i) {
+                if (uint32_t(i * N) >= D) break;
+#pragma unroll
+                for (int e = 0; e < N; e += 4) {
+#pragma unroll
+                    for (int r = 0; r < RM; ++r) {
+                        const float4 qv = *reinterpret_cast<const float4*>(qs + r * DMAX + i * N + e);
+                        sc[r] += qv.x * to_float(kv[i][e]) + qv.y * to_float(kv[i][e + 1]) +
+                                 qv.z * to_float(kv[i][e + 2]) + qv.w * to_float(kv[i][e + 3]);
+                    }
+                }
+            }
+        } else {
+            const T* krow = kh + uint64_t(key) * D;
+            for (uint32_t d = 0; d < D; ++d) {
+                const float kd = to_float(krow[d]);
+#pragma unroll
+                for (int r = 0; r < RM; ++r) sc[r] += qs[r * DMAX + d] * kd;
+            }
+        }
+    }
+    float m[RM], l[RM];
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        const uint32_t limit = p.start + uint32_t(r) % p.q_len;  // last key row r sees
+        const bool live = uint32_t(r) < R && lane < n && key <= limit;
+        const float x = live ? sc[r] * p.scale : -INFINITY;
+        m[r] = wave_max(x);
+        const float e = live ? exp_fast(x - m[r]) : 0.0f;
+        l[r] = e;  // this lane's share
+        ps[wave][r][lane] = e;
+    }
+    // the staged value rows have landed (vmcnt) and every wave's
+    // probabilities are in LDS (barrier)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    float o[RM][DPL];
+#pragma unroll
+    for (int r = 0; r < RM; ++r)
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) o[r][e] = 0.0f;
+    // eight keys at a time, their reads issued before the arithmetic; the
+    // LDS and the global variant are separate code so that each read is a
+    // plain ds_read or global_load (a pointer that may be either would make
+    // every read a flat access with a full wait).
+    auto pv = [&](const T* vbase) {
+        for (uint32_t j0 = 0; j0 < n; j0 += 8) {
+            float vv[8][DPL];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) {
+                    const uint32_t d = lane * DPL + e;
+                    vv[u][e] =
+                        (j0 + u < n && d < D) ? to_float(vbase[uint64_t(j0 + u) * D + d]) : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+#pragma unroll
+                for (int r = 0; r < RM; ++r) {
+                    const float pj = j0 + u < n ? ps[wave][r][j0 + u] : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < DPL; ++e) o[r][e] += pj * vv[u][e];
+                }
+            }
+        }
+    };
+    if (staged) {
+        pv(reinterpret_cast<const T*>(vstage[wave]));
+    } else {
+        pv(vh + uint64_t(base) * D);
+    }
+    // the four waves' states -> one partial per row
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        const float lsum = wave_sum(l[r]);
+        if (lane == 0) {
+            merge_m[wave][r] = m[r];
+            merge_l[wave][r] = lsum;
+        }
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) merge_o[wave][r][lane * DPL + e] = o[r][e];
+    }
+    __syncthreads();
+    const uint32_t stride = D + 2;
+    for (uint32_t r = wave; r < R; r += kSplitWaves) {
+        float mt = -INFINITY;
+        for (int w = 0; w < kSplitWaves; ++w) mt = fmaxf(mt, merge_m[w][r]);
+        float scale_w[kSplitWaves];
+        float lt = 0.0f;
+        for (int w = 0; w < kSplitWaves; ++w) {
+            scale_w[w] = merge_m[w][r] == -INFINITY ? 0.0f : exp_fast(merge_m[w][r] - mt);
+            lt += merge_l[w][r] * scale_w[w];
+        }
+        const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
+                             r % p.q_len;
+        float* dst = part + (row * splits + split) * stride;
+        for (uint32_t d = lane; d < D; d += 64) {
+            float acc = 0.0f;
+            for (int w = 0; w < kSplitWaves; ++w) acc += merge_o[w][r][d] * scale_w[w];
+            dst[2 + d] = acc;
+        }
+        if (lane == 0) {
+            dst[0] = mt;
+            dst[1] = lt;
+        }
+    }
+}
+
+// One wave per query row: merges the row's `splits` partials (the maxima and
+// sums read by all lanes at once, the weights kept in LDS).
+constexpr uint32_t kMaxSplits = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(64) void k_attention_combine(const float* __restrict__ part,
+                                                          T* __restrict__ out, uint32_t splits,
+                                                          uint32_t head_dim) {
+    __shared__ float w[kMaxSplits];
+    const uint64_t row = blockIdx.x;
+    const uint32_t stride = head_dim + 2;
+    const float* src = part + row * splits * stride;
+    float mt = -INFINITY;
+    for (uint32_t s = threadIdx.x; s < splits; s += 64) mt = fmaxf(mt, src[s * stride]);
+    mt = wave_max(mt);
+    float lt = 0.0f;
+    for (uint32_t s = threadIdx.x; s < splits; s += 64) {
+        const float ms = src[s * stride];
+        const float ws = ms == -INFINITY ? 0.0f : exp_fast(ms - mt);
+        w[s] = ws;
+        lt += src[s * stride + 1] * ws;
+    }
+    lt = wave_sum(lt);
+    __syncthreads();
+    const float inv = 1.0f / lt;
+    for (uint32_t d = threadIdx.x; d < head_dim; d += 64) {
+        float acc = 0.0f;
+#pragma unroll 8
+        for (uint32_t s = 0; s < splits; ++s) acc += src[s * stride + 2 + d] * w[s];
+        out[row * head_dim + d] = from_float<T>(acc * inv);
+    }
+}
+
 // ------------------------------------------------------------ validation
 
 struct AttnShape {
@@ -510,6 +756,9 @@ rl_status validate_attention(const rl_buffer* q, const rl_buffer* k, const rl_bu
 
 constexpr int kFlashQueryWaves = 4;
 constexpr int kFlashKeySplit = 2;
+constexpr int kFlashBlockKeys = 64;
+constexpr int kFlashStages = 1;
+constexpr int kFlashPriority = 0;
 
 // Which kernel a shape takes: the MFMA kernel for f16 with a head size of
 // 32, 64, 96 or 128 and aligned buffers; the row kernel otherwise (head
@@ -553,24 +802,64 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
     T* od = static_cast<T*>(out->data);
     const uint64_t heads = s.batch * s.q_heads;
 
+    const uint64_t rows = heads * s.q_len;
+    // Few rows per KV head (decode): split the keys over many workgroups.  Not while
+    // recording a graph: the partials live in a pool block that is released
+    // (and may be reused) once the launches are enqueued.
+    const uint64_t R = s.q_len * (s.q_heads / s.kv_heads);
+    const uint64_t dpl = ceil_div(s.head_dim, 64);
+    const uint64_t rm = R <= 4 ? 4 : R <= 8 ? 8 : R <= 16 ? 16 : 32;
+    const uint64_t needed = std::min<uint64_t>(s.kv_len, start + s.q_len);  // keys any row sees
+    const uint64_t splits = ceil_div(needed, kSplitKeys);
+    if (!ctx->capturing && R <= 32 && s.head_dim <= 256 && rm * dpl <= 32 && needed >= 512 &&
+        splits <= kMaxSplits) {
+        const bool vec_rows = s.head_dim % (16 / sizeof(T)) == 0 && aligned_to(kd, 16) &&
+                              aligned_to(vd, 16);
+        const uint64_t part_bytes = rows * splits * (s.head_dim + 2) * sizeof(float);
+        void* part = nullptr;
+        if (rl_status st = ctx->pool.allocate(part_bytes, &part)) return st;
+        const dim3 gs(static_cast<unsigned>(s.batch * s.kv_heads * splits)), bs(64 * kSplitWaves);
+        float* pf = static_cast<float*>(part);
+        const uint32_t sp = uint32_t(splits);
+#define RL_SPLIT(RMV, DPLV)                                                                    \
+    RL_LAUNCH(ctx, (k_attention_split<T, RMV, DPLV>), gs, bs, qd, kd, vd, pf, p, sp, vec_rows)
+        if (rm == 4 && dpl == 1) RL_SPLIT(4, 1);
+        else if (rm == 4 && dpl == 2) RL_SPLIT(4, 2);
+        else if (rm == 4) RL_SPLIT(4, 4);
+        else if (rm == 8 && dpl == 1) RL_SPLIT(8, 1);
+        else if (rm == 8 && dpl == 2) RL_SPLIT(8, 2);
+        else if (rm == 8) RL_SPLIT(8, 4);
+        else if (rm == 16 && dpl == 1) RL_SPLIT(16, 1);
+        else if (rm == 16) RL_SPLIT(16, 2);
+        else RL_SPLIT(32, 1);
+#undef RL_SPLIT
+        rl_status st = after_launch(ctx, name);
+        if (st == RL_OK) {
+            RL_LAUNCH(ctx, (k_attention_combine<T>), dim3(static_cast<unsigned>(rows)), dim3(64),
+                      pf, od, sp, uint32_t(s.head_dim));
+            st = after_launch(ctx, name);
+        }
+        ctx->pool.release(part);  // stream-ordered: later users run after these launches
+        return st;
+    }
     if constexpr (std::is_same<T, half_t>::value) {
         if (flash) {
             p.tiles = uint32_t(ceil_div(s.q_len, 32 * kFlashQueryWaves));
             p.pairs = (p.tiles + 1) / 2;
             const uint64_t grid = heads * p.pairs;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "attention grid exceeds u32");
-            constexpr int QW = kFlashQueryWaves, KSPLIT = kFlashKeySplit;
+            constexpr int QW = kFlashQueryWaves, KSPLIT = kFlashKeySplit, BN = kFlashBlockKeys,
+                          ST = kFlashStages, PR = kFlashPriority;
             const dim3 g(static_cast<unsigned>(grid)), b(64 * QW * KSPLIT);
             switch (s.head_dim / 32) {
-                case 1: RL_LAUNCH(ctx, (k_flash_attention<1, QW, KSPLIT>), g, b, qd, kd, vd, od, p); break;
-                case 2: RL_LAUNCH(ctx, (k_flash_attention<2, QW, KSPLIT>), g, b, qd, kd, vd, od, p); break;
-                case 3: RL_LAUNCH(ctx, (k_flash_attention<3, QW, KSPLIT>), g, b, qd, kd, vd, od, p); break;
-                default: RL_LAUNCH(ctx, (k_flash_attention<4, QW, KSPLIT>), g, b, qd, kd, vd, od, p); break;
+                case 1: RL_LAUNCH(ctx, (k_flash_attention<1, QW, KSPLIT, BN, ST, PR>), g, b, qd, kd, vd, od, p); break;
+                case 2: RL_LAUNCH(ctx, (k_flash_attention<2, QW, KSPLIT, BN, ST, PR>), g, b, qd, kd, vd, od, p); break;
+                case 3: RL_LAUNCH(ctx, (k_flash_attention<3, QW, KSPLIT, BN, ST, PR>), g, b, qd, kd, vd, od, p); break;
+                default: RL_LAUNCH(ctx, (k_flash_attention<4, QW, KSPLIT, BN, ST, PR>), g, b, qd, kd, vd, od, p); break;
             }
             return after_launch(ctx, name);
         }
     }
-    const uint64_t rows = heads * s.q_len;
     const dim3 g(static_cast<unsigned>(rows)), b(64);
     if (s.head_dim <= 64) {
         RL_LAUNCH(ctx, (k_attention_rows<T, 1>), g, b, qd, kd, vd, od, p);

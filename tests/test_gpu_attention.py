@@ -62,6 +62,17 @@ SHAPES = [
     (1, 2, 1, 9, 300, 300, 256, 291),
 ]
 
+# Few query rows per KV head over long key ranges: the split-key path
+# (rows per KV head 3..32, head sizes 64..256, f32 and f16).
+DECODE_SHAPES = [
+    (1, 15, 5, 1, 4096, 4096, 64, 4095),   # SmolLM2 decode at a full context
+    (2, 6, 2, 2, 1000, 1024, 64, 998),     # two new tokens, batch 2, 6 rows per KV head
+    (1, 8, 2, 4, 700, 800, 128, 696),      # 16 rows per KV head, D 128
+    (1, 4, 4, 1, 3000, 3000, 256, 2999),   # plain heads, D 256
+    (1, 32, 4, 4, 600, 600, 64, 596),      # 32 rows per KV head
+    (1, 3, 1, 1, 513, 520, 96, 512),       # just past the split threshold, D 96
+]
+
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
 @pytest.mark.parametrize("shape", SHAPES)
@@ -73,6 +84,12 @@ def test_attention_within_float64_bound(ctx, dtype, shape):
     scale = 1.0 / np.sqrt(hd)
     got = run_attention(ctx, q, k, v, scale, start, kl)
     check(got, q, k, v, scale, start, kl, f"attention {np.dtype(dtype).name} {shape}")
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+@pytest.mark.parametrize("shape", DECODE_SHAPES)
+def test_attention_decode_within_float64_bound(ctx, dtype, shape):
+    test_attention_within_float64_bound(ctx, dtype, shape)
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
