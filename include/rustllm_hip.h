@@ -407,6 +407,37 @@ rl_status rl_attention_f16(rl_context* ctx, const rl_buffer* q, const rl_buffer*
                            uint64_t kv_capacity, float scale, uint64_t query_start_pos,
                            const rl_buffer* out);
 
+/* Tensor::gqa_qk_matmul_encode (src/tensor/gqa_matmul.rs:23-61, kernels
+ * gqa_qk_f32/f16, kernels/gqa_matmul.metal:7-322): scores [batch, q_heads,
+ * q_len, kv_len] = Q K^T without repeating the KV heads; query head h reads
+ * KV head h / (q_heads / kv_heads).  q: contiguous [batch, q_heads, q_len,
+ * head_dim]; k: [batch, kv_heads, kv_capacity, head_dim], first kv_len rows
+ * per head used (the reference passes kv_capacity from K's head stride,
+ * :54-59).  f32 accumulation; the f16 score is rounded once.  Checks: head
+ * groups (RL_ERR_MODEL_FORMAT), the u32 limits of :192-212, kv_capacity >=
+ * kv_len, exact buffer lengths. */
+rl_status rl_gqa_qk_matmul_f32(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
+                               uint64_t batch, uint64_t q_heads, uint64_t kv_heads,
+                               uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                               uint64_t kv_capacity, const rl_buffer* out);
+rl_status rl_gqa_qk_matmul_f16(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
+                               uint64_t batch, uint64_t q_heads, uint64_t kv_heads,
+                               uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                               uint64_t kv_capacity, const rl_buffer* out);
+/* Tensor::gqa_pv_matmul_encode (src/tensor/gqa_matmul.rs:72-110, kernels
+ * gqa_pv_f32/f16, kernels/gqa_matmul.metal:323-629): out [batch, q_heads,
+ * q_len, head_dim] = P V for probabilities P [batch, q_heads, q_len, kv_len]
+ * (contiguous) and V [batch, kv_heads, kv_capacity, head_dim] (first kv_len
+ * rows per head).  Same checks as rl_gqa_qk_matmul_*. */
+rl_status rl_gqa_pv_matmul_f32(rl_context* ctx, const rl_buffer* probs, const rl_buffer* v,
+                               uint64_t batch, uint64_t q_heads, uint64_t kv_heads,
+                               uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                               uint64_t kv_capacity, const rl_buffer* out);
+rl_status rl_gqa_pv_matmul_f16(rl_context* ctx, const rl_buffer* probs, const rl_buffer* v,
+                               uint64_t batch, uint64_t q_heads, uint64_t kv_heads,
+                               uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                               uint64_t kv_capacity, const rl_buffer* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -141,6 +141,10 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                          _I32),
     "rl_attention_f32": ([_P, _BUF, _BUF, _BUF] + [_U64] * 7 + [_F, _U64, _BUF], _I32),
     "rl_attention_f16": ([_P, _BUF, _BUF, _BUF] + [_U64] * 7 + [_F, _U64, _BUF], _I32),
+    "rl_gqa_qk_matmul_f32": ([_P, _BUF, _BUF] + [_U64] * 7 + [_BUF], _I32),
+    "rl_gqa_qk_matmul_f16": ([_P, _BUF, _BUF] + [_U64] * 7 + [_BUF], _I32),
+    "rl_gqa_pv_matmul_f32": ([_P, _BUF, _BUF] + [_U64] * 7 + [_BUF], _I32),
+    "rl_gqa_pv_matmul_f16": ([_P, _BUF, _BUF] + [_U64] * 7 + [_BUF], _I32),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -465,6 +469,24 @@ class Context:
         out = out or self.empty(q.shape, q.dtype)
         self._call(f"rl_attention_{self._sfx(q)}", q, k, v, b, qh, kvh, ql, kv_len, hd, cap,
                    ctypes.c_float(scale), start, out)
+        return out
+
+    def gqa_qk(self, q, k, kv_len=None, out=None):
+        """Scores [B, QH, Q, kv_len] = Q K^T; k is [B, KVH, capacity, D]."""
+        b, qh, ql, hd = q.shape
+        kvh, cap = k.shape[1], k.shape[2]
+        kv_len = cap if kv_len is None else kv_len
+        out = out or self.empty((b, qh, ql, kv_len), q.dtype)
+        self._call(f"rl_gqa_qk_matmul_{self._sfx(q)}", q, k, b, qh, kvh, ql, kv_len, hd, cap, out)
+        return out
+
+    def gqa_pv(self, probs, v, out=None):
+        """[B, QH, Q, D] = P V for P [B, QH, Q, kv_len]; v is [B, KVH, capacity, D]."""
+        b, qh, ql, kv_len = probs.shape
+        kvh, cap, hd = v.shape[1], v.shape[2], v.shape[3]
+        out = out or self.empty((b, qh, ql, hd), probs.dtype)
+        self._call(f"rl_gqa_pv_matmul_{self._sfx(probs)}", probs, v, b, qh, kvh, ql, kv_len, hd,
+                   cap, out)
         return out
 
     def embedding(self, weight, token_ids, out=None):

@@ -27,7 +27,8 @@ CPP_TESTS = os.path.join(ROOT, "tests", "cpp", "tensor_tests.bin")
 
 ARCH = "gfx950"
 HIP_SOURCES = ["runtime.hip", "elementwise.hip", "movement.hip", "rmsnorm.hip", "softmax.hip",
-               "rope.hip", "kvcache.hip", "embedding.hip", "attention.hip"]
+               "rope.hip", "kvcache.hip", "embedding.hip", "attention.hip",
+               "gqa.hip"]
 
 
 def hipcc() -> str:

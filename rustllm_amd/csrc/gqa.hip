@@ -1,0 +1,466 @@
+// gqa.hip -- the grouped-query matmuls of the attention core for gfx950.
+//
+// gqa_qk_matmul (src/tensor/gqa_matmul.rs:23-61, kernels/gqa_matmul.metal:
+// 7-322): scores[b, h, i, j] = sum_d q[b, h, i, d] * k[b, h / g, j, d] over
+// the first kv_len of kv_capacity rows per KV head, f32 accumulation, the f16
+// score rounded once.  gqa_pv_matmul (:72-110, metal :323-629):
+// out[b, h, i, d] = sum_j p[b, h, i, j] * v[b, h / g, j, d].
+//
+// Both are bound by HBM (the [B, QH, Q, K] scores are written once or read
+// once; Q, K and V are small).  f16 with a head size of 32..128 in steps of
+// 32 takes the matrix cores (v_mfma_f32_32x32x16_f16):
+//  * QK^T computes S^T = K Q^T per wave (32 queries x 64 keys) with the keys
+//    of each 32-key tile read in the order that swaps bits 2 and 3 of the
+//    key index: every lane then holds two runs of 8 consecutive keys of one
+//    query row, stored as two 16-byte writes.  No LDS.
+//  * PV computes O^T = V^T P^T: each lane loads 8 consecutive probabilities
+//    of its query row (one 16-byte read), V blocks of 64 keys go through LDS
+//    and its transposed operand comes from ds_read_b64_tr_b16.
+// Other shapes (f32, other head sizes) take row kernels on the vector ALUs.
+#include "common.hpp"
+
+#include <type_traits>
+
+namespace rl {
+namespace {
+
+typedef half_t h8 __attribute__((ext_vector_type(8)));
+typedef half_t h4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+struct GqaParams {
+    uint32_t q_heads, group, q_len, kv_len, head_dim;
+    uint64_t kv_head_stride;  // elements between KV heads (kv_capacity * head_dim)
+    uint32_t q_tiles;         // query tiles per head (MFMA kernels)
+    uint32_t k_tiles;         // key tiles per query tile (QK^T MFMA kernel)
+};
+
+__device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
+    const uint32_t kv_heads = p.q_heads / p.group;
+    return (bh / p.q_heads) * kv_heads + (bh % p.q_heads) / p.group;
+}
+
+// Bits 2 and 3 swapped: row i of an S^T tile holds key perm32(i), and lane
+// l's register r then holds key 16 (r / 8) + 8 (l / 32) + r % 8.
+__device__ inline uint32_t perm32(uint32_t i) {
+    return (i & ~12u) | ((i & 4u) << 1) | ((i & 8u) >> 1);
+}
+
+// ------------------------------------------------------------ QK^T, MFMA
+
+template <int NT>
+__global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ q,
+                                                     const half_t* __restrict__ k,
+                                                     half_t* __restrict__ out, GqaParams p) {
+    constexpr int D = 32 * NT;
+    constexpr int DC = D / 16;
+    const uint32_t wave = threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t col = lane % 32;
+    const uint32_t hs = lane / 32;
+    // block = (head, 128-query tile, 128-key tile); wave = 32 queries x 64 keys
+    const uint32_t kt_blk = blockIdx.x % p.k_tiles;
+    const uint32_t rest = blockIdx.x / p.k_tiles;
+    const uint32_t qt = rest % p.q_tiles;
+    const uint32_t bh = rest / p.q_tiles;
+    const uint32_t q0 = qt * 128 + (wave % 4) * 32;
+    if (q0 >= p.q_len) return;
+    const half_t* kh = k + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
+    const uint32_t qi = q0 + col;
+    const bool q_valid = qi < p.q_len;
+    h8 qf[DC];
+    const half_t* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + 8 * hs;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+        if (q_valid) {
+            qf[c] = *reinterpret_cast<const h8*>(qrow + 16 * c);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[c][e] = half_t(0.0f);
+        }
+    }
+    half_t* orow = out + (uint64_t(bh) * p.q_len + qi) * p.kv_len;
+    const bool vec_store = p.kv_len % 8 == 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {  // four 32-key tiles of this block's 128 keys
+        const uint32_t k0 = kt_blk * 128 + t * 32;
+        if (k0 >= p.kv_len) break;
+        const uint32_t key = k0 + perm32(col);
+        const half_t* krow = kh + uint64_t(min(key, p.kv_len - 1)) * D + 8 * hs;
+        f32x16 s;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DC; ++c)
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(krow + 16 * c),
+                                                       qf[c], s, 0, 0, 0);
+        if (!q_valid) continue;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {  // keys k0 + 16 half + 8 hs + 0..7
+            const uint32_t kb = k0 + 16 * half + 8 * hs;
+            h8 w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) w[e] = half_t(s[8 * half + e]);
+            if (vec_store && kb + 8 <= p.kv_len) {
+                *reinterpret_cast<h8*>(orow + kb) = w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (kb + e < p.kv_len) orow[kb + e] = w[e];
+            }
+        }
+    }
+}
+
+// -------------------------------------------------------------- P V, MFMA
+
+__device__ inline h4 lds_read_transposed(const half_t* ptr) {
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(ptr));
+    return __builtin_bit_cast(h4, r);
+}
+
+template <int NT>
+__global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ probs,
+                                                     const half_t* __restrict__ v,
+                                                     half_t* __restrict__ out, GqaParams p) {
+    constexpr int D = 32 * NT;
+    constexpr int BN = 64;
+    constexpr int VS = D + 16;            // LDS row stride of V (transpose reads hit 32 banks)
+    constexpr int LOADS = BN * D / 8 / 256;
+    constexpr int ROW_CHUNKS = D / 8;
+    __shared__ __align__(16) half_t vs[BN * VS];
+    const uint32_t wave = threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t col = lane % 32;
+    const uint32_t hs = lane / 32;
+    const uint32_t qt = blockIdx.x % p.q_tiles;
+    const uint32_t bh = blockIdx.x / p.q_tiles;
+    const uint32_t q0 = qt * 128 + wave * 32;
+    const uint32_t qi = q0 + col;
+    const bool q_valid = qi < p.q_len;
+    const half_t* vh = v + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
+    const half_t* prow = probs + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * p.kv_len;
+    const bool vec_p = p.kv_len % 8 == 0;
+    const uint32_t tr_off = (8 * (lane / 32) + (lane % 16) / 4) * VS + 16 * ((lane / 16) % 2) +
+                            4 * (lane % 4);
+    f32x16 o[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+
+    const uint32_t blocks = (p.kv_len + BN - 1) / BN;
+    for (uint32_t blk = 0; blk < blocks; ++blk) {
+        // V block -> LDS (rows past kv_len as zeros)
+        __syncthreads();
+#pragma unroll
+        for (int li = 0; li < LOADS; ++li) {
+            const uint32_t chunk = threadIdx.x + 256 * li;
+            const uint32_t key = chunk / ROW_CHUNKS;
+            const uint32_t d0 = (chunk % ROW_CHUNKS) * 8;
+            const uint32_t gk = blk * BN + key;
+            h8 val = {};
+            if (gk < p.kv_len) val = *reinterpret_cast<const h8*>(vh + uint64_t(gk) * D + d0);
+            *reinterpret_cast<h8*>(vs + key * VS + d0) = val;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < BN / 16; ++c) {
+            // P^T operand: keys blk * 64 + 16 c + 8 hs + 0..7 of this lane's row
+            const uint32_t kb = blk * BN + 16 * c + 8 * hs;
+            h8 pb;
+            if (q_valid && vec_p && kb + 8 <= p.kv_len) {
+                pb = *reinterpret_cast<const h8*>(prow + kb);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    pb[e] = (q_valid && kb + e < p.kv_len) ? prow[kb + e] : half_t(0.0f);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const half_t* vsrc = vs + tr_off + 16 * c * VS + 32 * t;
+                const h4 lo = lds_read_transposed(vsrc);
+                const h4 hi = lds_read_transposed(vsrc + 4 * VS);
+                const h8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[t], 0, 0, 0);
+            }
+        }
+    }
+    if (q_valid) {
+        half_t* orow = out + (uint64_t(bh) * p.q_len + qi) * D + 4 * hs;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                h4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = half_t(o[t][4 * g + e]);
+                *reinterpret_cast<h4*>(orow + t * 32 + 8 * g) = w;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------ row kernels
+
+// QK^T: one workgroup per (query row, 256 keys); the query row is kept in
+// LDS as f32 and each thread forms one dot product in head order.
+template <typename T>
+__global__ __launch_bounds__(256) void k_gqa_qk_rows(const T* __restrict__ q,
+                                                     const T* __restrict__ k,
+                                                     T* __restrict__ out, GqaParams p,
+                                                     uint32_t key_blocks) {
+    extern __shared__ float qs[];
+    const uint64_t row = blockIdx.x / key_blocks;  // (b * QH + h) * q_len + i
+    const uint32_t key = (blockIdx.x % key_blocks) * 256 + threadIdx.x;
+    const uint32_t bh = uint32_t(row / p.q_len);
+    const uint32_t D = p.head_dim;
+    for (uint32_t d = threadIdx.x; d < D; d += 256) qs[d] = to_float(q[row * D + d]);
+    __syncthreads();
+    if (key >= p.kv_len) return;
+    const T* krow = k + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride + uint64_t(key) * D;
+    float sum = 0.0f;
+    for (uint32_t d = 0; d < D; ++d) sum += qs[d] * to_float(krow[d]);
+    out[row * p.kv_len + key] = from_float<T>(sum);
+}
+
+// P V: one workgroup per query row; the probabilities are kept in LDS as
+// f32 in chunks of 1024 keys, each thread owns output elements d and sums
+// over the keys in order.
+template <typename T>
+__global__ __launch_bounds__(256) void k_gqa_pv_rows(const T* __restrict__ probs,
+                                                     const T* __restrict__ v,
+                                                     T* __restrict__ out, GqaParams p) {
+    constexpr uint32_t CHUNK = 1024;
+    __shared__ float ps[CHUNK];
+    const uint64_t row = blockIdx.x;
+    const uint32_t bh = uint32_t(row / p.q_len);
+    const uint32_t D = p.head_dim;
+    const T* vh = v + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
+    const T* prow = probs + row * p.kv_len;
+    constexpr int DMAX = 4;  // head elements per thread (head sizes up to 1024)
+    float acc[DMAX] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t c0 = 0; c0 < p.kv_len; c0 += CHUNK) {
+        const uint32_t n = min(CHUNK, p.kv_len - c0);
+        __syncthreads();
+        for (uint32_t j = threadIdx.x; j < n; j += 256) ps[j] = to_float(prow[c0 + j]);
+        __syncthreads();
+        for (uint32_t j = 0; j < n; ++j) {
+            const float pj = ps[j];
+            const T* vrow = vh + uint64_t(c0 + j) * D;
+#pragma unroll
+            for (int e = 0; e < DMAX; ++e) {
+                const uint32_t d = threadIdx.x + 256 * e;
+                if (d < D) acc[e] += pj * to_float(vrow[d]);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < DMAX; ++e) {
+        const uint32_t d = threadIdx.x + 256 * e;
+        if (d < D) out[row * D + d] = from_float<T>(acc[e]);
+    }
+}
+
+// ------------------------------------------------------------ validation
+
+struct GqaShape {
+    uint64_t batch, q_heads, kv_heads, q_len, kv_len, head_dim, kv_capacity;
+};
+
+// gqa_matmul.rs: validate_head_groups (:174-182), then the u32 limits of
+// dispatch (:192-212).  Added: non-zero sizes (Shape::new, src/tensor/
+// shape.rs:9-23), kv_capacity >= kv_len and exact buffer lengths.
+rl_status validate_gqa(const char* op, const rl_buffer* left, const char* left_name,
+                       uint64_t left_len, const rl_buffer* right, const GqaShape& s,
+                       uint64_t es) {
+    if (rl_status st = check_buffer(left, left_name)) return st;
+    if (rl_status st = check_buffer(right, op[0] == 'Q' ? "key" : "value")) return st;
+    if (s.batch == 0 || s.q_heads == 0 || s.q_len == 0 || s.kv_len == 0 || s.head_dim == 0)
+        return fail(RL_ERR_INVALID_SHAPE, "GQA %s dimensions must be greater than zero", op);
+    if (s.kv_heads == 0 || s.q_heads % s.kv_heads != 0)
+        return fail(RL_ERR_MODEL_FORMAT, "Q heads %llu must be divisible by non-zero KV heads %llu",
+                    (unsigned long long)s.q_heads, (unsigned long long)s.kv_heads);
+    if (s.q_heads > UINT32_MAX || s.kv_heads > UINT32_MAX || s.q_len > UINT32_MAX ||
+        s.kv_len > UINT32_MAX || s.head_dim > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "GQA dimension exceeds u32");
+    if (s.kv_capacity > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "GQA KV capacity exceeds u32");
+    if (s.batch > UINT64_MAX / s.q_heads)
+        return fail(RL_ERR_INVALID_SHAPE, "GQA batch × query-head count overflow");
+    if (s.kv_capacity < s.kv_len)
+        return fail(RL_ERR_INVALID_SHAPE, "KV capacity %llu is smaller than the key length %llu",
+                    (unsigned long long)s.kv_capacity, (unsigned long long)s.kv_len);
+    const double kv_elems = double(s.batch) * double(s.kv_heads) * double(s.kv_capacity) *
+                            double(s.head_dim);
+    if (double(left_len) > double(UINT64_MAX / 16) || kv_elems > double(UINT64_MAX / 16))
+        return fail(RL_ERR_INVALID_SHAPE, "GQA %s operands are too large", op);
+    const uint64_t kvn = s.batch * s.kv_heads * s.kv_capacity * s.head_dim;
+    if (left->len != left_len || left->byte_len != left_len * es)
+        return fail(RL_ERR_INVALID_SHAPE, "%s buffer has %llu elements, expected %llu", left_name,
+                    (unsigned long long)left->len, (unsigned long long)left_len);
+    if (right->len != kvn || right->byte_len != kvn * es)
+        return fail(RL_ERR_INVALID_SHAPE, "%s buffer has %llu elements, expected %llu",
+                    op[0] == 'Q' ? "key" : "value", (unsigned long long)right->len,
+                    (unsigned long long)kvn);
+    if (s.batch * s.q_heads * s.q_len > UINT32_MAX)
+        return fail(RL_ERR_INVALID_SHAPE, "GQA row count exceeds u32");
+    return RL_OK;
+}
+
+GqaParams params_of(const GqaShape& s) {
+    GqaParams p{};
+    p.q_heads = uint32_t(s.q_heads);
+    p.group = uint32_t(s.q_heads / s.kv_heads);
+    p.q_len = uint32_t(s.q_len);
+    p.kv_len = uint32_t(s.kv_len);
+    p.head_dim = uint32_t(s.head_dim);
+    p.kv_head_stride = s.kv_capacity * s.head_dim;
+    return p;
+}
+
+template <typename T>
+bool use_mfma(const GqaShape& s, const void* a, const void* b, const void* o) {
+    if constexpr (!std::is_same<T, half_t>::value) {
+        return false;
+    } else {
+        return s.head_dim % 32 == 0 && s.head_dim <= 128 && aligned_to(a, 16) &&
+               aligned_to(b, 16) && aligned_to(o, 16);
+    }
+}
+
+template <typename T>
+rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const rl_buffer* k,
+                   const GqaShape& s, const rl_buffer* out) {
+    const uint64_t qn = s.batch * s.q_heads * s.q_len * s.head_dim;
+    if (rl_status st = validate_gqa("QK", q, "query", qn, k, s, sizeof(T))) return st;
+    const double on = double(s.batch) * double(s.q_heads) * double(s.q_len) * double(s.kv_len);
+    if (on > double(UINT64_MAX / 16))
+        return fail(RL_ERR_INVALID_SHAPE, "GQA QK output is too large");
+    if (rl_status st = check_output(out, s.batch * s.q_heads * s.q_len * s.kv_len, sizeof(T),
+                                    "GQA QK"))
+        return st;
+    if (rl_status st = require_context(ctx)) return st;
+    if (rl_status st = activate(ctx)) return st;
+    GqaParams p = params_of(s);
+    const T* qd = static_cast<const T*>(q->data);
+    const T* kd = static_cast<const T*>(k->data);
+    T* od = static_cast<T*>(out->data);
+    const uint64_t heads = s.batch * s.q_heads;
+    if constexpr (std::is_same<T, half_t>::value) {
+        if (use_mfma<T>(s, qd, kd, od)) {
+            p.q_tiles = uint32_t(ceil_div(s.q_len, 128));
+            p.k_tiles = uint32_t(ceil_div(s.kv_len, 128));
+            const uint64_t grid = heads * p.q_tiles * p.k_tiles;
+            if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
+            const dim3 g(static_cast<unsigned>(grid)), b(256);
+            switch (s.head_dim / 32) {
+                case 1: RL_LAUNCH(ctx, (k_gqa_qk_mfma<1>), g, b, qd, kd, od, p); break;
+                case 2: RL_LAUNCH(ctx, (k_gqa_qk_mfma<2>), g, b, qd, kd, od, p); break;
+                case 3: RL_LAUNCH(ctx, (k_gqa_qk_mfma<3>), g, b, qd, kd, od, p); break;
+                default: RL_LAUNCH(ctx, (k_gqa_qk_mfma<4>), g, b, qd, kd, od, p); break;
+            }
+            return after_launch(ctx, name);
+        }
+    }
+    const uint64_t key_blocks = ceil_div(s.kv_len, 256);
+    const uint64_t grid = heads * s.q_len * key_blocks;
+    if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
+    if (s.head_dim > 16384) return fail(RL_ERR_INVALID_SHAPE, "GQA QK head size exceeds 16384");
+    {
+        const dim3 g(static_cast<unsigned>(grid)), b(256);
+        const size_t lds = s.head_dim * sizeof(float);
+        if (ctx->timed_start != nullptr) {
+            hipExtLaunchKernelGGL((k_gqa_qk_rows<T>), g, b, lds, ctx->stream, ctx->timed_start,
+                                  ctx->timed_stop, 0, qd, kd, od, p, uint32_t(key_blocks));
+            ctx->timed_start = nullptr;
+            ctx->timed_stop = nullptr;
+        } else {
+            hipLaunchKernelGGL((k_gqa_qk_rows<T>), g, b, lds, ctx->stream, qd, kd, od, p,
+                               uint32_t(key_blocks));
+        }
+    }
+    return after_launch(ctx, name);
+}
+
+template <typename T>
+rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, const rl_buffer* v,
+                   const GqaShape& s, const rl_buffer* out) {
+    const double pn = double(s.batch) * double(s.q_heads) * double(s.q_len) * double(s.kv_len);
+    if (pn > double(UINT64_MAX / 16))
+        return fail(RL_ERR_INVALID_SHAPE, "GQA PV operands are too large");
+    const uint64_t plen = s.batch * s.q_heads * s.q_len * s.kv_len;
+    if (rl_status st = validate_gqa("PV", probs, "probability", plen, v, s, sizeof(T))) return st;
+    if (rl_status st = check_output(out, s.batch * s.q_heads * s.q_len * s.head_dim, sizeof(T),
+                                    "GQA PV"))
+        return st;
+    if (s.head_dim > 1024) return fail(RL_ERR_INVALID_SHAPE, "GQA PV head size exceeds 1024");
+    if (rl_status st = require_context(ctx)) return st;
+    if (rl_status st = activate(ctx)) return st;
+    GqaParams p = params_of(s);
+    const T* pd = static_cast<const T*>(probs->data);
+    const T* vd = static_cast<const T*>(v->data);
+    T* od = static_cast<T*>(out->data);
+    const uint64_t heads = s.batch * s.q_heads;
+    if constexpr (std::is_same<T, half_t>::value) {
+        if (use_mfma<T>(s, pd, vd, od)) {
+            p.q_tiles = uint32_t(ceil_div(s.q_len, 128));
+            const uint64_t grid = heads * p.q_tiles;
+            if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA PV grid exceeds u32");
+            const dim3 g(static_cast<unsigned>(grid)), b(256);
+            switch (s.head_dim / 32) {
+                case 1: RL_LAUNCH(ctx, (k_gqa_pv_mfma<1>), g, b, pd, vd, od, p); break;
+                case 2: RL_LAUNCH(ctx, (k_gqa_pv_mfma<2>), g, b, pd, vd, od, p); break;
+                case 3: RL_LAUNCH(ctx, (k_gqa_pv_mfma<3>), g, b, pd, vd, od, p); break;
+                default: RL_LAUNCH(ctx, (k_gqa_pv_mfma<4>), g, b, pd, vd, od, p); break;
+            }
+            return after_launch(ctx, name);
+        }
+    }
+    RL_LAUNCH(ctx, (k_gqa_pv_rows<T>), dim3(static_cast<unsigned>(heads * s.q_len)), dim3(256),
+              pd, vd, od, p);
+    return after_launch(ctx, name);
+}
+
+}  // namespace
+}  // namespace rl
+
+using namespace rl;
+
+extern "C" {
+
+rl_status rl_gqa_qk_matmul_f32(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
+                               uint64_t batch, uint64_t q_heads, uint64_t kv_heads,
+                               uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                               uint64_t kv_capacity, const rl_buffer* out) {
+    const GqaShape s{batch, q_heads, kv_heads, q_len, kv_len, head_dim, kv_capacity};
+    return qk_entry<float>(ctx, "gqa_qk_f32", q, k, s, out);
+}
+
+rl_status rl_gqa_qk_matmul_f16(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
+                               uint64_t batch, uint64_t q_heads, uint64_t kv_heads,
+                               uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                               uint64_t kv_capacity, const rl_buffer* out) {
+    const GqaShape s{batch, q_heads, kv_heads, q_len, kv_len, head_dim, kv_capacity};
+    return qk_entry<half_t>(ctx, "gqa_qk_f16", q, k, s, out);
+}
+
+rl_status rl_gqa_pv_matmul_f32(rl_context* ctx, const rl_buffer* probs, const rl_buffer* v,
+                               uint64_t batch, uint64_t q_heads, uint64_t kv_heads,
+                               uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                               uint64_t kv_capacity, const rl_buffer* out) {
+    const GqaShape s{batch, q_heads, kv_heads, q_len, kv_len, head_dim, kv_capacity};
+    return pv_entry<float>(ctx, "gqa_pv_f32", probs, v, s, out);
+}
+
+rl_status rl_gqa_pv_matmul_f16(rl_context* ctx, const rl_buffer* probs, const rl_buffer* v,
+                               uint64_t batch, uint64_t q_heads, uint64_t kv_heads,
+                               uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
+                               uint64_t kv_capacity, const rl_buffer* out) {
+    const GqaShape s{batch, q_heads, kv_heads, q_len, kv_len, head_dim, kv_capacity};
+    return pv_entry<half_t>(ctx, "gqa_pv_f16", probs, v, s, out);
+}
+
+}  // extern "C"

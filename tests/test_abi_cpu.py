@@ -415,3 +415,35 @@ def test_attention_validation(dt, es):
     assert st == SHAPE and "head size 520 exceeds 512" in msg
     st, msg = go(kl=1 << 33, cap=1 << 33, hd=1)
     assert st == SHAPE and "exceeds u32" in msg
+
+
+@pytest.mark.parametrize("op", ["qk", "pv"])
+@pytest.mark.parametrize("dt,es", [("f32", 4), ("f16", 2)])
+def test_gqa_matmul_validation(op, dt, es):
+    # gqa_matmul.rs: head groups (:174-182), the u32 limits of dispatch (:192-212),
+    # then the buffers
+    f = f"rl_gqa_{op}_matmul_{dt}"
+
+    def go(b=1, qh=6, kvh=2, ql=3, kl=5, hd=64, cap=8, ln=None, rn=None, on=None):
+        left = b * qh * ql * (hd if op == "qk" else kl)
+        out = b * qh * ql * (kl if op == "qk" else hd)
+        return call(f, buf(left if ln is None else ln, es),
+                    buf(b * kvh * cap * hd if rn is None else rn, es), b, qh, kvh, ql, kl, hd,
+                    cap, buf(out if on is None else on, es))
+
+    assert go()[0] == DEVICE
+    assert go(hd=48)[0] == DEVICE
+    st, msg = go(kl=0)
+    assert st == SHAPE and "greater than zero" in msg
+    st, msg = go(kvh=4)
+    assert st == FORMAT and "Q heads 6 must be divisible by non-zero KV heads 4" in msg
+    st, msg = go(kl=9)
+    assert st == SHAPE and "KV capacity 8 is smaller than the key length 9" in msg
+    st, msg = go(ln=7)
+    assert st == SHAPE and ("query buffer" in msg or "probability buffer" in msg)
+    st, msg = go(rn=7)
+    assert st == SHAPE and ("key buffer" in msg or "value buffer" in msg)
+    st, msg = go(on=7)
+    assert st == SHAPE and "output buffer" in msg
+    st, msg = go(kl=1 << 33, cap=1 << 33, hd=1, ql=1, qh=2, kvh=1)
+    assert st == SHAPE and "exceeds u32" in msg

@@ -143,3 +143,112 @@ def test_attention_smollm_layer_f16(ctx):
         assert np.all(err <= bound), f"row {r}: max error {err.max():.3g}"
     # row 0 attends to key 0 only: its output is V's first row of its KV head
     assert np.array_equal(got[0, :, 0], np.repeat(v[0, :, 0], 3, axis=0))
+
+
+# ------------------------------------------------- the reference's GQA matmuls
+
+U32 = 2.0 ** -24
+GQA_SHAPES = [  # batch, q_heads, kv_heads, q_len, kv_len, capacity, head_dim
+    (1, 15, 5, 130, 300, 320, 64),   # matrix-core path, ragged tiles, cache with spare rows
+    (2, 4, 4, 33, 64, 64, 128),      # plain heads, batch 2
+    (1, 6, 2, 7, 45, 50, 32),        # key count not a multiple of 8 (element stores)
+    (1, 3, 1, 17, 200, 200, 96),
+    (1, 2, 1, 9, 70, 80, 48),        # row kernels
+]
+
+
+def gqa_exact(q, k, kv_len):
+    from helpers import gqa_expand
+    ke = gqa_expand(k, q.shape[1], kv_len)
+    q64 = q.astype(np.float64)
+    return (np.matmul(q64, np.swapaxes(ke, -1, -2)),
+            np.matmul(np.abs(q64), np.swapaxes(np.abs(ke), -1, -2)))
+
+
+def ulp16(x):
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+@pytest.mark.parametrize("shape", GQA_SHAPES)
+def test_gqa_qk_within_float64_bound(ctx, dtype, shape):
+    """gqa_matmul.metal:7-322: f32 sums of the products (any order stays
+    within D u sum|q k| of the exact dot), the f16 score rounded once."""
+    b, qh, kvh, ql, kl, cap, hd = shape
+    q = synth.normal(synth.seed_for("gqa-q", *shape), (b, qh, ql, hd)).astype(dtype)
+    k = cache(synth.seed_for("gqa-k", *shape), b, kvh, cap, hd, kl, dtype)
+    ctx.begin()
+    got = ctx.gqa_qk(ctx.upload(q), ctx.upload(k), kl)
+    ctx.finish()
+    got = got.numpy().astype(np.float64)
+    exact, dot_abs = gqa_exact(q, k, kl)
+    bound = hd * U32 * dot_abs + (ulp16(exact) * 0.5001 if dtype == np.float16 else 0.0) + 1e-30
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+@pytest.mark.parametrize("shape", GQA_SHAPES)
+def test_gqa_pv_within_float64_bound(ctx, dtype, shape):
+    """gqa_matmul.metal:323-629: sum over kv_len keys of p v in f32."""
+    from helpers import gqa_expand
+    b, qh, kvh, ql, kl, cap, hd = shape
+    p = synth.uniform_range(synth.seed_for("gqa-p", *shape), (b, qh, ql, kl), 0.0, 1.0, dtype)
+    v = cache(synth.seed_for("gqa-v", *shape), b, kvh, cap, hd, kl, dtype)
+    ctx.begin()
+    got = ctx.gqa_pv(ctx.upload(p), ctx.upload(v))
+    ctx.finish()
+    got = got.numpy().astype(np.float64)
+    ve = gqa_expand(v, qh, kl)
+    exact = np.matmul(p.astype(np.float64), ve)
+    weight = np.matmul(p.astype(np.float64), np.abs(ve))
+    bound = kl * U32 * weight + (ulp16(exact) * 0.5001 if dtype == np.float16 else 0.0) + 1e-30
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_gqa_small_integers_match_the_oracle_bit_for_bit(ctx, dtype):
+    """Small-integer operands make every sum exact: the library (matrix cores
+    or row kernels) and the oracle agree exactly."""
+    for hd in (64, 48):
+        q = (np.arange(1 * 6 * 40 * hd) % 7 - 3).reshape(1, 6, 40, hd).astype(dtype)
+        k = (np.arange(1 * 2 * 72 * hd) % 5 - 2).reshape(1, 2, 72, hd).astype(dtype)
+        ctx.begin()
+        s = ctx.gqa_qk(ctx.upload(q), ctx.upload(k))
+        pv = ctx.gqa_pv(ctx.upload((o.gqa_qk(q, k) / 64).astype(dtype)), ctx.upload(k))
+        ctx.finish()
+        assert np.array_equal(s.numpy(), o.gqa_qk(q, k))
+        assert np.array_equal(pv.numpy(), o.gqa_pv((o.gqa_qk(q, k) / 64).astype(dtype), k))
+
+
+def test_unfused_chain_f16_within_the_reference_bound(ctx):
+    """The reference's four calls on the library (gqa_qk, scale/mask +
+    softmax, gqa_pv) with the reference's rounding points stay within the
+    forward bound of those roundings, like the oracle's composition."""
+    from helpers import attention_bound
+    b, qh, kvh, ql, kl, hd, start = 1, 15, 5, 200, 200, 64, 0
+    q = synth.normal(301, (b, qh, ql, hd)).astype(np.float16)
+    k = synth.normal(302, (b, kvh, kl, hd)).astype(np.float16)
+    v = synth.normal(303, (b, kvh, kl, hd)).astype(np.float16)
+    ctx.begin()
+    s = ctx.gqa_qk(ctx.upload(q), ctx.upload(k))
+    p = ctx.attention_softmax(s, 0.125, start)
+    got = ctx.gqa_pv(p, ctx.upload(v))
+    ctx.finish()
+    exact, bound = attention_bound(q, k, v, 0.125, start, kl, "f16_reference")
+    assert np.all(np.abs(got.numpy().astype(np.float64) - exact) <= bound)
+
+
+def test_gqa_qk_smollm_layer_f16_sampled_rows(ctx):
+    """Full SmolLM2 shape (Q [1, 15, 4096, 64] x K [1, 5, 4096, 64]^T, a
+    503 MB score tensor): sampled rows of every head against float64."""
+    q = synth.normal(311, (1, 15, 4096, 64)).astype(np.float16)
+    k = synth.normal(312, (1, 5, 4096, 64)).astype(np.float16)
+    ctx.begin()
+    s = ctx.gqa_qk(ctx.upload(q), ctx.upload(k))
+    ctx.finish()
+    got = s.numpy()
+    for r in (0, 127, 128, 2049, 4095):
+        exact, dot_abs = gqa_exact(q[:, :, r:r + 1], k, 4096)
+        bound = 64 * U32 * dot_abs + ulp16(exact) * 0.5001
+        assert np.all(np.abs(got[:, :, r:r + 1].astype(np.float64) - exact) <= bound), r
