@@ -35,6 +35,7 @@ sys.path.insert(0, ROOT)
 from rustllm_amd import abi, synth  # noqa: E402
 
 PEAK_GBS = 8000.0
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 METRIC = "achieved HBM GB/s & % of MI355X peak per op (RMSNorm, softmax, SwiGLU, RoPE)"
 F32, F16 = np.float32, np.float16
 T, H = 4096, 1536
@@ -506,8 +507,10 @@ def extra_rows(ctx, reps, quick):
     measure("layer.6 residual add_f16", "f16", [tok, hid], 3 * r.size * 2,
             lambda i: (ctx.upload(x), ctx.upload(r), ctx.empty(r.shape, F16)),
             lambda s: ctx.add(s[0], s[1], s[2]))
+    rows.extend(attention_rows(ctx, qh, kvh, hd, tok, reps))
     if not quick:
         rows.append(layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds))
+        rows.append(fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds))
     # [64, 768] f32 (the reference's CPU-runnable case), fused add + RMSNorm
     # (writes the sum and the norm)
     x0 = synth.normal(1, (64, 768), 0, 1, F32)
@@ -517,6 +520,150 @@ def extra_rows(ctx, reps, quick):
                        ctx.empty(x0.shape, F32)),
             lambda s: ctx.add_rmsnorm(s[0], s[1], w0, 1e-5, s[2], s[3]))
     return rows
+
+
+def attention_flops(qh, q_len, kv_len, hd, start):
+    """2 x 2 D flops per (query, visible key): QK^T and PV, causal."""
+    keys = sum(min(kv_len, start + i + 1) for i in range(q_len))
+    return 4.0 * hd * keys * qh
+
+
+def attention_rows(ctx, qh, kvh, hd, tok, reps):
+    """SmolLM2-360M attention core at 4096 tokens, f16: the fused pass
+    (rl_attention_f16, matrix cores; TFLOP/s vs the 2.5 PF dense f16 peak),
+    the reference's unfused calls (gqa_qk, scale/mask + softmax, gqa_pv) one
+    by one and as one graph, and a decode step over a 4096-row cache."""
+    rows = []
+    q = synth.normal(synth.seed_for("c5", "attn-q"), (1, qh, tok, hd), 0, 1, F16)
+    k = synth.normal(synth.seed_for("c5", "attn-k"), (1, kvh, tok, hd), 0, 1, F16)
+    v = synth.normal(synth.seed_for("c5", "attn-v"), (1, kvh, tok, hd), 0, 1, F16)
+    flops = attention_flops(qh, tok, tok, hd, 0)
+    sets = [(ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.empty(q.shape, F16))
+            for _ in range(4)]
+    io_bytes = (q.size + 2 * k.size + q.size) * 2
+    timing = kernel_times_us(ctx, [lambda s=s: ctx.attention(s[0], s[1], s[2], 0.125, 0, None,
+                                                                s[3]) for s in sets], reps)
+    row = op_row("layer.4 attention_f16 (fused, matrix cores)", "f16", [1, qh, tok, hd],
+                 io_bytes, timing)
+    us = row["us"]
+    row.update({"flops": flops, "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1),
+                "pct_peak_mfma": round(100 * flops / (us * 1e-6) / 1e12 / PEAK_F16_TFLOPS, 1)})
+    log(f"    -> {row['TFLOP/s']} TFLOP/s ({row['pct_peak_mfma']}% of the dense f16 peak)")
+    rows.append(row)
+    # the reference's calls: scores written (503 MB), softmaxed, read back
+    n_scores = qh * tok * tok
+    unmasked = qh * (tok * (tok + 1) // 2)
+    s0 = sets[0]
+    sc = [ctx.empty((1, qh, tok, tok), F16) for _ in range(2)]
+    pr = [ctx.empty((1, qh, tok, tok), F16) for _ in range(2)]
+    out = ctx.empty(q.shape, F16)
+    qk_bytes = (q.size + k.size + n_scores) * 2
+    rows.append(op_row("layer.4 gqa_qk_f16 (scores)", "f16", [1, qh, tok, tok], qk_bytes,
+                       kernel_times_us(ctx, [lambda i=i: ctx.gqa_qk(s0[0], s0[1], None, sc[i])
+                                             for i in range(2)], reps)))
+    pv_bytes = (n_scores + v.size + q.size) * 2
+    rows.append(op_row("layer.4 gqa_pv_f16", "f16", [1, qh, tok, hd], pv_bytes,
+                       kernel_times_us(ctx, [lambda i=i: ctx.gqa_pv(pr[i], s0[2], out)
+                                             for i in range(2)], reps)))
+
+    def chain(i):
+        ctx.gqa_qk(s0[0], s0[1], None, sc[i])
+        ctx.attention_softmax(sc[i], 0.125, 0, pr[i])
+        ctx.gqa_pv(pr[i], s0[2], out)
+
+    graphs = [capture(ctx, lambda i=i: chain(i)) for i in range(2)]
+    ms = time_graphs(ctx, graphs, 1, 10)
+    ctx.finish()
+    for g in graphs:
+        ctx.graph_destroy(g)
+    chain_us = ms * 1e3
+    chain_bytes = qk_bytes + unmasked * 2 + n_scores * 2 + pv_bytes
+    log(f"  {'layer.4 unfused QK, softmax, PV (graph)':34s} {chain_us:9.2f} us "
+        f"(fused: {us:.2f} us, {chain_us / us:.1f}x)")
+    rows.append({"op": "layer.4 unfused gqa_qk + scale/mask softmax + gqa_pv (one graph)",
+                 "dtype": "f16", "shape": [1, qh, tok, hd], "bytes": chain_bytes,
+                 "us": round(chain_us, 3), "us_min": None,
+                 "GB/s": round(chain_bytes / (chain_us * 1e-6) / 1e9, 1),
+                 "pct_peak": round(100 * chain_bytes / (chain_us * 1e-6) / 1e9 / PEAK_GBS, 1),
+                 "flops": flops, "TFLOP/s": round(flops / (chain_us * 1e-6) / 1e12, 1),
+                 "fused_speedup": round(chain_us / us, 2),
+                 "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None})
+    del sc, pr
+    # decode: one new token of 15 heads over a 4096-row KV cache (two launches:
+    # split keys, combine), timed with stream events around the call
+    qd = ctx.upload(q[:, :, :1].copy())
+    od = ctx.empty((1, qh, 1, hd), F16)
+    for _ in range(3):
+        ctx.attention(qd, s0[1], s0[2], 0.125, tok - 1, None, od)
+    ctx.finish()
+    evs = [(ctx.event(), ctx.event()) for _ in range(reps)]
+    for a, b in evs:
+        ctx.record(a)
+        ctx.attention(qd, s0[1], s0[2], 0.125, tok - 1, None, od)
+        ctx.record(b)
+    ctx.finish()
+    dec_us = float(np.median([ctx.elapsed_ms(a, b) * 1e3 for a, b in evs]))
+    for e in [e for pair in evs for e in pair]:
+        ctx.destroy_event(e)
+    dec_bytes = (2 * k.size + 2 * qh * hd) * 2
+    log(f"  {'decode attention_f16 over 4096 keys':34s} {dec_us:9.2f} us "
+        f"{dec_bytes / (dec_us * 1e-6) / 1e9:8.1f} GB/s (2 launches, event-timed)")
+    rows.append({"op": "decode attention_f16 (1 token, 4096-row cache, 2 launches)", "dtype": "f16",
+                 "shape": [1, qh, 1, hd], "bytes": dec_bytes, "us": round(dec_us, 3),
+                 "us_min": None, "GB/s": round(dec_bytes / (dec_us * 1e-6) / 1e9, 1),
+                 "pct_peak": round(100 * dec_bytes / (dec_us * 1e-6) / 1e9 / PEAK_GBS, 1),
+                 "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None})
+    return rows
+
+
+def fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20):
+    """One SmolLM2-360M layer's non-projection work with the attention fused:
+    RMSNorm, Q/K rotation + K/V append (one launch), the fused attention core,
+    SwiGLU, residual add -- 5 launches as one graph.  Bytes are the launches'
+    algorithmic bytes (the attention counted by its inputs and output)."""
+    qdims, qstrides = [1, qh, tok, hd], [tok * qh * hd, hd, qh * hd, 1]
+    kdims, kstrides = [1, kvh, tok, hd], [tok * kvh * hd, hd, kvh * hd, 1]
+    nbytes = (tok * hid * 4 + hid * 2                                    # RMSNorm
+              + 2 * (qh + 2 * kvh) * tok * hd * 2 + 2 * tok * (hd // 2) * 4  # QKV rotate + append
+              + (2 * qh + 2 * kvh) * tok * hd * 2                        # attention in/out
+              + 3 * tok * ffn * 2 + 3 * tok * hid * 2)                   # SwiGLU, residual
+
+    def make(i):
+        key = ("fused-layer", i)
+        b = {"x": ctx.upload(synth.normal(synth.seed_for(*key, "x"), (tok, hid), 0, 1, F16)),
+             "q": ctx.upload(synth.normal(synth.seed_for(*key, "q"), (1, tok, qh, hd), 0, 1, F16)),
+             "k": ctx.upload(synth.normal(synth.seed_for(*key, "k"), (1, tok, kvh, hd), 0, 1, F16)),
+             "v": ctx.upload(synth.normal(synth.seed_for(*key, "v"), (1, tok, kvh, hd), 0, 1, F16)),
+             "g": ctx.upload(synth.normal(synth.seed_for(*key, "g"), (tok, ffn), 0, 1, F16)),
+             "u": ctx.upload(synth.normal(synth.seed_for(*key, "u"), (tok, ffn), 0, 1, F16)),
+             "r": ctx.upload(synth.normal(synth.seed_for(*key, "r"), (tok, hid), 0, 1, F16))}
+        b.update({"xn": ctx.empty((tok, hid), F16), "qr": ctx.empty(qdims, F16),
+                  "kc": ctx.empty(kdims, F16), "vc": ctx.empty(kdims, F16),
+                  "a": ctx.empty(qdims, F16), "h": ctx.empty((tok, ffn), F16),
+                  "o": ctx.empty((tok, hid), F16)})
+        return b
+
+    def layer(b):
+        ctx.rmsnorm(b["x"], wn, 1e-5, b["xn"])
+        ctx.qkv_rope_kv_append((b["q"], qdims, qstrides), (b["k"], kdims, kstrides),
+                               (b["v"], kdims, kstrides), dc, ds, 0, b["kc"], b["vc"], b["qr"])
+        ctx.attention(b["qr"], b["kc"], b["vc"], 0.125, 0, None, b["a"])
+        ctx.swiglu(b["g"], b["u"], b["h"])
+        ctx.add(b["xn"], b["r"], b["o"])
+
+    bufs = [make(i) for i in range(sets)]
+    graphs = [capture(ctx, lambda b=b: layer(b)) for b in bufs]
+    ms = time_graphs(ctx, graphs, 1, reps)
+    ctx.finish()
+    for g in graphs:
+        ctx.graph_destroy(g)
+    us = ms * 1e3
+    log(f"  {'layer with fused attention (5 launches)':34s} {us:9.2f} us")
+    return {"op": "layer with fused attention (5 launches, one graph)", "dtype": "f16",
+            "shape": [tok, hid], "bytes": nbytes, "us": round(us, 3), "us_min": None,
+            "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_GBS, 1),
+            "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None}
 
 
 def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20):
