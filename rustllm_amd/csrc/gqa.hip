@@ -9,13 +9,15 @@
 // Both are bound by HBM (the [B, QH, Q, K] scores are written once or read
 // once; Q, K and V are small).  f16 with a head size of 32..128 in steps of
 // 32 takes the matrix cores (v_mfma_f32_32x32x16_f16):
-//  * QK^T computes S^T = K Q^T per wave (32 queries x 64 keys) with the keys
-//    of each 32-key tile read in the order that swaps bits 2 and 3 of the
-//    key index: every lane then holds two runs of 8 consecutive keys of one
-//    query row, stored as two 16-byte writes.  No LDS.
-//  * PV computes O^T = V^T P^T: each lane loads 8 consecutive probabilities
-//    of its query row (one 16-byte read), V blocks of 64 keys go through LDS
-//    and its transposed operand comes from ds_read_b64_tr_b16.
+//  * QK^T computes S^T = K Q^T per wave (32 queries x 128 keys): the
+//    workgroup's 128 key rows are loaded whole into LDS in the order that
+//    swaps bits 2 and 3 of the key index, so every lane ends up holding runs
+//    of 8 consecutive keys of one query row; each wave stages its score tile
+//    in LDS and writes whole 256-byte row segments per 16 lanes.
+//  * PV computes O^T = V^T P^T in steps of 128 keys: each wave stages its
+//    32 x 128 probabilities in LDS (whole 256-byte row segments per 16
+//    lanes), V goes through LDS row-major and its transposed operand comes
+//    from ds_read_b64_tr_b16; the next step's loads are in flight meanwhile.
 // Other shapes (f32, other head sizes) take row kernels on the vector ALUs.
 #include "common.hpp"
 
@@ -55,18 +57,35 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
                                                      half_t* __restrict__ out, GqaParams p) {
     constexpr int D = 32 * NT;
     constexpr int DC = D / 16;
+    constexpr int TS = 128 + 8;  // LDS row stride (halves) of a wave's 32 x 128 score tile
+    constexpr int KS = D + 8;    // LDS row stride (halves) of the key tile
+    constexpr int ROW_CHUNKS = D / 8;
+    __shared__ __align__(16) half_t tile[4][32 * TS];
+    __shared__ __align__(16) half_t ks[128 * KS];
     const uint32_t wave = threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t col = lane % 32;
     const uint32_t hs = lane / 32;
-    // block = (head, 128-query tile, 128-key tile); wave = 32 queries x 64 keys
+    // block = (head, 128-query tile, 128-key tile); wave = 32 queries x 128 keys
     const uint32_t kt_blk = blockIdx.x % p.k_tiles;
     const uint32_t rest = blockIdx.x / p.k_tiles;
     const uint32_t qt = rest % p.q_tiles;
     const uint32_t bh = rest / p.q_tiles;
-    const uint32_t q0 = qt * 128 + (wave % 4) * 32;
-    if (q0 >= p.q_len) return;
+    const uint32_t q0 = qt * 128 + wave * 32;
     const half_t* kh = k + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
+    const uint32_t kbase = kt_blk * 128;
+    // the block's 128 key rows -> LDS, whole rows per 8 (D 64) lanes; key row
+    // j goes to LDS row perm32(j) so that the S^T operand of lane i is row i.
+    // Keys past kv_len read row kv_len - 1 (their scores are not stored).
+#pragma unroll
+    for (int li = 0; li < 128 * ROW_CHUNKS / 256; ++li) {
+        const uint32_t chunk = threadIdx.x + 256 * li;
+        const uint32_t j = chunk / ROW_CHUNKS;
+        const uint32_t d0 = (chunk % ROW_CHUNKS) * 8;
+        const uint32_t key = min(kbase + j, p.kv_len - 1);
+        *reinterpret_cast<h8*>(ks + perm32(j) * KS + d0) =
+            *reinterpret_cast<const h8*>(kh + uint64_t(key) * D + d0);
+    }
     const uint32_t qi = q0 + col;
     const bool q_valid = qi < p.q_len;
     h8 qf[DC];
@@ -80,14 +99,14 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
             for (int e = 0; e < 8; ++e) qf[c][e] = half_t(0.0f);
         }
     }
-    half_t* orow = out + (uint64_t(bh) * p.q_len + qi) * p.kv_len;
-    const bool vec_store = p.kv_len % 8 == 0;
+    __syncthreads();
+    if (q0 >= p.q_len) return;  // (no barrier below)
+    half_t* my = tile[wave];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {  // four 32-key tiles of this block's 128 keys
-        const uint32_t k0 = kt_blk * 128 + t * 32;
+    for (int t = 0; t < 4; ++t) {  // four 32-key tiles
+        const uint32_t k0 = kbase + t * 32;
         if (k0 >= p.kv_len) break;
-        const uint32_t key = k0 + perm32(col);
-        const half_t* krow = kh + uint64_t(min(key, p.kv_len - 1)) * D + 8 * hs;
+        const half_t* krow = ks + (t * 32 + col) * KS + 8 * hs;
         f32x16 s;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[r] = 0.0f;
@@ -95,20 +114,34 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
         for (int c = 0; c < DC; ++c)
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(krow + 16 * c),
                                                        qf[c], s, 0, 0, 0);
-        if (!q_valid) continue;
+        // lane (query col, hs) holds keys k0 + 16 half + 8 hs + 0..7
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {  // keys k0 + 16 half + 8 hs + 0..7
-            const uint32_t kb = k0 + 16 * half + 8 * hs;
+        for (int half = 0; half < 2; ++half) {
             h8 w;
 #pragma unroll
             for (int e = 0; e < 8; ++e) w[e] = half_t(s[8 * half + e]);
-            if (vec_store && kb + 8 <= p.kv_len) {
-                *reinterpret_cast<h8*>(orow + kb) = w;
-            } else {
+            *reinterpret_cast<h8*>(my + col * TS + t * 32 + 16 * half + 8 * hs) = w;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // rows of the tile to memory: 16 lanes per 256-byte row segment
+    const uint32_t keys_here = min(128u, p.kv_len - kbase);
+    const bool vec_store = p.kv_len % 8 == 0;
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (kb + e < p.kv_len) orow[kb + e] = w[e];
-            }
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t r = i * 4 + lane / 16;  // tile row (query q0 + r)
+        const uint32_t c8 = (lane % 16) * 8;   // first key of this lane's 8
+        if (q0 + r >= p.q_len || c8 >= keys_here) continue;
+        const h8 w = *reinterpret_cast<const h8*>(my + r * TS + c8);
+        half_t* dst = out + (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase + c8;
+        if (vec_store && c8 + 8 <= keys_here) {
+            __builtin_nontemporal_store(w, reinterpret_cast<h8*>(dst));  // streamed out once
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (c8 + e < keys_here) dst[e] = w[e];
         }
     }
 }
@@ -126,11 +159,14 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
                                                      const half_t* __restrict__ v,
                                                      half_t* __restrict__ out, GqaParams p) {
     constexpr int D = 32 * NT;
-    constexpr int BN = 64;
+    constexpr int BN = 128;               // keys per step
+    constexpr int PC = BN / 16;           // 16-key slices per step
     constexpr int VS = D + 16;            // LDS row stride of V (transpose reads hit 32 banks)
+    constexpr int PS = BN + 8;            // LDS row stride of a wave's 32 x 128 probability tile
     constexpr int LOADS = BN * D / 8 / 256;
     constexpr int ROW_CHUNKS = D / 8;
     __shared__ __align__(16) half_t vs[BN * VS];
+    __shared__ __align__(16) half_t pt[4][32 * PS];
     const uint32_t wave = threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t col = lane % 32;
@@ -138,13 +174,55 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
     const uint32_t qt = blockIdx.x % p.q_tiles;
     const uint32_t bh = blockIdx.x / p.q_tiles;
     const uint32_t q0 = qt * 128 + wave * 32;
-    const uint32_t qi = q0 + col;
-    const bool q_valid = qi < p.q_len;
     const half_t* vh = v + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
-    const half_t* prow = probs + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * p.kv_len;
+    const half_t* pbase = probs + uint64_t(bh) * p.q_len * p.kv_len;
     const bool vec_p = p.kv_len % 8 == 0;
     const uint32_t tr_off = (8 * (lane / 32) + (lane % 16) / 4) * VS + 16 * ((lane / 16) % 2) +
                             4 * (lane % 4);
+    half_t* my = pt[wave];
+
+    // this wave's 32 x 128 probabilities of step blk, whole 256-byte row
+    // segments per 16 lanes (rows past q_len and keys past kv_len as zeros)
+    auto load_p = [&](uint32_t blk, h8 (&pr)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t r = i * 4 + lane / 16;
+            const uint32_t kb = blk * BN + (lane % 16) * 8;
+            const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + kb;
+            if (q0 + r < p.q_len && vec_p && kb + 8 <= p.kv_len) {
+                pr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(src));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    pr[i][e] = (q0 + r < p.q_len && kb + e < p.kv_len) ? src[e] : half_t(0.0f);
+            }
+        }
+    };
+    auto store_p = [&](const h8 (&pr)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<h8*>(my + (i * 4 + lane / 16) * PS + (lane % 16) * 8) = pr[i];
+    };
+    auto load_v = [&](uint32_t blk, h8 (&vr)[LOADS]) {
+#pragma unroll
+        for (int li = 0; li < LOADS; ++li) {
+            const uint32_t chunk = threadIdx.x + 256 * li;
+            const uint32_t gk = blk * BN + chunk / ROW_CHUNKS;
+            const uint32_t d0 = (chunk % ROW_CHUNKS) * 8;
+            const h8 zero = {};
+            vr[li] = gk < p.kv_len ? *reinterpret_cast<const h8*>(vh + uint64_t(gk) * D + d0)
+                                   : zero;
+        }
+    };
+    auto store_v = [&](const h8 (&vr)[LOADS]) {
+#pragma unroll
+        for (int li = 0; li < LOADS; ++li) {
+            const uint32_t chunk = threadIdx.x + 256 * li;
+            *reinterpret_cast<h8*>(vs + (chunk / ROW_CHUNKS) * VS + (chunk % ROW_CHUNKS) * 8) =
+                vr[li];
+        }
+    };
+
     f32x16 o[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -152,32 +230,22 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
         for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
 
     const uint32_t blocks = (p.kv_len + BN - 1) / BN;
+    h8 pnext[8], vnext[LOADS];
+    load_p(0, pnext);
+    load_v(0, vnext);
+    store_p(pnext);
+    store_v(vnext);
+    __syncthreads();
     for (uint32_t blk = 0; blk < blocks; ++blk) {
-        // V block -> LDS (rows past kv_len as zeros)
-        __syncthreads();
-#pragma unroll
-        for (int li = 0; li < LOADS; ++li) {
-            const uint32_t chunk = threadIdx.x + 256 * li;
-            const uint32_t key = chunk / ROW_CHUNKS;
-            const uint32_t d0 = (chunk % ROW_CHUNKS) * 8;
-            const uint32_t gk = blk * BN + key;
-            h8 val = {};
-            if (gk < p.kv_len) val = *reinterpret_cast<const h8*>(vh + uint64_t(gk) * D + d0);
-            *reinterpret_cast<h8*>(vs + key * VS + d0) = val;
+        const bool more = blk + 1 < blocks;
+        if (more) {  // next step's operands in flight during this step's products
+            load_p(blk + 1, pnext);
+            load_v(blk + 1, vnext);
         }
-        __syncthreads();
 #pragma unroll
-        for (int c = 0; c < BN / 16; ++c) {
-            // P^T operand: keys blk * 64 + 16 c + 8 hs + 0..7 of this lane's row
-            const uint32_t kb = blk * BN + 16 * c + 8 * hs;
-            h8 pb;
-            if (q_valid && vec_p && kb + 8 <= p.kv_len) {
-                pb = *reinterpret_cast<const h8*>(prow + kb);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    pb[e] = (q_valid && kb + e < p.kv_len) ? prow[kb + e] : half_t(0.0f);
-            }
+        for (int c = 0; c < PC; ++c) {
+            // P^T operand: keys 16 c + 8 hs + 0..7 of query row col
+            const h8 pb = *reinterpret_cast<const h8*>(my + col * PS + 16 * c + 8 * hs);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const half_t* vsrc = vs + tr_off + 16 * c * VS + 32 * t;
@@ -187,8 +255,15 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
                 o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[t], 0, 0, 0);
             }
         }
+        if (more) {
+            __syncthreads();
+            store_p(pnext);
+            store_v(vnext);
+            __syncthreads();
+        }
     }
-    if (q_valid) {
+    const uint32_t qi = q0 + col;
+    if (qi < p.q_len) {
         half_t* orow = out + (uint64_t(bh) * p.q_len + qi) * D + 4 * hs;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
