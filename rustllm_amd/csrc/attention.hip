@@ -93,27 +93,29 @@ __device__ inline h4 lds_read_transposed(const half_t* p) {
 // below 2^3, well inside f16 and f32 range.
 constexpr float kRescaleSlack = 3.0f;
 
-// QW waves of 32 queries each; KSPLIT groups of such waves split the key
+// QW waves of QG x 32 queries each (QG query groups share every K and V
+// operand a wave reads from LDS); KSPLIT groups of such waves split the key
 // blocks of the tile between them (group g takes blocks g, g + KSPLIT, ...)
-// and merge their partial (max, sum, output) through LDS at the end, so a
-// tile keeps KSPLIT x QW waves busy.
-template <int NT, int QW, int KSPLIT, int BN, int STAGES, int PRIO>
+// and merge their partial (max, sum, output) through LDS at the end.
+template <int NT, int QW, int KSPLIT, int BN, int STAGES, int PRIO, int QG>
 __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
     half_t* __restrict__ out, AttnParams p) {
     constexpr int D = 32 * NT;          // head size
     constexpr int DC = D / 16;          // 16-wide slices of a head (MFMA depth)
+    constexpr int KT = BN / 32;         // 32-key tiles per block
     // LDS rows: K at a stride of D + 8 halves (a 16-byte read of 8
     // consecutive rows hits 8 distinct bank quads), V at D + 16 (the four
     // rows a transpose read of 16 lanes touches hit 32 distinct banks).
     constexpr int KS = D + 8;
     constexpr int VS = D + 16;
     constexpr int THREADS = 64 * QW * KSPLIT;
+    constexpr int TILE_Q = 32 * QG * QW;               // queries per tile
     constexpr int BLOCK_CHUNKS = BN * D / 8;           // 16-byte chunks of one K (or V) block
     constexpr int LOADS = BLOCK_CHUNKS * KSPLIT / THREADS;
     constexpr int ROW_CHUNKS = D / 8;
     constexpr int KV_HALVES = BN * KS + BN * VS;       // one block of K and V
-    constexpr int MERGE = NT * 16 + 2;                 // floats a lane hands over
+    constexpr int MERGE = QG * (NT * 16 + 2);          // floats a lane hands over
     constexpr int LDS_BYTES = STAGES * KSPLIT * KV_HALVES * 2 > (KSPLIT - 1) * QW * 64 * MERGE * 4
                                   ? STAGES * KSPLIT * KV_HALVES * 2
                                   : (KSPLIT - 1) * QW * 64 * MERGE * 4;
@@ -129,10 +131,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     const half_t* vh = v + uint64_t(kv_head) * p.kv_head_stride;
 
     const uint32_t wave = threadIdx.x / 64;
-    const uint32_t qw = wave % QW;      // which 32 queries of the tile
+    const uint32_t qw = wave % QW;      // which QG x 32 queries of the tile
     const uint32_t sub = wave / QW;     // which share of the key blocks
     const uint32_t lane = threadIdx.x % 64;
-    const uint32_t col = lane % 32;     // query column of this lane
+    const uint32_t col = lane % 32;     // query column of this lane (in each group)
     const uint32_t hs = lane / 32;      // which 8 of 16 in an MFMA slice
     // Transpose reads of V for the A operand of O^T += V^T P^T: lane
     // 16g + 4j + a reads row 8(g / 2) + j (+ 16c + 4e2 for slice c, half e2)
@@ -147,43 +149,49 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
         const uint32_t tile = which == 0 ? p.tiles - 1 - pair : pair;
         if (which == 1 && tile >= p.tiles - 1 - pair) break;
 
-        const uint32_t q_first = tile * (32 * QW);
-        const uint32_t q_last = min(p.q_len, q_first + 32 * QW) - 1;
+        const uint32_t q_first = tile * TILE_Q;
+        const uint32_t q_last = min(p.q_len, q_first + TILE_Q) - 1;
         const uint32_t keys = min(p.kv_len, p.start + q_last + 1);
         const uint32_t blocks = (keys + BN - 1) / BN;
         const uint32_t steps = (blocks + KSPLIT - 1) / KSPLIT;
 
-        const uint32_t q0 = q_first + qw * 32;
-        const bool wave_active = q0 < p.q_len;
+        const uint32_t qw0 = q_first + qw * 32 * QG;  // first query of this wave
+        const bool wave_active = qw0 < p.q_len;
         const uint32_t wave_keys =
-            wave_active ? min(p.kv_len, p.start + min(q0 + 31, p.q_len - 1) + 1) : 0;
-        const uint32_t qi = q0 + col;
-        const bool q_valid = qi < p.q_len;
-        // Largest key this lane's query sees (padding columns see a few keys
-        // too, so their arithmetic stays finite; they are never stored).
-        const uint32_t key_limit = min(p.start + qi, p.kv_len - 1);
+            wave_active ? min(p.kv_len, p.start + min(qw0 + 32 * QG - 1, p.q_len - 1) + 1) : 0;
 
-        h8 qf[DC];
-        {
+        h8 qf[QG][DC];
+        uint32_t key_limit[QG];
+#pragma unroll
+        for (int g = 0; g < QG; ++g) {
+            const uint32_t qi = qw0 + 32 * g + col;
+            const bool q_valid = qi < p.q_len;
+            // Largest key this lane's query sees (padding columns see a few
+            // keys too, so their arithmetic stays finite; never stored).
+            key_limit[g] = min(p.start + qi, p.kv_len - 1);
             const half_t* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + 8 * hs;
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
                 if (q_valid) {
-                    qf[c] = *reinterpret_cast<const h8*>(qrow + 16 * c);
+                    qf[g][c] = *reinterpret_cast<const h8*>(qrow + 16 * c);
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) qf[c][e] = half_t(0.0f);
+                    for (int e = 0; e < 8; ++e) qf[g][c][e] = half_t(0.0f);
                 }
             }
         }
 
-        f32x16 o[NT];
+        f32x16 o[QG][NT];
+        float m[QG], l[QG];  // running max logit (log2 units), this lane's share of the sum
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+        for (int g = 0; g < QG; ++g) {
+            m[g] = -INFINITY;
+            l[g] = 0.0f;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
-        float m = -INFINITY;  // running max logit, log2 units
-        float l = 0.0f;       // this lane's share of the running sum
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[g][t][r] = 0.0f;
+        }
 
         h8 kreg[LOADS], vreg[LOADS];
         bool vlive[LOADS];
@@ -198,9 +206,9 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                 // Rows past kv_len are never read (they may hold anything): a
                 // key past the end loads row kv_len - 1 instead; its score is
                 // masked (selected to -inf) and its value row zeroed, so it
-                // adds nothing even if that row is not finite.
-                // (The zeroing happens at the LDS store, after the compute:
-                // a select here would make the wave wait for the load now.)
+                // adds nothing even if that row is not finite.  (The zeroing
+                // happens at the LDS store, after the compute: a select here
+                // would make the wave wait for the load now.)
                 const uint32_t row = min(key, p.kv_len - 1);
                 kreg[li] = *reinterpret_cast<const h8*>(kh + uint64_t(row) * D + d0);
                 vreg[li] = *reinterpret_cast<const h8*>(vh + uint64_t(row) * D + d0);
@@ -237,86 +245,102 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
             const half_t* ks = kv_lds + ((step % STAGES) * KSPLIT + sub) * KV_HALVES;
             const half_t* vs = ks + BN * KS;
             if (blk < blocks && blk * BN < wave_keys) {
-                // S^T = K Q^T for BN / 32 tiles of 32 keys.
-                constexpr int KT = BN / 32;
-                f32x16 s[KT];
+                // S^T = K Q^T: each K operand read once, used by every group.
+                f32x16 s[QG][KT];
                 // A wave issuing matrix work goes first, so the other wave of
                 // the SIMD fills the vector ALU meanwhile (wave priority only).
                 if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(PRIO);
 #pragma unroll
                 for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
+                    for (int g = 0; g < QG; ++g)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) s[g][kt][r] = 0.0f;
                     const half_t* krow = ks + (kt * 32 + col) * KS + 8 * hs;
 #pragma unroll
-                    for (int c = 0; c < DC; ++c)
-                        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            *reinterpret_cast<const h8*>(krow + 16 * c), qf[c], s[kt], 0, 0, 0);
+                    for (int c = 0; c < DC; ++c) {
+                        const h8 ka = *reinterpret_cast<const h8*>(krow + 16 * c);
+#pragma unroll
+                        for (int g = 0; g < QG; ++g)
+                            s[g][kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[g][c],
+                                                                             s[g][kt], 0, 0, 0);
+                    }
                 }
                 if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(0);
-                // mask; the block's max raw score of each query
                 const uint32_t kbase = blk * BN;
-                if (kbase + BN - 1 > p.start + q0 || kbase + BN > p.kv_len) {
+                const bool masking = kbase + BN - 1 > p.start + qw0 || kbase + BN > p.kv_len;
+                h8 pb[QG][BN / 16];
+#pragma unroll
+                for (int g = 0; g < QG; ++g) {
+                    // mask; the block's max raw score of each query
+                    if (masking) {
+#pragma unroll
+                        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const uint32_t key =
+                                    kbase + kt * 32 + 16 * (r >> 3) + 8 * hs + (r & 7);
+                                if (key > key_limit[g]) s[g][kt][r] = -INFINITY;
+                            }
+                    }
+                    // two independent max chains, joined at the end
+                    float mx = -INFINITY, my = -INFINITY;
 #pragma unroll
                     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const uint32_t key = kbase + kt * 32 + 16 * (r >> 3) + 8 * hs + (r & 7);
-                            if (key > key_limit) s[kt][r] = -INFINITY;
+                        for (int r = 0; r < 16; r += 4) {
+                            mx = max3(mx, s[g][kt][r], s[g][kt][r + 1]);
+                            my = max3(my, s[g][kt][r + 2], s[g][kt][r + 3]);
                         }
-                }
-                // two independent max chains, joined at the end
-                float mx = -INFINITY, my = -INFINITY;
+                    mx = fmaxf(mx, my);
+                    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                    const float mx_log2 = mx * p.scale_log2;
+                    if (__any(mx_log2 > m[g] + kRescaleSlack)) {
+                        const float m_new = fmaxf(m[g], mx_log2);
+                        const float alpha =
+                            m_new > m[g] ? __builtin_amdgcn_exp2f(m[g] - m_new) : 1.0f;
+                        m[g] = m_new;
+                        l[g] *= alpha;
 #pragma unroll
-                for (int kt = 0; kt < KT; ++kt)
+                        for (int t = 0; t < NT; ++t)
 #pragma unroll
-                    for (int r = 0; r < 16; r += 4) {
-                        mx = max3(mx, s[kt][r], s[kt][r + 1]);
-                        my = max3(my, s[kt][r + 2], s[kt][r + 3]);
+                            for (int r = 0; r < 16; ++r) o[g][t][r] *= alpha;
                     }
-                mx = fmaxf(mx, my);
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const float mx_log2 = mx * p.scale_log2;
-                if (__any(mx_log2 > m + kRescaleSlack)) {
-                    const float m_new = fmaxf(m, mx_log2);
-                    const float alpha = m_new > m ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
-                    m = m_new;
-                    l *= alpha;
+                    // p = 2^(s * scale * log2 e - m); a query that has seen no
+                    // key yet (m = -inf) has only -inf scores here, and p = 0.
+                    const float neg_m = m[g] == -INFINITY ? 0.0f : -m[g];
+                    // P as the f16 operand of the P V product: lane half hs
+                    // supplies keys 16c + 8hs .. +7, which it holds in
+                    // registers 8(c%2) .. +7 of tile c/2.  The running sum adds
+                    // the same f16 probabilities the product uses
+                    // (v_dot2_f32_f16 against ones, f32 accumulation).
+                    const h2 ones = {half_t(1.0f), half_t(1.0f)};
 #pragma unroll
-                    for (int t = 0; t < NT; ++t)
+                    for (int c = 0; c < BN / 16; ++c) {
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+                        for (int e = 0; e < 8; ++e)
+                            pb[g][c][e] = half_t(__builtin_amdgcn_exp2f(__builtin_fmaf(
+                                s[g][c >> 1][8 * (c & 1) + e], p.scale_log2, neg_m)));
+#pragma unroll
+                        for (int e = 0; e < 8; e += 2)
+                            l[g] = __builtin_amdgcn_fdot2(h2{pb[g][c][e], pb[g][c][e + 1]}, ones,
+                                                          l[g], false);
+                    }
                 }
-                // p = 2^(s * scale * log2 e - m); a query that has seen no key
-                // yet (m = -inf) has only -inf scores here, and p = 0.
-                const float neg_m = m == -INFINITY ? 0.0f : -m;
-#pragma unroll
-                for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        s[kt][r] =
-                            __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], p.scale_log2, neg_m));
-                // O^T += V^T P^T, 16 keys per MFMA: lane half hs supplies keys
-                // 16c + 8hs .. +7, which it holds in registers 8(c%2) .. +7 of tile c/2.
-                // The running sum adds the same f16 probabilities the product
-                // uses (v_dot2_f32_f16 against ones, f32 accumulation).
-                const h2 ones = {half_t(1.0f), half_t(1.0f)};
+                // O^T += V^T P^T, 16 keys per MFMA; each V operand read once.
                 if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(PRIO);
 #pragma unroll
                 for (int c = 0; c < BN / 16; ++c) {
-                    h8 pb;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) pb[e] = half_t(s[c >> 1][8 * (c & 1) + e]);
-#pragma unroll
-                    for (int e = 0; e < 8; e += 2)
-                        l = __builtin_amdgcn_fdot2(h2{pb[e], pb[e + 1]}, ones, l, false);
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         const half_t* vsrc = vs + tr_off + 16 * c * VS + 32 * t;
                         const h4 lo = lds_read_transposed(vsrc);
                         const h4 hi = lds_read_transposed(vsrc + 4 * VS);
                         const h8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[t], 0, 0, 0);
+#pragma unroll
+                        for (int g = 0; g < QG; ++g)
+                            o[g][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[g][c], o[g][t],
+                                                                            0, 0, 0);
                     }
                 }
                 if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(0);
@@ -331,46 +355,60 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
             float* mg = reinterpret_cast<float*>(lds);
             if (sub > 0) {
                 float* dst = mg + ((sub - 1) * QW * 64 + qw * 64 + lane) * MERGE;
-                dst[0] = m;
-                dst[1] = l;
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
+                for (int g = 0; g < QG; ++g) {
+                    float* dg = dst + g * (NT * 16 + 2);
+                    dg[0] = m[g];
+                    dg[1] = l[g];
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) dst[2 + 16 * t + r] = o[t][r];
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) dg[2 + 16 * t + r] = o[g][t][r];
+                }
             }
             __syncthreads();
             if (sub == 0) {
 #pragma unroll
-                for (int g = 1; g < KSPLIT; ++g) {
-                    const float* src = mg + ((g - 1) * QW * 64 + qw * 64 + lane) * MERGE;
-                    const float m2 = src[0];
-                    const float m_tot = fmaxf(m, m2);
-                    const float a1 = m_tot > m ? __builtin_amdgcn_exp2f(m - m_tot) : 1.0f;
-                    const float a2 = m_tot > m2 ? __builtin_amdgcn_exp2f(m2 - m_tot) : 1.0f;
-                    l = l * a1 + src[1] * a2;
+                for (int h = 1; h < KSPLIT; ++h) {
+                    const float* src = mg + ((h - 1) * QW * 64 + qw * 64 + lane) * MERGE;
 #pragma unroll
-                    for (int t = 0; t < NT; ++t)
+                    for (int g = 0; g < QG; ++g) {
+                        const float* sg = src + g * (NT * 16 + 2);
+                        const float m2 = sg[0];
+                        const float m_tot = fmaxf(m[g], m2);
+                        const float a1 = m_tot > m[g] ? __builtin_amdgcn_exp2f(m[g] - m_tot) : 1.0f;
+                        const float a2 = m_tot > m2 ? __builtin_amdgcn_exp2f(m2 - m_tot) : 1.0f;
+                        l[g] = l[g] * a1 + sg[1] * a2;
 #pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            o[t][r] = o[t][r] * a1 + src[2 + 16 * t + r] * a2;
-                    m = m_tot;
+                        for (int t = 0; t < NT; ++t)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                o[g][t][r] = o[g][t][r] * a1 + sg[2 + 16 * t + r] * a2;
+                        m[g] = m_tot;
+                    }
                 }
             }
             __syncthreads();  // the merge area is free again
         }
 
-        const float total = l + __shfl_xor(l, 32, 64);
-        const float inv = 1.0f / total;
-        if (q_valid && sub == 0) {
-            half_t* orow = out + (uint64_t(bh) * p.q_len + qi) * D + 4 * hs;
+        if (sub == 0) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
+            for (int g = 0; g < QG; ++g) {
+                const uint32_t qi = qw0 + 32 * g + col;
+                const float total = l[g] + __shfl_xor(l[g], 32, 64);
+                const float inv = 1.0f / total;
+                if (qi < p.q_len) {
+                    half_t* orow = out + (uint64_t(bh) * p.q_len + qi) * D + 4 * hs;
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    h4 w;
+                    for (int t = 0; t < NT; ++t) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) w[e] = half_t(o[t][4 * g + e] * inv);
-                    *reinterpret_cast<h4*>(orow + t * 32 + 8 * g) = w;
+                        for (int gg = 0; gg < 4; ++gg) {
+                            h4 w;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) w[e] = half_t(o[g][t][4 * gg + e] * inv);
+                            *reinterpret_cast<h4*>(orow + t * 32 + 8 * gg) = w;
+                        }
+                    }
                 }
             }
         }
@@ -759,6 +797,7 @@ constexpr int kFlashKeySplit = 2;
 constexpr int kFlashBlockKeys = 64;
 constexpr int kFlashStages = 1;
 constexpr int kFlashPriority = 0;
+constexpr int kFlashQueryGroups = 1;
 
 // Which kernel a shape takes: the MFMA kernel for f16 with a head size of
 // 32, 64, 96 or 128 and aligned buffers; the row kernel otherwise (head
@@ -844,18 +883,18 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
     }
     if constexpr (std::is_same<T, half_t>::value) {
         if (flash) {
-            p.tiles = uint32_t(ceil_div(s.q_len, 32 * kFlashQueryWaves));
+            p.tiles = uint32_t(ceil_div(s.q_len, 32 * kFlashQueryWaves * kFlashQueryGroups));
             p.pairs = (p.tiles + 1) / 2;
             const uint64_t grid = heads * p.pairs;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "attention grid exceeds u32");
             constexpr int QW = kFlashQueryWaves, KSPLIT = kFlashKeySplit, BN = kFlashBlockKeys,
-                          ST = kFlashStages, PR = kFlashPriority;
+                          ST = kFlashStages, PR = kFlashPriority, QG = kFlashQueryGroups;
             const dim3 g(static_cast<unsigned>(grid)), b(64 * QW * KSPLIT);
             switch (s.head_dim / 32) {
-                case 1: RL_LAUNCH(ctx, (k_flash_attention<1, QW, KSPLIT, BN, ST, PR>), g, b, qd, kd, vd, od, p); break;
-                case 2: RL_LAUNCH(ctx, (k_flash_attention<2, QW, KSPLIT, BN, ST, PR>), g, b, qd, kd, vd, od, p); break;
-                case 3: RL_LAUNCH(ctx, (k_flash_attention<3, QW, KSPLIT, BN, ST, PR>), g, b, qd, kd, vd, od, p); break;
-                default: RL_LAUNCH(ctx, (k_flash_attention<4, QW, KSPLIT, BN, ST, PR>), g, b, qd, kd, vd, od, p); break;
+                case 1: RL_LAUNCH(ctx, (k_flash_attention<1, QW, KSPLIT, BN, ST, PR, QG>), g, b, qd, kd, vd, od, p); break;
+                case 2: RL_LAUNCH(ctx, (k_flash_attention<2, QW, KSPLIT, BN, ST, PR, QG>), g, b, qd, kd, vd, od, p); break;
+                case 3: RL_LAUNCH(ctx, (k_flash_attention<3, QW, KSPLIT, BN, ST, PR, QG>), g, b, qd, kd, vd, od, p); break;
+                default: RL_LAUNCH(ctx, (k_flash_attention<4, QW, KSPLIT, BN, ST, PR, QG>), g, b, qd, kd, vd, od, p); break;
             }
             return after_launch(ctx, name);
         }
