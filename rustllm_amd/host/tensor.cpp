@@ -628,6 +628,110 @@ Tensor Tensor::repeat_kv(const Context& ctx, size_t repeats) const {
     return output;
 }
 
+// src/tensor/gqa_matmul.rs:135-182 (validate_qk / validate_pv and their helpers).
+static void validate_gqa(const Tensor& left, const Tensor& right, const char* op,
+                         const char* expected) {
+    if (left.dtype() != right.dtype())
+        throw TinyError(TinyError::Kind::UnsupportedDType,
+                        std::string("GQA ") + op + " dtype mismatch: " + dtype_name(left.dtype()) +
+                            " vs " + dtype_name(right.dtype()));
+    if (left.rank() != 4 || right.rank() != 4)
+        throw TinyError(TinyError::Kind::ModelFormat,
+                        std::string("GQA ") + op + " expects " + expected + ", got " +
+                            dims_str(left.shape().dims()) + " and " + dims_str(right.shape().dims()));
+}
+
+static void validate_head_groups(size_t q_heads, size_t kv_heads) {
+    if (kv_heads == 0 || q_heads % kv_heads != 0)
+        throw TinyError(TinyError::Kind::ModelFormat,
+                        "Q heads " + std::to_string(q_heads) +
+                            " must be divisible by non-zero KV heads " + std::to_string(kv_heads));
+}
+
+// A one-query [B, H, 1, D] view whose elements lie as in the contiguous
+// tensor (the head permutation of a [B, 1, H * D] projection).
+static bool one_query_in_place(const Tensor& q) {
+    const auto& st = q.strides().values();
+    return q.dim(2) == 1 && st[3] == 1 && st[1] == q.dim(3) &&
+           (q.dim(0) == 1 || st[0] == q.dim(1) * q.dim(3)) && q.buffer().len() == q.numel();
+}
+
+// A [B, H, S, D] operand the kernels can read in place: contiguous, or rows of
+// D elements with unit stride laid out as whole heads of `capacity` rows
+// (a narrowed LayerKvCache view).  Returns the capacity, 0 if not.
+static size_t rows_in_place(const Tensor& t) {
+    const auto& st = t.strides().values();
+    const size_t heads = t.dim(1), d = t.dim(3);
+    if (st[3] != 1 || st[2] != d || st[1] % d != 0) return 0;
+    const size_t capacity = st[1] / d;
+    if (capacity < t.dim(2) || (t.dim(0) > 1 && st[0] != heads * st[1])) return 0;
+    if (t.buffer().len() != t.dim(0) * heads * capacity * d) return 0;
+    return capacity;
+}
+
+Tensor Tensor::gqa_qk_matmul(const Context& ctx, const Tensor& key) const {
+    Execution e(ctx);
+    Tensor out = gqa_qk_matmul_encode(ctx, key);
+    e.finish();
+    return out;
+}
+
+// src/tensor/gqa_matmul.rs:23-61
+Tensor Tensor::gqa_qk_matmul_encode(const Context& ctx, const Tensor& key) const {
+    validate_gqa(*this, key, "QK", "Q [B,QH,Q,D] and K [B,KVH,K,D]");
+    const size_t batch = dim(0), q_heads = dim(1), q_len = dim(2), head_dim = dim(3);
+    if (batch != key.dim(0) || head_dim != key.dim(3))
+        throw shape_mismatch(shape_.dims(), key.shape().dims());
+    const size_t kv_heads = key.dim(1), kv_len = key.dim(2);
+    validate_head_groups(q_heads, kv_heads);
+    // A one-query head permutation is layout-equivalent to the contiguous
+    // tensor on device (gqa_matmul.rs:31-42); prefill makes both contiguous.
+    const bool one = q_len == 1;
+    const Tensor q = is_contiguous() || one_query_in_place(*this) ? *this : contiguous_encode(ctx);
+    size_t capacity = one ? rows_in_place(key) : 0;
+    const Tensor k = capacity ? key : key.contiguous_encode(ctx);
+    if (!capacity) capacity = kv_len;
+    Tensor out = Tensor::empty(ctx, {batch, q_heads, q_len, kv_len}, dtype_);
+    check(dtype_ == DType::F32
+              ? rl_gqa_qk_matmul_f32(ctx.raw(), q.buffer().raw(), k.buffer().raw(), batch, q_heads,
+                                     kv_heads, q_len, kv_len, head_dim, capacity,
+                                     out.buffer().raw())
+              : rl_gqa_qk_matmul_f16(ctx.raw(), q.buffer().raw(), k.buffer().raw(), batch, q_heads,
+                                     kv_heads, q_len, kv_len, head_dim, capacity,
+                                     out.buffer().raw()));
+    return out;
+}
+
+Tensor Tensor::gqa_pv_matmul(const Context& ctx, const Tensor& value) const {
+    Execution e(ctx);
+    Tensor out = gqa_pv_matmul_encode(ctx, value);
+    e.finish();
+    return out;
+}
+
+// src/tensor/gqa_matmul.rs:72-110
+Tensor Tensor::gqa_pv_matmul_encode(const Context& ctx, const Tensor& value) const {
+    validate_gqa(*this, value, "PV", "P [B,QH,Q,K] and V [B,KVH,K,D]");
+    const size_t batch = dim(0), q_heads = dim(1), q_len = dim(2), kv_len = dim(3);
+    if (batch != value.dim(0) || kv_len != value.dim(2))
+        throw shape_mismatch(shape_.dims(), value.shape().dims());
+    const size_t kv_heads = value.dim(1), head_dim = value.dim(3);
+    validate_head_groups(q_heads, kv_heads);
+    const Tensor probs = is_contiguous() ? *this : contiguous_encode(ctx);
+    size_t capacity = q_len == 1 ? rows_in_place(value) : 0;
+    const Tensor v = capacity ? value : value.contiguous_encode(ctx);
+    if (!capacity) capacity = kv_len;
+    Tensor out = Tensor::empty(ctx, {batch, q_heads, q_len, head_dim}, dtype_);
+    check(dtype_ == DType::F32
+              ? rl_gqa_pv_matmul_f32(ctx.raw(), probs.buffer().raw(), v.buffer().raw(), batch,
+                                     q_heads, kv_heads, q_len, kv_len, head_dim, capacity,
+                                     out.buffer().raw())
+              : rl_gqa_pv_matmul_f16(ctx.raw(), probs.buffer().raw(), v.buffer().raw(), batch,
+                                     q_heads, kv_heads, q_len, kv_len, head_dim, capacity,
+                                     out.buffer().raw()));
+    return out;
+}
+
 // -------------------------------------------------------------------- ops
 
 namespace ops {
@@ -1197,6 +1301,43 @@ Tensor SwiGlu::forward_encode(const Context& ctx, const Tensor& gate, const Tens
         return Tensor::from_buffer(std::move(out), gate.shape().dims(), gate.dtype());
     }
     return gate.silu_encode(ctx).mul_encode(ctx, up);
+}
+
+// src/nn/attention.rs:216-247 as one pass.  The checks of gqa_qk_matmul
+// (dtype, rank 4, batch and head size, head groups), then those of
+// attention_scale_mask (query range within the keys), then gqa_pv_matmul's
+// (value shape).  Key and value are read in place when they are contiguous
+// or the narrowed views of one LayerKvCache (same capacity); otherwise they
+// are made contiguous first.
+Tensor attention_core_encode(const Context& ctx, const Tensor& q, const Tensor& key,
+                             const Tensor& value, float scale, size_t start_pos) {
+    validate_gqa(q, key, "QK", "Q [B,QH,Q,D] and K [B,KVH,K,D]");
+    const size_t batch = q.dim(0), q_heads = q.dim(1), q_len = q.dim(2), head_dim = q.dim(3);
+    if (batch != key.dim(0) || head_dim != key.dim(3))
+        throw shape_mismatch(q.shape().dims(), key.shape().dims());
+    const size_t kv_heads = key.dim(1), kv_len = key.dim(2);
+    validate_head_groups(q_heads, kv_heads);
+    validate_gqa(q, value, "PV", "P [B,QH,Q,K] and V [B,KVH,K,D]");
+    if (value.dim(0) != batch || value.dim(1) != kv_heads || value.dim(2) != kv_len ||
+        value.dim(3) != head_dim)
+        throw shape_mismatch(key.shape().dims(), value.shape().dims());
+    const Tensor qc = q.is_contiguous() || one_query_in_place(q) ? q : q.contiguous_encode(ctx);
+    size_t capacity = rows_in_place(key);
+    Tensor k = key, v = value;
+    if (capacity == 0 || rows_in_place(value) != capacity) {
+        k = key.contiguous_encode(ctx);
+        v = value.contiguous_encode(ctx);
+        capacity = kv_len;
+    }
+    Tensor out = Tensor::empty(ctx, {batch, q_heads, q_len, head_dim}, q.dtype());
+    check(q.dtype() == DType::F32
+              ? rl_attention_f32(ctx.raw(), qc.buffer().raw(), k.buffer().raw(), v.buffer().raw(),
+                                 batch, q_heads, kv_heads, q_len, kv_len, head_dim, capacity, scale,
+                                 start_pos, out.buffer().raw())
+              : rl_attention_f16(ctx.raw(), qc.buffer().raw(), k.buffer().raw(), v.buffer().raw(),
+                                 batch, q_heads, kv_heads, q_len, kv_len, head_dim, capacity, scale,
+                                 start_pos, out.buffer().raw()));
+    return out;
 }
 
 }  // namespace nn

@@ -213,6 +213,14 @@ class Tensor {
     Tensor attention_softmax_encode(const Context& ctx, float scale,
                                     size_t query_start_pos) const;
     Tensor repeat_kv(const Context& ctx, size_t repeats) const;
+    // src/tensor/gqa_matmul.rs:16-110: Q [B, QH, Q, D] x K^T without
+    // repeating the KV heads, and P [B, QH, Q, K] x V.  A one-query Q (and the
+    // K / V it meets) is used in place -- a KV-cache view included -- as the
+    // reference does; otherwise the operands are made contiguous first.
+    Tensor gqa_qk_matmul(const Context& ctx, const Tensor& key) const;
+    Tensor gqa_qk_matmul_encode(const Context& ctx, const Tensor& key) const;
+    Tensor gqa_pv_matmul(const Context& ctx, const Tensor& value) const;
+    Tensor gqa_pv_matmul_encode(const Context& ctx, const Tensor& value) const;
 
    private:
     Tensor(std::shared_ptr<Storage> storage, Shape shape, Strides strides, DType dtype);
@@ -361,6 +369,14 @@ struct SwiGlu {
     static Tensor forward(const Context& ctx, const Tensor& gate, const Tensor& up);
     static Tensor forward_encode(const Context& ctx, const Tensor& gate, const Tensor& up);
 };
+
+// SelfAttention::attention_core_encode (src/nn/attention.rs:216-247) in one
+// pass: QK^T, scale/mask(scale, start_pos), softmax, PV, the scores never
+// written.  q [B, QH, Q, D]; key / value [B, KVH, K, D] (contiguous, or the
+// narrowed views of a LayerKvCache, read in place).  Checks of the four
+// calls it replaces, in their order.
+Tensor attention_core_encode(const Context& ctx, const Tensor& q, const Tensor& key,
+                             const Tensor& value, float scale, size_t start_pos);
 
 }  // namespace nn
 

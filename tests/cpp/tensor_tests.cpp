@@ -522,6 +522,95 @@ TEST(one_launch_query_rotation_and_append_equals_the_unfused_path) {
     }
 }
 
+// ---------------------------------------------------- src/nn/attention.rs
+
+// nn/attention.rs:590-668 (batched_attention_core_matches_op_by_op_submission):
+// the attention core in one pass equals QK^T, scale/mask, softmax and PV
+// issued one by one, within 1e-5, for (2, 2) and (3, 1) heads, head size 4,
+// 3 new positions after 2 cached.  (For equal head counts the reference's
+// op-by-op side uses batched_matmul over K^T; gqa_qk_matmul with one query
+// head per KV head computes the same sums.)
+TEST(batched_attention_core_matches_op_by_op_submission) {
+    for (auto heads : {std::pair<size_t, size_t>{2, 2}, {3, 1}}) {
+        const size_t num_heads = heads.first, num_kv_heads = heads.second;
+        const size_t head_dim = 4, seq_len = 3, start_pos = 2;
+        std::vector<float> query(num_heads * seq_len * head_dim);
+        for (size_t i = 0; i < query.size(); ++i) query[i] = std::fmod(float(i), 5.0f) - 2.0f;
+        std::vector<float> cached(num_kv_heads * (start_pos + seq_len) * head_dim);
+        for (size_t i = 0; i < cached.size(); ++i) cached[i] = std::fmod(float(i), 3.0f) - 1.0f;
+        auto q = Tensor::from_f32_slice(context, query, {1, num_heads, seq_len, head_dim});
+        auto key = Tensor::from_f32_slice(context, cached,
+                                          {1, num_kv_heads, start_pos + seq_len, head_dim});
+        auto value = key;
+        const float scale = 1.0f / std::sqrt(float(head_dim));
+        auto scores = q.gqa_qk_matmul(context, key);
+        scores = scores.attention_scale_mask(context, scale, start_pos);
+        auto probabilities = scores.softmax_last_dim(context);
+        auto expected = probabilities.gqa_pv_matmul(context, value);
+
+        Execution execution(context);
+        auto actual = nn::attention_core_encode(context, q, key, value, scale, start_pos);
+        execution.finish();
+        CHECK(actual.shape() == expected.shape());
+        assert_close(actual.to_f32_vec(), expected.to_f32_vec(), 1e-5f, true);
+    }
+}
+
+// gqa_matmul.rs:31-42 and :79-83: a decode step reads the narrowed KV-cache
+// views in place; the result equals the same step on contiguous copies.
+TEST(decode_attention_reads_cache_views_in_place) {
+    const size_t q_heads = 6, kv_heads = 2, hd = 64, max = 1024, len = 700;
+    for (DType dtype : {DType::F32, DType::F16}) {
+        model::LayerKvCache cache(context, kv_heads, max, hd, dtype);
+        std::vector<float> kd(len * kv_heads * hd), vd(len * kv_heads * hd), qd(q_heads * hd);
+        for (size_t i = 0; i < kd.size(); ++i) {
+            kd[i] = std::sin(0.013f * float(i)) * 2.0f;
+            vd[i] = std::cos(0.007f * float(i));
+        }
+        for (size_t i = 0; i < qd.size(); ++i) qd[i] = std::cos(0.31f * float(i));
+        auto k = Tensor::from_f32_slice(context, kd, {1, kv_heads, len, hd}).to_dtype(context, dtype);
+        auto v = Tensor::from_f32_slice(context, vd, {1, kv_heads, len, hd}).to_dtype(context, dtype);
+        cache.append(context, k, v);
+        auto q = Tensor::from_f32_slice(context, qd, {1, q_heads, 1, hd}).to_dtype(context, dtype);
+        CHECK(!cache.key().is_contiguous());
+        Execution a(context);
+        auto in_place = nn::attention_core_encode(context, q, cache.key(), cache.value(), 0.125f,
+                                                  len - 1);
+        auto scores = q.gqa_qk_matmul_encode(context, cache.key());
+        a.finish();
+        Execution b(context);
+        auto copied = nn::attention_core_encode(context, q, cache.key().contiguous_encode(context),
+                                                cache.value().contiguous_encode(context), 0.125f,
+                                                len - 1);
+        auto scores_copied = q.gqa_qk_matmul_encode(context, k);
+        b.finish();
+        assert_close(in_place.to_f32_vec(), copied.to_f32_vec(), 0.0f);
+        assert_close(scores.to_f32_vec(), scores_copied.to_f32_vec(), 0.0f);
+    }
+}
+
+// gqa_matmul.rs:135-182: dtype, rank, batch/head size, head groups -- in that order.
+TEST(gqa_matmuls_validate_like_the_reference) {
+    auto q = Tensor::zeros(context, {1, 6, 3, 8});
+    auto k = Tensor::zeros(context, {1, 2, 5, 8});
+    CHECK(expect_error([&] { q.gqa_qk_matmul(context, k.to_dtype(context, DType::F16)); }) ==
+          TinyError::Kind::UnsupportedDType);
+    CHECK(expect_error([&] { q.gqa_qk_matmul(context, Tensor::zeros(context, {2, 5, 8})); }) ==
+          TinyError::Kind::ModelFormat);
+    CHECK(expect_error([&] { q.gqa_qk_matmul(context, Tensor::zeros(context, {2, 2, 5, 8})); }) ==
+          TinyError::Kind::ShapeMismatch);
+    CHECK(expect_error([&] { q.gqa_qk_matmul(context, Tensor::zeros(context, {1, 4, 5, 8})); }) ==
+          TinyError::Kind::ModelFormat);
+    auto p = Tensor::zeros(context, {1, 6, 3, 5});
+    CHECK(expect_error([&] { p.gqa_pv_matmul(context, Tensor::zeros(context, {1, 2, 4, 8})); }) ==
+          TinyError::Kind::ShapeMismatch);
+    CHECK((q.gqa_qk_matmul(context, k).shape().dims() == std::vector<size_t>{1, 6, 3, 5}));
+    CHECK((p.gqa_pv_matmul(context, k).shape().dims() == std::vector<size_t>{1, 6, 3, 8}));
+    // the attention core's own scale/mask check: queries past the keys
+    CHECK(expect_error([&] { nn::attention_core_encode(context, q, k, k, 0.5f, 3); }) ==
+          TinyError::Kind::InvalidShape);
+}
+
 // ---------------------------------------------------- src/ops/embedding.rs
 
 // ops/embedding.rs:119-149: rows of the weight, token ids checked against the vocabulary.
