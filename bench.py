@@ -844,7 +844,19 @@ def probe(ctx, host, ops):
     vocab = 49152
     emb = ctx.upload(synth.normal(7, (vocab, hid), 0, 1, F16))
     ids = (synth.uniform(8, tok) * vocab).astype(np.uint32)
+    # attention core at the SmolLM2 layer shape (Q [1,15,4096,64], K/V [1,5,4096,64])
+    ka = ctx.upload(synth.normal(9, (1, 5, tok, 64), 0, 1, F16))
+    va = ctx.upload(synth.normal(10, (1, 5, tok, 64), 0, 1, F16))
+    scores = ctx.empty((1, 15, tok, tok), F16)
+    attn_io = (2 * 15 + 2 * 5) * tok * 64 * 2
+    n_scores = 15 * tok * tok
     for name, nbytes, fn in [
+        ("attention_f16 fused [1,15,4096,64] causal (inputs + output)", attn_io,
+         lambda: ctx.attention(q, ka, va, 0.125, 0, None, qo)),
+        ("gqa_qk_f16 [1,15,4096,4096]", (15 + 5) * tok * 64 * 2 + n_scores * 2,
+         lambda: ctx.gqa_qk(q, ka, None, scores)),
+        ("gqa_pv_f16 [1,15,4096,64]", n_scores * 2 + (5 + 15) * tok * 64 * 2,
+         lambda: ctx.gqa_pv(scores, va, qo)),
         ("rmsnorm_f16 [4096,960]", tok * hid * 4 + hid * 2, lambda: ctx.rmsnorm(x, w, 1e-5, y)),
         ("rmsnorm_f16 [16384,960]", 16384 * hid * 4 + hid * 2,
          lambda: ctx.rmsnorm(xl, w, 1e-5, yl)),

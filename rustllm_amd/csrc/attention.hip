@@ -77,6 +77,16 @@ __device__ inline float max3(float a, float b, float c) {
     return r;
 }
 
+// Row stride (halves) of V in LDS for the transpose reads: the 32 lanes one
+// LDS cycle serves read 4 rows x 2 runs of 16 bytes; with 64 banks of 4
+// bytes those land on distinct banks when the stride in dwords is 16 or 48
+// modulo 64.  Smallest such stride >= D (in steps of 8 halves).
+__host__ __device__ constexpr int v_stride_tr(int d) {
+    int s = d;
+    while ((s / 2) % 64 != 16 && (s / 2) % 64 != 48) s += 8;
+    return s;
+}
+
 // ds_read_b64_tr_b16: in each group of 16 lanes, lanes 4j .. 4j + 3 read 8
 // bytes each (row j of a 4 x 16 block of halves); lane i of the group
 // receives column i of that block, one half from each row.
@@ -104,11 +114,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     constexpr int D = 32 * NT;          // head size
     constexpr int DC = D / 16;          // 16-wide slices of a head (MFMA depth)
     constexpr int KT = BN / 32;         // 32-key tiles per block
-    // LDS rows: K at a stride of D + 8 halves (a 16-byte read of 8
-    // consecutive rows hits 8 distinct bank quads), V at D + 16 (the four
-    // rows a transpose read of 16 lanes touches hit 32 distinct banks).
+    // LDS rows: K at a stride of D + 8 halves (the 16-byte reads of 16
+    // consecutive rows hit distinct banks), V at v_stride_tr(D).
     constexpr int KS = D + 8;
-    constexpr int VS = D + 16;
+    constexpr int VS = v_stride_tr(D);
     constexpr int THREADS = 64 * QW * KSPLIT;
     constexpr int TILE_Q = 32 * QG * QW;               // queries per tile
     constexpr int BLOCK_CHUNKS = BN * D / 8;           // 16-byte chunks of one K (or V) block

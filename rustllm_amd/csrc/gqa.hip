@@ -148,6 +148,16 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
 
 // -------------------------------------------------------------- P V, MFMA
 
+// Row stride (halves) of V in LDS for the transpose reads: the 32 lanes one
+// LDS cycle serves read 4 rows x 2 runs of 16 bytes; with 64 banks of 4
+// bytes those land on distinct banks when the stride in dwords is 16 or 48
+// modulo 64.  Smallest such stride >= D (in steps of 8 halves).
+__host__ __device__ constexpr int v_stride_tr(int d) {
+    int s = d;
+    while ((s / 2) % 64 != 16 && (s / 2) % 64 != 48) s += 8;
+    return s;
+}
+
 __device__ inline h4 lds_read_transposed(const half_t* ptr) {
     const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (__attribute__((address_space(3))) s16x4*)(ptr));
@@ -161,7 +171,7 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
     constexpr int D = 32 * NT;
     constexpr int BN = 128;               // keys per step
     constexpr int PC = BN / 16;           // 16-key slices per step
-    constexpr int VS = D + 16;            // LDS row stride of V (transpose reads hit 32 banks)
+    constexpr int VS = v_stride_tr(D);    // LDS row stride of V
     constexpr int PS = BN + 8;            // LDS row stride of a wave's 32 x 128 probability tile
     constexpr int LOADS = BN * D / 8 / 256;
     constexpr int ROW_CHUNKS = D / 8;
