@@ -6,8 +6,8 @@
 // The scores make a [B, QH, Q, K] round trip through memory twice.  Here the
 // four are one pass ("flash" attention: Dao et al., 2022): each workgroup
 // keeps a tile of queries in registers, streams the keys and values of its
-// KV head through LDS in blocks of 64, and folds every block into a running
-// (max, sum, output) per query, so the scores never leave the chip.
+// KV head through LDS in blocks of 64 or 128, and folds every block into a
+// running (max, sum, output) per query, so the scores never leave the chip.
 //
 // f16 with a head size that is a multiple of 32 (32..128) takes the matrix
 // cores (v_mfma_f32_32x32x16_f16, f32 accumulation): per wave 32 queries,
@@ -17,8 +17,11 @@
 // holding eight consecutive keys of P -- exactly the operand layout of the
 // P V product, so P goes from registers to the second MFMA without moving.
 // K rows are stored in LDS in that key order; V stays row-major and its
-// transposed operand comes from the LDS transpose read (ds_read_b64_tr_b16).  Other shapes (f32, odd
-// head sizes, up to 512) take a one-wave-per-query kernel on the vector ALUs.
+// transposed operand comes from the LDS transpose read (ds_read_b64_tr_b16).
+// K and V blocks travel from memory to LDS by DMA (buffer loads into LDS,
+// two stages deep), so the next block streams in during this one's compute.
+// Other shapes (f32, odd head sizes, up to 512) take a one-wave-per-query
+// kernel on the vector ALUs.
 //
 // Arithmetic (both kernels): scores are f32 dot products of the (widened)
 // inputs; x * scale in f32 and masking as attention_scale_mask.metal:21-41
@@ -97,6 +100,48 @@ __device__ inline h4 lds_read_transposed(const half_t* p) {
     return __builtin_bit_cast(h4, r);
 }
 
+// Chunk order of the unpadded LDS rows the DMA-fed kernel uses: 16-byte
+// chunk c of row r sits at chunk c ^ lds_swizzle(r) of that row.  The MFMA
+// operand reads of K (16 rows x one chunk per 16 lanes) and the transpose
+// reads of V (4 rows x 4 chunks per 32 lanes) then each fall on 64 distinct
+// banks (64 banks of 4 bytes; a row is D / 8 chunks).
+template <int NT>
+__device__ inline uint32_t lds_swizzle(uint32_t r) {
+    if constexpr (NT == 1) return (r >> 2) & 3u;
+    else if constexpr (NT == 2) return ((r & 2u) << 1) | ((r >> 2) & 3u);
+    else if constexpr (NT == 4) return ((r & 3u) << 2) | ((r >> 2) & 3u);
+    else return 0u;
+}
+
+// Buffer resource (gfx9 descriptor: base, stride 0, size in bytes, 32-bit
+// data format) for raw loads from `base`: a load at or past `bytes` returns
+// zeros.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ inline i32x4 raw_buffer(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return i32x4{int(uint32_t(a)), int(uint32_t(a >> 32) & 0xffffu), int(bytes), 0x00020000};
+}
+
+// One 16-byte chunk per lane from a raw buffer straight into LDS
+// (buffer_load_dwordx4 ... lds): lane l's chunk lands at lds_addr + 16 l.
+// The LDS address goes through M0, saved and restored around the load.  In
+// assembly so that the compiler's wait counting, which cannot tell the LDS
+// stage being filled from the one being read, does not hold every LDS read
+// of the step until the transfer lands; the caller waits (vmcnt) before the
+// barrier that hands the stage over.
+__device__ inline void dma_to_lds(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+        : "memory");
+}
+
 // Rescaling threshold (log2 units): a query's running max m is only moved
 // when a block's max exceeds it by more than this, so most blocks skip the
 // rescale of the running sum and output; probabilities exp2(t - m) then stay
@@ -107,28 +152,44 @@ constexpr float kRescaleSlack = 3.0f;
 // operand a wave reads from LDS); KSPLIT groups of such waves split the key
 // blocks of the tile between them (group g takes blocks g, g + KSPLIT, ...)
 // and merge their partial (max, sum, output) through LDS at the end.
-template <int NT, int QW, int KSPLIT, int BN, int STAGES, int PRIO, int QG>
+//
+// DMA: K and V blocks go from memory straight into LDS (buffer_load ... lds,
+// no registers), two stages deep, so the next blocks stream in while this
+// one is computed; rows are unpadded with the chunk order of lds_swizzle.
+// Otherwise blocks pass through registers into rows padded for the bank
+// layout (head size 96, whose 12 chunks a row do not swizzle onto 64 banks),
+// one block at a time.
+template <int NT, int QW, int KSPLIT, int BN, int QG, bool DMA>
 __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
     half_t* __restrict__ out, AttnParams p) {
     constexpr int D = 32 * NT;          // head size
     constexpr int DC = D / 16;          // 16-wide slices of a head (MFMA depth)
     constexpr int KT = BN / 32;         // 32-key tiles per block
-    // LDS rows: K at a stride of D + 8 halves (the 16-byte reads of 16
-    // consecutive rows hit distinct banks), V at v_stride_tr(D).
-    constexpr int KS = D + 8;
-    constexpr int VS = v_stride_tr(D);
+    static_assert(!DMA || NT != 3, "no bank-spreading chunk order for 12-chunk rows");
+    // LDS rows: with DMA unpadded and swizzled; otherwise K at a stride of
+    // D + 8 halves (the 16-byte reads of 16 consecutive rows hit distinct
+    // banks), V at v_stride_tr(D).
+    constexpr int KS = DMA ? D : D + 8;
+    constexpr int VS = DMA ? D : v_stride_tr(D);
+    constexpr int NSTAGE = DMA ? 2 : 1;
     constexpr int THREADS = 64 * QW * KSPLIT;
     constexpr int TILE_Q = 32 * QG * QW;               // queries per tile
     constexpr int BLOCK_CHUNKS = BN * D / 8;           // 16-byte chunks of one K (or V) block
     constexpr int LOADS = BLOCK_CHUNKS * KSPLIT / THREADS;
+    constexpr int DMA_LOADS = 2 * LOADS;               // K and V chunks per lane (DMA)
+    constexpr int WAVES = THREADS / 64;
+    constexpr int ROUNDS = BLOCK_CHUNKS / (64 * WAVES);  // DMA instructions per region
     constexpr int ROW_CHUNKS = D / 8;
     constexpr int KV_HALVES = BN * KS + BN * VS;       // one block of K and V
+    constexpr int STAGE_BYTES = KSPLIT * KV_HALVES * 2;
     constexpr int MERGE = QG * (NT * 16 + 2);          // floats a lane hands over
-    constexpr int LDS_BYTES = STAGES * KSPLIT * KV_HALVES * 2 > (KSPLIT - 1) * QW * 64 * MERGE * 4
-                                  ? STAGES * KSPLIT * KV_HALVES * 2
+    constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES > (KSPLIT - 1) * QW * 64 * MERGE * 4
+                                  ? NSTAGE * STAGE_BYTES
                                   : (KSPLIT - 1) * QW * 64 * MERGE * 4;
     static_assert((BLOCK_CHUNKS * KSPLIT) % THREADS == 0, "blocks must split evenly");
+    static_assert(!DMA || BLOCK_CHUNKS % (64 * WAVES) == 0,
+                  "every wave's DMA instructions cover whole regions");
     __shared__ __align__(16) unsigned char lds[LDS_BYTES];
     half_t* const kv_lds = reinterpret_cast<half_t*>(lds);
 
@@ -149,8 +210,43 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     // 16g + 4j + a reads row 8(g / 2) + j (+ 16c + 4e2 for slice c, half e2)
     // at columns 16(g % 2) + 4a (+ 32t for head tile t); the hardware then
     // hands lane 16g + i the column 16(g % 2) + i of those four rows.
-    const uint32_t tr_off = (8 * (lane / 32) + (lane % 16) / 4) * VS + 16 * ((lane / 16) % 2) +
-                            4 * (lane % 4);
+    // Per lane: offsets of its K operand chunks (row `col`, chunk 2c + hs) and
+    // of its V transpose reads (e2 = rows 0-3 or 4-7 of the eight, t = head
+    // tile), in the chunk order of the LDS rows.
+    uint32_t koff[DC];
+#pragma unroll
+    for (int c = 0; c < DC; ++c)
+        koff[c] = col * KS + 8 * ((2 * c + hs) ^ (DMA ? lds_swizzle<NT>(col) : 0u));
+    uint32_t voff[2][NT];
+#pragma unroll
+    for (int e2 = 0; e2 < 2; ++e2) {
+        const uint32_t row = 8 * (lane / 32) + (lane % 16) / 4 + 4 * e2;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t ch = 2 * ((lane / 16) % 2) + (lane % 4) / 2 + 4 * t;
+            voff[e2][t] = row * VS + 8 * (ch ^ (DMA ? lds_swizzle<NT>(row) : 0u)) + 4 * (lane % 2);
+        }
+    }
+    // DMA: a stage holds, per key group, the K block then the V block
+    // (regions of BLOCK_CHUNKS 16-byte chunks).  Instruction li of a wave
+    // fills 64 chunks (lane order) of region li / ROUNDS, so the region --
+    // which block, K or V -- is a compile-time fact of li; the lane picks the
+    // source chunk that belongs at its place.
+    const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t dma_off[DMA_LOADS];
+#pragma unroll
+    for (int li = 0; li < DMA_LOADS; ++li) {
+        const bool is_v = (li / ROUNDS) % 2;
+        const uint32_t cf = ((li % ROUNDS) * WAVES + wave) * 64 + lane;  // chunk in the region
+        const uint32_t r = cf / ROW_CHUNKS;
+        const uint32_t ch = (cf % ROW_CHUNKS) ^ lds_swizzle<NT>(r);
+        const uint32_t key = is_v ? r : ((r & ~31u) | perm32(r & 31u));
+        dma_off[li] = key * (D * 2) + ch * 16;
+    }
+    const i32x4 k_rsrc = raw_buffer(kh, p.kv_len * (D * 2));
+    const i32x4 v_rsrc = raw_buffer(vh, p.kv_len * (D * 2));
+    const uint32_t lds_base = uint32_t(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)(lds)));
 
     // The causal tiles of a head are paired (t, tiles - 1 - t) so that every
     // workgroup streams about the same number of key blocks.
@@ -241,41 +337,67 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
             }
         };
 
-        load_step(0);
-        __syncthreads();  // the previous tile's LDS use is over
-        store_step(0);
-        __syncthreads();
+        // DMA of one step's blocks into stage step % 2.  Keys past kv_len
+        // read as zeros (the buffer ends at row kv_len): their scores are
+        // masked and their value rows add nothing.
+        auto issue_step = [&](uint32_t step) {
+            // LDS address of the wave's first chunk in this stage
+            const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(
+                lds_base + (step % 2) * STAGE_BYTES + 16 * 64 * wave_u);
+#pragma unroll
+            for (int li = 0; li < DMA_LOADS; ++li) {
+                constexpr int PER_BLOCK = 2 * ROUNDS;  // instructions per group (K and V)
+                const uint32_t blk = step * KSPLIT + li / PER_BLOCK;
+                if (blk >= blocks) continue;
+                const bool is_v = (li / ROUNDS) % 2;
+                const uint32_t region = li / ROUNDS, round = li % ROUNDS;
+                dma_to_lds(is_v ? v_rsrc : k_rsrc,
+                           wave_lds + 16 * (region * BLOCK_CHUNKS + round * WAVES * 64),
+                           dma_off[li] + blk * (BN * D * 2));
+            }
+        };
 
-        // With two stages the next block is stored into the other stage
-        // while this one is read: one barrier per step.
+        if constexpr (DMA) {
+            issue_step(0);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        } else {
+            load_step(0);
+            __syncthreads();  // the previous tile's LDS use is over
+            store_step(0);
+            __syncthreads();
+        }
+
+        // DMA: the blocks of step j + 1 stream into the other stage while
+        // step j is computed (one barrier per step).  Otherwise they wait in
+        // registers and are stored after the step's compute.
         for (uint32_t step = 0; step < steps; ++step) {
-            if (step + 1 < steps) load_step(step + 1);
+            if constexpr (DMA) {
+                issue_step(step + 1);  // nothing past the last block
+            } else {
+                if (step + 1 < steps) load_step(step + 1);
+            }
             const uint32_t blk = step * KSPLIT + sub;
-            const half_t* ks = kv_lds + ((step % STAGES) * KSPLIT + sub) * KV_HALVES;
+            const half_t* ks = kv_lds + ((step % NSTAGE) * KSPLIT + sub) * KV_HALVES;
             const half_t* vs = ks + BN * KS;
             if (blk < blocks && blk * BN < wave_keys) {
                 // S^T = K Q^T: each K operand read once, used by every group.
                 f32x16 s[QG][KT];
-                // A wave issuing matrix work goes first, so the other wave of
-                // the SIMD fills the vector ALU meanwhile (wave priority only).
-                if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(PRIO);
 #pragma unroll
                 for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
                     for (int g = 0; g < QG; ++g)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) s[g][kt][r] = 0.0f;
-                    const half_t* krow = ks + (kt * 32 + col) * KS + 8 * hs;
 #pragma unroll
                     for (int c = 0; c < DC; ++c) {
-                        const h8 ka = *reinterpret_cast<const h8*>(krow + 16 * c);
+                        const h8 ka = *reinterpret_cast<const h8*>(ks + kt * 32 * KS + koff[c]);
 #pragma unroll
                         for (int g = 0; g < QG; ++g)
                             s[g][kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[g][c],
                                                                              s[g][kt], 0, 0, 0);
                     }
                 }
-                if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(0);
                 const uint32_t kbase = blk * BN;
                 const bool masking = kbase + BN - 1 > p.start + qw0 || kbase + BN > p.kv_len;
                 h8 pb[QG][BN / 16];
@@ -337,14 +459,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                     }
                 }
                 // O^T += V^T P^T, 16 keys per MFMA; each V operand read once.
-                if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(PRIO);
 #pragma unroll
                 for (int c = 0; c < BN / 16; ++c) {
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
-                        const half_t* vsrc = vs + tr_off + 16 * c * VS + 32 * t;
-                        const h4 lo = lds_read_transposed(vsrc);
-                        const h4 hi = lds_read_transposed(vsrc + 4 * VS);
+                        const h4 lo = lds_read_transposed(vs + 16 * c * VS + voff[0][t]);
+                        const h4 hi = lds_read_transposed(vs + 16 * c * VS + voff[1][t]);
                         const h8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
                         for (int g = 0; g < QG; ++g)
@@ -352,10 +472,13 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                                                                             0, 0, 0);
                     }
                 }
-                if constexpr (PRIO > 0) __builtin_amdgcn_s_setprio(0);
             }
-            if constexpr (STAGES == 1) __syncthreads();
-            if (step + 1 < steps) store_step((step + 1) % STAGES);
+            if constexpr (DMA) {
+                __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed
+            } else {
+                __syncthreads();
+                if (step + 1 < steps) store_step(0);
+            }
             __syncthreads();
         }
 
@@ -801,23 +924,27 @@ rl_status validate_attention(const rl_buffer* q, const rl_buffer* k, const rl_bu
     return RL_OK;
 }
 
+// MFMA kernel shape: 4 waves of 32 queries, two key halves (8 waves); key
+// blocks of 128 for head sizes up to 64 and of 64 above (two DMA stages of
+// K and V then take 64, 128 and 128 KB of LDS for head sizes 32, 64, 128).
 constexpr int kFlashQueryWaves = 4;
 constexpr int kFlashKeySplit = 2;
-constexpr int kFlashBlockKeys = 64;
-constexpr int kFlashStages = 1;
-constexpr int kFlashPriority = 0;
+constexpr int kFlashMaxBlockKeys = 128;
 constexpr int kFlashQueryGroups = 1;
 
 // Which kernel a shape takes: the MFMA kernel for f16 with a head size of
-// 32, 64, 96 or 128 and aligned buffers; the row kernel otherwise (head
-// sizes up to 512).
+// 32, 64, 96 or 128 and aligned buffers (and byte offsets into one KV head,
+// a block past its end included, that fit the 32-bit buffer offsets of its
+// loads); the row kernel otherwise (head sizes up to 512).
 template <typename T>
 bool use_flash(const AttnShape& s, const void* q, const void* k, const void* v, const void* o) {
     if constexpr (!std::is_same<T, half_t>::value) {
         return false;
     } else {
-        return s.head_dim % 32 == 0 && s.head_dim <= 128 && aligned_to(q, 16) &&
-               aligned_to(k, 16) && aligned_to(v, 16) && aligned_to(o, 16);
+        const uint64_t span = (s.kv_len + uint64_t(kFlashMaxBlockKeys) * kFlashKeySplit) *
+                              s.head_dim * sizeof(T);
+        return s.head_dim % 32 == 0 && s.head_dim <= 128 && span <= UINT32_MAX &&
+               aligned_to(q, 16) && aligned_to(k, 16) && aligned_to(v, 16) && aligned_to(o, 16);
     }
 }
 
@@ -896,14 +1023,13 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
             p.pairs = (p.tiles + 1) / 2;
             const uint64_t grid = heads * p.pairs;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "attention grid exceeds u32");
-            constexpr int QW = kFlashQueryWaves, KSPLIT = kFlashKeySplit, BN = kFlashBlockKeys,
-                          ST = kFlashStages, PR = kFlashPriority, QG = kFlashQueryGroups;
+            constexpr int QW = kFlashQueryWaves, KSPLIT = kFlashKeySplit, QG = kFlashQueryGroups;
             const dim3 g(static_cast<unsigned>(grid)), b(64 * QW * KSPLIT);
             switch (s.head_dim / 32) {
-                case 1: RL_LAUNCH(ctx, (k_flash_attention<1, QW, KSPLIT, BN, ST, PR, QG>), g, b, qd, kd, vd, od, p); break;
-                case 2: RL_LAUNCH(ctx, (k_flash_attention<2, QW, KSPLIT, BN, ST, PR, QG>), g, b, qd, kd, vd, od, p); break;
-                case 3: RL_LAUNCH(ctx, (k_flash_attention<3, QW, KSPLIT, BN, ST, PR, QG>), g, b, qd, kd, vd, od, p); break;
-                default: RL_LAUNCH(ctx, (k_flash_attention<4, QW, KSPLIT, BN, ST, PR, QG>), g, b, qd, kd, vd, od, p); break;
+                case 1: RL_LAUNCH(ctx, (k_flash_attention<1, QW, KSPLIT, 128, QG, true>), g, b, qd, kd, vd, od, p); break;
+                case 2: RL_LAUNCH(ctx, (k_flash_attention<2, QW, KSPLIT, 128, QG, true>), g, b, qd, kd, vd, od, p); break;
+                case 3: RL_LAUNCH(ctx, (k_flash_attention<3, QW, KSPLIT, 64, QG, false>), g, b, qd, kd, vd, od, p); break;
+                default: RL_LAUNCH(ctx, (k_flash_attention<4, QW, KSPLIT, 64, QG, true>), g, b, qd, kd, vd, od, p); break;
             }
             return after_launch(ctx, name);
         }

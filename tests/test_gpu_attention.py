@@ -56,6 +56,8 @@ SHAPES = [
     (1, 3, 1, 257, 257, 257, 32, 0),    # three query tiles (paired 0/2, 1 alone)
     (1, 2, 1, 64, 64, 64, 96, 0),
     (1, 2, 2, 200, 300, 300, 128, 100),
+    (1, 8, 2, 256, 1500, 1536, 128, 1244),  # many key blocks per workgroup, D 128
+    (1, 6, 3, 384, 2000, 2048, 32, 1616),   # many key blocks, D 32, ragged last block
     (1, 6, 2, 1, 2048, 4096, 64, 2047),  # decode step from a half-full cache
     (1, 2, 1, 33, 40, 40, 48, 7),        # head size off the matrix-core path
     (1, 2, 2, 17, 17, 20, 80, 0),
