@@ -589,8 +589,9 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
                  "fused_speedup": round(chain_us / us, 2),
                  "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None})
     del sc, pr
-    # decode: one new token of 15 heads over a 4096-row KV cache (two launches:
-    # split keys, combine), timed with stream events around the call
+    # decode: one new token of 15 heads over a 4096-row KV cache (one launch:
+    # key splits whose last workgroup per KV head merges them), timed with
+    # stream events around the call
     qd = ctx.upload(q[:, :, :1].copy())
     od = ctx.empty((1, qh, 1, hd), F16)
     for _ in range(3):
@@ -607,8 +608,8 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
         ctx.destroy_event(e)
     dec_bytes = (2 * k.size + 2 * qh * hd) * 2
     log(f"  {'decode attention_f16 over 4096 keys':34s} {dec_us:9.2f} us "
-        f"{dec_bytes / (dec_us * 1e-6) / 1e9:8.1f} GB/s (2 launches, event-timed)")
-    rows.append({"op": "decode attention_f16 (1 token, 4096-row cache, 2 launches)", "dtype": "f16",
+        f"{dec_bytes / (dec_us * 1e-6) / 1e9:8.1f} GB/s (one launch, event-timed)")
+    rows.append({"op": "decode attention_f16 (1 token, 4096-row cache)", "dtype": "f16",
                  "shape": [1, qh, 1, hd], "bytes": dec_bytes, "us": round(dec_us, 3),
                  "us_min": None, "GB/s": round(dec_bytes / (dec_us * 1e-6) / 1e9, 1),
                  "pct_peak": round(100 * dec_bytes / (dec_us * 1e-6) / 1e9 / PEAK_GBS, 1),

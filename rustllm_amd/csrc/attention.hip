@@ -547,6 +547,43 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     }
 }
 
+// ------------------------------------------------- wave reductions
+
+// Wave-wide max / sum without LDS round trips (a __shfl_xor is an LDS
+// permute, ~100 cycles each): four DPP steps reduce every row of 16 lanes
+// (lane ^ 1, lane ^ 2, then the mirrors within 8 and within 16 lanes pair
+// the halves), and the four row results are read as scalars and combined,
+// so the result is the same in every lane.
+template <int CTRL>
+__device__ inline float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+__device__ inline float lane_value(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ inline float row16_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+    return fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+}
+__device__ inline float row16_sum(float v) {
+    v += dpp_move<0xB1>(v);
+    v += dpp_move<0x4E>(v);
+    v += dpp_move<0x141>(v);
+    return v + dpp_move<0x140>(v);
+}
+__device__ inline float wave_max_dpp(float v) {
+    v = row16_max(v);
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
+                 fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ inline float wave_sum_dpp(float v) {
+    v = row16_sum(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
 // ------------------------------------------------- one wave per query row
 
 // Keys are taken 256 at a time: each lane scores four (a full dot product
@@ -599,7 +636,7 @@ __global__ __launch_bounds__(64) void k_attention_rows(const T* __restrict__ q,
             }
             mx = fmaxf(mx, s[i]);
         }
-        mx = wave_max(mx);
+        mx = wave_max_dpp(mx);
         const float m_new = fmaxf(m, mx);
         const float alpha = exp_fast(m - m_new);
         m = m_new;
@@ -625,7 +662,7 @@ __global__ __launch_bounds__(64) void k_attention_rows(const T* __restrict__ q,
         }
         __syncthreads();
     }
-    const float inv = 1.0f / wave_sum(l);
+    const float inv = 1.0f / wave_sum_dpp(l);
     T* orow = out + uint64_t(row) * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
@@ -636,10 +673,45 @@ __global__ __launch_bounds__(64) void k_attention_rows(const T* __restrict__ q,
 
 // ------------------------------------------------- split keys (decode)
 
+// One wave merges one query row's `splits` partials (the maxima and sums
+// read by all lanes at once, the weights kept in `w`, this wave's LDS).
+constexpr uint32_t kMaxSplits = 1024;
+
+template <typename T>
+__device__ inline void merge_splits(const float* src, T* dst, uint32_t splits,
+                                    uint32_t head_dim, float* w) {
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t stride = head_dim + 2;
+    float mt = -INFINITY;
+    for (uint32_t s = lane; s < splits; s += 64) mt = fmaxf(mt, src[s * stride]);
+    mt = wave_max_dpp(mt);
+    float lt = 0.0f;
+    for (uint32_t s = lane; s < splits; s += 64) {
+        const float ms = src[s * stride];
+        const float ws = ms == -INFINITY ? 0.0f : exp_fast(ms - mt);
+        w[s] = ws;
+        lt += src[s * stride + 1] * ws;
+    }
+    lt = wave_sum_dpp(lt);
+    // the weights other lanes wrote
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float inv = 1.0f / lt;
+    for (uint32_t d = lane; d < head_dim; d += 64) {
+        float acc = 0.0f;
+#pragma unroll 8
+        for (uint32_t s = 0; s < splits; ++s) acc += src[s * stride + 2 + d] * w[s];
+        dst[d] = from_float<T>(acc * inv);
+    }
+}
+
+
 // Few query rows per KV head (a decode step: R = group * q_len rows): the
 // rows of one KV head share every K and V row read.  Workgroup (kv head,
 // split) takes 64 keys per wave and writes one partial (max, sum, output
-// row) per query row; k_attention_combine merges the splits.  A wave's loads
+// row) per query row; the workgroup that finishes a KV head's last split
+// merges them (one launch per decode step).  A wave's loads
 // are issued together -- its 64 value rows (contiguous in the cache) go
 // straight to LDS (global_load_lds), its key rows to registers -- so a split
 // costs one memory round trip.  RM bounds the rows, DPL the head elements
@@ -651,11 +723,12 @@ constexpr int kStageBytes = 64 * 256;          // LDS per wave for staged value 
 template <typename T, int RM, int DPL>
 __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    float* __restrict__ part, AttnParams p, uint32_t splits, bool vec_rows) {
+    float* __restrict__ part, uint32_t* __restrict__ tickets, T* __restrict__ out, AttnParams p,
+    uint32_t splits, bool vec_rows) {
     constexpr int DMAX = 64 * DPL;
     typedef typename Pack16<T>::type V;
     constexpr int N = Pack16<T>::N;
-    __shared__ __align__(16) float qs[RM * DMAX];
+    __shared__ __align__(16) T qs[RM * DMAX];  // the rows' queries, zero past the head size
     __shared__ float ps[kSplitWaves][RM][64];
     __shared__ __align__(16) unsigned char vstage[kSplitWaves][kStageBytes];
     __shared__ float merge_m[kSplitWaves][RM];
@@ -686,24 +759,30 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
                     src + uint64_t(c0 + lane) * 16,
                     (__attribute__((address_space(3))) void*)(vstage[wave] + c0 * 16), 16, 0, 0);
         }
+        // rows n .. 63 (a wave past the last key): zeros, so that the value
+        // reads below need no bounds
+        const uint32_t all = 64 * D * sizeof(T) / 16;
+        for (uint32_t c = chunks + lane; c < all; c += 64)
+            *reinterpret_cast<uint4*>(vstage[wave] + c * 16) = uint4{0, 0, 0, 0};
     }
-    // key rows (lane = key), every load before the first use
+    // key rows (lane = key), every load before the first use; packs past
+    // the head size are zero
     constexpr int PACKS = DMAX / N;
     V kv[PACKS];
     if (vec_rows && lane < n) {
         const T* krow = kh + uint64_t(key) * D;
 #pragma unroll
         for (int i = 0; i < PACKS; ++i)
-            if (uint32_t(i * N) < D) kv[i] = *reinterpret_cast<const V*>(krow + i * N);
+            kv[i] = uint32_t(i * N) < D ? *reinterpret_cast<const V*>(krow + i * N) : V{};
     }
     // row r = g * q_len + qi is query qi of head first_head + g
     for (uint32_t i = threadIdx.x; i < RM * DMAX; i += 64 * kSplitWaves) {
         const uint32_t r = i / DMAX, d = i % DMAX;
-        float x = 0.0f;
+        T x = T(0.0f);
         if (r < R && d < D) {
             const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
                                  r % p.q_len;
-            x = to_float(q[row * D + d]);
+            x = q[row * D + d];
         }
         qs[i] = x;
     }
@@ -714,16 +793,26 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
     for (int r = 0; r < RM; ++r) sc[r] = 0.0f;
     if (lane < n) {
         if (vec_rows) {
+            // per pack: every row's query values read first (one LDS wait
+            // per pack, not per read), then the products in f32 -- pairs of
+            // f16 products per v_dot2_f32_f16, f32 elements by FMA -- over
+            // the whole DMAX (both operands are zero past the head size)
 #pragma unroll
             for (int i = 0; i < PACKS; ++i) {
-                if (uint32_t(i * N) >= D) break;
+                V qv[RM];
 #pragma unroll
-                for (int e = 0; e < N; e += 4) {
+                for (int r = 0; r < RM; ++r)
+                    qv[r] = *reinterpret_cast<const V*>(qs + r * DMAX + i * N);
 #pragma unroll
-                    for (int r = 0; r < RM; ++r) {
-                        const float4 qv = *reinterpret_cast<const float4*>(qs + r * DMAX + i * N + e);
-                        sc[r] += qv.x * to_float(kv[i][e]) + qv.y * to_float(kv[i][e + 1]) +
-                                 qv.z * to_float(kv[i][e + 2]) + qv.w * to_float(kv[i][e + 3]);
+                for (int r = 0; r < RM; ++r) {
+                    if constexpr (std::is_same<T, half_t>::value) {
+#pragma unroll
+                        for (int e = 0; e < N; e += 2)
+                            sc[r] = __builtin_amdgcn_fdot2(h2{qv[r][e], qv[r][e + 1]},
+                                                           h2{kv[i][e], kv[i][e + 1]}, sc[r], false);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < N; ++e) sc[r] = __builtin_fmaf(qv[r][e], kv[i][e], sc[r]);
                     }
                 }
             }
@@ -732,7 +821,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
             for (uint32_t d = 0; d < D; ++d) {
                 const float kd = to_float(krow[d]);
 #pragma unroll
-                for (int r = 0; r < RM; ++r) sc[r] += qs[r * DMAX + d] * kd;
+                for (int r = 0; r < RM; ++r) sc[r] += to_float(qs[r * DMAX + d]) * kd;
             }
         }
     }
@@ -742,7 +831,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
         const uint32_t limit = p.start + uint32_t(r) % p.q_len;  // last key row r sees
         const bool live = uint32_t(r) < R && lane < n && key <= limit;
         const float x = live ? sc[r] * p.scale : -INFINITY;
-        m[r] = wave_max(x);
+        m[r] = wave_max_dpp(x);
         const float e = live ? exp_fast(x - m[r]) : 0.0f;
         l[r] = e;  // this lane's share
         ps[wave][r][lane] = e;
@@ -757,42 +846,59 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
     for (int r = 0; r < RM; ++r)
 #pragma unroll
         for (int e = 0; e < DPL; ++e) o[r][e] = 0.0f;
-    // eight keys at a time, their reads issued before the arithmetic; the
-    // LDS and the global variant are separate code so that each read is a
-    // plain ds_read or global_load (a pointer that may be either would make
-    // every read a flat access with a full wait).
-    auto pv = [&](const T* vbase) {
-        for (uint32_t j0 = 0; j0 < n; j0 += 8) {
+    // eight keys at a time, their reads issued before the arithmetic.  From
+    // the LDS stage every read is unconditional -- rows n .. 63 hold zeros and
+    // lanes past the head size read other stage bytes into outputs that are
+    // never stored -- so the reads are not serialised behind branches; from
+    // memory a read past the wave's rows is skipped.  The LDS and the global variant are
+    // separate code so that each read is a plain ds_read or global_load (a
+    // pointer that may be either would make every read a flat access with a
+    // full wait).
+    auto pv = [&](const T* vbase, auto from_lds) {
+        constexpr bool LDS = decltype(from_lds)::value;
+        auto eight_keys = [&](uint32_t j0) {
             float vv[8][DPL];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
 #pragma unroll
                 for (int e = 0; e < DPL; ++e) {
                     const uint32_t d = lane * DPL + e;
-                    vv[u][e] =
-                        (j0 + u < n && d < D) ? to_float(vbase[uint64_t(j0 + u) * D + d]) : 0.0f;
+                    if constexpr (LDS) {
+                        vv[u][e] = to_float(vbase[(j0 + u) * D + d]);  // inside the stage
+                    } else {
+                        vv[u][e] = j0 + u < n && d < D
+                                       ? to_float(vbase[uint64_t(j0 + u) * D + d]) : 0.0f;
+                    }
                 }
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
 #pragma unroll
                 for (int r = 0; r < RM; ++r) {
-                    const float pj = j0 + u < n ? ps[wave][r][j0 + u] : 0.0f;
+                    const float pj = ps[wave][r][j0 + u];  // 0 for keys past n
 #pragma unroll
                     for (int e = 0; e < DPL; ++e) o[r][e] += pj * vv[u][e];
                 }
             }
+        };
+        if constexpr (LDS) {
+            // all 64 rows (zeros past n), unrolled so that the reads of later
+            // keys issue under the products of earlier ones
+#pragma unroll
+            for (uint32_t j0 = 0; j0 < 64; j0 += 8) eight_keys(j0);
+        } else {
+            for (uint32_t j0 = 0; j0 < n; j0 += 8) eight_keys(j0);
         }
     };
     if (staged) {
-        pv(reinterpret_cast<const T*>(vstage[wave]));
+        pv(reinterpret_cast<const T*>(vstage[wave]), std::true_type{});
     } else {
-        pv(vh + uint64_t(base) * D);
+        pv(vh + uint64_t(base) * D, std::false_type{});
     }
     // the four waves' states -> one partial per row
 #pragma unroll
     for (int r = 0; r < RM; ++r) {
-        const float lsum = wave_sum(l[r]);
+        const float lsum = wave_sum_dpp(l[r]);
         if (lane == 0) {
             merge_m[wave][r] = m[r];
             merge_l[wave][r] = lsum;
@@ -824,38 +930,25 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
             dst[1] = lt;
         }
     }
-}
 
-// One wave per query row: merges the row's `splits` partials (the maxima and
-// sums read by all lanes at once, the weights kept in LDS).
-constexpr uint32_t kMaxSplits = 1024;
-
-template <typename T>
-__global__ __launch_bounds__(64) void k_attention_combine(const float* __restrict__ part,
-                                                          T* __restrict__ out, uint32_t splits,
-                                                          uint32_t head_dim) {
-    __shared__ float w[kMaxSplits];
-    const uint64_t row = blockIdx.x;
-    const uint32_t stride = head_dim + 2;
-    const float* src = part + row * splits * stride;
-    float mt = -INFINITY;
-    for (uint32_t s = threadIdx.x; s < splits; s += 64) mt = fmaxf(mt, src[s * stride]);
-    mt = wave_max(mt);
-    float lt = 0.0f;
-    for (uint32_t s = threadIdx.x; s < splits; s += 64) {
-        const float ms = src[s * stride];
-        const float ws = ms == -INFINITY ? 0.0f : exp_fast(ms - mt);
-        w[s] = ws;
-        lt += src[s * stride + 1] * ws;
-    }
-    lt = wave_sum(lt);
+    // Hand-off: the workgroup that completes a KV head's last split merges
+    // that head's rows (one wave per row), so a decode step is one launch.
+    // Every thread's partial stores are made visible device-wide before the
+    // ticket is drawn; the last workgroup reads after an acquire fence and
+    // puts the ticket back to zero for the next launch.
+    __shared__ uint32_t ticket;
+    __threadfence();
     __syncthreads();
-    const float inv = 1.0f / lt;
-    for (uint32_t d = threadIdx.x; d < head_dim; d += 64) {
-        float acc = 0.0f;
-#pragma unroll 8
-        for (uint32_t s = 0; s < splits; ++s) acc += src[s * stride + 2 + d] * w[s];
-        out[row * head_dim + d] = from_float<T>(acc * inv);
+    if (threadIdx.x == 0) ticket = atomicAdd(&tickets[kvb], 1u);
+    __syncthreads();
+    if (ticket != splits - 1) return;
+    __threadfence();
+    if (threadIdx.x == 0) tickets[kvb] = 0;
+    float* w = reinterpret_cast<float*>(vstage[wave]);  // the stage is free now
+    for (uint32_t r = wave; r < R; r += kSplitWaves) {
+        const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
+                             r % p.q_len;
+        merge_splits<T>(part + row * splits * stride, out + row * D, splits, D, w);
     }
 }
 
@@ -948,6 +1041,28 @@ bool use_flash(const AttnShape& s, const void* q, const void* k, const void* v, 
     }
 }
 
+// The decode hand-off counters: at least n of them, all zero.  Growing
+// waits for the stream (a launch in flight may hold the old array).
+rl_status ensure_tickets(rl_context* ctx, uint64_t n) {
+    if (ctx->ticket_count >= n) return RL_OK;
+    const uint64_t count = std::max<uint64_t>(n, 256);
+    hipError_t err = hipStreamSynchronize(ctx->stream);
+    if (err == hipSuccess && ctx->tickets != nullptr) err = hipFree(ctx->tickets);
+    if (err != hipSuccess) return fail(RL_ERR_DEVICE, "ticket array: %s", hipGetErrorString(err));
+    ctx->tickets = nullptr;
+    ctx->ticket_count = 0;
+    void* mem = nullptr;
+    err = hipMalloc(&mem, count * sizeof(uint32_t));
+    if (err == hipSuccess) err = hipMemsetAsync(mem, 0, count * sizeof(uint32_t), ctx->stream);
+    if (err != hipSuccess) {
+        if (mem != nullptr) (void)hipFree(mem);
+        return fail(RL_ERR_DEVICE, "ticket array: %s", hipGetErrorString(err));
+    }
+    ctx->tickets = static_cast<uint32_t*>(mem);
+    ctx->ticket_count = count;
+    return RL_OK;
+}
+
 template <typename T>
 rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
                           const rl_buffer* k, const rl_buffer* v, const AttnShape& s,
@@ -991,13 +1106,16 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
         const bool vec_rows = s.head_dim % (16 / sizeof(T)) == 0 && aligned_to(kd, 16) &&
                               aligned_to(vd, 16);
         const uint64_t part_bytes = rows * splits * (s.head_dim + 2) * sizeof(float);
+        if (rl_status st = ensure_tickets(ctx, s.batch * s.kv_heads)) return st;
         void* part = nullptr;
         if (rl_status st = ctx->pool.allocate(part_bytes, &part)) return st;
         const dim3 gs(static_cast<unsigned>(s.batch * s.kv_heads * splits)), bs(64 * kSplitWaves);
         float* pf = static_cast<float*>(part);
+        uint32_t* tk = ctx->tickets;
         const uint32_t sp = uint32_t(splits);
 #define RL_SPLIT(RMV, DPLV)                                                                    \
-    RL_LAUNCH(ctx, (k_attention_split<T, RMV, DPLV>), gs, bs, qd, kd, vd, pf, p, sp, vec_rows)
+    RL_LAUNCH(ctx, (k_attention_split<T, RMV, DPLV>), gs, bs, qd, kd, vd, pf, tk, od, p, sp,   \
+              vec_rows)
         if (rm == 4 && dpl == 1) RL_SPLIT(4, 1);
         else if (rm == 4 && dpl == 2) RL_SPLIT(4, 2);
         else if (rm == 4) RL_SPLIT(4, 4);
@@ -1008,13 +1126,8 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
         else if (rm == 16) RL_SPLIT(16, 2);
         else RL_SPLIT(32, 1);
 #undef RL_SPLIT
-        rl_status st = after_launch(ctx, name);
-        if (st == RL_OK) {
-            RL_LAUNCH(ctx, (k_attention_combine<T>), dim3(static_cast<unsigned>(rows)), dim3(64),
-                      pf, od, sp, uint32_t(s.head_dim));
-            st = after_launch(ctx, name);
-        }
-        ctx->pool.release(part);  // stream-ordered: later users run after these launches
+        const rl_status st = after_launch(ctx, name);
+        ctx->pool.release(part);  // stream-ordered: later users run after this launch
         return st;
     }
     if constexpr (std::is_same<T, half_t>::value) {

@@ -69,6 +69,12 @@ struct rl_context {
     uint64_t staging_bytes = 0;
     hipEvent_t staging_done = nullptr;
     bool staging_pending = false;
+
+    // One counter per (batch, KV head) for the decode attention's split
+    // hand-off: zero between launches (the workgroup that draws the last
+    // ticket puts it back).  Grown on demand, freed with the context.
+    uint32_t* tickets = nullptr;
+    uint64_t ticket_count = 0;
 };
 
 // Every kernel launch of the library: on the context's stream, and, when

@@ -237,6 +237,7 @@ void rl_context_destroy(rl_context* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->staging != nullptr) (void)hipHostFree(ctx->staging);
     if (ctx->staging_done != nullptr) (void)hipEventDestroy(ctx->staging_done);
+    if (ctx->tickets != nullptr) (void)hipFree(ctx->tickets);
     if (ctx->owns_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;  // the pool frees its blocks
 }
