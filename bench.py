@@ -36,6 +36,7 @@ from rustllm_amd import abi, synth  # noqa: E402
 
 PEAK_GBS = 8000.0
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
+PEAK_F32_TFLOPS = 157.3  # MI355X dense f32 MFMA
 METRIC = "achieved HBM GB/s & % of MI355X peak per op (RMSNorm, softmax, SwiGLU, RoPE)"
 F32, F16 = np.float32, np.float16
 T, H = 4096, 1536
@@ -530,7 +531,8 @@ def attention_flops(qh, q_len, kv_len, hd, start):
 
 def attention_rows(ctx, qh, kvh, hd, tok, reps):
     """SmolLM2-360M attention core at 4096 tokens, f16: the fused pass
-    (rl_attention_f16, matrix cores; TFLOP/s vs the 2.5 PF dense f16 peak),
+    (rl_attention_f16, matrix cores; TFLOP/s vs the 2.5 PF dense f16 peak; and
+    rl_attention_f32 on the same inputs vs the 157.3 TF f32 peak),
     the reference's unfused calls (gqa_qk, scale/mask + softmax, gqa_pv) one
     by one and as one graph, and a decode step over a 4096-row cache."""
     rows = []
@@ -550,6 +552,19 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
                 "pct_peak_mfma": round(100 * flops / (us * 1e-6) / 1e12 / PEAK_F16_TFLOPS, 1)})
     log(f"    -> {row['TFLOP/s']} TFLOP/s ({row['pct_peak_mfma']}% of the dense f16 peak)")
     rows.append(row)
+    # the same layer in f32 (the f32 matrix-core kernel; vs the 157.3 TFLOP/s f32 peak)
+    sets32 = [tuple(ctx.upload(x.astype(np.float32)) for x in (q, k, v)) +
+              (ctx.empty(q.shape, np.float32),) for _ in range(2)]
+    timing = kernel_times_us(ctx, [lambda s=s: ctx.attention(s[0], s[1], s[2], 0.125, 0, None,
+                                                                s[3]) for s in sets32], reps)
+    row32 = op_row("layer.4 attention_f32 (fused, matrix cores)", "f32", [1, qh, tok, hd],
+                   io_bytes * 2, timing)
+    row32.update({"flops": flops, "TFLOP/s": round(flops / (row32["us"] * 1e-6) / 1e12, 1),
+                  "pct_peak_mfma": round(100 * flops / (row32["us"] * 1e-6) / 1e12 /
+                                         PEAK_F32_TFLOPS, 1)})
+    log(f"    -> {row32['TFLOP/s']} TFLOP/s ({row32['pct_peak_mfma']}% of the dense f32 peak)")
+    rows.append(row32)
+    del sets32
     # the reference's calls: scores written (503 MB), softmaxed, read back
     n_scores = qh * tok * tok
     unmasked = qh * (tok * (tok + 1) // 2)
@@ -590,30 +605,15 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
                  "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None})
     del sc, pr
     # decode: one new token of 15 heads over a 4096-row KV cache (one launch:
-    # key splits whose last workgroup per KV head merges them), timed with
-    # stream events around the call
+    # key splits whose last workgroup per KV head merges them), kernel-stamped
+    # like every other line
     qd = ctx.upload(q[:, :, :1].copy())
     od = ctx.empty((1, qh, 1, hd), F16)
-    for _ in range(3):
-        ctx.attention(qd, s0[1], s0[2], 0.125, tok - 1, None, od)
-    ctx.finish()
-    evs = [(ctx.event(), ctx.event()) for _ in range(reps)]
-    for a, b in evs:
-        ctx.record(a)
-        ctx.attention(qd, s0[1], s0[2], 0.125, tok - 1, None, od)
-        ctx.record(b)
-    ctx.finish()
-    dec_us = float(np.median([ctx.elapsed_ms(a, b) * 1e3 for a, b in evs]))
-    for e in [e for pair in evs for e in pair]:
-        ctx.destroy_event(e)
     dec_bytes = (2 * k.size + 2 * qh * hd) * 2
-    log(f"  {'decode attention_f16 over 4096 keys':34s} {dec_us:9.2f} us "
-        f"{dec_bytes / (dec_us * 1e-6) / 1e9:8.1f} GB/s (one launch, event-timed)")
-    rows.append({"op": "decode attention_f16 (1 token, 4096-row cache)", "dtype": "f16",
-                 "shape": [1, qh, 1, hd], "bytes": dec_bytes, "us": round(dec_us, 3),
-                 "us_min": None, "GB/s": round(dec_bytes / (dec_us * 1e-6) / 1e9, 1),
-                 "pct_peak": round(100 * dec_bytes / (dec_us * 1e-6) / 1e9 / PEAK_GBS, 1),
-                 "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None})
+    rows.append(op_row("decode attention_f16 (1 token, 4096-row cache)", "f16", [1, qh, 1, hd],
+                       dec_bytes,
+                       kernel_times_us(ctx, [lambda: ctx.attention(qd, s0[1], s0[2], 0.125,
+                                                                   tok - 1, None, od)], reps)))
     return rows
 
 

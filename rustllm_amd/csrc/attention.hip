@@ -20,8 +20,10 @@
 // transposed operand comes from the LDS transpose read (ds_read_b64_tr_b16).
 // K and V blocks travel from memory to LDS by DMA (buffer loads into LDS,
 // two stages deep), so the next block streams in during this one's compute.
-// Other shapes (f32, odd head sizes, up to 512) take a one-wave-per-query
-// kernel on the vector ALUs.
+// f32 with the same head sizes takes v_mfma_f32_32x32x2_f32 in the same
+// tiling (its own key order, f32 probabilities).  Decode steps (few query
+// rows per KV head) split the keys over many workgroups; other head sizes
+// (up to 512) take a one-wave-per-query kernel on the vector ALUs.
 //
 // Arithmetic (both kernels): scores are f32 dot products of the (widened)
 // inputs; x * scale in f32 and masking as attention_scale_mask.metal:21-41
@@ -547,6 +549,272 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     }
 }
 
+// ------------------------------------------------- f32 on the matrix cores
+
+// f32 takes v_mfma_f32_32x32x2_f32 (two head elements per step, exact f32
+// products).  Key order inside a 32-key tile: LDS row i = 8a + 4h + b holds
+// key 8a + 2b + h (the low three bits rotated), so that register r of a lane
+// in half h of the S^T result holds key 2r + h of the tile -- exactly the B
+// operand (P^T) of the P V step over keys 2r and 2r + 1, with no data
+// movement.  key_row32 is the LDS row of key j.
+__device__ inline uint32_t key_row32(uint32_t j) {
+    return (j & ~7u) | ((j & 1u) << 2) | ((j >> 1) & 3u);
+}
+
+// Row strides (floats) of K and V in LDS.  A K operand read takes one
+// element of 32 rows (lanes 0-31) and the next element of the same rows
+// (lanes 32-63): a stride of 2 mod 64 puts the 64 reads on 64 banks.  A V
+// operand read takes 32 consecutive elements of two rows: a stride of 32 mod
+// 64 does.
+__host__ __device__ constexpr int f32_stride(int d, int residue) {
+    int s = d;
+    while (s % 64 != residue) ++s;
+    return s;
+}
+
+// Same tiling as k_flash_attention (QW waves of 32 queries, KSPLIT key
+// shares merged through LDS, causal tiles paired), blocks staged through
+// registers; scores, probabilities and the running sum stay in f32.
+template <int NT, int QW, int KSPLIT, int BN>
+__global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention_f32(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ out, AttnParams p) {
+    constexpr int D = 32 * NT;
+    constexpr int DS = D / 2;  // MFMA steps over the head
+    constexpr int KT = BN / 32;
+    constexpr int KS = f32_stride(D, 2);
+    constexpr int VS = f32_stride(D, 32);
+    constexpr int THREADS = 64 * QW * KSPLIT;
+    constexpr int TILE_Q = 32 * QW;
+    constexpr int ROW_CHUNKS = D / 4;                   // 16-byte chunks of a row
+    constexpr int BLOCK_CHUNKS = BN * ROW_CHUNKS;
+    constexpr int LOADS = BLOCK_CHUNKS * KSPLIT / THREADS;
+    constexpr int KV_FLOATS = BN * KS + BN * VS;        // one block of K and V
+    constexpr int MERGE = NT * 16 + 2;
+    constexpr int LDS_FLOATS = KSPLIT * KV_FLOATS > (KSPLIT - 1) * QW * 64 * MERGE
+                                   ? KSPLIT * KV_FLOATS
+                                   : (KSPLIT - 1) * QW * 64 * MERGE;
+    static_assert((BLOCK_CHUNKS * KSPLIT) % THREADS == 0, "blocks must split evenly");
+    __shared__ __align__(16) float lds[LDS_FLOATS];
+
+    const uint32_t bh = blockIdx.x / p.pairs;
+    const uint32_t pair = blockIdx.x % p.pairs;
+    const uint32_t kv_heads = p.q_heads / p.group;
+    const uint32_t kv_head = (bh / p.q_heads) * kv_heads + (bh % p.q_heads) / p.group;
+    const float* kh = k + uint64_t(kv_head) * p.kv_head_stride;
+    const float* vh = v + uint64_t(kv_head) * p.kv_head_stride;
+    const uint32_t wave = threadIdx.x / 64;
+    const uint32_t qw = wave % QW;
+    const uint32_t sub = wave / QW;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t col = lane % 32;
+    const uint32_t hs = lane / 32;
+
+    for (int which = 0; which < 2; ++which) {
+        const uint32_t tile = which == 0 ? p.tiles - 1 - pair : pair;
+        if (which == 1 && tile >= p.tiles - 1 - pair) break;
+        const uint32_t q_first = tile * TILE_Q;
+        const uint32_t q_last = min(p.q_len, q_first + TILE_Q) - 1;
+        const uint32_t keys = min(p.kv_len, p.start + q_last + 1);
+        const uint32_t blocks = (keys + BN - 1) / BN;
+        const uint32_t steps = (blocks + KSPLIT - 1) / KSPLIT;
+        const uint32_t qw0 = q_first + qw * 32;
+        const bool wave_active = qw0 < p.q_len;
+        const uint32_t wave_keys =
+            wave_active ? min(p.kv_len, p.start + min(qw0 + 31, p.q_len - 1) + 1) : 0;
+
+        // B operand of S^T = K Q^T: lane (col, hs) holds elements 2j + hs of
+        // its query for every step j.
+        const uint32_t qi = qw0 + col;
+        const bool q_valid = qi < p.q_len;
+        const uint32_t key_limit = min(p.start + qi, p.kv_len - 1);
+        float qf[DS];
+        const float* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + hs;
+#pragma unroll
+        for (int j = 0; j < DS; ++j) qf[j] = q_valid ? qrow[2 * j] : 0.0f;
+
+        f32x16 o[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+        float m = -INFINITY, l = 0.0f;
+
+        float4 kreg[LOADS], vreg[LOADS];
+        bool vlive[LOADS];
+        auto load_step = [&](uint32_t step) {
+#pragma unroll
+            for (int li = 0; li < LOADS; ++li) {
+                const uint32_t chunk = threadIdx.x + THREADS * li;
+                const uint32_t blk = step * KSPLIT + chunk / BLOCK_CHUNKS;
+                const uint32_t c = chunk % BLOCK_CHUNKS;
+                const uint32_t key = blk * BN + c / ROW_CHUNKS;
+                const uint32_t d0 = (c % ROW_CHUNKS) * 4;
+                // rows past kv_len are not read (they may hold anything): a
+                // key past the end loads row kv_len - 1, its score is masked
+                // and its value row zeroed at the LDS store
+                const uint32_t row = min(key, p.kv_len - 1);
+                kreg[li] = *reinterpret_cast<const float4*>(kh + uint64_t(row) * D + d0);
+                vreg[li] = *reinterpret_cast<const float4*>(vh + uint64_t(row) * D + d0);
+                vlive[li] = key < p.kv_len;
+            }
+        };
+        auto store_step = [&]() {
+#pragma unroll
+            for (int li = 0; li < LOADS; ++li) {
+                const uint32_t chunk = threadIdx.x + THREADS * li;
+                const uint32_t c = chunk % BLOCK_CHUNKS;
+                float* kdst = lds + (chunk / BLOCK_CHUNKS) * KV_FLOATS;
+                float* vdst = kdst + BN * KS;
+                const uint32_t key = c / ROW_CHUNKS;
+                const uint32_t d0 = (c % ROW_CHUNKS) * 4;
+                // K rows at the rotated order, 8-byte aligned (stride 2 mod 64)
+                float* kr = kdst + ((key & ~31u) | key_row32(key & 31u)) * KS + d0;
+                *reinterpret_cast<float2*>(kr) = float2{kreg[li].x, kreg[li].y};
+                *reinterpret_cast<float2*>(kr + 2) = float2{kreg[li].z, kreg[li].w};
+                const float4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+                *reinterpret_cast<float4*>(vdst + key * VS + d0) = vlive[li] ? vreg[li] : zero;
+            }
+        };
+
+        load_step(0);
+        __syncthreads();  // the previous tile's LDS use is over
+        store_step();
+        __syncthreads();
+        for (uint32_t step = 0; step < steps; ++step) {
+            if (step + 1 < steps) load_step(step + 1);
+            const uint32_t blk = step * KSPLIT + sub;
+            const float* ks = lds + sub * KV_FLOATS;
+            const float* vs = ks + BN * KS;
+            if (blk < blocks && blk * BN < wave_keys) {
+                f32x16 s[KT];
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
+                    const float* krow = ks + (kt * 32 + col) * KS + hs;
+#pragma unroll
+                    for (int j = 0; j < DS; ++j)
+                        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[2 * j], qf[j], s[kt], 0,
+                                                                      0, 0);
+                }
+                // register r of tile kt holds key kbase + 32 kt + 2r + hs
+                const uint32_t kbase = blk * BN;
+                if (kbase + BN - 1 > p.start + qw0 || kbase + BN > p.kv_len) {
+#pragma unroll
+                    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            if (kbase + kt * 32 + 2 * r + hs > key_limit) s[kt][r] = -INFINITY;
+                }
+                // scores in log2 units first, so that the largest one's
+                // probability is exactly 1 (2^(t - m) with t == m)
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s[kt][r] *= p.scale_log2;
+                float mx = -INFINITY, my = -INFINITY;
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; r += 4) {
+                        mx = max3(mx, s[kt][r], s[kt][r + 1]);
+                        my = max3(my, s[kt][r + 2], s[kt][r + 3]);
+                    }
+                mx = fmaxf(mx, my);
+                const float mx_log2 = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                if (__any(mx_log2 > m + kRescaleSlack)) {
+                    const float m_new = fmaxf(m, mx_log2);
+                    const float alpha = m_new > m ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+                    m = m_new;
+                    l *= alpha;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+                }
+                // p = 2^(t - m), in place; a query that has seen no key yet
+                // (m = -inf) has only -inf scores, and p = 0
+                const float neg_m = m == -INFINITY ? 0.0f : -m;
+                float la = 0.0f, lb = 0.0f;
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; r += 2) {
+                        s[kt][r] = __builtin_amdgcn_exp2f(s[kt][r] + neg_m);
+                        s[kt][r + 1] = __builtin_amdgcn_exp2f(s[kt][r + 1] + neg_m);
+                        la += s[kt][r];
+                        lb += s[kt][r + 1];
+                    }
+                l += la + lb;
+                // O^T += V^T P^T over keys 2r, 2r + 1 of each tile: lane
+                // (col, hs) supplies V[2r + hs][32t + col] and P of its query
+                // at key 2r + hs (register r).
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float* vrow = vs + (kt * 32 + 2 * r + hs) * VS + col;
+#pragma unroll
+                        for (int t = 0; t < NT; ++t)
+                            o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * t], s[kt][r],
+                                                                         o[t], 0, 0, 0);
+                    }
+            }
+            __syncthreads();
+            if (step + 1 < steps) store_step();
+            __syncthreads();
+        }
+
+        if constexpr (KSPLIT > 1) {
+            // Groups 1.. hand their (max, sum, output) to group 0 through LDS.
+            if (sub > 0) {
+                float* dst = lds + ((sub - 1) * QW * 64 + qw * 64 + lane) * MERGE;
+                dst[0] = m;
+                dst[1] = l;
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dst[2 + 16 * t + r] = o[t][r];
+            }
+            __syncthreads();
+            if (sub == 0) {
+#pragma unroll
+                for (int h = 1; h < KSPLIT; ++h) {
+                    const float* src = lds + ((h - 1) * QW * 64 + qw * 64 + lane) * MERGE;
+                    const float m2 = src[0];
+                    const float m_tot = fmaxf(m, m2);
+                    const float a1 = m_tot > m ? __builtin_amdgcn_exp2f(m - m_tot) : 1.0f;
+                    const float a2 = m_tot > m2 ? __builtin_amdgcn_exp2f(m2 - m_tot) : 1.0f;
+                    l = l * a1 + src[1] * a2;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            o[t][r] = o[t][r] * a1 + src[2 + 16 * t + r] * a2;
+                    m = m_tot;
+                }
+            }
+            __syncthreads();  // the merge area is free again
+        }
+
+        if (sub == 0) {
+            const float inv = 1.0f / (l + __shfl_xor(l, 32, 64));  // both halves of the query
+            if (q_valid) {
+                // register r of tile t: element 32t + 8(r / 4) + 4hs + r % 4
+                float* orow = out + (uint64_t(bh) * p.q_len + qi) * D + 4 * hs;
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        *reinterpret_cast<float4*>(orow + 32 * t + 8 * g) =
+                            float4{o[t][4 * g] * inv, o[t][4 * g + 1] * inv,
+                                   o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv};
+            }
+        }
+    }
+}
+
 // ------------------------------------------------- wave reductions
 
 // Wave-wide max / sum without LDS round trips (a __shfl_xor is an LDS
@@ -1020,24 +1288,76 @@ rl_status validate_attention(const rl_buffer* q, const rl_buffer* k, const rl_bu
 // MFMA kernel shape: 4 waves of 32 queries, two key halves (8 waves); key
 // blocks of 128 for head sizes up to 64 and of 64 above (two DMA stages of
 // K and V then take 64, 128 and 128 KB of LDS for head sizes 32, 64, 128).
-constexpr int kFlashQueryWaves = 4;
-constexpr int kFlashKeySplit = 2;
 constexpr int kFlashMaxBlockKeys = 128;
-constexpr int kFlashQueryGroups = 1;
+constexpr int kFlashMaxKeySplit = 4;
+constexpr uint64_t kFlashFillBlocks = 192;  // about 3/4 of the CUs
 
-// Which kernel a shape takes: the MFMA kernel for f16 with a head size of
-// 32, 64, 96 or 128 and aligned buffers (and byte offsets into one KV head,
-// a block past its end included, that fit the 32-bit buffer offsets of its
-// loads); the row kernel otherwise (head sizes up to 512).
+// Workgroup shape: 4 query waves x 2 key shares (128-query tiles) while that
+// gives about three quarters of the CUs a workgroup; otherwise 32-query
+// tiles, so that short or few-head prefills spread over more CUs: 1 query
+// wave x 2 key shares, or x 4 when the workgroups are still few or the head
+// is large (96, 128: more waves per workgroup keep all four SIMDs busy).
+enum class FlashShape { kWide, kNarrow2, kNarrow4 };
+FlashShape flash_shape(uint64_t heads, uint64_t q_len, uint64_t head_dim) {
+    if (heads * ((ceil_div(q_len, 128) + 1) / 2) >= kFlashFillBlocks) return FlashShape::kWide;
+    if (head_dim >= 96 || heads * ((ceil_div(q_len, 32) + 1) / 2) < 256) return FlashShape::kNarrow4;
+    return FlashShape::kNarrow2;
+}
+
+// The matrix-core kernels by head size: f16 in key blocks of 128 (head
+// size up to 64 with 128-query tiles) or 64 (32 for head size 128 with
+// 32-query tiles), from DMA-fed LDS except head size 96; f32 in blocks of
+// 64 (up to 64, 128-query tiles) or 32.
+template <int QW, int KS>
+void launch_flash(rl_context* ctx, dim3 g, uint32_t nt, const half_t* q, const half_t* k,
+                  const half_t* v, half_t* o, const AttnParams& p) {
+    constexpr int BN = QW == 4 ? 128 : 64;
+    constexpr int BN4 = KS == 4 ? 32 : 64;
+    const dim3 b(64 * QW * KS);
+    if (nt == 1) {
+        RL_LAUNCH(ctx, (k_flash_attention<1, QW, KS, BN, 1, true>), g, b, q, k, v, o, p);
+    } else if (nt == 2) {
+        RL_LAUNCH(ctx, (k_flash_attention<2, QW, KS, BN, 1, true>), g, b, q, k, v, o, p);
+    } else if constexpr (!(QW == 1 && KS == 2)) {  // that shape only for head sizes <= 64
+        if (nt == 3) {
+            RL_LAUNCH(ctx, (k_flash_attention<3, QW, KS, 64, 1, false>), g, b, q, k, v, o, p);
+        } else {
+            RL_LAUNCH(ctx, (k_flash_attention<4, QW, KS, BN4, 1, true>), g, b, q, k, v, o, p);
+        }
+    }
+}
+template <int QW, int KS>
+void launch_flash(rl_context* ctx, dim3 g, uint32_t nt, const float* q, const float* k,
+                  const float* v, float* o, const AttnParams& p) {
+    constexpr int BN = QW == 4 ? 64 : 32;
+    const dim3 b(64 * QW * KS);
+    if (nt == 1) {
+        RL_LAUNCH(ctx, (k_flash_attention_f32<1, QW, KS, BN>), g, b, q, k, v, o, p);
+    } else if (nt == 2) {
+        RL_LAUNCH(ctx, (k_flash_attention_f32<2, QW, KS, BN>), g, b, q, k, v, o, p);
+    } else if constexpr (!(QW == 1 && KS == 2)) {  // that shape only for head sizes <= 64
+        if (nt == 3) {
+            RL_LAUNCH(ctx, (k_flash_attention_f32<3, QW, KS, 32>), g, b, q, k, v, o, p);
+        } else {
+            RL_LAUNCH(ctx, (k_flash_attention_f32<4, QW, KS, 32>), g, b, q, k, v, o, p);
+        }
+    }
+}
+
+// Which kernel a shape takes: the MFMA kernels for a head size of 32, 64,
+// 96 or 128 and 16-byte aligned buffers (f16: also byte offsets into one KV
+// head, a block past its end included, that fit the 32-bit buffer offsets
+// of its loads); the row kernel otherwise (head sizes up to 512).
 template <typename T>
 bool use_flash(const AttnShape& s, const void* q, const void* k, const void* v, const void* o) {
+    const bool shape = s.head_dim % 32 == 0 && s.head_dim <= 128 && aligned_to(q, 16) &&
+                       aligned_to(k, 16) && aligned_to(v, 16) && aligned_to(o, 16);
     if constexpr (!std::is_same<T, half_t>::value) {
-        return false;
+        return shape;
     } else {
-        const uint64_t span = (s.kv_len + uint64_t(kFlashMaxBlockKeys) * kFlashKeySplit) *
+        const uint64_t span = (s.kv_len + uint64_t(kFlashMaxBlockKeys) * kFlashMaxKeySplit) *
                               s.head_dim * sizeof(T);
-        return s.head_dim % 32 == 0 && s.head_dim <= 128 && span <= UINT32_MAX &&
-               aligned_to(q, 16) && aligned_to(k, 16) && aligned_to(v, 16) && aligned_to(o, 16);
+        return shape && span <= UINT32_MAX;
     }
 }
 
@@ -1130,22 +1450,18 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
         ctx->pool.release(part);  // stream-ordered: later users run after this launch
         return st;
     }
-    if constexpr (std::is_same<T, half_t>::value) {
-        if (flash) {
-            p.tiles = uint32_t(ceil_div(s.q_len, 32 * kFlashQueryWaves * kFlashQueryGroups));
-            p.pairs = (p.tiles + 1) / 2;
-            const uint64_t grid = heads * p.pairs;
-            if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "attention grid exceeds u32");
-            constexpr int QW = kFlashQueryWaves, KSPLIT = kFlashKeySplit, QG = kFlashQueryGroups;
-            const dim3 g(static_cast<unsigned>(grid)), b(64 * QW * KSPLIT);
-            switch (s.head_dim / 32) {
-                case 1: RL_LAUNCH(ctx, (k_flash_attention<1, QW, KSPLIT, 128, QG, true>), g, b, qd, kd, vd, od, p); break;
-                case 2: RL_LAUNCH(ctx, (k_flash_attention<2, QW, KSPLIT, 128, QG, true>), g, b, qd, kd, vd, od, p); break;
-                case 3: RL_LAUNCH(ctx, (k_flash_attention<3, QW, KSPLIT, 64, QG, false>), g, b, qd, kd, vd, od, p); break;
-                default: RL_LAUNCH(ctx, (k_flash_attention<4, QW, KSPLIT, 64, QG, true>), g, b, qd, kd, vd, od, p); break;
-            }
-            return after_launch(ctx, name);
-        }
+    if (flash) {
+        const FlashShape shape = flash_shape(heads, s.q_len, s.head_dim);
+        p.tiles = uint32_t(ceil_div(s.q_len, shape == FlashShape::kWide ? 128 : 32));
+        p.pairs = (p.tiles + 1) / 2;
+        const uint64_t grid = heads * p.pairs;
+        if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "attention grid exceeds u32");
+        const dim3 g(static_cast<unsigned>(grid));
+        const uint32_t nt = uint32_t(s.head_dim / 32);
+        if (shape == FlashShape::kWide) launch_flash<4, 2>(ctx, g, nt, qd, kd, vd, od, p);
+        else if (shape == FlashShape::kNarrow2) launch_flash<1, 2>(ctx, g, nt, qd, kd, vd, od, p);
+        else launch_flash<1, 4>(ctx, g, nt, qd, kd, vd, od, p);
+        return after_launch(ctx, name);
     }
     const dim3 g(static_cast<unsigned>(rows)), b(64);
     if (s.head_dim <= 64) {

@@ -5,8 +5,9 @@ scale/mask, softmax and PV; the fused pass keeps scores and probabilities in
 f32, so it is compared with float64 attention under the forward error bound
 of its own roundings (helpers.attention_bound, "f32" / "f16_fused"), and the
 reference's four calls (the oracle) are held to the bound of theirs.  Shapes
-cover both kernels (the f16 matrix-core path for head sizes 32..128 in steps
-of 32, the row kernel for f32 and other head sizes), grouped and plain heads,
+cover every kernel (the f16 and f32 matrix-core kernels for head sizes
+32..128 in steps of 32 in their three workgroup shapes, the split-key decode
+kernel, the row kernel for other head sizes), grouped and plain heads,
 batches, ragged query/key counts, a start offset (chunked prefill and decode)
 and KV caches whose rows past kv_len hold NaN (never read).
 """
@@ -58,6 +59,7 @@ SHAPES = [
     (1, 2, 2, 200, 300, 300, 128, 100),
     (1, 8, 2, 256, 1500, 1536, 128, 1244),  # many key blocks per workgroup, D 128
     (1, 6, 3, 384, 2000, 2048, 32, 1616),   # many key blocks, D 32, ragged last block
+    (1, 9, 3, 2048, 2048, 2048, 64, 0),     # 9 heads x 2048: 32-query tiles, 2 key shares
     (1, 6, 2, 1, 2048, 4096, 64, 2047),  # decode step from a half-full cache
     (1, 2, 1, 33, 40, 40, 48, 7),        # head size off the matrix-core path
     (1, 2, 2, 17, 17, 20, 80, 0),
@@ -127,20 +129,22 @@ def test_attention_f16_is_closer_than_the_reference_composition(ctx):
     assert fused_err <= float(ref_err.max())
 
 
-def test_attention_smollm_layer_f16(ctx):
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_attention_smollm_layer(ctx, dtype):
     """SmolLM2-360M layer at 4096 tokens: Q [1, 15, 4096, 64], K/V
-    [1, 5, 4096, 64] f16, causal, scale 1/8.  Every output is finite and
-    sampled query rows of every head (first, last, tile edges, random) are
-    within the float64 bound."""
-    q = synth.normal(201, (1, 15, 4096, 64)).astype(np.float16)
-    k = synth.normal(202, (1, 5, 4096, 64)).astype(np.float16)
-    v = synth.normal(203, (1, 5, 4096, 64)).astype(np.float16)
+    [1, 5, 4096, 64], causal, scale 1/8 (f16, and f32 for the f32 matrix-core
+    kernel).  Every output is finite and sampled query rows of every head
+    (first, last, tile edges, random) are within the float64 bound."""
+    q = synth.normal(201, (1, 15, 4096, 64)).astype(dtype)
+    k = synth.normal(202, (1, 5, 4096, 64)).astype(dtype)
+    v = synth.normal(203, (1, 5, 4096, 64)).astype(dtype)
+    kind = "f16_fused" if dtype == np.float16 else "f32"
     got = run_attention(ctx, q, k, v, 0.125, 0, 4096)
     assert np.isfinite(got).all()
     rows = sorted({0, 1, 31, 32, 127, 128, 2047, 2048, 4094, 4095} |
                   set(np.random.default_rng(204).integers(0, 4096, 12).tolist()))
     for r in rows:
-        exact, bound = attention_bound(q[:, :, r:r + 1], k, v, 0.125, r, 4096, "f16_fused")
+        exact, bound = attention_bound(q[:, :, r:r + 1], k, v, 0.125, r, 4096, kind)
         err = np.abs(got[:, :, r:r + 1].astype(np.float64) - exact)
         assert np.all(err <= bound), f"row {r}: max error {err.max():.3g}"
     # row 0 attends to key 0 only: its output is V's first row of its KV head
