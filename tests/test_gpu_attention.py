@@ -12,12 +12,14 @@ batches, ragged query/key counts, a start offset (chunked prefill and decode)
 and KV caches whose rows past kv_len hold NaN (never read).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
 from helpers import attention_bound, attention_exact, kats
 from oracle import oracle as o
-from rustllm_amd import synth
+from rustllm_amd import abi, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -258,3 +260,51 @@ def test_gqa_qk_smollm_layer_f16_sampled_rows(ctx):
         exact, dot_abs = gqa_exact(q[:, :, r:r + 1], k, 4096)
         bound = 64 * U32 * dot_abs + ulp16(exact) * 0.5001
         assert np.all(np.abs(got[:, :, r:r + 1].astype(np.float64) - exact) <= bound), r
+
+
+# ------------------------------------------------- recorded in a graph
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_attention_in_a_graph_matches_eager(ctx, dtype):
+    """A prefill and a decode step recorded in one graph, replayed several
+    times with eager work in between: the prefill replays give the eager
+    result bit for bit (same kernel); the decode step, which takes the
+    matrix-core kernel while recording (the split-key kernel's partials live
+    in a pool block that a replay could not own), stays within the float64
+    bound on every replay."""
+    pre = (1, 6, 2, 300, 300, 320, 64, 0)
+    dec = (1, 15, 5, 1, 1024, 1024, 64, 1023)
+    bufs = []
+    for shape in (pre, dec):
+        b, qh, kvh, ql, kl, cap, hd, start = shape
+        q = synth.normal(synth.seed_for("graph-q", *shape), (b, qh, ql, hd)).astype(dtype)
+        k = cache(synth.seed_for("graph-k", *shape), b, kvh, cap, hd, kl, dtype)
+        v = cache(synth.seed_for("graph-v", *shape), b, kvh, cap, hd, kl, dtype)
+        bufs.append((shape, q, k, v, ctx.upload(q), ctx.upload(k), ctx.upload(v),
+                     ctx.empty(q.shape, dtype)))
+    eager = []
+    for shape, q, k, v, dq, dk, dv, out in bufs:
+        ctx.begin()
+        ctx.attention(dq, dk, dv, 0.125, shape[7], shape[4], out)
+        ctx.finish()
+        eager.append(out.numpy().copy())
+    ctx.capture_begin()
+    try:
+        for shape, q, k, v, dq, dk, dv, out in bufs:
+            ctx.attention(dq, dk, dv, 0.125, shape[7], shape[4], out)
+    finally:
+        graph = ctx.capture_end()
+    for i in range(3):
+        for _, _, _, _, _, _, _, out in bufs:  # a replay must write every element
+            nan = ctx.upload(np.full(out.shape, np.nan, dtype))
+            abi.check(ctx.lib.rl_buffer_copy(ctx.handle, ctypes.byref(nan.raw),
+                                             ctypes.byref(out.raw), out.byte_len))
+        ctx.graph_launch(graph)
+        ctx.finish()
+        (shape, q, k, v, *_, out_pre), (dshape, dq_, dk_, dv_, *_, out_dec) = bufs
+        assert np.array_equal(out_pre.numpy(), eager[0]), f"prefill replay {i}"
+        check(out_dec.numpy(), dq_, dk_, dv_, 0.125, dshape[7], dshape[4], f"decode replay {i}")
+        ctx.begin()
+        ctx.attention(bufs[1][4], bufs[1][5], bufs[1][6], 0.125, dshape[7], dshape[4])  # eager work
+        ctx.finish()
+    ctx.graph_destroy(graph)
