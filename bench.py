@@ -580,6 +580,24 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
     rows.append(op_row("layer.4 gqa_pv_f16", "f16", [1, qh, tok, hd], pv_bytes,
                        kernel_times_us(ctx, [lambda i=i: ctx.gqa_pv(pr[i], s0[2], out)
                                              for i in range(2)], reps)))
+    # the same two products in f32 (f32 matrix cores; 2 x 32.2 GFLOP over all keys)
+    q32, k32, v32 = (ctx.upload(x.astype(np.float32)) for x in (q, k, v))
+    sc32 = ctx.empty((1, qh, tok, tok), np.float32)
+    out32 = ctx.empty(q.shape, np.float32)
+    mm_flops = 2.0 * qh * tok * tok * hd
+    for name, fn, nbytes in (
+            ("layer.4 gqa_qk_f32 (scores)", lambda: ctx.gqa_qk(q32, k32, None, sc32),
+             qk_bytes * 2),
+            ("layer.4 gqa_pv_f32", lambda: ctx.gqa_pv(sc32, v32, out32), pv_bytes * 2)):
+        r32 = op_row(name, "f32", [1, qh, tok, tok if "qk" in name else hd], nbytes,
+                     kernel_times_us(ctx, [fn], max(10, reps // 5)))
+        r32.update({"flops": mm_flops,
+                    "TFLOP/s": round(mm_flops / (r32["us"] * 1e-6) / 1e12, 1),
+                    "pct_peak_mfma": round(100 * mm_flops / (r32["us"] * 1e-6) / 1e12 /
+                                           PEAK_F32_TFLOPS, 1)})
+        log(f"    -> {r32['TFLOP/s']} TFLOP/s ({r32['pct_peak_mfma']}% of the dense f32 peak)")
+        rows.append(r32)
+    del q32, k32, v32, sc32, out32
 
     def chain(i):
         ctx.gqa_qk(s0[0], s0[1], None, sc[i])

@@ -35,6 +35,7 @@
 // against float64).  The MFMA kernel feeds P to the second product as f16
 // (relative error 2^-11 per probability, inside the same bound).
 #include "common.hpp"
+#include "mfma_layout.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -42,11 +43,6 @@
 
 namespace rl {
 namespace {
-
-typedef half_t h8 __attribute__((ext_vector_type(8)));
-typedef half_t h4 __attribute__((ext_vector_type(4)));
-typedef half_t h2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -66,40 +62,12 @@ struct AttnParams {
 
 // ------------------------------------------------------------- MFMA kernel
 
-// Key order inside a 32-key tile: row i of the S^T tile holds key
-// perm32(i), bits 2 and 3 of i swapped.  With the 32x32 result layout (lane
-// l holds column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4 in register
-// r) register r of lane l then holds key 16 * (r / 8) + 8 * (l / 32) + r % 8.
-__device__ inline uint32_t perm32(uint32_t i) {
-    return (i & ~12u) | ((i & 4u) << 1) | ((i & 8u) >> 1);
-}
-
 // max(a, b, c) in one v_max3_f32.  (fmaxf on a value the compiler cannot
 // prove canonical, such as an MFMA result, costs an extra v_max_f32 x, x.)
 __device__ inline float max3(float a, float b, float c) {
     float r;
     asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
     return r;
-}
-
-// Row stride (halves) of V in LDS for the transpose reads: the 32 lanes one
-// LDS cycle serves read 4 rows x 2 runs of 16 bytes; with 64 banks of 4
-// bytes those land on distinct banks when the stride in dwords is 16 or 48
-// modulo 64.  Smallest such stride >= D (in steps of 8 halves).
-__host__ __device__ constexpr int v_stride_tr(int d) {
-    int s = d;
-    while ((s / 2) % 64 != 16 && (s / 2) % 64 != 48) s += 8;
-    return s;
-}
-
-// ds_read_b64_tr_b16: in each group of 16 lanes, lanes 4j .. 4j + 3 read 8
-// bytes each (row j of a 4 x 16 block of halves); lane i of the group
-// receives column i of that block, one half from each row.
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-__device__ inline h4 lds_read_transposed(const half_t* p) {
-    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4*)(p));
-    return __builtin_bit_cast(h4, r);
 }
 
 // Chunk order of the unpadded LDS rows the DMA-fed kernel uses: 16-byte
@@ -552,26 +520,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
 // ------------------------------------------------- f32 on the matrix cores
 
 // f32 takes v_mfma_f32_32x32x2_f32 (two head elements per step, exact f32
-// products).  Key order inside a 32-key tile: LDS row i = 8a + 4h + b holds
-// key 8a + 2b + h (the low three bits rotated), so that register r of a lane
-// in half h of the S^T result holds key 2r + h of the tile -- exactly the B
-// operand (P^T) of the P V step over keys 2r and 2r + 1, with no data
-// movement.  key_row32 is the LDS row of key j.
-__device__ inline uint32_t key_row32(uint32_t j) {
-    return (j & ~7u) | ((j & 1u) << 2) | ((j >> 1) & 3u);
-}
-
-// Row strides (floats) of K and V in LDS.  A K operand read takes one
-// element of 32 rows (lanes 0-31) and the next element of the same rows
-// (lanes 32-63): a stride of 2 mod 64 puts the 64 reads on 64 banks.  A V
-// operand read takes 32 consecutive elements of two rows: a stride of 32 mod
-// 64 does.
-__host__ __device__ constexpr int f32_stride(int d, int residue) {
-    int s = d;
-    while (s % 64 != residue) ++s;
-    return s;
-}
-
+// products) with K rows in the key_row32 order, so each lane's probabilities
+// are the B operand of the P V step as they stand; K rows at a stride of
+// 2 mod 64 floats and V rows at 32 mod 64 (f32_stride) keep the operand
+// reads on 64 distinct banks.
 // Same tiling as k_flash_attention (QW waves of 32 queries, KSPLIT key
 // shares merged through LDS, causal tiles paired), blocks staged through
 // registers; scores, probabilities and the running sum stay in f32.

@@ -20,16 +20,12 @@
 //    from ds_read_b64_tr_b16; the next step's loads are in flight meanwhile.
 // Other shapes (f32, other head sizes) take row kernels on the vector ALUs.
 #include "common.hpp"
+#include "mfma_layout.hpp"
 
 #include <type_traits>
 
 namespace rl {
 namespace {
-
-typedef half_t h8 __attribute__((ext_vector_type(8)));
-typedef half_t h4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 struct GqaParams {
     uint32_t q_heads, group, q_len, kv_len, head_dim;
@@ -41,12 +37,6 @@ struct GqaParams {
 __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
     const uint32_t kv_heads = p.q_heads / p.group;
     return (bh / p.q_heads) * kv_heads + (bh % p.q_heads) / p.group;
-}
-
-// Bits 2 and 3 swapped: row i of an S^T tile holds key perm32(i), and lane
-// l's register r then holds key 16 (r / 8) + 8 (l / 32) + r % 8.
-__device__ inline uint32_t perm32(uint32_t i) {
-    return (i & ~12u) | ((i & 4u) << 1) | ((i & 8u) >> 1);
 }
 
 // ------------------------------------------------------------ QK^T, MFMA
@@ -147,22 +137,6 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
 }
 
 // -------------------------------------------------------------- P V, MFMA
-
-// Row stride (halves) of V in LDS for the transpose reads: the 32 lanes one
-// LDS cycle serves read 4 rows x 2 runs of 16 bytes; with 64 banks of 4
-// bytes those land on distinct banks when the stride in dwords is 16 or 48
-// modulo 64.  Smallest such stride >= D (in steps of 8 halves).
-__host__ __device__ constexpr int v_stride_tr(int d) {
-    int s = d;
-    while ((s / 2) % 64 != 16 && (s / 2) % 64 != 48) s += 8;
-    return s;
-}
-
-__device__ inline h4 lds_read_transposed(const half_t* ptr) {
-    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4*)(ptr));
-    return __builtin_bit_cast(h4, r);
-}
 
 template <int NT>
 __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ probs,
@@ -288,6 +262,211 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
     }
 }
 
+// ----------------------------------------------------- f32, matrix cores
+
+// QK^T in f32 (v_mfma_f32_32x32x2_f32, exact f32 products): workgroup =
+// (head, 128 queries, 128 keys) as for f16, the key tile in LDS in key order
+// at a stride of 2 mod 64 floats (every operand read on its own bank).  Each
+// lane stores its result registers directly, four consecutive keys per
+// 16-byte store: a row receives 32-byte pieces that the L2 merges into whole
+// lines; the kernel is bound by the f32 matrix cores, not by these stores.
+template <int NT>
+__global__ __launch_bounds__(256) void k_gqa_qk_mfma_f32(const float* __restrict__ q,
+                                                         const float* __restrict__ k,
+                                                         float* __restrict__ out, GqaParams p) {
+    constexpr int D = 32 * NT;
+    constexpr int DS = D / 2;  // MFMA steps over the head
+    constexpr int KS = f32_stride(D, 2);
+    constexpr int ROW_CHUNKS = D / 4;
+    __shared__ __align__(16) float ks[128 * KS];
+    const uint32_t wave = threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t col = lane % 32;
+    const uint32_t hs = lane / 32;
+    const uint32_t kt_blk = blockIdx.x % p.k_tiles;
+    const uint32_t rest = blockIdx.x / p.k_tiles;
+    const uint32_t qt = rest % p.q_tiles;
+    const uint32_t bh = rest / p.q_tiles;
+    const uint32_t q0 = qt * 128 + wave * 32;
+    const float* kh = k + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
+    const uint32_t kbase = kt_blk * 128;
+    // keys past kv_len read row kv_len - 1 (their scores are not stored)
+#pragma unroll
+    for (int li = 0; li < 128 * ROW_CHUNKS / 256; ++li) {
+        const uint32_t chunk = threadIdx.x + 256 * li;
+        const uint32_t j = chunk / ROW_CHUNKS;
+        const uint32_t d0 = (chunk % ROW_CHUNKS) * 4;
+        const uint32_t key = min(kbase + j, p.kv_len - 1);
+        const float4 x = *reinterpret_cast<const float4*>(kh + uint64_t(key) * D + d0);
+        float* dst = ks + j * KS + d0;  // 8-byte aligned rows
+        *reinterpret_cast<float2*>(dst) = float2{x.x, x.y};
+        *reinterpret_cast<float2*>(dst + 2) = float2{x.z, x.w};
+    }
+    // B operand: lane (col, hs) holds elements 2j + hs of its query
+    const uint32_t qi = q0 + col;
+    const bool q_valid = qi < p.q_len;
+    const float* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + hs;
+    float qf[DS];
+#pragma unroll
+    for (int j = 0; j < DS; ++j) qf[j] = q_valid ? qrow[2 * j] : 0.0f;
+    __syncthreads();
+    if (q0 >= p.q_len) return;  // (no barrier below)
+    const bool vec_store = p.kv_len % 4 == 0;
+    float* orow = out + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * p.kv_len;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {  // four 32-key sub-tiles
+        const uint32_t k0 = kbase + st * 32;
+        if (k0 >= p.kv_len) break;
+        const float* krow = ks + (st * 32 + col) * KS + hs;
+        f32x16 s;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < DS; ++j)
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[2 * j], qf[j], s, 0, 0, 0);
+        if (!q_valid) continue;
+        // register 4g + e holds key k0 + 8g + 4hs + e
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t key = k0 + 8 * g + 4 * hs;
+            if (vec_store && key + 4 <= p.kv_len) {
+                *reinterpret_cast<float4*>(orow + key) =
+                    float4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (key + e < p.kv_len) orow[key + e] = s[4 * g + e];
+            }
+        }
+    }
+}
+
+// P V in f32: workgroup = (head, 128 queries), keys in steps of 64.  Each
+// wave stages its 32 x 64 probabilities in LDS (whole 256-byte row segments
+// per 16 lanes) at a row stride of 2 mod 64, so that lane (col, hs) reads the
+// probability of key 2s + hs of its query -- the B operand of the step over
+// keys 2s, 2s + 1 -- on its own bank; V rows at 32 mod 64 floats.  The next
+// step's operands are in flight during this step's products.
+template <int NT>
+__global__ __launch_bounds__(256) void k_gqa_pv_mfma_f32(const float* __restrict__ probs,
+                                                         const float* __restrict__ v,
+                                                         float* __restrict__ out, GqaParams p) {
+    constexpr int D = 32 * NT;
+    constexpr int BN = 64;                      // keys per step
+    constexpr int VS = f32_stride(D, 32);       // LDS row stride of V
+    constexpr int PS = f32_stride(BN, 2);       // LDS row stride of a wave's probabilities
+    constexpr int ROW_CHUNKS = D / 4;
+    constexpr int LOADS = BN * ROW_CHUNKS / 256;
+    __shared__ __align__(16) float vs[BN * VS];
+    __shared__ __align__(16) float pt[4][32 * PS];
+    const uint32_t wave = threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t col = lane % 32;
+    const uint32_t hs = lane / 32;
+    const uint32_t qt = blockIdx.x % p.q_tiles;
+    const uint32_t bh = blockIdx.x / p.q_tiles;
+    const uint32_t q0 = qt * 128 + wave * 32;
+    const float* vh = v + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
+    const float* pbase = probs + uint64_t(bh) * p.q_len * p.kv_len;
+    const bool vec_p = p.kv_len % 4 == 0;
+    float* my = pt[wave];
+
+    // rows past q_len and keys past kv_len as zeros
+    auto load_p = [&](uint32_t blk, f32x4 (&pr)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t r = i * 4 + lane / 16;
+            const uint32_t kb = blk * BN + (lane % 16) * 4;
+            const float* src = pbase + uint64_t(q0 + r) * p.kv_len + kb;
+            if (q0 + r < p.q_len && vec_p && kb + 4 <= p.kv_len) {
+                pr[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src));
+            } else {
+                const bool row = q0 + r < p.q_len;
+                pr[i] = f32x4{row && kb < p.kv_len ? src[0] : 0.0f,
+                              row && kb + 1 < p.kv_len ? src[1] : 0.0f,
+                              row && kb + 2 < p.kv_len ? src[2] : 0.0f,
+                              row && kb + 3 < p.kv_len ? src[3] : 0.0f};
+            }
+        }
+    };
+    auto store_p = [&](const f32x4 (&pr)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float* dst = my + (i * 4 + lane / 16) * PS + (lane % 16) * 4;  // 8-byte aligned
+            *reinterpret_cast<float2*>(dst) = float2{pr[i][0], pr[i][1]};
+            *reinterpret_cast<float2*>(dst + 2) = float2{pr[i][2], pr[i][3]};
+        }
+    };
+    auto load_v = [&](uint32_t blk, float4 (&vr)[LOADS]) {
+#pragma unroll
+        for (int li = 0; li < LOADS; ++li) {
+            const uint32_t chunk = threadIdx.x + 256 * li;
+            const uint32_t gk = blk * BN + chunk / ROW_CHUNKS;
+            const uint32_t d0 = (chunk % ROW_CHUNKS) * 4;
+            vr[li] = gk < p.kv_len
+                         ? *reinterpret_cast<const float4*>(vh + uint64_t(gk) * D + d0)
+                         : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+    auto store_v = [&](const float4 (&vr)[LOADS]) {
+#pragma unroll
+        for (int li = 0; li < LOADS; ++li) {
+            const uint32_t chunk = threadIdx.x + 256 * li;
+            *reinterpret_cast<float4*>(vs + (chunk / ROW_CHUNKS) * VS + (chunk % ROW_CHUNKS) * 4) =
+                vr[li];
+        }
+    };
+
+    f32x16 o[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+
+    const uint32_t blocks = (p.kv_len + BN - 1) / BN;
+    f32x4 pnext[8];
+    float4 vnext[LOADS];
+    load_p(0, pnext);
+    load_v(0, vnext);
+    store_p(pnext);
+    store_v(vnext);
+    __syncthreads();
+    for (uint32_t blk = 0; blk < blocks; ++blk) {
+        const bool more = blk + 1 < blocks;
+        if (more) {
+            load_p(blk + 1, pnext);
+            load_v(blk + 1, vnext);
+        }
+        const float* prow = my + col * PS + hs;
+        const float* vcol = vs + hs * VS + col;
+#pragma unroll
+        for (int s = 0; s < BN / 2; ++s) {
+            const float pb = prow[2 * s];  // P of key 2s + hs
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vcol[2 * s * VS + 32 * t], pb, o[t],
+                                                             0, 0, 0);
+        }
+        if (more) {
+            __syncthreads();
+            store_p(pnext);
+            store_v(vnext);
+            __syncthreads();
+        }
+    }
+    const uint32_t qi = q0 + col;
+    if (qi < p.q_len) {
+        // register r of tile t: element 32t + 8(r / 4) + 4hs + r % 4
+        float* orow = out + (uint64_t(bh) * p.q_len + qi) * D + 4 * hs;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<float4*>(orow + 32 * t + 8 * g) =
+                    float4{o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]};
+    }
+}
+
 // ------------------------------------------------------------ row kernels
 
 // QK^T: one workgroup per (query row, 256 keys); the query row is kept in
@@ -408,12 +587,8 @@ GqaParams params_of(const GqaShape& s) {
 
 template <typename T>
 bool use_mfma(const GqaShape& s, const void* a, const void* b, const void* o) {
-    if constexpr (!std::is_same<T, half_t>::value) {
-        return false;
-    } else {
-        return s.head_dim % 32 == 0 && s.head_dim <= 128 && aligned_to(a, 16) &&
-               aligned_to(b, 16) && aligned_to(o, 16);
-    }
+    return s.head_dim % 32 == 0 && s.head_dim <= 128 && aligned_to(a, 16) && aligned_to(b, 16) &&
+           aligned_to(o, 16);
 }
 
 template <typename T>
@@ -446,6 +621,21 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
                 case 2: RL_LAUNCH(ctx, (k_gqa_qk_mfma<2>), g, b, qd, kd, od, p); break;
                 case 3: RL_LAUNCH(ctx, (k_gqa_qk_mfma<3>), g, b, qd, kd, od, p); break;
                 default: RL_LAUNCH(ctx, (k_gqa_qk_mfma<4>), g, b, qd, kd, od, p); break;
+            }
+            return after_launch(ctx, name);
+        }
+    } else {
+        if (use_mfma<T>(s, qd, kd, od)) {
+            p.q_tiles = uint32_t(ceil_div(s.q_len, 128));
+            p.k_tiles = uint32_t(ceil_div(s.kv_len, 128));
+            const uint64_t grid = heads * p.q_tiles * p.k_tiles;
+            if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
+            const dim3 g(static_cast<unsigned>(grid)), b(256);
+            switch (s.head_dim / 32) {
+                case 1: RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<1>), g, b, qd, kd, od, p); break;
+                case 2: RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<2>), g, b, qd, kd, od, p); break;
+                case 3: RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<3>), g, b, qd, kd, od, p); break;
+                default: RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<4>), g, b, qd, kd, od, p); break;
             }
             return after_launch(ctx, name);
         }
@@ -500,6 +690,20 @@ rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, co
                 case 2: RL_LAUNCH(ctx, (k_gqa_pv_mfma<2>), g, b, pd, vd, od, p); break;
                 case 3: RL_LAUNCH(ctx, (k_gqa_pv_mfma<3>), g, b, pd, vd, od, p); break;
                 default: RL_LAUNCH(ctx, (k_gqa_pv_mfma<4>), g, b, pd, vd, od, p); break;
+            }
+            return after_launch(ctx, name);
+        }
+    } else {
+        if (use_mfma<T>(s, pd, vd, od)) {
+            p.q_tiles = uint32_t(ceil_div(s.q_len, 128));
+            const uint64_t grid = heads * p.q_tiles;
+            if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA PV grid exceeds u32");
+            const dim3 g(static_cast<unsigned>(grid)), b(256);
+            switch (s.head_dim / 32) {
+                case 1: RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<1>), g, b, pd, vd, od, p); break;
+                case 2: RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<2>), g, b, pd, vd, od, p); break;
+                case 3: RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<3>), g, b, pd, vd, od, p); break;
+                default: RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<4>), g, b, pd, vd, od, p); break;
             }
             return after_launch(ctx, name);
         }
