@@ -6,9 +6,10 @@
 // score rounded once.  gqa_pv_matmul (:72-110, metal :323-629):
 // out[b, h, i, d] = sum_j p[b, h, i, j] * v[b, h / g, j, d].
 //
-// Both are bound by HBM (the [B, QH, Q, K] scores are written once or read
-// once; Q, K and V are small).  f16 with a head size of 32..128 in steps of
-// 32 takes the matrix cores (v_mfma_f32_32x32x16_f16):
+// In f16 both are bound by HBM (the [B, QH, Q, K] scores are written once
+// or read once; Q, K and V are small), in f32 by the f32 matrix cores.  A
+// head size of 32..128 in steps of 32 takes the matrix cores
+// (v_mfma_f32_32x32x16_f16 for f16):
 //  * QK^T computes S^T = K Q^T per wave (32 queries x 128 keys): the
 //    workgroup's 128 key rows are loaded whole into LDS in the order that
 //    swaps bits 2 and 3 of the key index, so every lane ends up holding runs
@@ -18,7 +19,8 @@
 //    32 x 128 probabilities in LDS (whole 256-byte row segments per 16
 //    lanes), V goes through LDS row-major and its transposed operand comes
 //    from ds_read_b64_tr_b16; the next step's loads are in flight meanwhile.
-// Other shapes (f32, other head sizes) take row kernels on the vector ALUs.
+// f32 takes v_mfma_f32_32x32x2_f32 with the same workgroups (the f32
+// kernels below); other head sizes take row kernels on the vector ALUs.
 #include "common.hpp"
 #include "mfma_layout.hpp"
 
