@@ -118,8 +118,7 @@ __device__ inline void dma_to_lds(i32x4 rsrc, uint32_t lds_addr, uint32_t voffse
 // below 2^3, well inside f16 and f32 range.
 constexpr float kRescaleSlack = 3.0f;
 
-// QW waves of QG x 32 queries each (QG query groups share every K and V
-// operand a wave reads from LDS); KSPLIT groups of such waves split the key
+// QW waves of 32 queries each; KSPLIT groups of such waves split the key
 // blocks of the tile between them (group g takes blocks g, g + KSPLIT, ...)
 // and merge their partial (max, sum, output) through LDS at the end.
 //
@@ -129,7 +128,7 @@ constexpr float kRescaleSlack = 3.0f;
 // Otherwise blocks pass through registers into rows padded for the bank
 // layout (head size 96, whose 12 chunks a row do not swizzle onto 64 banks),
 // one block at a time.
-template <int NT, int QW, int KSPLIT, int BN, int QG, bool DMA>
+template <int NT, int QW, int KSPLIT, int BN, bool DMA>
 __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
     half_t* __restrict__ out, AttnParams p) {
@@ -144,7 +143,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     constexpr int VS = DMA ? D : v_stride_tr(D);
     constexpr int NSTAGE = DMA ? 2 : 1;
     constexpr int THREADS = 64 * QW * KSPLIT;
-    constexpr int TILE_Q = 32 * QG * QW;               // queries per tile
+    constexpr int TILE_Q = 32 * QW;                    // queries per tile
     constexpr int BLOCK_CHUNKS = BN * D / 8;           // 16-byte chunks of one K (or V) block
     constexpr int LOADS = BLOCK_CHUNKS * KSPLIT / THREADS;
     constexpr int DMA_LOADS = 2 * LOADS;               // K and V chunks per lane (DMA)
@@ -153,7 +152,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     constexpr int ROW_CHUNKS = D / 8;
     constexpr int KV_HALVES = BN * KS + BN * VS;       // one block of K and V
     constexpr int STAGE_BYTES = KSPLIT * KV_HALVES * 2;
-    constexpr int MERGE = QG * (NT * 16 + 2);          // floats a lane hands over
+    constexpr int MERGE = NT * 16 + 2;                 // floats a lane hands over
     constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES > (KSPLIT - 1) * QW * 64 * MERGE * 4
                                   ? NSTAGE * STAGE_BYTES
                                   : (KSPLIT - 1) * QW * 64 * MERGE * 4;
@@ -171,10 +170,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     const half_t* vh = v + uint64_t(kv_head) * p.kv_head_stride;
 
     const uint32_t wave = threadIdx.x / 64;
-    const uint32_t qw = wave % QW;      // which QG x 32 queries of the tile
+    const uint32_t qw = wave % QW;      // which 32 queries of the tile
     const uint32_t sub = wave / QW;     // which share of the key blocks
     const uint32_t lane = threadIdx.x % 64;
-    const uint32_t col = lane % 32;     // query column of this lane (in each group)
+    const uint32_t col = lane % 32;     // query column of this lane
     const uint32_t hs = lane / 32;      // which 8 of 16 in an MFMA slice
     // Transpose reads of V for the A operand of O^T += V^T P^T: lane
     // 16g + 4j + a reads row 8(g / 2) + j (+ 16c + 4e2 for slice c, half e2)
@@ -230,43 +229,36 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
         const uint32_t blocks = (keys + BN - 1) / BN;
         const uint32_t steps = (blocks + KSPLIT - 1) / KSPLIT;
 
-        const uint32_t qw0 = q_first + qw * 32 * QG;  // first query of this wave
+        const uint32_t qw0 = q_first + qw * 32;  // first query of this wave
         const bool wave_active = qw0 < p.q_len;
         const uint32_t wave_keys =
-            wave_active ? min(p.kv_len, p.start + min(qw0 + 32 * QG - 1, p.q_len - 1) + 1) : 0;
+            wave_active ? min(p.kv_len, p.start + min(qw0 + 31, p.q_len - 1) + 1) : 0;
 
-        h8 qf[QG][DC];
-        uint32_t key_limit[QG];
+        // B operand of S^T = K Q^T: lane (col, hs) holds elements
+        // 16c + 8hs .. + 7 of its query for every slice c
+        const uint32_t qi = qw0 + col;
+        const bool q_valid = qi < p.q_len;
+        // Largest key this lane's query sees (padding columns see a few keys
+        // too, so their arithmetic stays finite; never stored).
+        const uint32_t key_limit = min(p.start + qi, p.kv_len - 1);
+        h8 qf[DC];
+        const half_t* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + 8 * hs;
 #pragma unroll
-        for (int g = 0; g < QG; ++g) {
-            const uint32_t qi = qw0 + 32 * g + col;
-            const bool q_valid = qi < p.q_len;
-            // Largest key this lane's query sees (padding columns see a few
-            // keys too, so their arithmetic stays finite; never stored).
-            key_limit[g] = min(p.start + qi, p.kv_len - 1);
-            const half_t* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + 8 * hs;
+        for (int c = 0; c < DC; ++c) {
+            if (q_valid) {
+                qf[c] = *reinterpret_cast<const h8*>(qrow + 16 * c);
+            } else {
 #pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                if (q_valid) {
-                    qf[g][c] = *reinterpret_cast<const h8*>(qrow + 16 * c);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) qf[g][c][e] = half_t(0.0f);
-                }
+                for (int e = 0; e < 8; ++e) qf[c][e] = half_t(0.0f);
             }
         }
 
-        f32x16 o[QG][NT];
-        float m[QG], l[QG];  // running max logit (log2 units), this lane's share of the sum
+        f32x16 o[NT];
+        float m = -INFINITY, l = 0.0f;  // running max logit (log2 units), this lane's share of the sum
 #pragma unroll
-        for (int g = 0; g < QG; ++g) {
-            m[g] = -INFINITY;
-            l[g] = 0.0f;
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[g][t][r] = 0.0f;
-        }
+            for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
 
         h8 kreg[LOADS], vreg[LOADS];
         bool vlive[LOADS];
@@ -351,82 +343,70 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
             const half_t* ks = kv_lds + ((step % NSTAGE) * KSPLIT + sub) * KV_HALVES;
             const half_t* vs = ks + BN * KS;
             if (blk < blocks && blk * BN < wave_keys) {
-                // S^T = K Q^T: each K operand read once, used by every group.
-                f32x16 s[QG][KT];
+                // S^T = K Q^T, 32 keys per tile
+                f32x16 s[KT];
 #pragma unroll
                 for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-                    for (int g = 0; g < QG; ++g)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) s[g][kt][r] = 0.0f;
+                    for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
 #pragma unroll
                     for (int c = 0; c < DC; ++c) {
                         const h8 ka = *reinterpret_cast<const h8*>(ks + kt * 32 * KS + koff[c]);
-#pragma unroll
-                        for (int g = 0; g < QG; ++g)
-                            s[g][kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[g][c],
-                                                                             s[g][kt], 0, 0, 0);
+                        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[c], s[kt], 0, 0, 0);
                     }
                 }
+                // mask; the block's max raw score of each query
                 const uint32_t kbase = blk * BN;
-                const bool masking = kbase + BN - 1 > p.start + qw0 || kbase + BN > p.kv_len;
-                h8 pb[QG][BN / 16];
-#pragma unroll
-                for (int g = 0; g < QG; ++g) {
-                    // mask; the block's max raw score of each query
-                    if (masking) {
-#pragma unroll
-                        for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) {
-                                const uint32_t key =
-                                    kbase + kt * 32 + 16 * (r >> 3) + 8 * hs + (r & 7);
-                                if (key > key_limit[g]) s[g][kt][r] = -INFINITY;
-                            }
-                    }
-                    // two independent max chains, joined at the end
-                    float mx = -INFINITY, my = -INFINITY;
+                if (kbase + BN - 1 > p.start + qw0 || kbase + BN > p.kv_len) {
 #pragma unroll
                     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                        for (int r = 0; r < 16; r += 4) {
-                            mx = max3(mx, s[g][kt][r], s[g][kt][r + 1]);
-                            my = max3(my, s[g][kt][r + 2], s[g][kt][r + 3]);
+                        for (int r = 0; r < 16; ++r) {
+                            const uint32_t key = kbase + kt * 32 + 16 * (r >> 3) + 8 * hs + (r & 7);
+                            if (key > key_limit) s[kt][r] = -INFINITY;
                         }
-                    mx = fmaxf(mx, my);
-                    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                    const float mx_log2 = mx * p.scale_log2;
-                    if (__any(mx_log2 > m[g] + kRescaleSlack)) {
-                        const float m_new = fmaxf(m[g], mx_log2);
-                        const float alpha =
-                            m_new > m[g] ? __builtin_amdgcn_exp2f(m[g] - m_new) : 1.0f;
-                        m[g] = m_new;
-                        l[g] *= alpha;
+                }
+                // two independent max chains, joined at the end
+                float mx = -INFINITY, my = -INFINITY;
 #pragma unroll
-                        for (int t = 0; t < NT; ++t)
+                for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                            for (int r = 0; r < 16; ++r) o[g][t][r] *= alpha;
+                    for (int r = 0; r < 16; r += 4) {
+                        mx = max3(mx, s[kt][r], s[kt][r + 1]);
+                        my = max3(my, s[kt][r + 2], s[kt][r + 3]);
                     }
-                    // p = 2^(s * scale * log2 e - m); a query that has seen no
-                    // key yet (m = -inf) has only -inf scores here, and p = 0.
-                    const float neg_m = m[g] == -INFINITY ? 0.0f : -m[g];
-                    // P as the f16 operand of the P V product: lane half hs
-                    // supplies keys 16c + 8hs .. +7, which it holds in
-                    // registers 8(c%2) .. +7 of tile c/2.  The running sum adds
-                    // the same f16 probabilities the product uses
-                    // (v_dot2_f32_f16 against ones, f32 accumulation).
-                    const h2 ones = {half_t(1.0f), half_t(1.0f)};
+                mx = fmaxf(mx, my);
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mx_log2 = mx * p.scale_log2;
+                if (__any(mx_log2 > m + kRescaleSlack)) {
+                    const float m_new = fmaxf(m, mx_log2);
+                    const float alpha = m_new > m ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+                    m = m_new;
+                    l *= alpha;
 #pragma unroll
-                    for (int c = 0; c < BN / 16; ++c) {
+                    for (int t = 0; t < NT; ++t)
 #pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            pb[g][c][e] = half_t(__builtin_amdgcn_exp2f(__builtin_fmaf(
-                                s[g][c >> 1][8 * (c & 1) + e], p.scale_log2, neg_m)));
+                        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+                }
+                // p = 2^(s * scale * log2 e - m); a query that has seen no
+                // key yet (m = -inf) has only -inf scores here, and p = 0.
+                const float neg_m = m == -INFINITY ? 0.0f : -m;
+                // P as the f16 operand of the P V product: lane half hs
+                // supplies keys 16c + 8hs .. +7, which it holds in registers
+                // 8(c%2) .. +7 of tile c/2.  The running sum adds the same f16
+                // probabilities the product uses (v_dot2_f32_f16 against
+                // ones, f32 accumulation).
+                const h2 ones = {half_t(1.0f), half_t(1.0f)};
+                h8 pb[BN / 16];
 #pragma unroll
-                        for (int e = 0; e < 8; e += 2)
-                            l[g] = __builtin_amdgcn_fdot2(h2{pb[g][c][e], pb[g][c][e + 1]}, ones,
-                                                          l[g], false);
-                    }
+                for (int c = 0; c < BN / 16; ++c) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        pb[c][e] = half_t(__builtin_amdgcn_exp2f(
+                            __builtin_fmaf(s[c >> 1][8 * (c & 1) + e], p.scale_log2, neg_m)));
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2)
+                        l = __builtin_amdgcn_fdot2(h2{pb[c][e], pb[c][e + 1]}, ones, l, false);
                 }
                 // O^T += V^T P^T, 16 keys per MFMA; each V operand read once.
 #pragma unroll
@@ -436,10 +416,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                         const h4 lo = lds_read_transposed(vs + 16 * c * VS + voff[0][t]);
                         const h4 hi = lds_read_transposed(vs + 16 * c * VS + voff[1][t]);
                         const h8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-                        for (int g = 0; g < QG; ++g)
-                            o[g][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[g][c], o[g][t],
-                                                                            0, 0, 0);
+                        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], o[t], 0, 0, 0);
                     }
                 }
             }
@@ -457,59 +434,47 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
             float* mg = reinterpret_cast<float*>(lds);
             if (sub > 0) {
                 float* dst = mg + ((sub - 1) * QW * 64 + qw * 64 + lane) * MERGE;
+                dst[0] = m;
+                dst[1] = l;
 #pragma unroll
-                for (int g = 0; g < QG; ++g) {
-                    float* dg = dst + g * (NT * 16 + 2);
-                    dg[0] = m[g];
-                    dg[1] = l[g];
+                for (int t = 0; t < NT; ++t)
 #pragma unroll
-                    for (int t = 0; t < NT; ++t)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) dg[2 + 16 * t + r] = o[g][t][r];
-                }
+                    for (int r = 0; r < 16; ++r) dst[2 + 16 * t + r] = o[t][r];
             }
             __syncthreads();
             if (sub == 0) {
 #pragma unroll
                 for (int h = 1; h < KSPLIT; ++h) {
                     const float* src = mg + ((h - 1) * QW * 64 + qw * 64 + lane) * MERGE;
+                    const float m2 = src[0];
+                    const float m_tot = fmaxf(m, m2);
+                    const float a1 = m_tot > m ? __builtin_amdgcn_exp2f(m - m_tot) : 1.0f;
+                    const float a2 = m_tot > m2 ? __builtin_amdgcn_exp2f(m2 - m_tot) : 1.0f;
+                    l = l * a1 + src[1] * a2;
 #pragma unroll
-                    for (int g = 0; g < QG; ++g) {
-                        const float* sg = src + g * (NT * 16 + 2);
-                        const float m2 = sg[0];
-                        const float m_tot = fmaxf(m[g], m2);
-                        const float a1 = m_tot > m[g] ? __builtin_amdgcn_exp2f(m[g] - m_tot) : 1.0f;
-                        const float a2 = m_tot > m2 ? __builtin_amdgcn_exp2f(m2 - m_tot) : 1.0f;
-                        l[g] = l[g] * a1 + sg[1] * a2;
+                    for (int t = 0; t < NT; ++t)
 #pragma unroll
-                        for (int t = 0; t < NT; ++t)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r)
-                                o[g][t][r] = o[g][t][r] * a1 + sg[2 + 16 * t + r] * a2;
-                        m[g] = m_tot;
-                    }
+                        for (int r = 0; r < 16; ++r)
+                            o[t][r] = o[t][r] * a1 + src[2 + 16 * t + r] * a2;
+                    m = m_tot;
                 }
             }
             __syncthreads();  // the merge area is free again
         }
 
         if (sub == 0) {
+            const float inv = 1.0f / (l + __shfl_xor(l, 32, 64));  // both halves of the query
+            if (q_valid) {
+                // register r of tile t: element 32t + 8(r / 4) + 4hs + r % 4
+                half_t* orow = out + (uint64_t(bh) * p.q_len + qi) * D + 4 * hs;
 #pragma unroll
-            for (int g = 0; g < QG; ++g) {
-                const uint32_t qi = qw0 + 32 * g + col;
-                const float total = l[g] + __shfl_xor(l[g], 32, 64);
-                const float inv = 1.0f / total;
-                if (qi < p.q_len) {
-                    half_t* orow = out + (uint64_t(bh) * p.q_len + qi) * D + 4 * hs;
+                for (int t = 0; t < NT; ++t) {
 #pragma unroll
-                    for (int t = 0; t < NT; ++t) {
+                    for (int g = 0; g < 4; ++g) {
+                        h4 w;
 #pragma unroll
-                        for (int gg = 0; gg < 4; ++gg) {
-                            h4 w;
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) w[e] = half_t(o[g][t][4 * gg + e] * inv);
-                            *reinterpret_cast<h4*>(orow + t * 32 + 8 * gg) = w;
-                        }
+                        for (int e = 0; e < 4; ++e) w[e] = half_t(o[t][4 * g + e] * inv);
+                        *reinterpret_cast<h4*>(orow + t * 32 + 8 * g) = w;
                     }
                 }
             }
@@ -1267,14 +1232,14 @@ void launch_flash(rl_context* ctx, dim3 g, uint32_t nt, const half_t* q, const h
     constexpr int BN4 = KS == 4 ? 32 : 64;
     const dim3 b(64 * QW * KS);
     if (nt == 1) {
-        RL_LAUNCH(ctx, (k_flash_attention<1, QW, KS, BN, 1, true>), g, b, q, k, v, o, p);
+        RL_LAUNCH(ctx, (k_flash_attention<1, QW, KS, BN, true>), g, b, q, k, v, o, p);
     } else if (nt == 2) {
-        RL_LAUNCH(ctx, (k_flash_attention<2, QW, KS, BN, 1, true>), g, b, q, k, v, o, p);
+        RL_LAUNCH(ctx, (k_flash_attention<2, QW, KS, BN, true>), g, b, q, k, v, o, p);
     } else if constexpr (!(QW == 1 && KS == 2)) {  // that shape only for head sizes <= 64
         if (nt == 3) {
-            RL_LAUNCH(ctx, (k_flash_attention<3, QW, KS, 64, 1, false>), g, b, q, k, v, o, p);
+            RL_LAUNCH(ctx, (k_flash_attention<3, QW, KS, 64, false>), g, b, q, k, v, o, p);
         } else {
-            RL_LAUNCH(ctx, (k_flash_attention<4, QW, KS, BN4, 1, true>), g, b, q, k, v, o, p);
+            RL_LAUNCH(ctx, (k_flash_attention<4, QW, KS, BN4, true>), g, b, q, k, v, o, p);
         }
     }
 }
