@@ -358,13 +358,13 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                 // mask; the block's max raw score of each query
                 const uint32_t kbase = blk * BN;
                 if (kbase + BN - 1 > p.start + qw0 || kbase + BN > p.kv_len) {
+                    // register r of tile kt holds key kbase + 8hs + (a constant)
+                    const int lim = int(key_limit) - int(kbase + 8 * hs);
 #pragma unroll
                     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const uint32_t key = kbase + kt * 32 + 16 * (r >> 3) + 8 * hs + (r & 7);
-                            if (key > key_limit) s[kt][r] = -INFINITY;
-                        }
+                        for (int r = 0; r < 16; ++r)
+                            if (kt * 32 + 16 * (r >> 3) + (r & 7) > lim) s[kt][r] = -INFINITY;
                 }
                 // two independent max chains, joined at the end
                 float mx = -INFINITY, my = -INFINITY;
@@ -618,11 +618,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention_f32(
                 // register r of tile kt holds key kbase + 32 kt + 2r + hs
                 const uint32_t kbase = blk * BN;
                 if (kbase + BN - 1 > p.start + qw0 || kbase + BN > p.kv_len) {
+                    const int lim = int(key_limit) - int(kbase + hs);
 #pragma unroll
                     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
-                            if (kbase + kt * 32 + 2 * r + hs > key_limit) s[kt][r] = -INFINITY;
+                            if (kt * 32 + 2 * r > lim) s[kt][r] = -INFINITY;
                 }
                 // scores in log2 units first, so that the largest one's
                 // probability is exactly 1 (2^(t - m) with t == m)
