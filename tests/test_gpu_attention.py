@@ -161,6 +161,7 @@ GQA_SHAPES = [  # batch, q_heads, kv_heads, q_len, kv_len, capacity, head_dim
     (2, 4, 4, 33, 64, 64, 128),      # plain heads, batch 2
     (1, 6, 2, 7, 45, 50, 32),        # key count not a multiple of 8 (element stores)
     (1, 3, 1, 17, 200, 200, 96),
+    (1, 8, 2, 300, 1000, 1024, 128),  # many key tiles and PV steps
     (1, 2, 1, 9, 70, 80, 48),        # row kernels
 ]
 
