@@ -33,7 +33,9 @@ struct GqaParams {
     uint32_t q_heads, group, q_len, kv_len, head_dim;
     uint64_t kv_head_stride;  // elements between KV heads (kv_capacity * head_dim)
     uint32_t q_tiles;         // query tiles per head (MFMA kernels)
-    uint32_t k_tiles;         // key tiles per query tile (QK^T MFMA kernel)
+    uint32_t k_tiles;         // 128-key tiles per query tile (QK^T MFMA kernels)
+    uint32_t k_per_block;     // key tiles one f32 QK^T workgroup computes in turn
+    uint32_t k_groups;        // f32 QK^T workgroups per query tile
 };
 
 __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
@@ -266,12 +268,14 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
 
 // ----------------------------------------------------- f32, matrix cores
 
-// QK^T in f32 (v_mfma_f32_32x32x2_f32, exact f32 products): workgroup =
-// (head, 128 queries, 128 keys) as for f16, the key tile in LDS in key order
-// at a stride of 2 mod 64 floats (every operand read on its own bank).  Each
-// lane stores its result registers directly, four consecutive keys per
-// 16-byte store: a row receives 32-byte pieces that the L2 merges into whole
-// lines; the kernel is bound by the f32 matrix cores, not by these stores.
+// QK^T in f32 (v_mfma_f32_32x32x2_f32, exact f32 products; bound by the
+// f32 matrix cores): workgroup = (head, 128 queries, run of k_per_block
+// 128-key tiles), wave = 32 queries.  The queries stay in registers for the
+// whole run; key tiles pass through registers into one of two LDS buffers
+// (tile t + 1 loads while tile t is multiplied), in key order at a stride of
+// 2 mod 64 floats (every operand read on its own bank).  Each lane stores
+// its result registers directly, four consecutive keys per 16-byte store: a
+// row receives 32-byte pieces that the L2 merges into whole lines.
 template <int NT>
 __global__ __launch_bounds__(256) void k_gqa_qk_mfma_f32(const float* __restrict__ q,
                                                          const float* __restrict__ k,
@@ -280,30 +284,42 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma_f32(const float* __restrict
     constexpr int DS = D / 2;  // MFMA steps over the head
     constexpr int KS = f32_stride(D, 2);
     constexpr int ROW_CHUNKS = D / 4;
-    __shared__ __align__(16) float ks[128 * KS];
+    constexpr int LOADS = 128 * ROW_CHUNKS / 256;  // 16-byte pieces of a key tile per thread
+    __shared__ __align__(16) float ks[2][128 * KS];
     const uint32_t wave = threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t col = lane % 32;
     const uint32_t hs = lane / 32;
-    const uint32_t kt_blk = blockIdx.x % p.k_tiles;
-    const uint32_t rest = blockIdx.x / p.k_tiles;
+    const uint32_t kg = blockIdx.x % p.k_groups;
+    const uint32_t rest = blockIdx.x / p.k_groups;
     const uint32_t qt = rest % p.q_tiles;
     const uint32_t bh = rest / p.q_tiles;
     const uint32_t q0 = qt * 128 + wave * 32;
     const float* kh = k + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
-    const uint32_t kbase = kt_blk * 128;
+    const uint32_t t_first = kg * p.k_per_block;
+    const uint32_t t_end = min(p.k_tiles, t_first + p.k_per_block);
+
     // keys past kv_len read row kv_len - 1 (their scores are not stored)
+    float4 kreg[LOADS];
+    auto load_tile = [&](uint32_t t) {
 #pragma unroll
-    for (int li = 0; li < 128 * ROW_CHUNKS / 256; ++li) {
-        const uint32_t chunk = threadIdx.x + 256 * li;
-        const uint32_t j = chunk / ROW_CHUNKS;
-        const uint32_t d0 = (chunk % ROW_CHUNKS) * 4;
-        const uint32_t key = min(kbase + j, p.kv_len - 1);
-        const float4 x = *reinterpret_cast<const float4*>(kh + uint64_t(key) * D + d0);
-        float* dst = ks + j * KS + d0;  // 8-byte aligned rows
-        *reinterpret_cast<float2*>(dst) = float2{x.x, x.y};
-        *reinterpret_cast<float2*>(dst + 2) = float2{x.z, x.w};
-    }
+        for (int li = 0; li < LOADS; ++li) {
+            const uint32_t chunk = threadIdx.x + 256 * li;
+            const uint32_t key = min(t * 128 + chunk / ROW_CHUNKS, p.kv_len - 1);
+            kreg[li] = *reinterpret_cast<const float4*>(kh + uint64_t(key) * D +
+                                                        (chunk % ROW_CHUNKS) * 4);
+        }
+    };
+    auto store_tile = [&](float* dst) {
+#pragma unroll
+        for (int li = 0; li < LOADS; ++li) {
+            const uint32_t chunk = threadIdx.x + 256 * li;
+            float* row = dst + (chunk / ROW_CHUNKS) * KS + (chunk % ROW_CHUNKS) * 4;  // 8-byte aligned
+            *reinterpret_cast<float2*>(row) = float2{kreg[li].x, kreg[li].y};
+            *reinterpret_cast<float2*>(row + 2) = float2{kreg[li].z, kreg[li].w};
+        }
+    };
+    load_tile(t_first);
     // B operand: lane (col, hs) holds elements 2j + hs of its query
     const uint32_t qi = q0 + col;
     const bool q_valid = qi < p.q_len;
@@ -311,35 +327,43 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma_f32(const float* __restrict
     float qf[DS];
 #pragma unroll
     for (int j = 0; j < DS; ++j) qf[j] = q_valid ? qrow[2 * j] : 0.0f;
+    store_tile(ks[0]);
     __syncthreads();
-    if (q0 >= p.q_len) return;  // (no barrier below)
+
     const bool vec_store = p.kv_len % 4 == 0;
     float* orow = out + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * p.kv_len;
+    for (uint32_t t = t_first; t < t_end; ++t) {
+        const uint32_t buf = (t - t_first) % 2;
+        if (t + 1 < t_end) load_tile(t + 1);
+        if (q0 < p.q_len) {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {  // four 32-key sub-tiles
-        const uint32_t k0 = kbase + st * 32;
-        if (k0 >= p.kv_len) break;
-        const float* krow = ks + (st * 32 + col) * KS + hs;
-        f32x16 s;
+            for (int st = 0; st < 4; ++st) {  // four 32-key sub-tiles
+                const uint32_t k0 = t * 128 + st * 32;
+                const float* krow = ks[buf] + (st * 32 + col) * KS + hs;
+                f32x16 s;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+                for (int r = 0; r < 16; ++r) s[r] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < DS; ++j)
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[2 * j], qf[j], s, 0, 0, 0);
-        if (!q_valid) continue;
-        // register 4g + e holds key k0 + 8g + 4hs + e
+                for (int j = 0; j < DS; ++j)
+                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[2 * j], qf[j], s, 0, 0, 0);
+                if (!q_valid) continue;
+                // register 4g + e holds key k0 + 8g + 4hs + e
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint32_t key = k0 + 8 * g + 4 * hs;
-            if (vec_store && key + 4 <= p.kv_len) {
-                *reinterpret_cast<float4*>(orow + key) =
-                    float4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
-            } else {
+                for (int g = 0; g < 4; ++g) {
+                    const uint32_t key = k0 + 8 * g + 4 * hs;
+                    if (vec_store && key + 4 <= p.kv_len) {
+                        *reinterpret_cast<float4*>(orow + key) =
+                            float4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
+                    } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (key + e < p.kv_len) orow[key + e] = s[4 * g + e];
+                        for (int e = 0; e < 4; ++e)
+                            if (key + e < p.kv_len) orow[key + e] = s[4 * g + e];
+                    }
+                }
             }
         }
+        if (t + 1 < t_end) store_tile(ks[buf ^ 1]);  // read during step t - 1, before its barrier
+        __syncthreads();
     }
 }
 
@@ -630,7 +654,16 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
         if (use_mfma<T>(s, qd, kd, od)) {
             p.q_tiles = uint32_t(ceil_div(s.q_len, 128));
             p.k_tiles = uint32_t(ceil_div(s.kv_len, 128));
-            const uint64_t grid = heads * p.q_tiles * p.k_tiles;
+            // Workgroups walk runs of key tiles; a query tile's keys split
+            // over several only when the query tiles alone do not fill the
+            // resident workgroups (two per CU up to head size 64, one above).
+            const uint64_t base = heads * p.q_tiles;
+            const uint64_t resident = s.head_dim <= 64 ? 512 : 256;
+            const uint64_t groups =
+                std::min<uint64_t>(p.k_tiles, std::max<uint64_t>(1, resident / base));
+            p.k_per_block = uint32_t(ceil_div(p.k_tiles, groups));
+            p.k_groups = uint32_t(ceil_div(p.k_tiles, p.k_per_block));
+            const uint64_t grid = base * p.k_groups;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
             switch (s.head_dim / 32) {
