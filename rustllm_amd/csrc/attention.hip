@@ -1119,16 +1119,22 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
 
     // Hand-off: the workgroup that completes a KV head's last split merges
     // that head's rows (one wave per row), so a decode step is one launch.
-    // Every thread's partial stores are made visible device-wide before the
-    // ticket is drawn; the last workgroup reads after an acquire fence and
-    // puts the ticket back to zero for the next launch.
+    // Every wave waits for its partial stores to complete (vmcnt), the
+    // barrier orders them before the thread that draws the ticket, and that
+    // thread's device-scope release publishes them (one L2 write-back per
+    // workgroup -- the XCDs' L2s are not coherent); the last workgroup reads
+    // after an acquire and puts the ticket back to zero for the next launch.
     __shared__ uint32_t ticket;
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) ticket = atomicAdd(&tickets[kvb], 1u);
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        ticket = __hip_atomic_fetch_add(&tickets[kvb], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    }
     __syncthreads();
     if (ticket != splits - 1) return;
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (threadIdx.x == 0) tickets[kvb] = 0;
     float* w = reinterpret_cast<float*>(vstage[wave]);  // the stage is free now
     for (uint32_t r = wave; r < R; r += kSplitWaves) {
