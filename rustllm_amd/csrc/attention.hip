@@ -589,8 +589,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention_f32(
                 float* kr = kdst + ((key & ~31u) | key_row32(key & 31u)) * KS + d0;
                 *reinterpret_cast<float2*>(kr) = float2{kreg[li].x, kreg[li].y};
                 *reinterpret_cast<float2*>(kr + 2) = float2{kreg[li].z, kreg[li].w};
-                const float4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-                *reinterpret_cast<float4*>(vdst + key * VS + d0) = vlive[li] ? vreg[li] : zero;
+                // per-component selects: a select of two float4 structs goes
+                // through private memory
+                const bool live = vlive[li];
+                *reinterpret_cast<float4*>(vdst + key * VS + d0) =
+                    float4{live ? vreg[li].x : 0.0f, live ? vreg[li].y : 0.0f,
+                           live ? vreg[li].z : 0.0f, live ? vreg[li].w : 0.0f};
             }
         };
 
