@@ -45,7 +45,14 @@ __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
 
 // ------------------------------------------------------------ QK^T, MFMA
 
-template <int NT>
+// SHIFT: kv_len is not a multiple of 8, so a score row starts `lead`
+// elements past a 16-byte boundary (the output buffer itself is 16-byte
+// aligned).  The row's tile then sits `lead` columns to the right in LDS, so
+// that LDS chunk j (8 columns) is the j-th 16-byte chunk of memory from the
+// boundary before the row's first score: 17 chunks per row, the 15 inner
+// ones whole 16-byte stores, the two it shares with the neighbouring tiles
+// element by element (this tile's scores only).
+template <int NT, bool SHIFT>
 __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ q,
                                                      const half_t* __restrict__ k,
                                                      half_t* __restrict__ out, GqaParams p) {
@@ -96,6 +103,13 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     __syncthreads();
     if (q0 >= p.q_len) return;  // (no barrier below)
     half_t* my = tile[wave];
+    // elements between a row's first score of this tile and the 16-byte
+    // boundary at or before it: (row index x kv_len) mod 8, exact in 32-bit
+    // arithmetic (kbase is a multiple of 128)
+    auto lead_of = [&](uint32_t r) -> uint32_t {
+        return ((bh * p.q_len + q0 + r) * p.kv_len) & 7u;
+    };
+    const uint32_t my_lead = SHIFT ? lead_of(col) : 0u;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {  // four 32-key tiles
         const uint32_t k0 = kbase + t * 32;
@@ -114,7 +128,13 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
             h8 w;
 #pragma unroll
             for (int e = 0; e < 8; ++e) w[e] = half_t(s[8 * half + e]);
-            *reinterpret_cast<h8*>(my + col * TS + t * 32 + 16 * half + 8 * hs) = w;
+            half_t* dst = my + col * TS + t * 32 + 16 * half + 8 * hs;
+            if constexpr (SHIFT) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dst[my_lead + e] = w[e];
+            } else {
+                *reinterpret_cast<h8*>(dst) = w;
+            }
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -122,6 +142,39 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // rows of the tile to memory: 16 lanes per 256-byte row segment
     const uint32_t keys_here = min(128u, p.kv_len - kbase);
+    if constexpr (SHIFT) {
+        // Chunk c of row r covers LDS columns 8c .. 8c + 7, the row's scores
+        // 8c - lead ..  Whole chunks: 32 rows x 17 slots over the lanes.
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            const uint32_t slot = i * 64 + lane;
+            const uint32_t r = slot / 17, lo = 8 * (slot % 17);
+            if (slot >= 32 * 17 || q0 + r >= p.q_len) continue;
+            const uint32_t lead = lead_of(r);
+            if (lo < lead || lo + 8 > lead + keys_here) continue;  // not a whole chunk
+            const h8 w = *reinterpret_cast<const h8*>(my + r * TS + lo);
+            const uint64_t first = (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase;
+            __builtin_nontemporal_store(w, reinterpret_cast<h8*>(out + (first - lead + lo)));
+        }
+        // The (at most) two chunks a row shares with its neighbours, one per
+        // lane: lane 2r + 0 the row's first chunk, 2r + 1 its last.
+        const uint32_t r = lane / 2;
+        if (q0 + r < p.q_len) {
+            const uint32_t lead = lead_of(r);
+            const uint32_t last = (lead + keys_here - 1) / 8;
+            const bool first_edge = lead > 0 || lead + keys_here < 8;
+            const bool last_edge = last > 0 && (lead + keys_here) % 8 != 0;
+            if (lane % 2 == 0 ? first_edge : last_edge) {
+                const uint32_t lo = lane % 2 == 0 ? 0u : 8 * last;
+                const uint64_t first = (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (lo + e >= lead && lo + e < lead + keys_here)
+                        out[first + (lo + e - lead)] = my[r * TS + lo + e];
+            }
+        }
+        return;
+    }
     const bool vec_store = p.kv_len % 8 == 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -142,7 +195,13 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
 
 // -------------------------------------------------------------- P V, MFMA
 
-template <int NT>
+// SHIFT: kv_len is not a multiple of 8 (probs 16-byte aligned).  A row's
+// 128 probabilities of a step are read as the 17 16-byte chunks from the
+// boundary at or before its first one (the 15 inner chunks whole, the two
+// shared with neighbouring steps or rows element by element, one per lane)
+// and kept on that chunk grid in LDS; the products read the row's columns
+// from its lead on, 2 bytes at a time.
+template <int NT, bool SHIFT>
 __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ probs,
                                                      const half_t* __restrict__ v,
                                                      half_t* __restrict__ out, GqaParams p) {
@@ -168,10 +227,51 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
     const uint32_t tr_off = (8 * (lane / 32) + (lane % 16) / 4) * VS + 16 * ((lane / 16) % 2) +
                             4 * (lane % 4);
     half_t* my = pt[wave];
+    constexpr int P_LOADS = SHIFT ? 10 : 8;
+    // a row's lead, (row index x kv_len) mod 8 (the same for every step: a
+    // step is 128 keys)
+    auto lead_of = [&](uint32_t r) -> uint32_t {
+        return ((bh * p.q_len + q0 + r) * p.kv_len) & 7u;
+    };
 
     // this wave's 32 x 128 probabilities of step blk, whole 256-byte row
     // segments per 16 lanes (rows past q_len and keys past kv_len as zeros)
-    auto load_p = [&](uint32_t blk, h8 (&pr)[8]) {
+    auto load_p = [&](uint32_t blk, h8 (&pr)[P_LOADS]) {
+        if constexpr (SHIFT) {
+            const uint32_t n = min(uint32_t(BN), p.kv_len - blk * BN);  // keys of this step
+            // whole chunks: 32 rows x 17 slots over the lanes
+#pragma unroll
+            for (int i = 0; i < 9; ++i) {
+                const uint32_t slot = i * 64 + lane;
+                const uint32_t r = slot / 17, lo = 8 * (slot % 17);
+                const h8 zero = {};
+                pr[i] = zero;
+                if (slot >= 32 * 17 || q0 + r >= p.q_len) continue;
+                const uint32_t lead = lead_of(r);
+                if (lo < lead || lo + 8 > lead + n) continue;
+                // the row's first probability of the step
+                const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + blk * BN;
+                pr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(src + lo - lead));
+            }
+            // the chunks shared with the neighbours, one per lane (as in QK^T)
+            const uint32_t r = lane / 2;
+            const h8 zero = {};
+            pr[9] = zero;
+            if (q0 + r < p.q_len) {
+                const uint32_t lead = lead_of(r);
+                const uint32_t last = (lead + n - 1) / 8;
+                const uint32_t lo = lane % 2 == 0 ? 0u : 8 * last;
+                const bool edge = lane % 2 == 0 ? (lead > 0 || lead + n < 8)
+                                                : (last > 0 && (lead + n) % 8 != 0);
+                if (edge) {
+                    const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + blk * BN;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (lo + e >= lead && lo + e < lead + n) pr[9][e] = src[lo + e - lead];
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t r = i * 4 + lane / 16;
@@ -186,7 +286,29 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
             }
         }
     };
-    auto store_p = [&](const h8 (&pr)[8]) {
+    auto store_p = [&](uint32_t blk, const h8 (&pr)[P_LOADS]) {
+        if constexpr (SHIFT) {
+            // LDS row r holds its step on the memory's chunk grid: column x is
+            // the row's key x - lead of the step (the products read columns
+            // lead .. lead + 127).  Slots carry whole chunks or zeros; the
+            // shared chunks are written last, over the slots' zeros.
+            const uint32_t n = min(uint32_t(BN), p.kv_len - blk * BN);
+#pragma unroll
+            for (int i = 0; i < 9; ++i) {
+                const uint32_t slot = i * 64 + lane;
+                if (slot < 32 * 17)
+                    *reinterpret_cast<h8*>(my + (slot / 17) * PS + 8 * (slot % 17)) = pr[i];
+            }
+            const uint32_t r = lane / 2;
+            const uint32_t lead = lead_of(r);
+            const uint32_t last = (lead + n - 1) / 8;
+            const uint32_t lo = lane % 2 == 0 ? 0u : 8 * last;
+            const bool edge = lane % 2 == 0 ? (lead > 0 || lead + n < 8)
+                                            : (last > 0 && (lead + n) % 8 != 0);
+            if (edge && q0 + r < p.q_len) *reinterpret_cast<h8*>(my + r * PS + lo) = pr[9];
+            return;
+        }
+        (void)blk;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             *reinterpret_cast<h8*>(my + (i * 4 + lane / 16) * PS + (lane % 16) * 8) = pr[i];
@@ -218,10 +340,11 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
         for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
 
     const uint32_t blocks = (p.kv_len + BN - 1) / BN;
-    h8 pnext[8], vnext[LOADS];
+    const half_t* prow = my + col * PS + (SHIFT ? lead_of(col) : 0u) + 8 * hs;
+    h8 pnext[P_LOADS], vnext[LOADS];
     load_p(0, pnext);
     load_v(0, vnext);
-    store_p(pnext);
+    store_p(0, pnext);
     store_v(vnext);
     __syncthreads();
     for (uint32_t blk = 0; blk < blocks; ++blk) {
@@ -232,8 +355,15 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
         }
 #pragma unroll
         for (int c = 0; c < PC; ++c) {
-            // P^T operand: keys 16 c + 8 hs + 0..7 of query row col
-            const h8 pb = *reinterpret_cast<const h8*>(my + col * PS + 16 * c + 8 * hs);
+            // P^T operand: keys 16 c + 8 hs + 0..7 of query row col (with
+            // SHIFT at columns shifted by the row's lead: 2-byte reads)
+            h8 pb;
+            if constexpr (SHIFT) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pb[e] = prow[16 * c + e];
+            } else {
+                pb = *reinterpret_cast<const h8*>(my + col * PS + 16 * c + 8 * hs);
+            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const half_t* vsrc = vs + tr_off + 16 * c * VS + 32 * t;
@@ -245,7 +375,7 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
         }
         if (more) {
             __syncthreads();
-            store_p(pnext);
+            store_p(blk + 1, pnext);
             store_v(vnext);
             __syncthreads();
         }
@@ -642,12 +772,21 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
             const uint64_t grid = heads * p.q_tiles * p.k_tiles;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
+            const bool shift = s.kv_len % 8 != 0;
+#define RL_QK(NT)                                                                      \
+    do {                                                                               \
+        if (shift)                                                                     \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, true>), g, b, qd, kd, od, p);            \
+        else                                                                           \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, false>), g, b, qd, kd, od, p);           \
+    } while (0)
             switch (s.head_dim / 32) {
-                case 1: RL_LAUNCH(ctx, (k_gqa_qk_mfma<1>), g, b, qd, kd, od, p); break;
-                case 2: RL_LAUNCH(ctx, (k_gqa_qk_mfma<2>), g, b, qd, kd, od, p); break;
-                case 3: RL_LAUNCH(ctx, (k_gqa_qk_mfma<3>), g, b, qd, kd, od, p); break;
-                default: RL_LAUNCH(ctx, (k_gqa_qk_mfma<4>), g, b, qd, kd, od, p); break;
+                case 1: RL_QK(1); break;
+                case 2: RL_QK(2); break;
+                case 3: RL_QK(3); break;
+                default: RL_QK(4); break;
             }
+#undef RL_QK
             return after_launch(ctx, name);
         }
     } else {
@@ -720,12 +859,21 @@ rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, co
             const uint64_t grid = heads * p.q_tiles;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA PV grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
+            const bool shift = s.kv_len % 8 != 0;
+#define RL_PV(NT)                                                                      \
+    do {                                                                               \
+        if (shift)                                                                     \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true>), g, b, pd, vd, od, p);            \
+        else                                                                           \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false>), g, b, pd, vd, od, p);           \
+    } while (0)
             switch (s.head_dim / 32) {
-                case 1: RL_LAUNCH(ctx, (k_gqa_pv_mfma<1>), g, b, pd, vd, od, p); break;
-                case 2: RL_LAUNCH(ctx, (k_gqa_pv_mfma<2>), g, b, pd, vd, od, p); break;
-                case 3: RL_LAUNCH(ctx, (k_gqa_pv_mfma<3>), g, b, pd, vd, od, p); break;
-                default: RL_LAUNCH(ctx, (k_gqa_pv_mfma<4>), g, b, pd, vd, od, p); break;
+                case 1: RL_PV(1); break;
+                case 2: RL_PV(2); break;
+                case 3: RL_PV(3); break;
+                default: RL_PV(4); break;
             }
+#undef RL_PV
             return after_launch(ctx, name);
         }
     } else {

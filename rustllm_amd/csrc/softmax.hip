@@ -116,7 +116,13 @@ __device__ inline float group_sum(float v, float* lds) {
 // Threads of a group past the last row take part in the barriers with no
 // memory accesses.  (One group per block, no grid-stride loop: the loop
 // doubled the VGPR count of the masked f16 variant.)
-template <typename T, int N, int NV, int TPR, bool MASK>
+// RAGGED: the width is not a multiple of N, so a row starts `lead` elements
+// past a 16-byte boundary.  Its packs stay on the buffer's 16-byte grid: pack
+// p holds the row's elements p * N - lead ..; a pack wholly inside the row
+// moves as one 16-byte access, the two packs it shares with its neighbours
+// move element by element (only this row's elements), so no access leaves
+// the row.
+template <typename T, int N, int NV, int TPR, bool MASK, bool RAGGED>
 __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__ in,
                                                            T* __restrict__ out, uint32_t row_base,
                                                            uint32_t rows, uint32_t width,
@@ -131,9 +137,11 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
         const uint64_t row64 = uint64_t(row_base) + uint64_t(blockIdx.x) * RPB + threadIdx.x / TPR;
         const bool active = row64 < rows;
         const uint32_t row = uint32_t(row64);
-        const uint64_t row_off = uint64_t(active ? row : 0) * w_packs;
-        const V* src = reinterpret_cast<const V*>(in) + row_off;
-        V* dst = reinterpret_cast<V*>(out) + row_off;
+        const uint64_t e0 = uint64_t(active ? row : 0) * width;  // the row's first element
+        const uint32_t lead = RAGGED ? uint32_t(e0 % N) : 0u;
+        const uint32_t n_packs = RAGGED ? (lead + width + N - 1) / N : w_packs;
+        const V* src = reinterpret_cast<const V*>(in + (e0 - lead));
+        V* dst = reinterpret_cast<V*>(out + (e0 - lead));
         const uint32_t kept = !active ? 0u : MASK ? kept_keys(row, width, mp) : width;
 
         float v[NV][N];
@@ -141,9 +149,25 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const uint32_t p = lane + k * TPR;
-            if (p < w_packs && p * N < kept) {
+            // row index of the pack's first element (negative only in a
+            // ragged row's first pack)
+            const int x0 = int(p * N) - int(lead);
+            if (RAGGED && p < n_packs && x0 < int(kept) && (x0 < 0 || x0 + N > int(kept))) {
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    const int x = x0 + j;
+                    float f = -INFINITY;
+                    if (x >= 0 && x < int(kept)) {
+                        const T raw = in[e0 + uint32_t(x)];
+                        f = MASK ? scaled_score(raw, mp.scale) : to_float(raw);
+                    }
+                    v[k][j] = f;
+                    m = fmaxf(m, f);
+                }
+            } else if (p < n_packs && p * N < kept + lead) {
                 V raw = load_stream(src + p);
-                if (!MASK || (p + 1) * N <= kept) {  // the whole pack is kept
+                // (a ragged row's partial packs took the branch above)
+                if (RAGGED || !MASK || (p + 1) * N <= kept) {  // the whole pack is kept
 #pragma unroll
                     for (int j = 0; j < N; ++j) {
                         const float f = MASK ? scaled_score(raw[j], mp.scale) : to_float(raw[j]);
@@ -171,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const uint32_t p = lane + k * TPR;
-            if (!zero_row && p < w_packs && p * N < kept) {
+            if (!zero_row && p < n_packs && p * N < kept + lead) {
 #pragma unroll
                 for (int j = 0; j < N; ++j) {
                     float e = exp_row<T>(v[k][j] - m);
@@ -188,7 +212,15 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const uint32_t p = lane + k * TPR;
-            if (active && p < w_packs) {
+            const int x0 = int(p * N) - int(lead);
+            if (RAGGED && active && p < n_packs && (x0 < 0 || x0 + N > int(width))) {
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    const int x = x0 + j;
+                    if (x >= 0 && x < int(width))
+                        out[e0 + uint32_t(x)] = from_float<T>(v[k][j] * inv);
+                }
+            } else if (active && p < n_packs) {
                 V o;
 #pragma unroll
                 for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
@@ -277,25 +309,40 @@ __global__ __launch_bounds__(kThreads) void k_softmax_stream(const T* __restrict
 
 // ------------------------------------------------------ scale/mask alone
 
-template <typename T, int N>
+// RAGGED: rows on the buffer's 16-byte pack grid as in k_softmax_rows.
+template <typename T, int N, bool RAGGED>
 __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ in,
                                                          T* __restrict__ out, uint32_t rows,
                                                          uint32_t width, MaskParams mp) {
     typedef typename VecOf<T, N>::type V;
     const uint32_t w_packs = width / N;
     for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        const uint64_t row_off = uint64_t(row) * w_packs;
-        const V* src = reinterpret_cast<const V*>(in) + row_off;
-        V* dst = reinterpret_cast<V*>(out) + row_off;
+        const uint64_t e0 = uint64_t(row) * width;
+        const uint32_t lead = RAGGED ? uint32_t(e0 % N) : 0u;
+        const uint32_t n_packs = RAGGED ? (lead + width + N - 1) / N : w_packs;
+        const V* src = reinterpret_cast<const V*>(in + (e0 - lead));
+        V* dst = reinterpret_cast<V*>(out + (e0 - lead));
         const uint32_t kept = kept_keys(row, width, mp);
-        for (uint32_t p = threadIdx.x; p < w_packs; p += kThreads) {
+        for (uint32_t p = threadIdx.x; p < n_packs; p += kThreads) {
+            if (RAGGED && (p * N < lead || p * N + N > lead + width)) {
+                // a pack shared with a neighbouring row: this row's elements only
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    const uint32_t pj = p * N + j;
+                    if (pj < lead || pj >= lead + width) continue;
+                    const uint32_t x = pj - lead;
+                    out[e0 + x] = x < kept ? from_float<T>(to_float(in[e0 + x]) * mp.scale)
+                                           : from_float<T>(-INFINITY);
+                }
+                continue;
+            }
             V o;
-            if (p * N < kept) {
+            if (p * N < kept + lead) {
                 V raw = load_stream(src + p);
 #pragma unroll
                 for (int j = 0; j < N; ++j)
-                    o[j] = (p * N + j < kept) ? from_float<T>(to_float(raw[j]) * mp.scale)
-                                              : from_float<T>(-INFINITY);
+                    o[j] = (p * N + j < kept + lead) ? from_float<T>(to_float(raw[j]) * mp.scale)
+                                                     : from_float<T>(-INFINITY);
             } else {
 #pragma unroll
                 for (int j = 0; j < N; ++j) o[j] = from_float<T>(-INFINITY);
@@ -318,18 +365,29 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
     if (rl_status st = activate(ctx)) return st;
     constexpr int N = 16 / sizeof(T);
     const uint32_t r32 = uint32_t(rows), w32 = uint32_t(width);
-    const bool packs_ok = width % N == 0 && aligned_to(in, 16) && aligned_to(out, 16);
-    const uint64_t w_packs = width / N;
+    // Rows on the buffer's 16-byte pack grid; a width that is not a multiple
+    // of the pack takes the ragged variant, whose rows span at most one pack
+    // more (one more per thread).
+    const bool packs_ok = aligned_to(in, 16) && aligned_to(out, 16);
+    const bool ragged = width % N != 0;
+    const uint64_t w_packs = ceil_div(width, N);
     const dim3 block(kThreads);
     // Row chunks of at most 2^30 blocks each (one launch for any real shape).
-#define RL_SOFTMAX_ROWS(NV, TPR)                                                                 \
+#define RL_SOFTMAX_ROWS_R(NV, TPR, R)                                                            \
     do {                                                                                         \
         for (uint64_t base = 0; base < rows; base += (uint64_t(1) << 30) * (kThreads / TPR)) { \
             const uint64_t left = ceil_div(rows - base, kThreads / TPR);                         \
-            RL_LAUNCH(ctx, (k_softmax_rows<T, N, NV, TPR, MASK>),                                \
+            RL_LAUNCH(ctx, (k_softmax_rows<T, N, NV, TPR, MASK, R>),                             \
                       dim3(unsigned(left < (uint64_t(1) << 30) ? left : (uint64_t(1) << 30))),   \
                       block, in, out, uint32_t(base), r32, w32, mp);                             \
         }                                                                                        \
+    } while (0)
+#define RL_SOFTMAX_ROWS(NV, TPR)                  \
+    do {                                          \
+        if (ragged)                               \
+            RL_SOFTMAX_ROWS_R(NV + 1, TPR, true); \
+        else                                      \
+            RL_SOFTMAX_ROWS_R(NV, TPR, false);    \
     } while (0)
     if (packs_ok && w_packs <= 64)
         RL_SOFTMAX_ROWS(1, 64);
@@ -349,6 +407,7 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
         RL_LAUNCH(ctx, (k_softmax_stream<T, MASK>), dim3(row_grid(rows)), block, in, out, r32,
                   w32, mp);
 #undef RL_SOFTMAX_ROWS
+#undef RL_SOFTMAX_ROWS_R
     return after_launch(ctx, name);
 }
 
@@ -357,13 +416,16 @@ rl_status launch_scale_mask(rl_context* ctx, const char* name, const T* in, T* o
                             uint64_t rows, uint64_t width, MaskParams mp) {
     if (rl_status st = activate(ctx)) return st;
     constexpr int N = 16 / sizeof(T);
-    const bool packs_ok = width % N == 0 && aligned_to(in, 16) && aligned_to(out, 16);
-    if (packs_ok)
-        RL_LAUNCH(ctx, (k_scale_mask<T, N>), dim3(row_grid(rows)), dim3(kThreads), in, out,
-                  uint32_t(rows), uint32_t(width), mp);
+    const bool packs_ok = aligned_to(in, 16) && aligned_to(out, 16);
+    if (packs_ok && width % N == 0)
+        RL_LAUNCH(ctx, (k_scale_mask<T, N, false>), dim3(row_grid(rows)), dim3(kThreads), in,
+                  out, uint32_t(rows), uint32_t(width), mp);
+    else if (packs_ok)
+        RL_LAUNCH(ctx, (k_scale_mask<T, N, true>), dim3(row_grid(rows)), dim3(kThreads), in,
+                  out, uint32_t(rows), uint32_t(width), mp);
     else
-        RL_LAUNCH(ctx, (k_scale_mask<T, 1>), dim3(row_grid(rows)), dim3(kThreads), in, out,
-                  uint32_t(rows), uint32_t(width), mp);
+        RL_LAUNCH(ctx, (k_scale_mask<T, 1, false>), dim3(row_grid(rows)), dim3(kThreads), in,
+                  out, uint32_t(rows), uint32_t(width), mp);
     return after_launch(ctx, name);
 }
 

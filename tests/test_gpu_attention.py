@@ -163,6 +163,9 @@ GQA_SHAPES = [  # batch, q_heads, kv_heads, q_len, kv_len, capacity, head_dim
     (1, 3, 1, 17, 200, 200, 96),
     (1, 8, 2, 300, 1000, 1024, 128),  # many key tiles and PV steps
     (1, 2, 1, 9, 70, 80, 48),        # row kernels
+    (1, 15, 5, 200, 1001, 1024, 64),  # odd key count: rows off the 16-byte grid, 8 key tiles
+    (2, 4, 2, 129, 259, 264, 128),    # batch 2, key count 3 mod 8, ragged query tiles
+    (1, 6, 3, 33, 130, 136, 32),      # key count 2 mod 8: a last tile of 2 keys
 ]
 
 
@@ -218,10 +221,11 @@ def test_gqa_pv_within_float64_bound(ctx, dtype, shape):
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
 def test_gqa_small_integers_match_the_oracle_bit_for_bit(ctx, dtype):
     """Small-integer operands make every sum exact: the library (matrix cores
-    or row kernels) and the oracle agree exactly."""
-    for hd in (64, 48):
-        q = (np.arange(1 * 6 * 40 * hd) % 7 - 3).reshape(1, 6, 40, hd).astype(dtype)
-        k = (np.arange(1 * 2 * 72 * hd) % 5 - 2).reshape(1, 2, 72, hd).astype(dtype)
+    or row kernels) and the oracle agree exactly -- also where the key count
+    puts the score rows off the 16-byte grid (every element in its place)."""
+    for hd, ql, kl in ((64, 40, 72), (48, 40, 72), (64, 130, 301), (128, 70, 1003), (32, 5, 9)):
+        q = (np.arange(1 * 6 * ql * hd) % 7 - 3).reshape(1, 6, ql, hd).astype(dtype)
+        k = (np.arange(1 * 2 * kl * hd) % 5 - 2).reshape(1, 2, kl, hd).astype(dtype)
         ctx.begin()
         s = ctx.gqa_qk(ctx.upload(q), ctx.upload(k))
         pv = ctx.gqa_pv(ctx.upload((o.gqa_qk(q, k) / 64).astype(dtype)), ctx.upload(k))

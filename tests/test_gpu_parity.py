@@ -321,14 +321,16 @@ def _logits(key, shape, dtype=np.float32):
 
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("rows,width", [(2, 3), (7, 33), (64, 2048), (9, 4096), (5, 5000),
-                                        (3, 9000), (2, 70000), (1, 1)])
+                                        (3, 9000), (2, 70000), (1, 1),
+                                        # widths off the pack grid: rows at every lead
+                                        (13, 4093), (6, 1001), (4, 9003), (9, 130)])
 def test_softmax(ctx, dtype, rows, width):
     x = _logits(("sm",), (rows, width), dtype)
     got = run(ctx, lambda: ctx.softmax(ctx.upload(x))).numpy()
     check_float(got, o.softmax(x), f"softmax {rows}x{width}")
 
 
-@pytest.mark.parametrize("width", [8, 3, 5000, 70000])
+@pytest.mark.parametrize("width", [8, 3, 5000, 70000, 1001])
 def test_softmax_special_rows(ctx, width):
     # all -inf: f32 NaN (no guard, softmax.metal:7-132), f16 zeros (:166-173);
     # a NaN score poisons its row; -inf entries get exact zeros; scores 85..110
@@ -352,7 +354,10 @@ def test_softmax_special_rows(ctx, width):
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("shape,start", [((9, 2048, 2048), 0), ((9, 1, 2048), 2047),
                                          ((1, 1, 3, 3), 0), ((2, 5, 40), 11),
-                                         ((3, 4, 6000), 100), ((1, 2, 70000), 3)])
+                                         ((3, 4, 6000), 100), ((1, 2, 70000), 3),
+                                         # key lengths off the pack grid
+                                         ((3, 7, 4093), 0), ((2, 9, 1001), 500),
+                                         ((4, 5, 35), 30), ((1, 13, 1003), 990)])
 def test_scale_mask_and_fused_softmax(ctx, dtype, shape, start):
     x = _logits(("att",), shape, dtype)
     scale = 1.0 / 8.0
