@@ -264,10 +264,22 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
                 const bool edge = lane % 2 == 0 ? (lead > 0 || lead + n < 8)
                                                 : (last > 0 && (lead + n) % 8 != 0);
                 if (edge) {
+                    // read whole where the chunk lies in the buffer (its other
+                    // elements masked off), element-wise past the buffer's end
                     const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + blk * BN;
+                    const uint64_t total = uint64_t(gridDim.x / p.q_tiles) * p.q_len * p.kv_len;
+                    const uint64_t chunk = uint64_t(src - probs) - lead + lo;  // first element
+                    if (chunk + 8 <= total) {
+                        const h8 w = __builtin_nontemporal_load(
+                            reinterpret_cast<const h8*>(probs + chunk));
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (lo + e >= lead && lo + e < lead + n) pr[9][e] = src[lo + e - lead];
+                        for (int e = 0; e < 8; ++e)
+                            pr[9][e] = (lo + e >= lead && lo + e < lead + n) ? w[e] : half_t(0.0f);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (lo + e >= lead && lo + e < lead + n) pr[9][e] = src[lo + e - lead];
+                    }
                 }
             }
             return;

@@ -153,14 +153,24 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
             // ragged row's first pack)
             const int x0 = int(p * N) - int(lead);
             if (RAGGED && p < n_packs && x0 < int(kept) && (x0 < 0 || x0 + N > int(kept))) {
+                // A pack shared with a neighbouring row (or holding the last
+                // kept key) is read whole -- its other elements lie in the
+                // buffer and are masked off here -- unless it runs past the
+                // buffer's end (the last row's last pack): then element-wise.
+                V raw = {};
+                if (e0 - lead + uint64_t(p + 1) * N <= uint64_t(rows) * width) {
+                    raw = load_stream(src + p);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < N; ++j)
+                        if (x0 + j >= 0 && x0 + j < int(width)) raw[j] = in[e0 + uint32_t(x0 + j)];
+                }
 #pragma unroll
                 for (int j = 0; j < N; ++j) {
                     const int x = x0 + j;
-                    float f = -INFINITY;
-                    if (x >= 0 && x < int(kept)) {
-                        const T raw = in[e0 + uint32_t(x)];
-                        f = MASK ? scaled_score(raw, mp.scale) : to_float(raw);
-                    }
+                    const float f = (x >= 0 && x < int(kept))
+                                        ? (MASK ? scaled_score(raw[j], mp.scale) : to_float(raw[j]))
+                                        : -INFINITY;
                     v[k][j] = f;
                     m = fmaxf(m, f);
                 }
@@ -325,13 +335,23 @@ __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ i
         const uint32_t kept = kept_keys(row, width, mp);
         for (uint32_t p = threadIdx.x; p < n_packs; p += kThreads) {
             if (RAGGED && (p * N < lead || p * N + N > lead + width)) {
-                // a pack shared with a neighbouring row: this row's elements only
+                // a pack shared with a neighbouring row: read whole where it
+                // lies in the buffer, this row's elements written one by one
+                V raw = {};
+                if (e0 - lead + uint64_t(p + 1) * N <= uint64_t(rows) * width) {
+                    raw = load_stream(src + p);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < N; ++j)
+                        if (p * N + j >= lead && p * N + j < lead + width)
+                            raw[j] = in[e0 + (p * N + j - lead)];
+                }
 #pragma unroll
                 for (int j = 0; j < N; ++j) {
                     const uint32_t pj = p * N + j;
                     if (pj < lead || pj >= lead + width) continue;
                     const uint32_t x = pj - lead;
-                    out[e0 + x] = x < kept ? from_float<T>(to_float(in[e0 + x]) * mp.scale)
+                    out[e0 + x] = x < kept ? from_float<T>(to_float(raw[j]) * mp.scale)
                                            : from_float<T>(-INFINITY);
                 }
                 continue;
@@ -382,21 +402,25 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
                       block, in, out, uint32_t(base), r32, w32, mp);                             \
         }                                                                                        \
     } while (0)
-#define RL_SOFTMAX_ROWS(NV, TPR)                  \
-    do {                                          \
-        if (ragged)                               \
-            RL_SOFTMAX_ROWS_R(NV + 1, TPR, true); \
-        else                                      \
-            RL_SOFTMAX_ROWS_R(NV, TPR, false);    \
+    // (NV, TPR) for aligned rows, (NVR, TPRR) with room for the extra pack
+    // for ragged ones: rows of 257..512 packs spread over more threads, as
+    // five packs per thread cost the f16 rows half their occupancy.
+#define RL_SOFTMAX_ROWS2(NV, TPR, NVR, TPRR)        \
+    do {                                            \
+        if (ragged)                                 \
+            RL_SOFTMAX_ROWS_R(NVR, TPRR, true);     \
+        else                                        \
+            RL_SOFTMAX_ROWS_R(NV, TPR, false);      \
     } while (0)
+#define RL_SOFTMAX_ROWS(NV, TPR) RL_SOFTMAX_ROWS2(NV, TPR, NV + 1, TPR)
     if (packs_ok && w_packs <= 64)
         RL_SOFTMAX_ROWS(1, 64);
     else if (packs_ok && w_packs <= 128)
         RL_SOFTMAX_ROWS(2, 64);
     else if (packs_ok && w_packs <= 256)
-        RL_SOFTMAX_ROWS(4, 64);
+        RL_SOFTMAX_ROWS2(4, 64, 3, 128);
     else if (packs_ok && w_packs <= 512)
-        RL_SOFTMAX_ROWS(4, 128);
+        RL_SOFTMAX_ROWS2(4, 128, 3, 256);
     else if (packs_ok && w_packs <= 1024)
         RL_SOFTMAX_ROWS(4, 256);
     else if (packs_ok && w_packs <= 2048)
@@ -407,6 +431,7 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
         RL_LAUNCH(ctx, (k_softmax_stream<T, MASK>), dim3(row_grid(rows)), block, in, out, r32,
                   w32, mp);
 #undef RL_SOFTMAX_ROWS
+#undef RL_SOFTMAX_ROWS2
 #undef RL_SOFTMAX_ROWS_R
     return after_launch(ctx, name);
 }
