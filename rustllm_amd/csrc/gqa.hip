@@ -47,11 +47,13 @@ __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
 
 // SHIFT: kv_len is not a multiple of 8, so a score row starts `lead`
 // elements past a 16-byte boundary (the output buffer itself is 16-byte
-// aligned).  The row's tile then sits `lead` columns to the right in LDS, so
-// that LDS chunk j (8 columns) is the j-th 16-byte chunk of memory from the
-// boundary before the row's first score: 17 chunks per row, the 15 inner
-// ones whole 16-byte stores, the two it shares with the neighbouring tiles
-// element by element (this tile's scores only).
+// aligned).  A tile then owns the 16-byte chunks of its rows that start at
+// keys kbase - lead .. kbase + 127 - lead: it also scores the (up to 7) keys
+// before kbase, with v_dot2 on the vector ALUs, and leaves its last `lead`
+// keys to the next tile, so every chunk is one whole store.  In LDS a row
+// sits `lead` columns to the right (LDS column y = key kbase - lead + y).
+// Only a row's first chunk (tile 0) and last chunk (the last tile) reach
+// past the row; those are stored element by element.
 template <int NT, bool SHIFT>
 __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ q,
                                                      const half_t* __restrict__ k,
@@ -62,7 +64,7 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     constexpr int KS = D + 8;    // LDS row stride (halves) of the key tile
     constexpr int ROW_CHUNKS = D / 8;
     __shared__ __align__(16) half_t tile[4][32 * TS];
-    __shared__ __align__(16) half_t ks[128 * KS];
+    __shared__ __align__(16) half_t ks[(128 + (SHIFT ? 8 : 0)) * KS];  // SHIFT: + 8 rows before
     const uint32_t wave = threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t col = lane % 32;
@@ -86,6 +88,18 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
         const uint32_t key = min(kbase + j, p.kv_len - 1);
         *reinterpret_cast<h8*>(ks + perm32(j) * KS + d0) =
             *reinterpret_cast<const h8*>(kh + uint64_t(key) * D + d0);
+    }
+    if constexpr (SHIFT) {
+        // key rows kbase - 8 .. kbase - 1 (tile 0 has none: rows 0.. then,
+        // whose scores are not used)
+        half_t* kpre = ks + 128 * KS;
+        for (uint32_t chunk = threadIdx.x; chunk < 8 * ROW_CHUNKS; chunk += 256) {
+            const uint32_t j = chunk / ROW_CHUNKS;
+            const uint32_t d0 = (chunk % ROW_CHUNKS) * 8;
+            const uint32_t key = kbase >= 8 ? kbase - 8 + j : min(j, p.kv_len - 1);
+            *reinterpret_cast<h8*>(kpre + j * KS + d0) =
+                *reinterpret_cast<const h8*>(kh + uint64_t(key) * D + d0);
+        }
     }
     const uint32_t qi = q0 + col;
     const bool q_valid = qi < p.q_len;
@@ -137,40 +151,76 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
             }
         }
     }
+    if constexpr (SHIFT) {
+        if (kbase > 0) {
+            // the scores of keys kbase - 8 + j of this lane's query: its half
+            // of the head (v_dot2, f32 sums), plus the other half's
+            const half_t* kpre = ks + 128 * KS + 8 * hs;
+            float ex[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float a = 0.0f;
+#pragma unroll
+                for (int c = 0; c < DC; ++c) {
+                    const h8 kk = *reinterpret_cast<const h8*>(kpre + j * KS + 16 * c);
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2)
+                        a = __builtin_amdgcn_fdot2(h2{qf[c][e], qf[c][e + 1]},
+                                                   h2{kk[e], kk[e + 1]}, a, false);
+                }
+                ex[j] = a + __shfl_xor(a, 32, 64);
+            }
+            // LDS columns 0 .. lead - 1: keys kbase - lead .. kbase - 1
+            if (hs == 0) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (j + my_lead >= 8) my[col * TS + (j + my_lead - 8)] = half_t(ex[j]);
+            }
+        }
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // rows of the tile to memory: 16 lanes per 256-byte row segment
     const uint32_t keys_here = min(128u, p.kv_len - kbase);
     if constexpr (SHIFT) {
-        // Chunk c of row r covers LDS columns 8c .. 8c + 7, the row's scores
-        // 8c - lead ..  Whole chunks: 32 rows x 17 slots over the lanes.
+        // Chunk c of row r: LDS columns 8c .. 8c + 7, the row's keys
+        // kbase - lead + 8c ..  The tile owns keys [own_lo, own_hi) of the row:
+        // from kbase - lead (0 in tile 0) to kbase + 128 - lead (kv_len in the
+        // last tile).  Whole chunks: 32 rows x 17 slots over the lanes.
+        const bool last_tile = kbase + 128 >= p.kv_len;
 #pragma unroll
         for (int i = 0; i < 9; ++i) {
             const uint32_t slot = i * 64 + lane;
             const uint32_t r = slot / 17, lo = 8 * (slot % 17);
             if (slot >= 32 * 17 || q0 + r >= p.q_len) continue;
             const uint32_t lead = lead_of(r);
-            if (lo < lead || lo + 8 > lead + keys_here) continue;  // not a whole chunk
+            // owned LDS columns [y_lo, y_hi)
+            const uint32_t y_lo = kbase == 0 ? lead : 0u;
+            const uint32_t y_hi = last_tile ? lead + keys_here : 128u;
+            if (lo < y_lo || lo + 8 > y_hi) continue;  // not a whole owned chunk
             const h8 w = *reinterpret_cast<const h8*>(my + r * TS + lo);
             const uint64_t first = (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase;
             __builtin_nontemporal_store(w, reinterpret_cast<h8*>(out + (first - lead + lo)));
         }
-        // The (at most) two chunks a row shares with its neighbours, one per
-        // lane: lane 2r + 0 the row's first chunk, 2r + 1 its last.
+        // A row's first chunk (tile 0, lead > 0) and last chunk (last tile)
+        // reach past the row: lane 2r + 0 stores the one, 2r + 1 the other,
+        // element by element.
         const uint32_t r = lane / 2;
         if (q0 + r < p.q_len) {
             const uint32_t lead = lead_of(r);
-            const uint32_t last = (lead + keys_here - 1) / 8;
-            const bool first_edge = lead > 0 || lead + keys_here < 8;
-            const bool last_edge = last > 0 && (lead + keys_here) % 8 != 0;
+            const uint32_t y_lo = kbase == 0 ? lead : 0u;
+            const uint32_t y_hi = last_tile ? lead + keys_here : 128u;
+            const uint32_t last = (y_hi - 1) / 8;
+            const bool first_edge = y_lo > 0 || y_hi < 8;
+            const bool last_edge = last > 0 && y_hi % 8 != 0;
             if (lane % 2 == 0 ? first_edge : last_edge) {
                 const uint32_t lo = lane % 2 == 0 ? 0u : 8 * last;
                 const uint64_t first = (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    if (lo + e >= lead && lo + e < lead + keys_here)
-                        out[first + (lo + e - lead)] = my[r * TS + lo + e];
+                    if (lo + e >= y_lo && lo + e < y_hi)
+                        out[first - lead + (lo + e)] = my[r * TS + lo + e];
             }
         }
         return;
