@@ -323,7 +323,8 @@ def _logits(key, shape, dtype=np.float32):
 @pytest.mark.parametrize("rows,width", [(2, 3), (7, 33), (64, 2048), (9, 4096), (5, 5000),
                                         (3, 9000), (2, 70000), (1, 1),
                                         # widths off the pack grid: rows at every lead
-                                        (13, 4093), (6, 1001), (4, 9003), (9, 130)])
+                                        (13, 4093), (6, 1001), (4, 9003), (9, 130),
+                                        (5, 2041)])
 def test_softmax(ctx, dtype, rows, width):
     x = _logits(("sm",), (rows, width), dtype)
     got = run(ctx, lambda: ctx.softmax(ctx.upload(x))).numpy()
@@ -357,7 +358,8 @@ def test_softmax_special_rows(ctx, width):
                                          ((3, 4, 6000), 100), ((1, 2, 70000), 3),
                                          # key lengths off the pack grid
                                          ((3, 7, 4093), 0), ((2, 9, 1001), 500),
-                                         ((4, 5, 35), 30), ((1, 13, 1003), 990)])
+                                         ((4, 5, 35), 30), ((1, 13, 1003), 990),
+                                         ((2, 6, 2041), 7)])
 def test_scale_mask_and_fused_softmax(ctx, dtype, shape, start):
     x = _logits(("att",), shape, dtype)
     scale = 1.0 / 8.0
