@@ -38,6 +38,29 @@ struct GqaParams {
     uint32_t k_groups;        // f32 QK^T workgroups per query tile
 };
 
+// 16-byte store / load of f16 scores, streamed past the caches (STREAM,
+// non-temporal) or plain.  Measured on [15, 4096, kv_len] scores: QK^T rows
+// that are whole 128-byte lines stream (4096 keys: 99 us, plain 176), rows
+// on the 16-byte grid but not the line grid store plainly so the L2 merges
+// the lines they share (1000 keys: 36 us, streamed 52), ragged rows stream
+// (224 us, plain 259); PV reads ragged rows plainly (142 us, streamed 165).
+// A template parameter, not a flag: the compiler merges the two stores of
+// a run-time choice into one plain store.
+template <bool STREAM>
+__device__ inline void put_scores(h8* dst, h8 w) {
+    if constexpr (STREAM)
+        __builtin_nontemporal_store(w, dst);
+    else
+        *dst = w;
+}
+template <bool STREAM>
+__device__ inline h8 get_scores(const h8* src) {
+    if constexpr (STREAM)
+        return __builtin_nontemporal_load(src);
+    else
+        return *src;
+}
+
 __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
     const uint32_t kv_heads = p.q_heads / p.group;
     return (bh / p.q_heads) * kv_heads + (bh % p.q_heads) / p.group;
@@ -54,7 +77,7 @@ __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
 // sits `lead` columns to the right (LDS column y = key kbase - lead + y).
 // Only a row's first chunk (tile 0) and last chunk (the last tile) reach
 // past the row; those are stored element by element.
-template <int NT, bool SHIFT>
+template <int NT, bool SHIFT, bool STREAM>
 __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ q,
                                                      const half_t* __restrict__ k,
                                                      half_t* __restrict__ out, GqaParams p) {
@@ -201,7 +224,7 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
             if (lo < y_lo || lo + 8 > y_hi) continue;  // not a whole owned chunk
             const h8 w = *reinterpret_cast<const h8*>(my + r * TS + lo);
             const uint64_t first = (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase;
-            __builtin_nontemporal_store(w, reinterpret_cast<h8*>(out + (first - lead + lo)));
+            put_scores<STREAM>(reinterpret_cast<h8*>(out + (first - lead + lo)), w);
         }
         // A row's first chunk (tile 0, lead > 0) and last chunk (last tile)
         // reach past the row: lane 2r + 0 stores the one, 2r + 1 the other,
@@ -234,7 +257,7 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
         const h8 w = *reinterpret_cast<const h8*>(my + r * TS + c8);
         half_t* dst = out + (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase + c8;
         if (vec_store && c8 + 8 <= keys_here) {
-            __builtin_nontemporal_store(w, reinterpret_cast<h8*>(dst));  // streamed out once
+            put_scores<STREAM>(reinterpret_cast<h8*>(dst), w);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e)
@@ -251,7 +274,7 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
 // shared with neighbouring steps or rows element by element, one per lane)
 // and kept on that chunk grid in LDS; the products read the row's columns
 // from its lead on, 2 bytes at a time.
-template <int NT, bool SHIFT>
+template <int NT, bool SHIFT, bool STREAM>
 __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ probs,
                                                      const half_t* __restrict__ v,
                                                      half_t* __restrict__ out, GqaParams p) {
@@ -301,7 +324,7 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
                 if (lo < lead || lo + 8 > lead + n) continue;
                 // the row's first probability of the step
                 const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + blk * BN;
-                pr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(src + lo - lead));
+                pr[i] = get_scores<STREAM>(reinterpret_cast<const h8*>(src + lo - lead));
             }
             // the chunks shared with the neighbours, one per lane (as in QK^T)
             const uint32_t r = lane / 2;
@@ -320,8 +343,7 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
                     const uint64_t total = uint64_t(gridDim.x / p.q_tiles) * p.q_len * p.kv_len;
                     const uint64_t chunk = uint64_t(src - probs) - lead + lo;  // first element
                     if (chunk + 8 <= total) {
-                        const h8 w = __builtin_nontemporal_load(
-                            reinterpret_cast<const h8*>(probs + chunk));
+                        const h8 w = get_scores<STREAM>(reinterpret_cast<const h8*>(probs + chunk));
 #pragma unroll
                         for (int e = 0; e < 8; ++e)
                             pr[9][e] = (lo + e >= lead && lo + e < lead + n) ? w[e] : half_t(0.0f);
@@ -340,7 +362,7 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
             const uint32_t kb = blk * BN + (lane % 16) * 8;
             const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + kb;
             if (q0 + r < p.q_len && vec_p && kb + 8 <= p.kv_len) {
-                pr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(src));
+                pr[i] = get_scores<STREAM>(reinterpret_cast<const h8*>(src));
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
@@ -835,12 +857,15 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
             const bool shift = s.kv_len % 8 != 0;
+            const bool lines = s.kv_len % 64 == 0;  // score rows are whole 128-byte lines
 #define RL_QK(NT)                                                                      \
     do {                                                                               \
         if (shift)                                                                     \
-            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, true>), g, b, qd, kd, od, p);            \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, true, true>), g, b, qd, kd, od, p);      \
+        else if (lines)                                                                \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, false, true>), g, b, qd, kd, od, p);     \
         else                                                                           \
-            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, false>), g, b, qd, kd, od, p);           \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, false, false>), g, b, qd, kd, od, p);    \
     } while (0)
             switch (s.head_dim / 32) {
                 case 1: RL_QK(1); break;
@@ -925,9 +950,9 @@ rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, co
 #define RL_PV(NT)                                                                      \
     do {                                                                               \
         if (shift)                                                                     \
-            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true>), g, b, pd, vd, od, p);            \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true, false>), g, b, pd, vd, od, p);     \
         else                                                                           \
-            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false>), g, b, pd, vd, od, p);           \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false, true>), g, b, pd, vd, od, p);     \
     } while (0)
             switch (s.head_dim / 32) {
                 case 1: RL_PV(1); break;
