@@ -43,7 +43,8 @@ struct GqaParams {
 // that are whole 128-byte lines stream (4096 keys: 99 us, plain 176), rows
 // on the 16-byte grid but not the line grid store plainly so the L2 merges
 // the lines they share (1000 keys: 36 us, streamed 52), ragged rows stream
-// (224 us, plain 259); PV reads ragged rows plainly (142 us, streamed 165).
+// (224 us, plain 259); PV reads ragged rows and rows off the line grid
+// plainly (142 us, streamed 165; 1000 keys 24.6 us, streamed 27.1).
 // A template parameter, not a flag: the compiler merges the two stores of
 // a run-time choice into one plain store.
 template <bool STREAM>
@@ -947,12 +948,15 @@ rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, co
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA PV grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
             const bool shift = s.kv_len % 8 != 0;
+            const bool lines = s.kv_len % 64 == 0;  // probability rows are whole 128-byte lines
 #define RL_PV(NT)                                                                      \
     do {                                                                               \
         if (shift)                                                                     \
             RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true, false>), g, b, pd, vd, od, p);     \
-        else                                                                           \
+        else if (lines)                                                                \
             RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false, true>), g, b, pd, vd, od, p);     \
+        else                                                                           \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false, false>), g, b, pd, vd, od, p);    \
     } while (0)
             switch (s.head_dim / 32) {
                 case 1: RL_PV(1); break;
