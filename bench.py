@@ -622,6 +622,29 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
                  "fused_speedup": round(chain_us / us, 2),
                  "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None})
     del sc, pr
+    # the same unfused calls at an odd length (4093 tokens): score rows that
+    # start off the 16-byte grid
+    rl_tok = tok - 3
+    q_r = ctx.upload(np.ascontiguousarray(q[:, :, :rl_tok]))
+    n_r = qh * rl_tok * rl_tok
+    unmasked_r = qh * (rl_tok * (rl_tok + 1) // 2)
+    sc_r = [ctx.empty((1, qh, rl_tok, rl_tok), F16) for _ in range(2)]
+    pr_r = [ctx.empty((1, qh, rl_tok, rl_tok), F16) for _ in range(2)]
+    out_r = ctx.empty((1, qh, rl_tok, hd), F16)
+    kv_r = kvh * rl_tok * hd
+    for name, fns, nbytes in (
+            ("layer.4 ragged gqa_qk_f16 (4093 keys)",
+             [lambda i=i: ctx.gqa_qk(q_r, s0[1], rl_tok, sc_r[i]) for i in range(2)],
+             (qh * rl_tok * hd + kv_r + n_r) * 2),
+            ("layer.4 ragged attention_softmax_f16 (4093 keys)",
+             [lambda i=i: ctx.attention_softmax(sc_r[i], 0.125, 0, pr_r[i]) for i in range(2)],
+             (unmasked_r + n_r) * 2),
+            ("layer.4 ragged gqa_pv_f16 (4093 keys)",
+             [lambda i=i: ctx.gqa_pv(pr_r[i], s0[2], out_r) for i in range(2)],
+             (n_r + kv_r + qh * rl_tok * hd) * 2)):
+        shape = [1, qh, rl_tok, rl_tok if "pv" not in name else hd]
+        rows.append(op_row(name, "f16", shape, nbytes, kernel_times_us(ctx, fns, reps)))
+    del sc_r, pr_r, out_r, q_r
     # decode: one new token of 15 heads over a 4096-row KV cache (one launch:
     # key splits whose last workgroup per KV head merges them), kernel-stamped
     # like every other line
