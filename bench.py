@@ -274,7 +274,7 @@ def time_step_streams(ctx, aux, ops, sets, steps, warmup):
     return ms / steps
 
 
-def kernel_times_us(ctx, launches, reps):
+def kernel_times_us(ctx, launches, reps, batch=True):
     """Device time of `reps` launches (cycling through `launches`, one kernel
     each), every one bracketed by events that the kernel itself stamps at its
     start and end -- the same per-dispatch duration a kernel trace reports.
@@ -293,19 +293,24 @@ def kernel_times_us(ctx, launches, reps):
     us = [ctx.elapsed_ms(start, stop) * 1e3 for start, stop in evs]
     for e in [e for pair in evs for e in pair]:
         ctx.destroy_event(e)
-    return us, (graph_batch_us(ctx, launches) if GRAPH_BATCH else None)
+    return us, (graph_batch_us(ctx, launches) if GRAPH_BATCH and batch else None)
 
 
-# --graph-batch: also time each op as 32 back-to-back launches recorded in a
-# graph.  Off by default: under `rocprofv3 --kernel-trace` the replay of
-# these short-lived graphs crashed the traced process inside hipGraphLaunch
-# (a host read of a device-memory address in the tracer's launch hook),
-# while the long-lived step graphs trace cleanly.
-GRAPH_BATCH = False
+# Sustained figures: each op also timed as back-to-back launches recorded in
+# one graph and replayed.  On by default; `--no-graph-batch` leaves them out
+# (the traced profile command passes it: under `rocprofv3 --kernel-trace` a
+# run that created, replayed and destroyed one such graph per op ended in a
+# SIGSEGV inside hipGraphLaunch).  The graphs are kept until the process
+# exits rather than destroyed after their op.
+GRAPH_BATCH = True
+_LIVE_GRAPHS = []
 
 
-def graph_batch_us(ctx, launches, per_graph=32, replays=8):
-    """us per launch of `per_graph` back-to-back launches replayed as a graph."""
+def graph_batch_us(ctx, launches, min_per_graph=32, replays=8):
+    """us per launch of back-to-back launches replayed as a graph: one launch
+    on each of the op's buffer sets (>= 1 GiB in total, so a replay streams
+    from HBM, not from the 256 MB Infinity Cache), at least `min_per_graph`."""
+    per_graph = max(min_per_graph, len(launches))
     ctx.capture_begin()
     failed = False
     try:
@@ -315,12 +320,11 @@ def graph_batch_us(ctx, launches, per_graph=32, replays=8):
         failed = True
     finally:
         graph = ctx.capture_end()
+    _LIVE_GRAPHS.append(graph)
     if failed:
-        ctx.graph_destroy(graph)
         return None
     ms = time_graphs(ctx, [graph], per_graph, replays)
     ctx.finish()
-    ctx.graph_destroy(graph)
     return ms * 1e3
 
 
@@ -654,7 +658,8 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
     rows.append(op_row("decode attention_f16 (1 token, 4096-row cache)", "f16", [1, qh, 1, hd],
                        dec_bytes,
                        kernel_times_us(ctx, [lambda: ctx.attention(qd, s0[1], s0[2], 0.125,
-                                                                   tok - 1, None, od)], reps)))
+                                                                   tok - 1, None, od)], reps,
+                                       batch=False)))
     return rows
 
 
@@ -710,13 +715,17 @@ def fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
 
 def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20):
     """The whole non-GEMM chain of one SmolLM2-360M layer in order -- RMSNorm,
-    RoPE of Q and K (from the projections' [1, H, S, D] views), repeat_kv of K
-    and V, causal scale/mask + softmax, SwiGLU, residual add: 8 launches
-    recorded as one graph per buffer set and replayed; bytes are the sum of
-    the launches' algorithmic bytes."""
+    RoPE of Q and K (read straight from the [1, H, S, D] views of the
+    normalised rows that the Q and K projections would produce), repeat_kv of
+    the rotated K and of V, causal scale/mask + softmax, SwiGLU, residual add:
+    8 launches recorded as one graph per buffer set and replayed.  Where a
+    GEMM sits between two stages (V, the scores, gate/up, the down
+    projection) the stage reads a seeded stand-in.  Bytes are the sum of the
+    launches' algorithmic bytes.  After timing, every output of the first
+    set is compared with the oracle on that set's inputs."""
     rng_key = ("chain",)
-    qdims, qstrides = [1, qh, tok, hd], [tok * qh * hd, hd, qh * hd, 1]
-    kdims, kstrides = [1, kvh, tok, hd], [tok * kvh * hd, hd, kvh * hd, 1]
+    qdims, qstrides = [1, qh, tok, hd], [tok * hid, hd, hid, 1]
+    kdims, kstrides = [1, kvh, tok, hd], [tok * hid, hd, hid, 1]
     unmasked = qh * (tok * (tok + 1) // 2)
     nbytes = (tok * hid * 4 + hid * 2                                   # RMSNorm
               + 2 * (qh + kvh) * tok * hd * 2 + 2 * 2 * tok * (hd // 2) * 4  # RoPE Q, K
@@ -727,19 +736,18 @@ def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
 
     scores = np.random.default_rng(7).standard_normal((qh, tok, tok), dtype=np.float32)
     scores = scores.astype(F16)
+    host = {}
 
     def make(i):
-        b = {"x": ctx.upload(synth.normal(synth.seed_for(*rng_key, "x", i), (tok, hid), 0, 1, F16)),
-             "q": ctx.upload(synth.normal(synth.seed_for(*rng_key, "q", i), (1, tok, qh, hd), 0, 1,
-                                          F16)),
-             "k": ctx.upload(synth.normal(synth.seed_for(*rng_key, "k", i), (1, tok, kvh, hd), 0,
-                                          1, F16)),
-             "v": ctx.upload(synth.normal(synth.seed_for(*rng_key, "v", i), (1, kvh, tok, hd), 0,
-                                          1, F16)),
-             "s": ctx.upload(scores),
-             "g": ctx.upload(synth.normal(synth.seed_for(*rng_key, "g", i), (tok, ffn), 0, 1, F16)),
-             "u": ctx.upload(synth.normal(synth.seed_for(*rng_key, "u", i), (tok, ffn), 0, 1, F16)),
-             "r": ctx.upload(synth.normal(synth.seed_for(*rng_key, "r", i), (tok, hid), 0, 1, F16))}
+        h = {"x": synth.normal(synth.seed_for(*rng_key, "x", i), (tok, hid), 0, 1, F16),
+             "v": synth.normal(synth.seed_for(*rng_key, "v", i), (1, kvh, tok, hd), 0, 1, F16),
+             "g": synth.normal(synth.seed_for(*rng_key, "g", i), (tok, ffn), 0, 1, F16),
+             "u": synth.normal(synth.seed_for(*rng_key, "u", i), (tok, ffn), 0, 1, F16),
+             "r": synth.normal(synth.seed_for(*rng_key, "r", i), (tok, hid), 0, 1, F16)}
+        if i == 0:
+            host.update(h)
+        b = {k: ctx.upload(v) for k, v in h.items()}
+        b["s"] = ctx.upload(scores)
         b.update({"xn": ctx.empty((tok, hid), F16), "qr": ctx.empty(qdims, F16),
                   "kr": ctx.empty(kdims, F16), "kq": ctx.empty(qdims, F16),
                   "vq": ctx.empty(qdims, F16), "p": ctx.empty((qh, tok, tok), F16),
@@ -748,8 +756,8 @@ def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
 
     def chain(b):
         ctx.rmsnorm(b["x"], wn, 1e-5, b["xn"])
-        ctx.rope_strided(b["q"], qdims, qstrides, dc, ds, 0, b["qr"])
-        ctx.rope_strided(b["k"], kdims, kstrides, dc, ds, 0, b["kr"])
+        ctx.rope_strided(b["xn"], qdims, qstrides, dc, ds, 0, b["qr"])
+        ctx.rope_strided(b["xn"], kdims, kstrides, dc, ds, 0, b["kr"])
         ctx.repeat_kv(b["kr"], qh // kvh, b["kq"])
         ctx.repeat_kv(b["v"], qh // kvh, b["vq"])
         ctx.attention_softmax(b["s"], 0.125, 0, b["p"])
@@ -766,11 +774,65 @@ def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
     gbs = nbytes / (us * 1e-6) / 1e9
     log(f"  {'layer chain (8 launches, one graph)':34s} {us:9.2f} us {gbs:8.1f} GB/s "
         f"({100 * gbs / PEAK_GBS:5.1f}%)")
+    bad = check_chain(bufs[0], host, scores, wn.numpy(), dc.numpy(), ds.numpy(), qh, kvh, hd, tok)
+    if bad:
+        log(f"  layer chain: MISMATCH against the oracle in {bad}")
+    else:
+        log("  layer chain: every stage matches the oracle")
     return {"op": "layer chain (8 launches, one graph)", "dtype": "f16",
             "shape": [tok, hid], "bytes": nbytes, "us": round(us, 3), "us_min": None,
             "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
             "us_graph_batch": round(us, 3), "GB/s_graph_batch": round(gbs, 1),
-            "pct_peak_graph_batch": round(100 * gbs / PEAK_GBS, 1)}
+            "pct_peak_graph_batch": round(100 * gbs / PEAK_GBS, 1),
+            "outputs_match_oracle": not bad, "mismatched_stages": bad}
+
+
+def check_chain(b, host, scores, wn, cos, sin, qh, kvh, hd, tok) -> list[str]:
+    """The layer chain's outputs against the oracle on the same inputs:
+    bit-exact RoPE, repeat_kv and add; f16 RMSNorm, softmax and SwiGLU
+    within 2 ulp.  Returns the stages that differ."""
+    from oracle import oracle as o
+
+    o.set_threads(cpu_threads())
+    bad = []
+
+    def ulp(got, ref):
+        gi = got.view(np.int16).astype(np.int32)
+        ri = ref.view(np.int16).astype(np.int32)
+        gi = np.where(gi < 0, -(gi & 0x7FFF), gi)
+        ri = np.where(ri < 0, -(ri & 0x7FFF), ri)
+        return int(np.max(np.abs(gi - ri)))
+
+    xn = b["xn"].numpy()
+    if ulp(xn, o.rmsnorm(host["x"], wn, 1e-5)) > 2:
+        bad.append("rmsnorm")
+    hid = xn.shape[1]
+    q_view = np.ascontiguousarray(xn.reshape(1, tok, qh, hd).transpose(0, 2, 1, 3))
+    k_view = np.ascontiguousarray(xn[:, :kvh * hd].reshape(1, tok, kvh, hd).transpose(0, 2, 1, 3))
+    kr = b["kr"].numpy()
+    if not np.array_equal(b["qr"].numpy().view(np.uint16),
+                          o.rope(q_view, cos, sin, 0).view(np.uint16)):
+        bad.append("rope_Q")
+    if not np.array_equal(kr.view(np.uint16), o.rope(k_view, cos, sin, 0).view(np.uint16)):
+        bad.append("rope_K")
+    if not np.array_equal(b["kq"].numpy().view(np.uint16),
+                          o.repeat_kv(kr, qh // kvh).view(np.uint16)):
+        bad.append("repeat_kv_K")
+    if not np.array_equal(b["vq"].numpy().view(np.uint16),
+                          o.repeat_kv(host["v"], qh // kvh).view(np.uint16)):
+        bad.append("repeat_kv_V")
+    p = b["p"].numpy()
+    ref = o.attention_softmax(scores, 0.125, 0)
+    if ulp(p, ref) > 2:
+        bad.append("attention_softmax")
+    del p, ref
+    if ulp(b["h"].numpy(), o.swiglu(host["g"], host["u"])) > 2:
+        bad.append("swiglu")
+    if not np.array_equal(b["o"].numpy().view(np.uint16),
+                          o.add(xn, host["r"]).view(np.uint16)):
+        bad.append("residual_add")
+    assert hid == qh * hd
+    return bad
 
 
 def _rope_table(head_dim, max_seq, theta=10000.0):
@@ -964,14 +1026,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
     ap.add_argument("--quick", action="store_true", help="fewer extra shapes")
-    ap.add_argument("--graph-batch", action="store_true",
-                    help="also time every op as back-to-back launches replayed from a graph")
+    ap.add_argument("--no-graph-batch", action="store_true",
+                    help="leave out the sustained (back-to-back, graph-replayed) time of each op")
     ap.add_argument("--probe", action="store_true",
                     help="no timing: run each batch op 3 times on one buffer set, then a "
                          "256 MiB device-to-device copy 3 times (for hardware-counter runs)")
     args = ap.parse_args()
     global GRAPH_BATCH
-    GRAPH_BATCH = args.graph_batch
+    GRAPH_BATCH = not args.no_graph_batch
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every op runs on one MI355X and shards across GPUs "
@@ -1034,6 +1096,11 @@ def main():
             log(f"MISMATCH against the oracle: {bad}")
         log(f"cpu: {cpu_gbs:.2f} GB/s over {steps} steps")
         threads = cpu_threads()
+        cpu["host_cores_available"] = threads
+        if threads == 1:
+            cpu["all_cores"] = None
+            cpu["note"] = ("this process could use one core of the host (its affinity set / "
+                           "OMP_NUM_THREADS), so no multi-core figure was taken")
         if threads > 1:
             secs = args.cpu_seconds / 2
             log(f"cpu baseline: oracle, {threads} threads, ~{secs:.0f} s of whole steps")
@@ -1057,7 +1124,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32/f16",
         "data": "synthetic",
         "config": {"workload": "elementwise+broadcast batch [4096,1536], f32 and "
                                "f16 storage (add, mul, silu, swiglu, bias add, casts, "

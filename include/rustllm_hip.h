@@ -84,6 +84,36 @@ typedef struct rl_profile {
 /* ---------------------------------------------------------------- errors */
 /* Message of the calling thread's last failure ("" if none). */
 const char* rl_last_error_message(void);
+
+/* The integer fields of the TinyError variants that carry data
+ * (src/error.rs:7-24), for the calling thread's last failure.  `code` is
+ * that failure's status (RL_OK if none) and selects which fields are set;
+ * the others are zero.
+ *  - RL_ERR_SHAPE_MISMATCH: TinyError::ShapeMismatch { left, right }
+ *    (raised by the buffer ops as in src/tensor/elementwise.rs:119-124 and
+ *    src/ops/rmsnorm.rs:232-237): left_rank/left and right_rank/right.
+ *  - RL_ERR_POSITION_OUT_OF_RANGE: TinyError::PositionOutOfRange
+ *    { start_pos, seq_len, max_seq_len } (src/ops/kv_cache_write.rs:101-110).
+ *  - RL_ERR_INVALID_TOKEN_ID: TinyError::InvalidTokenId { token_id,
+ *    vocab_size } (src/ops/embedding.rs:129-136).
+ * Shapes of more than RL_ERROR_MAX_RANK dims keep their first
+ * RL_ERROR_MAX_RANK dims; the rank fields hold the full rank. */
+#define RL_ERROR_MAX_RANK 16
+typedef struct rl_error_payload {
+    rl_status code;
+    uint32_t left_rank;
+    uint32_t right_rank;
+    uint32_t token_id;
+    uint64_t left[RL_ERROR_MAX_RANK];
+    uint64_t right[RL_ERROR_MAX_RANK];
+    uint64_t start_pos;
+    uint64_t seq_len;
+    uint64_t max_seq_len;
+    uint64_t vocab_size;
+} rl_error_payload;
+/* Copies the calling thread's last failure payload to *out and returns its
+ * code (RL_OK if the thread has no failure recorded, or out is NULL). */
+rl_status rl_last_error_payload(rl_error_payload* out);
 /* Library version string. */
 const char* rl_version(void);
 

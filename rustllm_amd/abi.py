@@ -46,12 +46,30 @@ class RlProfile(ctypes.Structure):
         "buffer_allocations", "allocated_bytes")]
 
 
-class RustLLMError(RuntimeError):
-    """A non-zero rl_status, named after the TinyError variant it maps to."""
+ERROR_MAX_RANK = 16
 
-    def __init__(self, status: int, message: str):
+
+class RlErrorPayload(ctypes.Structure):
+    """rl_error_payload: the fields of the TinyError variants that carry data."""
+    _fields_ = [("code", ctypes.c_int32), ("left_rank", ctypes.c_uint32),
+                ("right_rank", ctypes.c_uint32), ("token_id", ctypes.c_uint32),
+                ("left", ctypes.c_uint64 * ERROR_MAX_RANK),
+                ("right", ctypes.c_uint64 * ERROR_MAX_RANK),
+                ("start_pos", ctypes.c_uint64), ("seq_len", ctypes.c_uint64),
+                ("max_seq_len", ctypes.c_uint64), ("vocab_size", ctypes.c_uint64)]
+
+
+class RustLLMError(RuntimeError):
+    """A non-zero rl_status, named after the TinyError variant it maps to.
+
+    `fields` holds the variant's data for ShapeMismatch ({left, right}),
+    PositionOutOfRange ({start_pos, seq_len, max_seq_len}) and InvalidTokenId
+    ({token_id, vocab_size}); it is empty for the other variants."""
+
+    def __init__(self, status: int, message: str, fields: dict | None = None):
         self.status = status
         self.kind = STATUS_NAMES.get(status, f"status{status}")
+        self.fields = fields or {}
         super().__init__(f"{self.kind}: {message}")
 
 
@@ -66,6 +84,7 @@ _U64P = ctypes.POINTER(ctypes.c_uint64)
 # name -> (argtypes, restype); every symbol include/rustllm_hip.h declares.
 SIGNATURES: dict[str, tuple[list, object]] = {
     "rl_last_error_message": ([], ctypes.c_char_p),
+    "rl_last_error_payload": ([ctypes.POINTER(RlErrorPayload)], _I32),
     "rl_version": ([], ctypes.c_char_p),
     "rl_context_create": ([_I32, ctypes.POINTER(_P)], _I32),
     "rl_context_create_on_stream": ([_I32, _P, ctypes.POINTER(_P)], _I32),
@@ -170,9 +189,26 @@ def last_error() -> str:
     return load().rl_last_error_message().decode()
 
 
+def last_error_fields() -> tuple[int, dict]:
+    """The thread's last failure code and its variant's fields (see RustLLMError)."""
+    p = RlErrorPayload()
+    code = int(load().rl_last_error_payload(ctypes.byref(p)))
+    fields: dict = {}
+    if code == 3:
+        fields = {"left": [int(v) for v in p.left[:min(p.left_rank, ERROR_MAX_RANK)]],
+                  "right": [int(v) for v in p.right[:min(p.right_rank, ERROR_MAX_RANK)]]}
+    elif code == 7:
+        fields = {"start_pos": int(p.start_pos), "seq_len": int(p.seq_len),
+                  "max_seq_len": int(p.max_seq_len)}
+    elif code == 10:
+        fields = {"token_id": int(p.token_id), "vocab_size": int(p.vocab_size)}
+    return code, fields
+
+
 def check(status: int) -> None:
     if status != RL_OK:
-        raise RustLLMError(status, last_error())
+        code, fields = last_error_fields()
+        raise RustLLMError(status, last_error(), fields if code == status else None)
 
 
 def device_count() -> int:

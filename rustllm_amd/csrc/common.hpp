@@ -23,6 +23,14 @@ namespace rl {
 rl_status fail(rl_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 
+// Failures whose TinyError variant carries data: the message is the
+// reference's Display text (src/error.rs:56-95) and the fields are kept for
+// rl_last_error_payload.
+rl_status fail_shape_mismatch(const uint64_t* left, uint32_t left_rank, const uint64_t* right,
+                              uint32_t right_rank);
+rl_status fail_position_out_of_range(uint64_t start_pos, uint64_t seq_len, uint64_t max_seq_len);
+rl_status fail_invalid_token_id(uint32_t token_id, uint64_t vocab_size);
+
 // ------------------------------------------------------------------ pool
 
 // Stream-ordered caching allocator.  All work of a context runs in order on

@@ -48,8 +48,14 @@ struct SiluF16Op {
         return x * rcp_fast(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896340736f));
     }
 };
-struct SwigluF16Op {  // silu.metal:44-45: (g / (1 + exp(-g))) * u, rounded once
-    __device__ float operator()(float g, float u) const { return silu_fast(g) * u; }
+// silu.metal:44-45: (g / (1 + exp(-g))) * u, rounded once to f16.  As in
+// SiluF16Op the sigmoid is not rescaled: where it flushes to zero
+// (g < -87.3) the exact |silu(g) u| is below 2^-100 for every finite half u,
+// which rounds to a zero of the same sign in f16.
+struct SwigluF16Op {
+    __device__ float operator()(float g, float u) const {
+        return (g * rcp_fast(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896340736f))) * u;
+    }
 };
 struct SwigluF32Op {  // nn/swiglu.rs:15-37 F32 branch: silu_f32(g) then mul_f32
     __device__ float operator()(float g, float u) const { return SiluF32Op()(g, 0.0f) * u; }
@@ -429,9 +435,10 @@ static rl_status validate_broadcast(const rl_buffer* x, const rl_buffer* bias, u
         return fail(RL_ERR_INVALID_SHAPE, "input has %llu elements, expected %llu x %llu",
                     (unsigned long long)x->len, (unsigned long long)rows,
                     (unsigned long long)cols);
-    if (bias->len != cols)
-        return fail(RL_ERR_SHAPE_MISMATCH, "bias has %llu elements, expected %llu",
-                    (unsigned long long)bias->len, (unsigned long long)cols);
+    if (bias->len != cols) {  // [rows, cols] + [bias len]: the shapes the add would see
+        const uint64_t left[2] = {rows, cols}, right[1] = {bias->len};
+        return fail_shape_mismatch(left, 2, right, 1);
+    }
     return check_output(out, x->len, es, "add");
 }
 

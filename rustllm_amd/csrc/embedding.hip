@@ -111,8 +111,7 @@ rl_status embedding_entry(rl_context* ctx, const char* name, const rl_buffer* we
                     (unsigned long long)vocab_size, (unsigned long long)hidden_size);
     for (uint64_t t = 0; t < n_tokens; ++t)
         if (uint64_t(token_ids[t]) >= vocab_size)
-            return fail(RL_ERR_INVALID_TOKEN_ID, "invalid token id %u: vocabulary size is %llu",
-                        token_ids[t], (unsigned long long)vocab_size);
+            return fail_invalid_token_id(token_ids[t], vocab_size);
     if (hidden_size == 0 || n_tokens > UINT64_MAX / hidden_size)
         return fail(RL_ERR_INVALID_SHAPE, "embedding dimension exceeds u32");
     const uint64_t out_elements = n_tokens * hidden_size;

@@ -128,10 +128,7 @@ rl_status validate_kv_write(const char* name, const rl_buffer* cache, uint64_t m
                          src->len != heads * seq * head_dim))
         return fail(RL_ERR_INVALID_SHAPE, "invalid KV cache write shape");
     if (start > UINT64_MAX - seq || start + seq > max_seq)
-        return fail(RL_ERR_POSITION_OUT_OF_RANGE,
-                    "position range [%llu, %llu) exceeds max sequence length %llu",
-                    (unsigned long long)start, (unsigned long long)(start + seq),
-                    (unsigned long long)max_seq);
+        return fail_position_out_of_range(start, seq, max_seq);
     const uint64_t numel = heads * seq * head_dim;
     if (start > UINT32_MAX || seq > UINT32_MAX || max_seq > UINT32_MAX ||
         head_dim > UINT32_MAX || numel > UINT32_MAX)

@@ -260,8 +260,10 @@ rl_status launch_rmsnorm(rl_context* ctx, const char* name, const T* x, const T*
     return after_launch(ctx, name);
 }
 
-// src/ops/rmsnorm.rs:38-116 / :142-206 in order, plus eps (checked by the
-// Tensor-level ops::rmsnorm at :226-230) and the row-count limits of the grid.
+// src/ops/rmsnorm.rs:38-116 / :142-206 in order, plus the byte lengths and
+// the row-count limit of the grid.  Any eps is accepted here, as by the
+// reference's buffer-level rmsnorm_f32/_f16; the Tensor-level ops::rmsnorm
+// (:226-230) checks that it is finite and positive.
 rl_status validate(const rl_buffer* input, const rl_buffer* weight, uint64_t rows,
                    uint64_t hidden, float eps, uint64_t es) {
     if (rl_status st = check_buffer(input, "input")) return st;
@@ -281,9 +283,6 @@ rl_status validate(const rl_buffer* input, const rl_buffer* weight, uint64_t row
     if (hidden > UINT32_MAX)
         return fail(RL_ERR_INVALID_SHAPE, "RMSNorm hidden size exceeds u32");
     if (rows > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "RMSNorm row count exceeds u32");
-    if (!(eps > 0.0f) || eps == INFINITY)
-        return fail(RL_ERR_INVALID_SHAPE, "RMSNorm epsilon must be positive and finite, got %g",
-                    double(eps));
     return RL_OK;
 }
 
@@ -307,9 +306,10 @@ rl_status add_rmsnorm_entry(rl_context* ctx, const char* name, const rl_buffer* 
                             const rl_buffer* norm_out) {
     if (rl_status st = check_buffer(residual, "residual")) return st;
     if (rl_status st = check_buffer(x, "input")) return st;
-    if (x->len != residual->len)  // Tensor::add: shapes must match (elementwise.rs:249-254)
-        return fail(RL_ERR_SHAPE_MISMATCH, "add requires equal buffer lengths, got %llu and %llu",
-                    (unsigned long long)x->len, (unsigned long long)residual->len);
+    if (x->len != residual->len) {  // Tensor::add's check (elementwise.rs:119-124) on lengths
+        const uint64_t left[1] = {x->len}, right[1] = {residual->len};
+        return fail_shape_mismatch(left, 1, right, 1);
+    }
     if (residual->byte_len < residual->len * sizeof(T))
         return fail(RL_ERR_INVALID_SHAPE, "residual buffer does not hold %zu-byte elements",
                     sizeof(T));

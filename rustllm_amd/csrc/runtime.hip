@@ -9,6 +9,7 @@
 namespace rl {
 
 static thread_local std::string g_last_error;
+static thread_local rl_error_payload g_last_payload{};
 
 rl_status fail(rl_status code, const char* fmt, ...) {
     char buf[1024];
@@ -17,10 +18,57 @@ rl_status fail(rl_status code, const char* fmt, ...) {
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
     g_last_error = buf;
+    g_last_payload = rl_error_payload{};
+    g_last_payload.code = code;
     return code;
 }
 
-void clear_error() { g_last_error.clear(); }
+void clear_error() {
+    g_last_error.clear();
+    g_last_payload = rl_error_payload{};
+}
+
+static std::string dims_text(const uint64_t* dims, uint32_t rank) {
+    std::string s = "[";
+    for (uint32_t i = 0; i < rank; ++i) {
+        if (i) s += ", ";
+        s += std::to_string(dims[i]);
+    }
+    return s + "]";
+}
+
+rl_status fail_shape_mismatch(const uint64_t* left, uint32_t left_rank, const uint64_t* right,
+                              uint32_t right_rank) {
+    fail(RL_ERR_SHAPE_MISMATCH, "left=%s, right=%s", dims_text(left, left_rank).c_str(),
+         dims_text(right, right_rank).c_str());
+    g_last_payload.left_rank = left_rank;
+    g_last_payload.right_rank = right_rank;
+    for (uint32_t i = 0; i < left_rank && i < RL_ERROR_MAX_RANK; ++i)
+        g_last_payload.left[i] = left[i];
+    for (uint32_t i = 0; i < right_rank && i < RL_ERROR_MAX_RANK; ++i)
+        g_last_payload.right[i] = right[i];
+    return RL_ERR_SHAPE_MISMATCH;
+}
+
+rl_status fail_position_out_of_range(uint64_t start_pos, uint64_t seq_len, uint64_t max_seq_len) {
+    // The end is printed as the reference does (start_pos + seq_len); an
+    // overflowing sum prints its wrapped value there as well.
+    fail(RL_ERR_POSITION_OUT_OF_RANGE, "position range [%llu, %llu) exceeds max sequence length %llu",
+         (unsigned long long)start_pos, (unsigned long long)(start_pos + seq_len),
+         (unsigned long long)max_seq_len);
+    g_last_payload.start_pos = start_pos;
+    g_last_payload.seq_len = seq_len;
+    g_last_payload.max_seq_len = max_seq_len;
+    return RL_ERR_POSITION_OUT_OF_RANGE;
+}
+
+rl_status fail_invalid_token_id(uint32_t token_id, uint64_t vocab_size) {
+    fail(RL_ERR_INVALID_TOKEN_ID, "invalid token id %u: vocabulary size is %llu", token_id,
+         (unsigned long long)vocab_size);
+    g_last_payload.token_id = token_id;
+    g_last_payload.vocab_size = vocab_size;
+    return RL_ERR_INVALID_TOKEN_ID;
+}
 
 static rl_status hip_fail(hipError_t err, const char* what) {
     return fail(RL_ERR_DEVICE, "%s: %s", what, hipGetErrorString(err));
@@ -178,6 +226,12 @@ struct rl_event {
 extern "C" {
 
 const char* rl_last_error_message(void) { return g_last_error.c_str(); }
+
+rl_status rl_last_error_payload(rl_error_payload* out) {
+    if (out == nullptr) return RL_OK;
+    *out = g_last_payload;
+    return g_last_payload.code;
+}
 
 const char* rl_version(void) { return "rustllm-hip 0.1.0 (gfx950)"; }
 

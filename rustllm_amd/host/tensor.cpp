@@ -2,6 +2,7 @@
 // Every function cites the reference item it restates.
 #include "tensor.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <sstream>
@@ -22,7 +23,21 @@ TinyError::TinyError(Kind kind, const std::string& message)
 
 TinyError TinyError::from_status(rl_status status) {
     Kind kind = (status >= 1 && status <= 10) ? Kind(status - 1) : Kind::Device;
-    return TinyError(kind, rl_last_error_message());
+    TinyError e(kind, rl_last_error_message());
+    rl_error_payload p{};
+    if (rl_last_error_payload(&p) != status) return e;
+    if (kind == Kind::ShapeMismatch) {
+        e.left.assign(p.left, p.left + std::min<uint32_t>(p.left_rank, RL_ERROR_MAX_RANK));
+        e.right.assign(p.right, p.right + std::min<uint32_t>(p.right_rank, RL_ERROR_MAX_RANK));
+    } else if (kind == Kind::PositionOutOfRange) {
+        e.start_pos = p.start_pos;
+        e.seq_len = p.seq_len;
+        e.max_seq_len = p.max_seq_len;
+    } else if (kind == Kind::InvalidTokenId) {
+        e.token_id = p.token_id;
+        e.vocab_size = p.vocab_size;
+    }
+    return e;
 }
 
 static void check(rl_status status) {
@@ -37,9 +52,34 @@ static std::string dims_str(const std::vector<size_t>& dims) {
     return os.str();
 }
 
+TinyError TinyError::shape_mismatch(std::vector<size_t> left, std::vector<size_t> right) {
+    TinyError e(Kind::ShapeMismatch, "left=" + dims_str(left) + ", right=" + dims_str(right));
+    e.left = std::move(left);
+    e.right = std::move(right);
+    return e;
+}
+
+TinyError TinyError::position_out_of_range(size_t start_pos, size_t seq_len, size_t max_seq_len) {
+    TinyError e(Kind::PositionOutOfRange,
+                "position range [" + std::to_string(start_pos) + ", " +
+                    std::to_string(start_pos + seq_len) + ") exceeds max sequence length " +
+                    std::to_string(max_seq_len));
+    e.start_pos = start_pos;
+    e.seq_len = seq_len;
+    e.max_seq_len = max_seq_len;
+    return e;
+}
+
+TinyError TinyError::invalid_token_id(uint32_t token_id, size_t vocab_size) {
+    TinyError e(Kind::InvalidTokenId, "invalid token id " + std::to_string(token_id) +
+                                          ": vocabulary size is " + std::to_string(vocab_size));
+    e.token_id = token_id;
+    e.vocab_size = vocab_size;
+    return e;
+}
+
 static TinyError shape_mismatch(const std::vector<size_t>& left, const std::vector<size_t>& right) {
-    return TinyError(TinyError::Kind::ShapeMismatch,
-                     "left=" + dims_str(left) + ", right=" + dims_str(right));
+    return TinyError::shape_mismatch(left, right);
 }
 
 // ------------------------------------------------------------- dtype/shape
@@ -1138,10 +1178,7 @@ static void kv_cache_write_tensor_encode(const Context& ctx, const Tensor& cache
         throw TinyError(TinyError::Kind::InvalidShape, "invalid KV cache write shape");
     const size_t seq = source.dim(2), max_seq = cache.dim(2);
     if (start + seq < start || start + seq > max_seq)
-        throw TinyError(TinyError::Kind::PositionOutOfRange,
-                        "position range [" + std::to_string(start) + ", " +
-                            std::to_string(start + seq) + ") exceeds max sequence length " +
-                            std::to_string(max_seq));
+        throw TinyError::position_out_of_range(start, seq, max_seq);
     if (!source.is_contiguous())
         throw TinyError(TinyError::Kind::NonContiguousTensor,
                         "batched KV cache write requires a contiguous source");
@@ -1273,10 +1310,7 @@ Tensor RotaryEmbedding::forward(const Context& ctx, const Tensor& input, size_t 
     if (start_pos + seq_len < start_pos)
         throw TinyError(TinyError::Kind::InvalidShape, "RoPE position overflow");
     if (start_pos + seq_len > max_seq_len_)
-        throw TinyError(TinyError::Kind::PositionOutOfRange,
-                        "position range [" + std::to_string(start_pos) + ", " +
-                            std::to_string(start_pos + seq_len) + ") exceeds max sequence length " +
-                            std::to_string(max_seq_len_));
+        throw TinyError::position_out_of_range(start_pos, seq_len, max_seq_len_);
     return ops::rope(ctx, input, cos_, sin_, start_pos);
 }
 
@@ -1381,10 +1415,7 @@ void LayerKvCache::validate_append(const Tensor& key, const Tensor& value) const
                             std::to_string(key.dim(1)) + " heads");
     const size_t seq = key.dim(2);
     if (len_ + seq < len_ || len_ + seq > max_seq_len_)
-        throw TinyError(TinyError::Kind::PositionOutOfRange,
-                        "position range [" + std::to_string(len_) + ", " +
-                            std::to_string(len_ + seq) + ") exceeds max sequence length " +
-                            std::to_string(max_seq_len_));
+        throw TinyError::position_out_of_range(len_, seq, max_seq_len_);
 }
 
 // One tensor of append_encode (kv_cache.rs:123-137): contiguous_encode then

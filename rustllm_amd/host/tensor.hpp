@@ -45,7 +45,22 @@ class TinyError : public std::runtime_error {
     };
     TinyError(Kind kind, const std::string& message);
     Kind kind() const { return kind_; }
+    // The library's failure as the variant it names, with the payload of
+    // ShapeMismatch / PositionOutOfRange / InvalidTokenId (rl_last_error_payload).
     static TinyError from_status(rl_status status);
+    // The variants that carry data (src/error.rs:7-24), with the reference's
+    // Display text as the message.
+    static TinyError shape_mismatch(std::vector<size_t> left, std::vector<size_t> right);
+    static TinyError position_out_of_range(size_t start_pos, size_t seq_len, size_t max_seq_len);
+    static TinyError invalid_token_id(uint32_t token_id, size_t vocab_size);
+
+    // ShapeMismatch { left, right }
+    std::vector<size_t> left, right;
+    // PositionOutOfRange { start_pos, seq_len, max_seq_len }
+    size_t start_pos = 0, seq_len = 0, max_seq_len = 0;
+    // InvalidTokenId { token_id, vocab_size }
+    uint32_t token_id = 0;
+    size_t vocab_size = 0;
 
    private:
     Kind kind_;

@@ -49,6 +49,16 @@ struct Registrar {
     } while (0)
 
 template <typename Fn>
+TinyError catch_error(Fn fn) {
+    try {
+        fn();
+    } catch (const TinyError& e) {
+        return e;
+    }
+    throw Failure{"expected a TinyError"};
+}
+
+template <typename Fn>
 TinyError::Kind expect_error(Fn fn) {
     try {
         fn();
@@ -289,8 +299,10 @@ TEST(rmsnorm_tensor_validation_matches_reference_errors) {
     CHECK(expect_error([&] { ops::rmsnorm(context, x, w, 0.0f); }) ==
           TinyError::Kind::InvalidShape);
     auto w3 = Tensor::from_f32_slice(context, {1, 2, 3}, {3});
-    CHECK(expect_error([&] { ops::rmsnorm(context, x, w3, 1e-5f); }) ==
-          TinyError::Kind::ShapeMismatch);
+    const TinyError mismatch = catch_error([&] { ops::rmsnorm(context, x, w3, 1e-5f); });
+    CHECK(mismatch.kind() == TinyError::Kind::ShapeMismatch);
+    CHECK((mismatch.left == std::vector<size_t>{2, 4}));  // ops/rmsnorm.rs:232-237
+    CHECK((mismatch.right == std::vector<size_t>{3}));
     // F16 RMSNorm rejects a strided view (ops/rmsnorm.rs:240-246)
     auto x16t = x.to_dtype(context, DType::F16).transpose(0, 1);
     auto w16_2 = Tensor::from_f32_slice(context, {1, 1}, {2}).to_dtype(context, DType::F16);
@@ -629,8 +641,11 @@ TEST(embedding_gathers_rows_and_rejects_bad_ids) {
     CHECK((out16.as_f16_slice() ==
            std::vector<uint16_t>{to_f16(w)[3], to_f16(w)[4], to_f16(w)[5], to_f16(w)[9],
                                  to_f16(w)[10], to_f16(w)[11]}));
-    CHECK(expect_error([&] { ops::embedding_f32(context, weight, {1, 5}, vocab, hidden); }) ==
-          TinyError::Kind::InvalidTokenId);
+    // raised by the library (ops/embedding.rs:129-136), payload carried across the ABI
+    const TinyError bad_id =
+        catch_error([&] { ops::embedding_f32(context, weight, {1, 7}, vocab, hidden); });
+    CHECK(bad_id.kind() == TinyError::Kind::InvalidTokenId);
+    CHECK(bad_id.token_id == 7 && bad_id.vocab_size == vocab);
     CHECK(expect_error([&] { ops::embedding_f32(context, weight, {}, vocab, hidden); }) ==
           TinyError::Kind::InvalidShape);
     CHECK(expect_error([&] { ops::embedding_f32(context, weight, {1}, vocab, hidden + 1); }) ==

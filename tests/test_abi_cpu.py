@@ -118,18 +118,30 @@ def test_rmsnorm_validation_order():
     assert st == SHAPE and "RMSNorm input has 9 elements, expected 8" in msg
     st, msg = call("rl_rmsnorm_f32", buf(8, 4), buf(5, 4), 2, 4, ctypes.c_float(1e-5), buf(8, 4))
     assert st == SHAPE and "RMSNorm weight has 5 elements, expected 4" in msg
-    for eps in (0.0, -1.0, float("inf"), float("nan")):
-        st, msg = call("rl_rmsnorm_f16", buf(8, 2), buf(4, 2), 2, 4, ctypes.c_float(eps),
-                       buf(8, 2))
-        assert st == SHAPE and "epsilon" in msg
     assert call("rl_rmsnorm_f16", buf(8, 2), buf(4, 2), 2, 4, ctypes.c_float(1e-5),
                 buf(8, 2))[0] == DEVICE
 
 
+@pytest.mark.parametrize("name,es", [("rl_rmsnorm_f32", 4), ("rl_rmsnorm_f16", 2),
+                                     ("rl_add_rmsnorm_f32", 4), ("rl_add_rmsnorm_f16", 2)])
+@pytest.mark.parametrize("eps", [0.0, -1.0, float("inf"), float("nan")])
+def test_rmsnorm_buffer_level_accepts_any_epsilon(name, es, eps):
+    # src/ops/rmsnorm.rs:38-116 checks no epsilon; only the Tensor-level
+    # ops::rmsnorm (:226-230) and RmsNorm::new (nn/rmsnorm.rs:29-33) do.
+    if "add" in name:
+        args = (buf(8, es), buf(8, es), buf(4, es), 2, 4, ctypes.c_float(eps), buf(8, es),
+                buf(8, es))
+    else:
+        args = (buf(8, es), buf(4, es), 2, 4, ctypes.c_float(eps), buf(8, es))
+    st, msg = call(name, *args)
+    assert st == DEVICE and "no HIP context" in msg
+
+
 def test_add_rmsnorm_validation():
-    st, _ = call("rl_add_rmsnorm_f32", buf(8, 4), buf(6, 4), buf(4, 4), 2, 4,
-                 ctypes.c_float(1e-5), buf(8, 4), buf(8, 4))
-    assert st == MISMATCH
+    st, msg = call("rl_add_rmsnorm_f32", buf(8, 4), buf(6, 4), buf(4, 4), 2, 4,
+                   ctypes.c_float(1e-5), buf(8, 4), buf(8, 4))
+    assert st == MISMATCH and msg == "left=[8], right=[6]"
+    assert abi.last_error_fields() == (MISMATCH, {"left": [8], "right": [6]})
     st, _ = call("rl_add_rmsnorm_f32", buf(8, 4), buf(8, 4), buf(4, 4), 2, 4,
                  ctypes.c_float(1e-5), buf(8, 4), buf(8, 4))
     assert st == DEVICE
@@ -221,8 +233,9 @@ def test_repeat_kv_validation():
 
 
 def test_broadcast_validation():
-    st, _ = call("rl_add_broadcast_f32", buf(12, 4), buf(5, 4), 3, 4, buf(12, 4))
-    assert st == MISMATCH
+    st, msg = call("rl_add_broadcast_f32", buf(12, 4), buf(5, 4), 3, 4, buf(12, 4))
+    assert st == MISMATCH and msg == "left=[3, 4], right=[5]"
+    assert abi.last_error_fields() == (MISMATCH, {"left": [3, 4], "right": [5]})
     assert call("rl_add_broadcast_f32", buf(12, 4), buf(4, 4), 3, 4, buf(12, 4))[0] == DEVICE
 
 
@@ -278,7 +291,16 @@ def test_kv_cache_write_validation():
     assert st == SHAPE and "greater than zero" in msg
     st, msg = call(f, cache, 2, 8, 4, buf(16, 2), 2, 7)
     assert st == POS and "position range [7, 9) exceeds max sequence length 8" in msg
+    # TinyError::PositionOutOfRange { start_pos, seq_len, max_seq_len }
+    # (src/ops/kv_cache_write.rs:101-110) crosses the ABI as integers
+    assert abi.last_error_fields() == (POS, {"start_pos": 7, "seq_len": 2, "max_seq_len": 8})
+    with pytest.raises(abi.RustLLMError) as err:
+        abi.check(st)
+    assert err.value.kind == "PositionOutOfRange"
+    assert err.value.fields == {"start_pos": 7, "seq_len": 2, "max_seq_len": 8}
     assert call(f, cache, 2, 8, 4, buf(16, 2), 2, 6)[0] == DEVICE
+    # a later failure without a payload replaces it
+    assert abi.last_error_fields() == (DEVICE, {})
 
 
 def test_kv_cache_write_strided_validation():
@@ -336,6 +358,11 @@ def test_embedding_validation():
     bad = (ctypes.c_uint32 * 3)(0, 10, 2)
     st, msg = call(f, buf(40, 4), 10, 4, bad, 3, buf(12, 4))
     assert st == TOKEN and "invalid token id 10: vocabulary size is 10" in msg
+    # TinyError::InvalidTokenId { token_id, vocab_size } (src/ops/embedding.rs:129-136)
+    assert abi.last_error_fields() == (TOKEN, {"token_id": 10, "vocab_size": 10})
+    big = (ctypes.c_uint32 * 2)(1, 0xFFFFFFFF)
+    assert call(f, buf(40, 4), 10, 4, big, 2, buf(8, 4))[0] == TOKEN
+    assert abi.last_error_fields() == (TOKEN, {"token_id": 0xFFFFFFFF, "vocab_size": 10})
     st, msg = call(f, buf(40, 4), 10, 4, ids, 3, buf(11, 4))
     assert st == SHAPE and "output buffer" in msg
     assert call(f, buf(40, 4), 10, 4, ids, 3, buf(12, 4))[0] == DEVICE

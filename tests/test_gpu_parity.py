@@ -77,6 +77,25 @@ def test_silu_swiglu(ctx, dtype, n):
     check_float(run(ctx, lambda: ctx.swiglu(dg, du)).numpy(), o.swiglu(g, u), f"swiglu n={n}")
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("op,shape", [("swiglu", (4096, 2560)), ("silu", (4096, 2560)),
+                                      ("add", (4096, 960)), ("mul", (4096, 960))])
+def test_smollm_layer_shapes(ctx, dtype, op, shape):
+    """The SmolLM2-360M layer's element-wise shapes at 4096 tokens: SwiGLU on
+    the [4096, 2560] FFN activations, the residual add on [4096, 960]."""
+    a = norm(("layer", op, "a"), shape, dtype)
+    b = norm(("layer", op, "b"), shape, dtype)
+    da, db = ctx.upload(a), ctx.upload(b)
+    if op in ("add", "mul"):
+        got = run(ctx, lambda: getattr(ctx, op)(da, db)).numpy()
+        assert_bitexact(got, getattr(o, op)(a, b), f"{op} {shape}")
+    elif op == "silu":
+        check_float(run(ctx, lambda: ctx.silu(da)).numpy(), o.silu(a), f"silu {shape}")
+    else:
+        check_float(run(ctx, lambda: ctx.swiglu(da, db)).numpy(), o.swiglu(a, b),
+                    f"swiglu {shape}")
+
+
 def test_silu_extremes(ctx):
     x = np.array([-1e30, -100, -88.7, -20, -1, -1e-30, -0.0, 0.0, 1e-30, 1, 20, 88.7, 100, 1e30,
                   np.inf, -np.inf], dtype=np.float32)
