@@ -437,6 +437,25 @@ rl_status rl_attention_f16(rl_context* ctx, const rl_buffer* q, const rl_buffer*
                            uint64_t kv_capacity, float scale, uint64_t query_start_pos,
                            const rl_buffer* out);
 
+/* No counterpart in the reference.  rl_attention_f16 for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): same arguments, checks and results, but
+ * the decode path (few query rows per KV head, >= 512 visible keys) keeps
+ * its per-split partials and hand-off counters in a file-scope device array
+ * of 8 MiB (16 KiB of counters, the rest partials) that each GPU holds from
+ * the library's load until the process ends, instead of a pool block and
+ * the context's counters; the other paths allocate nothing anyway.  A decode
+ * shape needing more -- batch*q_heads*q_len * ceil(keys/256) * (head_dim+2)
+ * floats above 8 MiB - 16 KiB, or more than 4096 batch*kv_heads counters --
+ * is RL_ERR_INVALID_SHAPE.  Every call on one GPU shares that array: calls
+ * that overlap on one GPU (other streams, other threads) race.  Allowed
+ * while recording a graph. */
+rl_status rl_attention_f16_noalloc(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
+                                   const rl_buffer* v, uint64_t batch, uint64_t q_heads,
+                                   uint64_t kv_heads, uint64_t q_len, uint64_t kv_len,
+                                   uint64_t head_dim, uint64_t kv_capacity, float scale,
+                                   uint64_t query_start_pos, const rl_buffer* out);
+
 /* Tensor::gqa_qk_matmul_encode (src/tensor/gqa_matmul.rs:23-61, kernels
  * gqa_qk_f32/f16, kernels/gqa_matmul.metal:7-322): scores [batch, q_heads,
  * q_len, kv_len] = Q K^T without repeating the KV heads; query head h reads

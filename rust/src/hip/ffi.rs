@@ -551,6 +551,22 @@ extern "C" {
         query_start_pos: u64,
         out: *const rl_buffer,
     ) -> rl_status;
+    pub fn rl_attention_f16_noalloc(
+        ctx: *mut rl_context,
+        q: *const rl_buffer,
+        k: *const rl_buffer,
+        v: *const rl_buffer,
+        batch: u64,
+        q_heads: u64,
+        kv_heads: u64,
+        q_len: u64,
+        kv_len: u64,
+        head_dim: u64,
+        kv_capacity: u64,
+        scale: f32,
+        query_start_pos: u64,
+        out: *const rl_buffer,
+    ) -> rl_status;
     pub fn rl_gqa_qk_matmul_f32(
         ctx: *mut rl_context,
         q: *const rl_buffer,

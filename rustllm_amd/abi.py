@@ -160,6 +160,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                          _I32),
     "rl_attention_f32": ([_P, _BUF, _BUF, _BUF] + [_U64] * 7 + [_F, _U64, _BUF], _I32),
     "rl_attention_f16": ([_P, _BUF, _BUF, _BUF] + [_U64] * 7 + [_F, _U64, _BUF], _I32),
+    "rl_attention_f16_noalloc": ([_P, _BUF, _BUF, _BUF] + [_U64] * 7 + [_F, _U64, _BUF], _I32),
     "rl_gqa_qk_matmul_f32": ([_P, _BUF, _BUF] + [_U64] * 7 + [_BUF], _I32),
     "rl_gqa_qk_matmul_f16": ([_P, _BUF, _BUF] + [_U64] * 7 + [_BUF], _I32),
     "rl_gqa_pv_matmul_f32": ([_P, _BUF, _BUF] + [_U64] * 7 + [_BUF], _I32),
@@ -504,6 +505,18 @@ class Context:
         kv_len = cap if kv_len is None else kv_len
         out = out or self.empty(q.shape, q.dtype)
         self._call(f"rl_attention_{self._sfx(q)}", q, k, v, b, qh, kvh, ql, kv_len, hd, cap,
+                   ctypes.c_float(scale), start, out)
+        return out
+
+    def attention_noalloc(self, q, k, v, scale: float, start: int, kv_len=None, out=None):
+        """rl_attention_f16_noalloc: as attention() (f16), the decode path's
+        partials and counters in the library's static scratch (the caller
+        still passes the output)."""
+        b, qh, ql, hd = q.shape
+        kvh, cap = k.shape[1], k.shape[2]
+        kv_len = cap if kv_len is None else kv_len
+        out = out or self.empty(q.shape, q.dtype)
+        self._call("rl_attention_f16_noalloc", q, k, v, b, qh, kvh, ql, kv_len, hd, cap,
                    ctypes.c_float(scale), start, out)
         return out
 

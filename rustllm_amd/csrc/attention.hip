@@ -39,6 +39,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 namespace rl {
@@ -1289,6 +1290,62 @@ bool use_flash(const AttnShape& s, const void* q, const void* k, const void* v, 
     }
 }
 
+// ---------------------------------------------- allocation-free decode
+
+// The scratch of rl_attention_f16_noalloc: the decode path's hand-off
+// counters (the first kScratchTicketBytes) and its per-split partials (the
+// rest), in one file-scope device array instead of the context's counters
+// and a pool block.  Each GPU holds its own copy from the library's load
+// until the process ends.  The counters are zero at load, the set-up below
+// clears them once more, and every launch leaves them zero (the merging
+// workgroup puts its counter back); the partials need no clearing (a
+// launch writes every slot it reads).  All calls on one GPU share the
+// array, so calls that overlap on one GPU (other streams, other threads)
+// race; calls on one stream are ordered.
+constexpr uint64_t kScratchBytes = uint64_t(8) << 20;
+constexpr uint64_t kScratchTicketBytes = uint64_t(16) << 10;
+constexpr uint64_t kScratchTickets = kScratchTicketBytes / sizeof(uint32_t);
+constexpr uint64_t kScratchPartialBytes = kScratchBytes - kScratchTicketBytes;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ __launch_bounds__(256) void k_zero_u32(uint32_t* __restrict__ p, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// The device address of `scratch` on each device, looked up once per device
+// with that device current (the array's name is only a host-side stand-in).
+constexpr int kMaxScratchDevices = 64;
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxScratchDevices];
+
+rl_status scratch_on_device(rl_context* ctx, void** out) {
+    *out = nullptr;
+    if (ctx->device < 0 || ctx->device >= kMaxScratchDevices)
+        return fail(RL_ERR_DEVICE, "device %d has no scratch slot", ctx->device);
+    ScratchSlot& slot = g_scratch[ctx->device];
+    std::call_once(slot.once, [&] {
+        void* ptr = nullptr;
+        hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err == hipSuccess) {
+            hipLaunchKernelGGL(k_zero_u32, dim3(unsigned(kScratchTickets / 256)), dim3(256), 0,
+                               ctx->stream, static_cast<uint32_t*>(ptr),
+                               uint32_t(kScratchTickets));
+            err = hipGetLastError();
+        }
+        slot.err = err;
+        slot.ptr = err == hipSuccess ? ptr : nullptr;
+    });
+    if (slot.err != hipSuccess)
+        return fail(RL_ERR_DEVICE, "scratch address: %s", hipGetErrorString(slot.err));
+    *out = slot.ptr;
+    return RL_OK;
+}
+
 // The decode hand-off counters: at least n of them, all zero.  Growing
 // waits for the stream (a launch in flight may hold the old array).
 rl_status ensure_tickets(rl_context* ctx, uint64_t n) {
@@ -1311,16 +1368,40 @@ rl_status ensure_tickets(rl_context* ctx, uint64_t n) {
     return RL_OK;
 }
 
+// Where the decode path keeps its partials and hand-off counters: a pool
+// block and the context's counters, or the file-scope scratch.
+enum class DecodeScratch { kPool, kStatic };
+
 template <typename T>
 rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
                           const rl_buffer* k, const rl_buffer* v, const AttnShape& s,
-                          float scale, uint64_t start, const rl_buffer* out) {
+                          float scale, uint64_t start, const rl_buffer* out,
+                          DecodeScratch mode = DecodeScratch::kPool) {
     if (rl_status st = validate_attention(q, k, v, s, scale, start, sizeof(T))) return st;
     if (rl_status st = check_output(out, q->len, sizeof(T), "attention")) return st;
     const bool flash = use_flash<T>(s, q->data, k->data, v->data, out->data);
     if (!flash && s.head_dim > 512)
         return fail(RL_ERR_INVALID_SHAPE, "attention head size %llu exceeds 512",
                     (unsigned long long)s.head_dim);
+    // Few rows per KV head (decode): split the keys over many workgroups.
+    const uint64_t heads = s.batch * s.q_heads;
+    const uint64_t rows = heads * s.q_len;
+    const uint64_t R = s.q_len * (s.q_heads / s.kv_heads);
+    const uint64_t dpl = ceil_div(s.head_dim, 64);
+    const uint64_t rm = R <= 4 ? 4 : R <= 8 ? 8 : R <= 16 ? 16 : 32;
+    const uint64_t needed = std::min<uint64_t>(s.kv_len, start + s.q_len);  // keys any row sees
+    const uint64_t splits = ceil_div(needed, kSplitKeys);
+    const bool split_shape = R <= 32 && s.head_dim <= 256 && rm * dpl <= 32 && needed >= 512 &&
+                             splits <= kMaxSplits;
+    const uint64_t part_bytes = rows * splits * (s.head_dim + 2) * sizeof(float);
+    if (mode == DecodeScratch::kStatic && split_shape &&
+        (part_bytes > kScratchPartialBytes || s.batch * s.kv_heads > kScratchTickets))
+        return fail(RL_ERR_INVALID_SHAPE,
+                    "decode attention needs %llu bytes of partials and %llu counters; the "
+                    "allocation-free entry holds %llu bytes and %llu counters",
+                    (unsigned long long)part_bytes, (unsigned long long)(s.batch * s.kv_heads),
+                    (unsigned long long)kScratchPartialBytes,
+                    (unsigned long long)kScratchTickets);
     if (rl_status st = require_context(ctx)) return st;
     if (rl_status st = activate(ctx)) return st;
 
@@ -1338,28 +1419,27 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
     const T* kd = static_cast<const T*>(k->data);
     const T* vd = static_cast<const T*>(v->data);
     T* od = static_cast<T*>(out->data);
-    const uint64_t heads = s.batch * s.q_heads;
 
-    const uint64_t rows = heads * s.q_len;
-    // Few rows per KV head (decode): split the keys over many workgroups.  Not while
-    // recording a graph: the partials live in a pool block that is released
-    // (and may be reused) once the launches are enqueued.
-    const uint64_t R = s.q_len * (s.q_heads / s.kv_heads);
-    const uint64_t dpl = ceil_div(s.head_dim, 64);
-    const uint64_t rm = R <= 4 ? 4 : R <= 8 ? 8 : R <= 16 ? 16 : 32;
-    const uint64_t needed = std::min<uint64_t>(s.kv_len, start + s.q_len);  // keys any row sees
-    const uint64_t splits = ceil_div(needed, kSplitKeys);
-    if (!ctx->capturing && R <= 32 && s.head_dim <= 256 && rm * dpl <= 32 && needed >= 512 &&
-        splits <= kMaxSplits) {
+    // The pooled partials are not used while recording a graph: the block is
+    // released (and may be reused) once the launch is enqueued.  The static
+    // scratch has no such lifetime.
+    if (split_shape && (mode == DecodeScratch::kStatic || !ctx->capturing)) {
         const bool vec_rows = s.head_dim % (16 / sizeof(T)) == 0 && aligned_to(kd, 16) &&
                               aligned_to(vd, 16);
-        const uint64_t part_bytes = rows * splits * (s.head_dim + 2) * sizeof(float);
-        if (rl_status st = ensure_tickets(ctx, s.batch * s.kv_heads)) return st;
         void* part = nullptr;
-        if (rl_status st = ctx->pool.allocate(part_bytes, &part)) return st;
+        uint32_t* tk = nullptr;
+        if (mode == DecodeScratch::kStatic) {
+            void* base = nullptr;
+            if (rl_status st = scratch_on_device(ctx, &base)) return st;
+            tk = static_cast<uint32_t*>(base);
+            part = static_cast<unsigned char*>(base) + kScratchTicketBytes;
+        } else {
+            if (rl_status st = ensure_tickets(ctx, s.batch * s.kv_heads)) return st;
+            if (rl_status st = ctx->pool.allocate(part_bytes, &part)) return st;
+            tk = ctx->tickets;
+        }
         const dim3 gs(static_cast<unsigned>(s.batch * s.kv_heads * splits)), bs(64 * kSplitWaves);
         float* pf = static_cast<float*>(part);
-        uint32_t* tk = ctx->tickets;
         const uint32_t sp = uint32_t(splits);
 #define RL_SPLIT(RMV, DPLV)                                                                    \
     RL_LAUNCH(ctx, (k_attention_split<T, RMV, DPLV>), gs, bs, qd, kd, vd, pf, tk, od, p, sp,   \
@@ -1375,7 +1455,8 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
         else RL_SPLIT(32, 1);
 #undef RL_SPLIT
         const rl_status st = after_launch(ctx, name);
-        ctx->pool.release(part);  // stream-ordered: later users run after this launch
+        if (mode == DecodeScratch::kPool)
+            ctx->pool.release(part);  // stream-ordered: later users run after this launch
         return st;
     }
     if (flash) {
@@ -1428,6 +1509,16 @@ rl_status rl_attention_f16(rl_context* ctx, const rl_buffer* q, const rl_buffer*
     const AttnShape s{batch, q_heads, kv_heads, q_len, kv_len, head_dim, kv_capacity};
     return attention_entry<half_t>(ctx, "attention_f16", q, k, v, s, scale, query_start_pos,
                                    out);
+}
+
+rl_status rl_attention_f16_noalloc(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
+                                   const rl_buffer* v, uint64_t batch, uint64_t q_heads,
+                                   uint64_t kv_heads, uint64_t q_len, uint64_t kv_len,
+                                   uint64_t head_dim, uint64_t kv_capacity, float scale,
+                                   uint64_t query_start_pos, const rl_buffer* out) {
+    const AttnShape s{batch, q_heads, kv_heads, q_len, kv_len, head_dim, kv_capacity};
+    return attention_entry<half_t>(ctx, "attention_f16", q, k, v, s, scale, query_start_pos,
+                                   out, DecodeScratch::kStatic);
 }
 
 }  // extern "C"
