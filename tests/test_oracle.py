@@ -372,6 +372,56 @@ def test_rope_identity_at_position_zero_and_inverse():
     assert np.allclose(back, x, rtol=0, atol=1e-6)
 
 
+def _rope_f16_ulp_where_conditioned(got, x16, c, s, start):
+    """Max f16 ulp distance of `got` from the exact rotation of the f16 inputs
+    by the f32 table (float64, rounded once to f16), over outputs whose value
+    is at least 1/64 of the magnitude |a c| + |b s| (where an f32 evaluation
+    is within 2^-17 relative of the exact value, so one rounding to f16 is
+    off by at most 1 ulp)."""
+    from helpers import f16_ulp_distance
+    seq, half = x16.shape[-2], x16.shape[-1] // 2
+    a = x16[..., :half].astype(np.float64)
+    b = x16[..., half:].astype(np.float64)
+    cc = c[start:start + seq].astype(np.float64)
+    ss = s[start:start + seq].astype(np.float64)
+    exact = np.concatenate([a * cc - b * ss, b * cc + a * ss], axis=-1)
+    mag = np.concatenate([np.abs(a * cc) + np.abs(b * ss), np.abs(b * cc) + np.abs(a * ss)],
+                         axis=-1)
+    keep = np.abs(exact) >= mag / 64
+    assert keep.mean() > 0.9
+    return f16_ulp_distance(got[keep], exact.astype(np.float16)[keep])
+
+
+def test_rope_f16_is_one_rounding_of_the_exact_rotation():
+    """oracle_rope_f16 (rope.metal:66-97): halves widened, the rotation in
+    f32, one rounding to f16 -- within 1 ulp of the correctly rounded exact
+    rotation wherever cancellation is limited, at the SmolLM2 layer's table
+    (head 64, theta 1e4) over positions 0..4095."""
+    c, s = o.rope_table(64, 4096, 10000.0)
+    for start, seq in ((0, 4096), (3000, 700)):
+        x16 = synth.normal(synth.seed_for("rope-f16-pin", start), (1, 3, seq, 64),
+                           0.0, 2.0).astype(np.float16)
+        assert _rope_f16_ulp_where_conditioned(o.rope(x16, c, s, start), x16, c, s,
+                                               start) <= 1
+
+
+def test_rope_f16_pin_catches_an_extra_rounding():
+    """A plausible slip -- each product rounded to f16 before the sum -- fails
+    the same check on the same inputs."""
+    c, s = o.rope_table(64, 4096, 10000.0)
+    x16 = synth.normal(synth.seed_for("rope-f16-pin", 0), (1, 3, 4096, 64), 0.0,
+                       2.0).astype(np.float16)
+    half = 32
+    a = x16[..., :half].astype(np.float32)
+    b = x16[..., half:].astype(np.float32)
+    cc, ss = c[:4096], s[:4096]
+    h = np.float16
+    slip = np.concatenate([(a * cc).astype(h).astype(np.float32) - (b * ss).astype(h),
+                           (b * cc).astype(h).astype(np.float32) + (a * ss).astype(h)],
+                          axis=-1).astype(h)
+    assert _rope_f16_ulp_where_conditioned(slip, x16, c, s, 0) > 1
+
+
 def test_rope_kat_f16_vs_f32():
     kat = K["rope_f16_vs_f32"]
     c, s = o.rope_table(kat["head_dim"], kat["max_seq_len"], kat["theta"])
