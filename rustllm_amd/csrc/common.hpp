@@ -313,6 +313,57 @@ __device__ inline float silu_fast(float x) {
     return big ? (x * r) * 0x1p-64f : x * r;
 }
 
+// Wave-wide max / sum without LDS round trips (a __shfl_xor is an LDS
+// permute, ~100 cycles each): four DPP steps reduce every row of 16 lanes
+// (lane ^ 1, lane ^ 2, then the mirrors within 8 and within 16 lanes pair
+// the halves), and the four row results are read as scalars and combined,
+// so the result is the same in every lane.
+template <int CTRL>
+__device__ inline float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+__device__ inline float lane_value(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ inline float row16_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+    return fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+}
+__device__ inline float row16_sum(float v) {
+    v += dpp_move<0xB1>(v);
+    v += dpp_move<0x4E>(v);
+    v += dpp_move<0x141>(v);
+    return v + dpp_move<0x140>(v);
+}
+__device__ inline float wave_max_dpp(float v) {
+    v = row16_max(v);
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
+                 fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ inline float wave_sum_dpp(float v) {
+    v = row16_sum(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+// Sum over the aligned group of TPR lanes (16, 32 or 64) a lane belongs to,
+// the same in every lane of the group.
+template <int TPR>
+__device__ inline float lane_group_sum_dpp(float v) {
+    static_assert(TPR == 16 || TPR == 32 || TPR == 64, "lane groups of 16, 32 or 64");
+    v = row16_sum(v);
+    if constexpr (TPR == 16) {
+        return v;
+    } else if constexpr (TPR == 32) {
+        const float lo = lane_value(v, 0) + lane_value(v, 16);
+        const float hi = lane_value(v, 32) + lane_value(v, 48);
+        return (threadIdx.x & 32) ? hi : lo;
+    } else {
+        return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+    }
+}
+
 // wave64 butterfly reductions (every lane ends with the result).
 __device__ inline float wave_sum(float v) {
 #pragma unroll

@@ -76,6 +76,7 @@ struct MapShape {
     static constexpr int unroll = 1;
     static constexpr bool nt_store = true;
 };
+
 template <typename TIn, typename TOut>
 struct MapShape<AddOp, TIn, TOut> {  // f32: 72% -> 74%, f16: 62% -> 66-69%
     static constexpr int unroll = sizeof(TIn) == 4 ? 4 : 2;
@@ -200,6 +201,38 @@ __global__ __launch_bounds__(kThreads) void k_add_broadcast(const T* __restrict_
     }
 }
 
+// out[r, c] = x[r, c] + bias[c] for rows of at most 1024 packs: thread t of
+// a block owns column pack t -- its bias pack is loaded once and kept in
+// registers -- and adds it to that pack of R consecutive rows (R loads in
+// flight per thread, no index division, no bias reloads).  Consecutive
+// threads read consecutive packs of a row.
+template <typename T, int N, int R>
+__global__ __launch_bounds__(1024) void k_add_bias_rows(const T* __restrict__ x,
+                                                        const T* __restrict__ bias,
+                                                        T* __restrict__ out, uint32_t rows,
+                                                        uint32_t col_packs) {
+    typedef typename VecOf<T, N>::type V;
+    const uint32_t c = threadIdx.x;
+    if (c >= col_packs) return;
+    const V* vx = reinterpret_cast<const V*>(x);
+    V* vo = reinterpret_cast<V*>(out);
+    const V b = reinterpret_cast<const V*>(bias)[c];
+    const uint32_t r0 = blockIdx.x * R;
+    V rx[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+        if (r0 + u < rows) rx[u] = load_stream(vx + uint64_t(r0 + u) * col_packs + c);
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        if (r0 + u < rows) {
+            V r;
+#pragma unroll
+            for (int k = 0; k < N; ++k) r[k] = from_float<T>(to_float(rx[u][k]) + to_float(b[k]));
+            store_stream(vo + uint64_t(r0 + u) * col_packs + c, r);
+        }
+    }
+}
+
 // Scalar fallback for buffers that are not pack-aligned or too large for
 // 32-bit pack indices.
 template <typename T>
@@ -259,15 +292,27 @@ rl_status launch_add_broadcast(rl_context* ctx, const char* name, const rl_buffe
     if (n == 0) return RL_OK;
     if (rl_status st = activate(ctx)) return st;
     constexpr int N = 16 / sizeof(T);
-    // Four packs per thread: f32 65% -> 69%, f16 53% -> 56% of peak on
-    // [4096, 1536] (same sweep as MapShape).
+    // Four packs per thread: f16 53% -> 56% of peak on [4096, 1536] (same
+    // sweep as MapShape).
     constexpr int UNROLL = 4;
     const T* px = static_cast<const T*>(x->data);
     const T* pbias = static_cast<const T*>(bias->data);
     T* po = static_cast<T*>(out->data);
     const bool vec = cols % N == 0 && aligned_to(px, 16) && aligned_to(pbias, 16) &&
                      aligned_to(po, 16) && n / N <= UINT32_MAX;
-    if (vec) {
+    const uint64_t col_packs = cols / N;
+    if (vec && sizeof(T) == 4 && col_packs <= 1024 && rows <= UINT32_MAX) {
+        // f32 rows of up to 1024 packs: a block per 8 rows, a thread per
+        // column pack (threads rounded up to whole waves).  [4096, 1536]:
+        // 8.7 us (72% of peak) against 10.2 us for the per-pack column
+        // division below (4 rows per block: 9.4 us, 2: 10.4 us).  f16 rows
+        // (half the bytes per row) measured no gain (5.4-6.7 us against
+        // 5.2-5.9 us) and keep that kernel.
+        constexpr int R = 8;
+        const unsigned threads = unsigned(ceil_div(col_packs, 64) * 64);
+        RL_LAUNCH(ctx, (k_add_bias_rows<T, N, R>), dim3(unsigned(ceil_div(rows, R))),
+                  dim3(threads), px, pbias, po, uint32_t(rows), uint32_t(col_packs));
+    } else if (vec) {
         uint64_t n_packs = n / N;
         RL_LAUNCH(ctx, (k_add_broadcast<T, N, UNROLL>), dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads), px, pbias, po, n_packs, FastDiv(uint32_t(cols / N)));
     } else {

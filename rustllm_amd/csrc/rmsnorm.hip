@@ -5,13 +5,14 @@
 // group with an 8-barrier shared-memory tree and reads x twice.  Here a
 // group of TPR lanes (16, 32 or 64: a quarter, half or whole wave64) owns
 // one row: it loads the row once into VGPRs as 16-byte packs, NV packs per
-// lane, loads the weight packs alongside (they stay L2-resident), reduces
-// the sum of squares with a butterfly of cross-lane shuffles inside the
-// group (no LDS, no barrier) and writes y from registers, so x is read from
-// HBM exactly once.  TPR is picked per row length so that every lane holds
-// 3-12 packs with few idle lanes: 2-5 packs per lane left the loads too
-// short to cover HBM latency (f16 rows of 576-960 reached 50-63% of peak
-// with a wave per row, 63-73% with 16-32 lanes per row).  Rows longer than
+// lane (all loads issued back to back), loads the weight packs (they stay
+// L2-resident), reduces the sum of squares with DPP moves inside each row of
+// 16 lanes and scalar lane reads across them (no LDS, no barrier) and writes
+// y from registers, so x is read from HBM exactly once.  TPR is picked per
+// row length so that every lane holds 3-12 packs with few idle lanes: 2-5
+// packs per lane left the loads too short to cover HBM latency (f16 rows of
+// 576-960 reached 50-63% of peak with a wave per row, 63-73% with 16-32
+// lanes per row).  Rows longer than
 // 64 x 16 packs fall back to a block per row with an LDS step across its
 // four waves and a second (L2-resident) read.
 //
@@ -25,23 +26,19 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
+
+// Pack p of a row, or the row's last pack for p past its end.
+__device__ inline uint32_t clamp_pack(uint32_t p, uint32_t h_packs) {
+    return p < h_packs ? p : h_packs - 1;
+}
 // Rows per launch chunk: keeps blocks x threads far below 2^32.
 constexpr uint32_t kRowChunk = 1u << 22;
-
-// Sum over the TPR lanes of an aligned lane group (TPR <= 64 divides the
-// wave; xor offsets below TPR stay inside the group).
-template <int TPR>
-__device__ inline float lane_group_sum(float v) {
-#pragma unroll
-    for (int offset = TPR / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
-    return v;
-}
 
 // Rows [row_base, row_base + rows) of the launch chunk; TPR lanes per row,
 // kThreads / TPR rows per block.  Lanes of a group stride over the row's
 // packs (pack p = lane + k * TPR), so each load instruction covers TPR
 // consecutive packs of every row in the wave.
-template <typename T, int N, int NV, int TPR, bool ADD>
+template <typename T, int N, int NV, int TPR, bool ADD, bool WLATE>
 __global__ __launch_bounds__(kThreads) void k_rmsnorm_rows(
     const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ weight,
     T* __restrict__ sum_out, T* __restrict__ y, uint32_t row_base, uint32_t rows,
@@ -56,33 +53,35 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_rows(
     const V* wr = reinterpret_cast<const V*>(weight);
     V v[NV];
     V w[NV];
+    // Every load is issued, at an index clamped into the row (packs past the
+    // row are reloads of its last pack, never used): a load under a per-pack
+    // branch made the compiler wait for each f16 load before issuing the next.
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const uint32_t p = lane + k * TPR;
-        if (p < h_packs) v[k] = load_stream(xr + p);
-    }
+    for (int k = 0; k < NV; ++k) v[k] = load_stream(xr + clamp_pack(lane + k * TPR, h_packs));
     if constexpr (ADD) {
         const V* rr = reinterpret_cast<const V*>(residual) + row_off;
         V* sr = reinterpret_cast<V*>(sum_out) + row_off;
+        V r[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) r[k] = load_stream(rr + clamp_pack(lane + k * TPR, h_packs));
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const uint32_t p = lane + k * TPR;
-            if (p < h_packs) {
-                V r = load_stream(rr + p);
-                V s;
+            V s;
 #pragma unroll
-                for (int j = 0; j < N; ++j) s[j] = from_float<T>(to_float(v[k][j]) + to_float(r[j]));
-                v[k] = s;
-                store_stream(sr + p, s);
-            }
+            for (int j = 0; j < N; ++j) s[j] = from_float<T>(to_float(v[k][j]) + to_float(r[k][j]));
+            v[k] = s;
+            if (p < h_packs) store_stream(sr + p, s);
         }
     }
-    // The weight (h elements shared by every row) comes from L2; issuing its
-    // loads before the reduction hides their latency behind the shuffles.
+    // The weight (h elements shared by every row) comes from L2.  With two
+    // packs per lane its loads go out with the row's, so their latency hides
+    // behind the reduction; with three or more (WLATE) every wave of a large
+    // launch asking for the same few weight lines at its start slowed the
+    // f16 [16384, h] launches by 10-20%, so they follow the reduction there.
+    if constexpr (!WLATE) {
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const uint32_t p = lane + k * TPR;
-        if (p < h_packs) w[k] = wr[p];
+        for (int k = 0; k < NV; ++k) w[k] = wr[clamp_pack(lane + k * TPR, h_packs)];
     }
     float ss = 0.0f;
 #pragma unroll
@@ -96,7 +95,11 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_rows(
             }
         }
     }
-    ss = lane_group_sum<TPR>(ss);
+    if constexpr (WLATE) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) w[k] = wr[clamp_pack(lane + k * TPR, h_packs)];
+    }
+    ss = lane_group_sum_dpp<TPR>(ss);  // DPP within rows of 16, scalar reads across
     const float inverse_rms = rsqrtf(ss / hidden + eps);  // rmsnorm.metal:55-60
     V* yr = reinterpret_cast<V*>(y) + row_off;
 #pragma unroll
@@ -168,10 +171,10 @@ struct RowPlan {
 // group; then widen the group while the launch would have fewer than 4096
 // waves (4 per SIMD), where more, shorter waves hide latency better
 // ([4096, 960] f16: 4.4 us with 64 lanes per row, 4.9 us with 32).
-RowPlan plan_by_length(uint64_t h_packs);
+RowPlan plan_by_length(uint64_t h_packs, bool narrow_ties);
 
-RowPlan plan_rows(uint64_t h_packs, uint64_t rows) {
-    RowPlan plan = plan_by_length(h_packs);
+RowPlan plan_rows(uint64_t h_packs, uint64_t rows, bool narrow_ties) {
+    RowPlan plan = plan_by_length(h_packs, narrow_ties);
     while (plan.tpr < 64 && rows * uint64_t(plan.tpr) < 4096ull * kWave) {
         const int tpr = plan.tpr * 2;
         const uint64_t need = ceil_div(h_packs, uint64_t(tpr));
@@ -182,7 +185,10 @@ RowPlan plan_rows(uint64_t h_packs, uint64_t rows) {
     return plan;
 }
 
-RowPlan plan_by_length(uint64_t h_packs) {
+// narrow_ties: between groups of equal lane use, take the narrower one (more
+// packs per lane): f16 [16384, 960] runs 8% faster on 16 lanes x 8 packs than
+// on 32 x 4, while f32 rows keep the wider group on a tie.
+RowPlan plan_by_length(uint64_t h_packs, bool narrow_ties) {
     RowPlan best{0, 0};
     bool best_ok = false;
     uint64_t best_num = 0, best_den = 1;  // lane use = num / den
@@ -194,7 +200,8 @@ RowPlan plan_by_length(uint64_t h_packs) {
         if (nv == 0) continue;
         const bool ok = need >= 3 && need <= 12;
         const uint64_t num = h_packs, den = uint64_t(tpr) * need;
-        const bool better_use = num * best_den > best_num * den;
+        const bool better_use = num * best_den > best_num * den ||
+                                (narrow_ties && num * best_den == best_num * den);
         if (best.tpr == 0 || (ok && !best_ok) || (ok == best_ok && better_use)) {
             best = {tpr, nv};
             best_ok = ok;
@@ -213,8 +220,8 @@ void launch_rows(rl_context* ctx, const T* x, const T* residual, const T* weight
     for (uint32_t base = 0; base < rows; base += kRowChunk) {
         const uint32_t n = rows - base < kRowChunk ? rows - base : kRowChunk;
         const dim3 grid(unsigned(ceil_div(n, kRowsPerBlock))), block(kThreads);
-        RL_LAUNCH(ctx, (k_rmsnorm_rows<T, N, NV, TPR, ADD>), grid, block, x, residual, weight,
-                  sum_out, y, base, rows, h_packs, hidden, eps);
+        RL_LAUNCH(ctx, (k_rmsnorm_rows<T, N, NV, TPR, ADD, (NV >= 3)>), grid, block, x,
+                  residual, weight, sum_out, y, base, rows, h_packs, hidden, eps);
         if (rows - base <= kRowChunk) break;
     }
 }
@@ -231,7 +238,7 @@ rl_status launch_rmsnorm(rl_context* ctx, const char* name, const T* x, const T*
     const uint64_t h_packs = hidden / N;
     const uint32_t r32 = uint32_t(rows);
     if (packs_ok && h_packs <= 16 * kWave) {
-        const RowPlan plan = plan_rows(h_packs, rows);
+        const RowPlan plan = plan_rows(h_packs, rows, sizeof(T) == 2);
         const uint32_t hp = uint32_t(h_packs);
         const float hf = float(hidden);
 #define RL_RMS_PLAN(TPR_, NV_)                                                                \

@@ -76,11 +76,11 @@ __device__ inline uint32_t kept_keys(uint32_t row, uint32_t width, const MaskPar
 }
 
 // Max / sum over the TPR threads of a row group (the waves of a group are
-// consecutive).  `lds` holds one slot per wave of the block and is written
+// consecutive): DPP within each wave, LDS across its waves.  `lds` holds one slot per wave of the block and is written
 // once per call; callers separate consecutive uses by a barrier.
 template <int TPR>
 __device__ inline float group_max(float v, float* lds) {
-    v = wave_max(v);
+    v = wave_max_dpp(v);
     if constexpr (TPR > kWave) {
         constexpr int WPR = TPR / kWave;
         if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
@@ -96,7 +96,7 @@ __device__ inline float group_max(float v, float* lds) {
 
 template <int TPR>
 __device__ inline float group_sum(float v, float* lds) {
-    v = wave_sum(v);
+    v = wave_sum_dpp(v);
     if constexpr (TPR > kWave) {
         constexpr int WPR = TPR / kWave;
         if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;

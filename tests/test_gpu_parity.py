@@ -153,7 +153,8 @@ def test_cast_rounding_probe(ctx):
 
 
 @pytest.mark.parametrize("dtype", DT)
-@pytest.mark.parametrize("rows,cols", [(4096, 1536), (3, 5), (17, 24), (1, 8)])
+@pytest.mark.parametrize("rows,cols", [(4096, 1536), (3, 5), (17, 24), (1, 8), (4095, 960),
+                                       (6, 4096), (5, 8200), (2, 8192 + 8)])
 def test_add_broadcast_bitexact(ctx, dtype, rows, cols):
     x = norm(("bias", "x"), (rows, cols), dtype)
     b = norm(("bias", "b"), (cols,), dtype)
