@@ -101,6 +101,14 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     const uint32_t q0 = qt * 128 + wave * 32;
     const half_t* kh = k + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
     const uint32_t kbase = kt_blk * 128;
+    // this wave's queries first, so their loads overlap the key tile's; a
+    // query past q_len reads row 0 (its scores are not stored)
+    const uint32_t qi = q0 + col;
+    const bool q_valid = qi < p.q_len;
+    h8 qf[DC];
+    const half_t* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + 8 * hs;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) qf[c] = *reinterpret_cast<const h8*>(qrow + 16 * c);
     // the block's 128 key rows -> LDS, whole rows per 8 (D 64) lanes; key row
     // j goes to LDS row perm32(j) so that the S^T operand of lane i is row i.
     // Keys past kv_len read row kv_len - 1 (their scores are not stored).
@@ -123,19 +131,6 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
             const uint32_t key = kbase >= 8 ? kbase - 8 + j : min(j, p.kv_len - 1);
             *reinterpret_cast<h8*>(kpre + j * KS + d0) =
                 *reinterpret_cast<const h8*>(kh + uint64_t(key) * D + d0);
-        }
-    }
-    const uint32_t qi = q0 + col;
-    const bool q_valid = qi < p.q_len;
-    h8 qf[DC];
-    const half_t* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + 8 * hs;
-#pragma unroll
-    for (int c = 0; c < DC; ++c) {
-        if (q_valid) {
-            qf[c] = *reinterpret_cast<const h8*>(qrow + 16 * c);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qf[c][e] = half_t(0.0f);
         }
     }
     __syncthreads();
@@ -250,6 +245,23 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
         return;
     }
     const bool vec_store = p.kv_len % 8 == 0;
+    if (vec_store && keys_here == 128 && q0 + 31 < p.q_len) {
+        // A whole tile (the common case): every LDS read, then every store,
+        // with no branch between them (under per-store branches the compiler
+        // waited for each read before its store).
+        h8 w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            w[i] = *reinterpret_cast<const h8*>(my + (i * 4 + lane / 16) * TS + (lane % 16) * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t r = i * 4 + lane / 16;
+            half_t* dst = out + (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase +
+                          (lane % 16) * 8;
+            put_scores<STREAM>(reinterpret_cast<h8*>(dst), w[i]);
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint32_t r = i * 4 + lane / 16;  // tile row (query q0 + r)

@@ -146,8 +146,34 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
 
         float v[NV][N];
         float m = -INFINITY;
+        if constexpr (!RAGGED) {
+            // Every lane issues all its loads before using any: a pack past
+            // the row's last kept key (or past the row) reloads that last
+            // kept pack -- a line the wave reads anyway -- and its elements
+            // are masked by a select.  With a branch per pack the compiler
+            // waited for each load before issuing the next.
+            const uint32_t live = (kept + N - 1) / N;  // packs holding a kept key
+            const uint32_t last = live > 0 ? live - 1 : 0u;
+            V raw[NV];
 #pragma unroll
-        for (int k = 0; k < NV; ++k) {
+            for (int k = 0; k < NV; ++k) {
+                const uint32_t p = lane + k * TPR;
+                raw[k] = load_stream(src + (p < last ? p : last));
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the arithmetic
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                const uint32_t p = lane + k * TPR;
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    const float f = MASK ? scaled_score(raw[k][j], mp.scale) : to_float(raw[k][j]);
+                    v[k][j] = p * N + j < kept ? f : -INFINITY;
+                    m = fmaxf(m, v[k][j]);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NV && RAGGED; ++k) {
             const uint32_t p = lane + k * TPR;
             // row index of the pack's first element (negative only in a
             // ragged row's first pack)
