@@ -179,13 +179,15 @@ struct FastDiv {
 // view's own row-major order (e.g. the head of a [1, H, S, D] view), which
 // places the row in a contiguous or cache-shaped destination.
 constexpr int kMaxRowRank = 16;
-struct RowDims {
+template <int R>
+struct RowDimsN {
     uint32_t rank;
     uint32_t seq_dim;
-    FastDiv dim[kMaxRowRank];
-    uint64_t stride[kMaxRowRank];
-    uint32_t group_mult[kMaxRowRank];
+    FastDiv dim[R];
+    uint64_t stride[R];
+    uint32_t group_mult[R];
 };
+typedef RowDimsN<kMaxRowRank> RowDims;
 
 // Rows enumerated in the view's memory order (row dims sorted by source
 // stride, smallest first), so consecutive rows read consecutive memory where
@@ -193,10 +195,12 @@ struct RowDims {
 // the heads of one position come together, reading the projection straight
 // through and sharing that position's table row.  dims/strides: outermost
 // first, `rank` >= 2 including the innermost dim.
-inline RowDims make_row_dims(const uint64_t* dims, const uint64_t* strides, uint32_t rank) {
-    RowDims rd{};
+// RowDimsN<R> holds views of up to R row dims (rank <= R + 1).
+template <int R = kMaxRowRank>
+inline RowDimsN<R> make_row_dims(const uint64_t* dims, const uint64_t* strides, uint32_t rank) {
+    RowDimsN<R> rd{};
     const uint32_t n = rank - 1;  // row dims: 0 .. rank - 2; the sequence dim is rank - 2
-    uint32_t order[kMaxRowRank];
+    uint32_t order[R];
     for (uint32_t i = 0; i < n; ++i) order[i] = n - 1 - i;  // innermost first
     for (uint32_t i = 1; i < n; ++i) {  // stable insertion sort by stride
         const uint32_t v = order[i];
@@ -224,7 +228,8 @@ inline RowDims make_row_dims(const uint64_t* dims, const uint64_t* strides, uint
     return rd;
 }
 
-__device__ inline void decode_row(const RowDims& rd, uint32_t row, uint64_t& src_off,
+template <int R>
+__device__ inline void decode_row(const RowDimsN<R>& rd, uint32_t row, uint64_t& src_off,
                                   uint32_t& position, uint32_t& group) {
     src_off = 0;
     position = 0;

@@ -94,6 +94,218 @@ __global__ __launch_bounds__(kThreads) void k_rope(const T* __restrict__ src,
     }
 }
 
+// ---------------------------------------------- row blocks of 16-byte lanes
+//
+// The layout for rows of 32, 64, 128 or 256 bytes (head_dim 16..128 in f16,
+// 8..64 in f32): L = row bytes / 16 lanes per row, each loading one 16-byte
+// pack, so a lane group reads and writes its whole row in one access.  The
+// rotation partner of a pack -- the pack half_dim elements away -- sits in
+// another lane of the group and comes over with one DPP move per dword:
+// quad_perm for L = 2 and 4, row_ror:8 for L = 16, and row_half_mirror for
+// L = 8, where lane j >= 4 holds pack 11 - j so that the partners of lanes j
+// and 7 - j are each other.  A block serves kThreads / L consecutive rows in
+// the view's memory order (make_row_dims), so it reads one contiguous
+// stretch of the source, and the heads of one position, coming together in
+// a [1, S, H, D] projection, share their cos/sin row.
+
+constexpr int kMaxJobRank = 6;  // row dims of a job's view
+
+// One view rotated (or copied) into `dst` rows
+// group * dst_rows.group_rows + dst_rows.first_row + position and, when `rep`
+// is set, into rows (group * n_rep + r) * rep_rows + rep_first + position of
+// `rep` for r < n_rep.  A null `dst` skips the first write.
+struct RowJob {
+    const void* src;
+    void* dst;
+    void* rep;
+    RowDimsN<kMaxJobRank> rows;
+    DstRows dst_rows;
+    uint32_t n_rows;
+    uint32_t n_rep;
+    uint32_t rep_rows;
+    uint32_t rep_first;
+    uint32_t first_block;  // blocks [first_block, next job's first_block)
+    uint32_t rotate;
+};
+
+constexpr int kMaxJobs = 5;
+struct RowJobs {
+    RowJob job[kMaxJobs];
+};
+
+template <int L>
+__device__ inline int partner_dword(int v) {
+    if constexpr (L == 2)
+        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+    else if constexpr (L == 4)
+        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+    else if constexpr (L == 8)
+        return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    else
+        return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);  // row_ror:8
+}
+
+// decode_row over all kMaxJobRank dims with no branch, so the scalar loads of
+// every dim go out together.  Dims past rd.rank are make_row_dims' zero
+// initialisation -- divisor 1, stride 0, group multiplier 0 -- and leave the
+// row, the offset and the group as they are.
+__device__ inline void decode_job_row(const RowDimsN<kMaxJobRank>& rd, uint32_t row,
+                                      uint64_t& src_off, uint32_t& position, uint32_t& group) {
+    src_off = 0;
+    position = 0;
+    group = 0;
+#pragma unroll
+    for (uint32_t d = 0; d < uint32_t(kMaxJobRank); ++d) {
+        uint32_t q, r;
+        rd.dim[d].divmod(row, q, r);
+        src_off += uint64_t(r) * rd.stride[d];
+        position = d == rd.seq_dim ? r : position;
+        group += r * rd.group_mult[d];
+        row = q;
+    }
+}
+
+template <typename T, int L>
+__global__ __launch_bounds__(kThreads) void k_rope_blocks(RowJobs jobs,
+                                                          const float* __restrict__ cos_table,
+                                                          const float* __restrict__ sin_table,
+                                                          uint32_t start) {
+    constexpr int N = 16 / int(sizeof(T));  // elements per lane
+    constexpr uint32_t D = uint32_t(L * N);
+    constexpr uint32_t kHalf = D / 2;
+    constexpr uint32_t kRows = kThreads / L;  // rows per block
+    typedef typename VecOf<T, N>::type V;
+    typedef typename VecOf<float, N>::type VF;
+    uint32_t k = 0;
+#pragma unroll
+    for (int t = 1; t < kMaxJobs; ++t) k += blockIdx.x >= jobs.job[t].first_block ? 1u : 0u;
+    const RowJob& job = jobs.job[k];
+    const bool rotate = job.rotate != 0;
+    uint32_t row = (blockIdx.x - job.first_block) * kRows + threadIdx.x / L;
+    const bool live = row < job.n_rows;
+    if (!live) row = job.n_rows - 1;  // a valid row: every lane takes part in the DPP moves
+    uint64_t src_off;
+    uint32_t pos, group;
+    decode_job_row(job.rows, row, src_off, pos, group);
+    const uint32_t lane = threadIdx.x % L;
+    const uint32_t pack = (L == 8 && lane >= 4) ? 11 - lane : lane;
+    const uint32_t pair = (pack % (L / 2)) * N;
+    // The three loads go out back to back.  A copy job reads table row 0
+    // (valid for every job here) and ignores it, which keeps them branch-free.
+    const uint64_t t = rotate ? uint64_t(start + pos) * kHalf + pair : pair;
+    const VF c = *reinterpret_cast<const VF*>(cos_table + t);
+    const VF s = *reinterpret_cast<const VF*>(sin_table + t);
+    const V x = load_stream(reinterpret_cast<const V*>(static_cast<const T*>(job.src) + src_off +
+                                                       pack * N));
+    // The rotation is computed for copy jobs too and then not used: a branch
+    // around it would let the compiler sink the table loads into it, behind
+    // a wait for x.
+    int w[4], m[4];
+    __builtin_memcpy(w, &x, 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m[i] = partner_dword<L>(w[i]);
+    V other;
+    __builtin_memcpy(&other, m, 16);
+    // First half: first*c - second*s; second half: second*c + first*s.
+    // Negating the partner is exact, so each result keeps the reference's
+    // two rounded products and one rounded sum.
+    const bool first_half = pack < uint32_t(L / 2);
+    V o;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const float own = to_float(x[j]);
+        const float partner = first_half ? -to_float(other[j]) : to_float(other[j]);
+        o[j] = rotate ? from_float<T>(own * c[j] + partner * s[j]) : x[j];
+    }
+    if (!live) return;
+    if (job.dst) {
+        const uint64_t r =
+            uint64_t(group) * job.dst_rows.group_rows + job.dst_rows.first_row + pos;
+        store_stream(reinterpret_cast<V*>(static_cast<T*>(job.dst) + r * D + pack * N), o);
+    }
+    if (job.rep) {
+        for (uint32_t i = 0; i < job.n_rep; ++i) {
+            const uint64_t r = (uint64_t(group) * job.n_rep + i) * job.rep_rows + job.rep_first + pos;
+            store_stream(reinterpret_cast<V*>(static_cast<T*>(job.rep) + r * D + pack * N), o);
+        }
+    }
+}
+
+// Lanes per row for the row-block kernel, or 0 when the row is not 32, 64,
+// 128 or 256 bytes.
+template <typename T>
+int row_lanes(uint64_t head_dim) {
+    switch (head_dim * sizeof(T)) {
+        case 32: return 2;
+        case 64: return 4;
+        case 128: return 8;
+        case 256: return 16;
+        default: return 0;
+    }
+}
+
+// A job for a [..., S, D] view, or false when the view does not fit the
+// row-block kernel (more row dims than it decodes, a row start off a 16-byte
+// boundary, or more than u32 rows).
+template <typename T>
+bool make_job(RowJob& job, const void* src, const uint64_t* dims, const uint64_t* strides,
+              uint32_t rank, void* dst, DstRows dst_rows, bool rotate) {
+    constexpr uint64_t N = 16 / sizeof(T);
+    if (rank < 2 || rank - 1 > uint32_t(kMaxJobRank) || strides[rank - 1] != 1) return false;
+    if (!aligned_to(src, 16) || (dst && !aligned_to(dst, 16))) return false;
+    uint64_t rows = 1;
+    for (uint32_t d = 0; d + 1 < rank; ++d) {
+        if (strides[d] % N != 0 || dims[d] > UINT32_MAX) return false;
+        rows *= dims[d];
+        if (rows > UINT32_MAX) return false;
+    }
+    job = RowJob{};
+    job.src = src;
+    job.dst = dst;
+    job.rows = make_row_dims<kMaxJobRank>(dims, strides, rank);
+    job.dst_rows = dst_rows;
+    job.n_rows = uint32_t(rows);
+    job.rotate = rotate ? 1u : 0u;
+    return true;
+}
+
+// Assigns first blocks to jobs[0 .. n) (jobs with no rows get none) and
+// launches; false when the grid would be too large.
+template <typename T>
+bool launch_jobs(rl_context* ctx, RowJobs& jobs, int n, int lanes, const float* cos_table,
+                 const float* sin_table, uint64_t start) {
+    const uint64_t rows_per_block = uint64_t(kThreads) / lanes;
+    uint64_t blocks = 0;
+    for (int t = 0; t < kMaxJobs; ++t) {
+        RowJob& job = jobs.job[t];
+        if (t >= n) {
+            job.first_block = UINT32_MAX;
+            continue;
+        }
+        job.first_block = uint32_t(blocks);
+        blocks += ceil_div(uint64_t(job.n_rows), rows_per_block);
+        if (blocks >= (1u << 30)) return false;
+    }
+    if (blocks == 0) return true;
+    const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+    const uint32_t s32 = uint32_t(start);
+    switch (lanes) {
+        case 2:
+            RL_LAUNCH(ctx, (k_rope_blocks<T, 2>), grid, block, jobs, cos_table, sin_table, s32);
+            break;
+        case 4:
+            RL_LAUNCH(ctx, (k_rope_blocks<T, 4>), grid, block, jobs, cos_table, sin_table, s32);
+            break;
+        case 8:
+            RL_LAUNCH(ctx, (k_rope_blocks<T, 8>), grid, block, jobs, cos_table, sin_table, s32);
+            break;
+        default:
+            RL_LAUNCH(ctx, (k_rope_blocks<T, 16>), grid, block, jobs, cos_table, sin_table, s32);
+            break;
+    }
+    return true;
+}
+
 inline unsigned grid_for(uint64_t items, uint64_t per_block) {
     uint64_t blocks = ceil_div(items, per_block);
     if (blocks < 1) blocks = 1;
@@ -111,6 +323,14 @@ rl_status launch_rope(rl_context* ctx, const char* name, const T* src, const uin
     if (rl_status st = activate(ctx)) return st;
     const uint64_t head_dim = dims[rank - 1];
     const uint64_t half = head_dim / 2;
+    if (dst.group_rows == 0) dst = DstRows{uint32_t(dims[rank - 2]), 0};
+    if (const int lanes = row_lanes<T>(head_dim);
+        lanes && aligned_to(cos_table, 64 / sizeof(T)) && aligned_to(sin_table, 64 / sizeof(T))) {
+        RowJobs jobs{};
+        if (make_job<T>(jobs.job[0], src, dims, strides, rank, out, dst, true) &&
+            launch_jobs<T>(ctx, jobs, 1, lanes, cos_table, sin_table, start))
+            return after_launch(ctx, name);
+    }
     uint64_t rows = 1;
     for (uint32_t d = 0; d + 1 < rank; ++d) rows *= dims[d];
     // Widest pack of pairs (<= 16 B of T, <= 4 or 8 lanes) that keeps every
@@ -130,7 +350,6 @@ rl_status launch_rope(rl_context* ctx, const char* name, const T* src, const uin
     constexpr int U = 1;
     const dim3 grid(grid_for(n_items, uint64_t(kThreads) * U)), block(kThreads);
     const uint32_t h32 = uint32_t(half), s32 = uint32_t(start), ni = uint32_t(n_items);
-    if (dst.group_rows == 0) dst = DstRows{uint32_t(dims[rank - 2]), 0};
     switch (n) {
         case 8:
             RL_LAUNCH(ctx, (k_rope<T, 8, U>), grid, block, src, cos_table, sin_table, out, ni, ppr, rd, h32, s32, dst);
@@ -465,6 +684,18 @@ rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
     void* dsts[3] = {q_out->data, k_cache->data, v_cache->data};
     const uint64_t* dims[3] = {q_dims, k_dims, v_dims};
     const uint64_t* strides[3] = {q_strides, k_strides, v_strides};
+    if (const int lanes = row_lanes<T>(q_dims[3]);
+        lanes && aligned_to(cs, 64 / sizeof(T)) && aligned_to(sn, 64 / sizeof(T))) {
+        RowJobs jobs{};
+        bool ok = true;
+        for (int t = 0; t < 3 && ok; ++t)
+            ok = make_job<T>(jobs.job[t], srcs[t], dims[t], strides[t], 4, dsts[t],
+                             t == 0 ? DstRows{uint32_t(dims[t][2]), 0}
+                                    : DstRows{uint32_t(max_seq), uint32_t(start)},
+                             t < 2);
+        if (ok && launch_jobs<T>(ctx, jobs, 3, lanes, cs, sn, start))
+            return after_launch(ctx, name);
+    }
     int n = 16 / int(sizeof(T));
     while (n > 1) {
         bool ok = half % n == 0 && aligned_to(cs, n * 4) && aligned_to(sn, n * 4);

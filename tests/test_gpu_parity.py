@@ -472,6 +472,51 @@ def test_rope_fused_transpose_gather(ctx, dtype, seq, heads):
     assert_bitexact(got, ref, f"fused rope {seq}x{heads}")
 
 
+ROW_BLOCK_DIMS = {"f16": [16, 32, 64, 128], "f32": [8, 16, 32, 64]}
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("lane_case", [0, 1, 2, 3])
+@pytest.mark.parametrize("seq,start", [(1, 0), (33, 7), (300, 0)])
+def test_rope_every_row_width(ctx, dtype, lane_case, seq, start):
+    """Rows of 32, 64, 128 and 256 bytes (2, 4, 8 and 16 lanes of 16 bytes
+    each), position counts that do and do not fill whole blocks, a start
+    offset, a contiguous [2, 3, S, D] input and a rank-5 permuted view."""
+    hd = ROW_BLOCK_DIMS["f16" if dtype == np.float16 else "f32"][lane_case]
+    c, s = o.rope_table(hd, seq + start + 3, 10000.0)
+    dc, ds = ctx.upload(c), ctx.upload(s)
+    x = norm(("ropeW", hd), (2, 3, seq, hd), dtype)
+    got = run(ctx, lambda: ctx.rope(ctx.upload(x), dc, ds, start)).numpy()
+    assert_bitexact(got, o.rope(x, c, s, start), f"rope D={hd} S={seq} start={start}")
+    # [2, S, 2, 3, D] seen as [2, 3, 2, S, D]
+    base = norm(("ropeW5", hd), (2, seq, 2, 3, hd), dtype)
+    dims = [2, 3, 2, seq, hd]
+    strides = [seq * 6 * hd, hd, 3 * hd, 6 * hd, 1]
+    ref = o.rope(o.contiguous(base.ravel(), dims, strides), c, s, start)
+    got = run(ctx, lambda: ctx.rope_strided(ctx.upload(base), dims, strides, dc, ds,
+                                            start)).numpy()
+    assert_bitexact(got, ref, f"rank-5 view D={hd} S={seq}")
+
+
+@pytest.mark.parametrize("dtype", DT)
+def test_rope_rows_off_the_fast_layout(ctx, dtype):
+    """Rows that the 16-byte-lane kernel does not take: f32 rows of 512 bytes,
+    and a view whose row starts are 4 bytes apart from 16-byte alignment."""
+    c, s = o.rope_table(128, 64, 10000.0)
+    dc, ds = ctx.upload(c), ctx.upload(s)
+    x = norm(("ropeF", 128), (1, 2, 33, 128), dtype)
+    got = run(ctx, lambda: ctx.rope(ctx.upload(x), dc, ds, 5)).numpy()
+    assert_bitexact(got, o.rope(x, c, s, 5), "D=128")
+    c, s = o.rope_table(64, 64, 10000.0)
+    dc, ds = ctx.upload(c), ctx.upload(s)
+    base = norm(("ropeF", 66), (1, 40, 3, 66), dtype)
+    dims, strides = [1, 3, 40, 64], [40 * 3 * 66, 66, 3 * 66, 1]
+    ref = o.rope(o.contiguous(base.ravel(), dims, strides), c, s, 2)
+    got = run(ctx, lambda: ctx.rope_strided(ctx.upload(base), dims, strides, dc, ds,
+                                            2)).numpy()
+    assert_bitexact(got, ref, "stride 66 view")
+
+
 def test_rope_reference_kats(ctx):
     kat = K["rope_f16_vs_f32"]
     c, s = o.rope_table(kat["head_dim"], kat["max_seq_len"], kat["theta"])
@@ -544,6 +589,9 @@ def test_rope_kv_cache_write_bitexact(ctx, dtype, heads, max_seq, hd, seq, start
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("qh,kvh,seq,hd,start,max_seq", [(15, 5, 4096, 64, 0, 4096),
                                                          (15, 5, 1, 64, 100, 4096),
+                                                         (6, 2, 77, 32, 9, 90),
+                                                         (4, 4, 40, 16, 0, 40),
+                                                         (3, 1, 19, 128, 2, 30),
                                                          (4, 2, 7, 6, 3, 12),
                                                          (2, 2, 5, 2, 0, 5)])
 def test_qkv_rope_kv_append_one_launch(ctx, dtype, qh, kvh, seq, hd, start, max_seq):
