@@ -482,6 +482,18 @@ def extra_rows(ctx, reps, quick):
             lambda s: ctx.qkv_rope_kv_append((s[0], qdims, qstrides), (s[1], kdims, kstrides),
                                              (s[2], kdims, kstrides), dc, ds, 0, s[4], s[5],
                                              s[3]))
+    # ... and repeat_kv of both caches (5 -> 15 heads) in the same launch
+    n_rep = qh // kvh
+    measure("layer.2 QKV + KV append + repeat_kv (one launch)", "f16",
+            [1, qh + 2 * kvh, tok, hd],
+            2 * proj_q.size * 2 + 2 * proj_k.size * (1 + 1 + n_rep) * 2
+            + 2 * tok * (hd // 2) * 4,
+            lambda i: (ctx.upload(proj_q), ctx.upload(proj_k), ctx.upload(proj_k),
+                       ctx.empty(qdims, F16), ctx.empty(kdims, F16), ctx.empty(kdims, F16),
+                       ctx.empty(qdims, F16), ctx.empty(qdims, F16)),
+            lambda s: ctx.qkv_rope_kv_append_repeat(
+                (s[0], qdims, qstrides), (s[1], kdims, kstrides), (s[2], kdims, kstrides), dc,
+                ds, 0, s[4], s[5], n_rep, s[3], s[6], s[7]))
     # token embedding gather: 4096 ids into a [49152, 960] f16 table
     # (each set has its own 94 MB table, so the gathered rows come from HBM)
     vocab = 49152
@@ -515,6 +527,8 @@ def extra_rows(ctx, reps, quick):
     rows.extend(attention_rows(ctx, qh, kvh, hd, tok, reps))
     if not quick:
         rows.append(layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds))
+        rows.append(layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds,
+                                    fused_prologue=True))
         rows.append(fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds))
     # [64, 768] f32 (the reference's CPU-runnable case), fused add + RMSNorm
     # (writes the sum and the norm)
@@ -713,7 +727,8 @@ def fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
             "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None}
 
 
-def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20):
+def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20,
+                    fused_prologue=False):
     """The whole non-GEMM chain of one SmolLM2-360M layer in order -- RMSNorm,
     RoPE of Q and K (read straight from the [1, H, S, D] views of the
     normalised rows that the Q and K projections would produce), repeat_kv of
@@ -722,10 +737,16 @@ def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
     GEMM sits between two stages (V, the scores, gate/up, the down
     projection) the stage reads a seeded stand-in.  Bytes are the sum of the
     launches' algorithmic bytes.  After timing, every output of the first
-    set is compared with the oracle on that set's inputs."""
+    set is compared with the oracle on that set's inputs.
+
+    fused_prologue: RoPE of Q and K, the KV-cache append of K and V
+    (start 0, a cache of tok rows) and repeat_kv of both caches as one launch
+    (rl_qkv_rope_kv_append_repeat_f16), 5 launches in all; the cache writes
+    add their bytes."""
     rng_key = ("chain",)
     qdims, qstrides = [1, qh, tok, hd], [tok * hid, hd, hid, 1]
     kdims, kstrides = [1, kvh, tok, hd], [tok * hid, hd, hid, 1]
+    vdims, vstrides = [1, kvh, tok, hd], [kvh * tok * hd, tok * hd, hd, 1]
     unmasked = qh * (tok * (tok + 1) // 2)
     nbytes = (tok * hid * 4 + hid * 2                                   # RMSNorm
               + 2 * (qh + kvh) * tok * hd * 2 + 2 * 2 * tok * (hd // 2) * 4  # RoPE Q, K
@@ -733,6 +754,14 @@ def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
               + unmasked * 2 + qh * tok * tok * 2                       # scale/mask + softmax
               + 3 * tok * ffn * 2                                       # SwiGLU
               + 3 * tok * hid * 2)                                      # residual add
+    if fused_prologue:
+        # one pass: Q and K read once, rotated K to the cache and repeated;
+        # V read once, to the cache and repeated
+        nbytes -= 2 * (qh + kvh) * tok * hd * 2 + 2 * (kvh + qh) * tok * hd * 2
+        nbytes += (2 * qh * tok * hd * 2                                # Q in, out
+                   + 2 * (kvh + kvh + qh) * tok * hd * 2)               # K, V in, cache, repeat
+    label = ("layer chain, prologue in one launch (5 launches)" if fused_prologue
+             else "layer chain (8 launches, one graph)")
 
     scores = np.random.default_rng(7).standard_normal((qh, tok, tok), dtype=np.float32)
     scores = scores.astype(F16)
@@ -751,15 +780,21 @@ def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
         b.update({"xn": ctx.empty((tok, hid), F16), "qr": ctx.empty(qdims, F16),
                   "kr": ctx.empty(kdims, F16), "kq": ctx.empty(qdims, F16),
                   "vq": ctx.empty(qdims, F16), "p": ctx.empty((qh, tok, tok), F16),
-                  "h": ctx.empty((tok, ffn), F16), "o": ctx.empty((tok, hid), F16)})
+                  "h": ctx.empty((tok, ffn), F16), "o": ctx.empty((tok, hid), F16),
+                  "vc": ctx.empty(kdims, F16)})
         return b
 
     def chain(b):
         ctx.rmsnorm(b["x"], wn, 1e-5, b["xn"])
-        ctx.rope_strided(b["xn"], qdims, qstrides, dc, ds, 0, b["qr"])
-        ctx.rope_strided(b["xn"], kdims, kstrides, dc, ds, 0, b["kr"])
-        ctx.repeat_kv(b["kr"], qh // kvh, b["kq"])
-        ctx.repeat_kv(b["v"], qh // kvh, b["vq"])
+        if fused_prologue:  # "kr" and "vc" are the caches
+            ctx.qkv_rope_kv_append_repeat((b["xn"], qdims, qstrides), (b["xn"], kdims, kstrides),
+                                          (b["v"], vdims, vstrides), dc, ds, 0, b["kr"], b["vc"],
+                                          qh // kvh, b["qr"], b["kq"], b["vq"])
+        else:
+            ctx.rope_strided(b["xn"], qdims, qstrides, dc, ds, 0, b["qr"])
+            ctx.rope_strided(b["xn"], kdims, kstrides, dc, ds, 0, b["kr"])
+            ctx.repeat_kv(b["kr"], qh // kvh, b["kq"])
+            ctx.repeat_kv(b["v"], qh // kvh, b["vq"])
         ctx.attention_softmax(b["s"], 0.125, 0, b["p"])
         ctx.swiglu(b["g"], b["u"], b["h"])
         ctx.add(b["xn"], b["r"], b["o"])
@@ -772,14 +807,16 @@ def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
         ctx.graph_destroy(g)
     us = ms * 1e3
     gbs = nbytes / (us * 1e-6) / 1e9
-    log(f"  {'layer chain (8 launches, one graph)':34s} {us:9.2f} us {gbs:8.1f} GB/s "
-        f"({100 * gbs / PEAK_GBS:5.1f}%)")
+    log(f"  {label:34s} {us:9.2f} us {gbs:8.1f} GB/s ({100 * gbs / PEAK_GBS:5.1f}%)")
     bad = check_chain(bufs[0], host, scores, wn.numpy(), dc.numpy(), ds.numpy(), qh, kvh, hd, tok)
+    if fused_prologue and not np.array_equal(bufs[0]["vc"].numpy().view(np.uint16),
+                                             host["v"].view(np.uint16)):
+        bad.append("V_cache")
     if bad:
-        log(f"  layer chain: MISMATCH against the oracle in {bad}")
+        log(f"  {label}: MISMATCH against the oracle in {bad}")
     else:
-        log("  layer chain: every stage matches the oracle")
-    return {"op": "layer chain (8 launches, one graph)", "dtype": "f16",
+        log(f"  {label}: every stage matches the oracle")
+    return {"op": label, "dtype": "f16",
             "shape": [tok, hid], "bytes": nbytes, "us": round(us, 3), "us_min": None,
             "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
             "us_graph_batch": round(us, 3), "GB/s_graph_batch": round(gbs, 1),

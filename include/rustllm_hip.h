@@ -392,6 +392,33 @@ rl_status rl_qkv_rope_kv_append_f16(rl_context* ctx, const rl_buffer* q_src,
                                     const rl_buffer* q_out, const rl_buffer* k_cache,
                                     const rl_buffer* v_cache, uint64_t max_seq);
 
+/* rl_qkv_rope_kv_append_* followed, in the same launch, by
+ * tensor::repeat_kv (src/tensor/repeat_kv.rs:13-130) of the two caches'
+ * prefixes after the append -- the [1, KVH, start_pos + S, D] key() and
+ * value() views (src/model/kv_cache.rs:87-99) -- into the contiguous
+ * [1, KVH * n_rep, start_pos + S, D] k_rep and v_rep: the C5 layer chain's
+ * "RoPE(Q, K) -> repeat_kv(K, V)" prologue, which the reference runs as
+ * separate calls.  Checks: those of rl_qkv_rope_kv_append_*, then
+ * repeat_kv's (n_rep == 0 and a head-count overflow are
+ * RL_ERR_MODEL_FORMAT), then the output sizes.  With n_rep == 1 the outputs
+ * are copies of the prefixes (repeat_kv returns its input there). */
+rl_status rl_qkv_rope_kv_append_repeat_f32(
+    rl_context* ctx, const rl_buffer* q_src, const uint64_t* q_dims, const uint64_t* q_strides,
+    const rl_buffer* k_src, const uint64_t* k_dims, const uint64_t* k_strides,
+    const rl_buffer* v_src, const uint64_t* v_dims, const uint64_t* v_strides,
+    const rl_buffer* cos_table, const rl_buffer* sin_table, uint64_t table_rows,
+    uint64_t start_pos, const rl_buffer* q_out, const rl_buffer* k_cache,
+    const rl_buffer* v_cache, uint64_t max_seq, uint64_t n_rep, const rl_buffer* k_rep,
+    const rl_buffer* v_rep);
+rl_status rl_qkv_rope_kv_append_repeat_f16(
+    rl_context* ctx, const rl_buffer* q_src, const uint64_t* q_dims, const uint64_t* q_strides,
+    const rl_buffer* k_src, const uint64_t* k_dims, const uint64_t* k_strides,
+    const rl_buffer* v_src, const uint64_t* v_dims, const uint64_t* v_strides,
+    const rl_buffer* cos_table, const rl_buffer* sin_table, uint64_t table_rows,
+    uint64_t start_pos, const rl_buffer* q_out, const rl_buffer* k_cache,
+    const rl_buffer* v_cache, uint64_t max_seq, uint64_t n_rep, const rl_buffer* k_rep,
+    const rl_buffer* v_rep);
+
 /* ============================================================= embedding */
 /* ops::embedding_f32_encode (src/ops/embedding.rs:32-57,119-193):
  * out[t, :] = weight[token_ids[t], :] for a [vocab_size, hidden_size] weight.

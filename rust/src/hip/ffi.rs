@@ -499,6 +499,53 @@ extern "C" {
         v_cache: *const rl_buffer,
         max_seq: u64,
     ) -> rl_status;
+    // the same plus repeat_kv of the cache prefixes (src/tensor/repeat_kv.rs)
+    pub fn rl_qkv_rope_kv_append_repeat_f32(
+        ctx: *mut rl_context,
+        q_src: *const rl_buffer,
+        q_dims: *const u64,
+        q_strides: *const u64,
+        k_src: *const rl_buffer,
+        k_dims: *const u64,
+        k_strides: *const u64,
+        v_src: *const rl_buffer,
+        v_dims: *const u64,
+        v_strides: *const u64,
+        cos_table: *const rl_buffer,
+        sin_table: *const rl_buffer,
+        table_rows: u64,
+        start_pos: u64,
+        q_out: *const rl_buffer,
+        k_cache: *const rl_buffer,
+        v_cache: *const rl_buffer,
+        max_seq: u64,
+        n_rep: u64,
+        k_rep: *const rl_buffer,
+        v_rep: *const rl_buffer,
+    ) -> rl_status;
+    pub fn rl_qkv_rope_kv_append_repeat_f16(
+        ctx: *mut rl_context,
+        q_src: *const rl_buffer,
+        q_dims: *const u64,
+        q_strides: *const u64,
+        k_src: *const rl_buffer,
+        k_dims: *const u64,
+        k_strides: *const u64,
+        v_src: *const rl_buffer,
+        v_dims: *const u64,
+        v_strides: *const u64,
+        cos_table: *const rl_buffer,
+        sin_table: *const rl_buffer,
+        table_rows: u64,
+        start_pos: u64,
+        q_out: *const rl_buffer,
+        k_cache: *const rl_buffer,
+        v_cache: *const rl_buffer,
+        max_seq: u64,
+        n_rep: u64,
+        k_rep: *const rl_buffer,
+        v_rep: *const rl_buffer,
+    ) -> rl_status;
     // embedding (src/ops/embedding.rs)
     pub fn rl_embedding_f32(
         ctx: *mut rl_context,

@@ -92,7 +92,8 @@ const KERNEL_NAMES: &[&str] = &[
     "attention_softmax_f32", "attention_softmax_f16", "rope_f32", "rope_f16",
     "rope_strided_f32", "rope_strided_f16", "kv_cache_write_f32", "kv_cache_write_f16",
     "rope_kv_cache_write_f32", "rope_kv_cache_write_f16", "qkv_rope_kv_append_f32",
-    "qkv_rope_kv_append_f16", "embedding_f32", "embedding_f16", "attention_f32",
+    "qkv_rope_kv_append_f16", "qkv_rope_kv_append_repeat_f32", "qkv_rope_kv_append_repeat_f16",
+    "embedding_f32", "embedding_f16", "attention_f32",
     "attention_f16", "gqa_qk_f32", "gqa_qk_f16", "gqa_pv_f32", "gqa_pv_f16",
 ];
 

@@ -154,6 +154,12 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                                    _U64P, _BUF, _BUF, _U64, _U64, _BUF, _BUF, _BUF, _U64], _I32),
     "rl_qkv_rope_kv_append_f16": ([_P, _BUF, _U64P, _U64P, _BUF, _U64P, _U64P, _BUF, _U64P,
                                    _U64P, _BUF, _BUF, _U64, _U64, _BUF, _BUF, _BUF, _U64], _I32),
+    "rl_qkv_rope_kv_append_repeat_f32": ([_P, _BUF, _U64P, _U64P, _BUF, _U64P, _U64P, _BUF,
+                                          _U64P, _U64P, _BUF, _BUF, _U64, _U64, _BUF, _BUF,
+                                          _BUF, _U64, _U64, _BUF, _BUF], _I32),
+    "rl_qkv_rope_kv_append_repeat_f16": ([_P, _BUF, _U64P, _U64P, _BUF, _U64P, _U64P, _BUF,
+                                          _U64P, _U64P, _BUF, _BUF, _U64, _U64, _BUF, _BUF,
+                                          _BUF, _U64, _U64, _BUF, _BUF], _I32),
     "rl_embedding_f32": ([_P, _BUF, _U64, _U64, ctypes.POINTER(ctypes.c_uint32), _U64, _BUF],
                          _I32),
     "rl_embedding_f16": ([_P, _BUF, _U64, _U64, ctypes.POINTER(ctypes.c_uint32), _U64, _BUF],
@@ -496,6 +502,22 @@ class Context:
                    kb, _u64_array(kd), _u64_array(ks), vb, _u64_array(vd), _u64_array(vs), cos,
                    sin, cos.shape[0], start, q_out, k_cache, v_cache, k_cache.shape[2])
         return q_out
+
+    def qkv_rope_kv_append_repeat(self, q, k, v, cos, sin, start: int, k_cache, v_cache,
+                                  n_rep: int, q_out=None, k_rep=None, v_rep=None):
+        """qkv_rope_kv_append, then repeat_kv of the caches' first start + S
+        rows into contiguous [1, KVH * n_rep, start + S, D] outputs, in one
+        launch.  Returns (q_out, k_rep, v_rep)."""
+        (qb, qd, qs), (kb, kd, ks), (vb, vd, vs) = q, k, v
+        q_out = q_out or self.empty(qd, qb.dtype)
+        rep_shape = (kd[0], kd[1] * max(n_rep, 1), start + kd[2], kd[3])
+        k_rep = k_rep or self.empty(rep_shape, kb.dtype)
+        v_rep = v_rep or self.empty(rep_shape, vb.dtype)
+        self._call(f"rl_qkv_rope_kv_append_repeat_{self._sfx(qb)}", qb, _u64_array(qd),
+                   _u64_array(qs), kb, _u64_array(kd), _u64_array(ks), vb, _u64_array(vd),
+                   _u64_array(vs), cos, sin, cos.shape[0], start, q_out, k_cache, v_cache,
+                   k_cache.shape[2], n_rep, k_rep, v_rep)
+        return q_out, k_rep, v_rep
 
     def attention(self, q, k, v, scale: float, start: int, kv_len=None, out=None):
         """Fused attention core: q [B, QH, Q, D]; k, v [B, KVH, capacity, D]

@@ -519,24 +519,29 @@ rl_status rope_kv_entry(rl_context* ctx, const char* name, const char* write_nam
 
 // ------------------------------------------- Q, K and V of a layer, one launch
 
-// One [1, H, S, D] view moved to its destination rows, rotated or copied.
+// One [1, H, S, D] view moved to its destination rows, rotated or copied,
+// with the same optional second destination as RowJob.
 struct RowTask {
     const void* src;
     void* dst;
-    RowDims rd;
+    void* rep;
+    RowDimsN<3> rd;
     FastDiv packs_per_row;  // packs of pairs per row (half_dim / N)
     DstRows dst_rows;
     uint32_t n_items;       // rows * packs_per_row
+    uint32_t n_rep;
+    uint32_t rep_rows;
+    uint32_t rep_first;
     uint32_t first_block;   // blocks [first_block, next task's first_block)
     uint32_t rotate;
 };
 
 struct RowTasks {
-    RowTask task[3];
+    RowTask task[kMaxJobs];
 };
 
-// Blocks are split between the three tasks; each block serves one task
-// (a uniform branch), each thread UNROLL packs of pairs of it.
+// Blocks are split between the tasks; each block serves one task (a
+// uniform branch), each thread UNROLL packs of pairs of it.
 template <typename T, int N, int UNROLL>
 __global__ __launch_bounds__(kThreads) void k_rope_tasks(RowTasks tasks,
                                                          const float* __restrict__ cos_table,
@@ -544,16 +549,18 @@ __global__ __launch_bounds__(kThreads) void k_rope_tasks(RowTasks tasks,
                                                          uint32_t half_dim, uint32_t start) {
     typedef typename VecOf<T, N>::type V;
     typedef typename VecOf<float, N>::type VF;
-    const uint32_t k = (blockIdx.x >= tasks.task[1].first_block ? 1u : 0u) +
-                       (blockIdx.x >= tasks.task[2].first_block ? 1u : 0u);
+    uint32_t k = 0;
+#pragma unroll
+    for (int t = 1; t < kMaxJobs; ++t) k += blockIdx.x >= tasks.task[t].first_block ? 1u : 0u;
     const RowTask& task = tasks.task[k];
     const T* src = static_cast<const T*>(task.src);
     T* out = static_cast<T*>(task.dst);
+    T* rep = static_cast<T*>(task.rep);
     const uint64_t base =
         uint64_t(blockIdx.x - task.first_block) * kThreads * UNROLL + threadIdx.x;
     V a[UNROLL], b[UNROLL];
     VF c[UNROLL], s[UNROLL];
-    uint64_t dst_off[UNROLL];
+    uint64_t dst_off[UNROLL], rep_off[UNROLL];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
         const uint64_t i = base + uint64_t(u) * kThreads;
@@ -574,6 +581,8 @@ __global__ __launch_bounds__(kThreads) void k_rope_tasks(RowTasks tasks,
             const uint64_t dst_row =
                 uint64_t(group) * task.dst_rows.group_rows + task.dst_rows.first_row + position;
             dst_off[u] = dst_row * (2 * half_dim) + pair;
+            rep_off[u] = (uint64_t(group) * task.n_rep * task.rep_rows + task.rep_first +
+                          position) * (2 * half_dim) + pair;
         }
     }
 #pragma unroll
@@ -590,8 +599,17 @@ __global__ __launch_bounds__(kThreads) void k_rope_tasks(RowTasks tasks,
                     o2[j] = from_float<T>(second * c[u][j] + first * s[u][j]);
                 }
             }
-            store_stream(reinterpret_cast<V*>(out + dst_off[u]), o1);
-            store_stream(reinterpret_cast<V*>(out + dst_off[u] + half_dim), o2);
+            if (out) {
+                store_stream(reinterpret_cast<V*>(out + dst_off[u]), o1);
+                store_stream(reinterpret_cast<V*>(out + dst_off[u] + half_dim), o2);
+            }
+            if (rep) {
+                const uint64_t step = uint64_t(task.rep_rows) * (2 * half_dim);
+                for (uint32_t r = 0; r < task.n_rep; ++r) {
+                    store_stream(reinterpret_cast<V*>(rep + rep_off[u] + r * step), o1);
+                    store_stream(reinterpret_cast<V*>(rep + rep_off[u] + r * step + half_dim), o2);
+                }
+            }
         }
     }
 }
@@ -632,6 +650,14 @@ rl_status check_head_view(const rl_buffer* src, const uint64_t* dims, const uint
 // contiguous [1, QH, S, D] output, K rotated and V copied into rows start ..
 // start + S of their caches.  Checks in the reference's order: RoPE on Q,
 // RoPE on K, the append's shape check (ModelFormat), the two cache writes.
+//
+// With k_rep set, the same launch also writes tensor::repeat_kv of the
+// caches' prefix after the append -- rows 0 .. start + S, the cache's key()
+// and value() views (kv_cache.rs:87-99) -- as contiguous
+// [1, KVH * n_rep, start + S, D] tensors: the new rows straight from the
+// registers that hold them, the older rows 0 .. start copied from the cache
+// by two more jobs, which read only rows this launch does not write.
+// repeat_kv's checks (src/tensor/repeat_kv.rs:13-50) follow the append's.
 template <typename T>
 rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
                     const uint64_t* q_dims, const uint64_t* q_strides, const rl_buffer* k_src,
@@ -639,7 +665,9 @@ rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
                     const uint64_t* v_dims, const uint64_t* v_strides,
                     const rl_buffer* cos_table, const rl_buffer* sin_table, uint64_t table_rows,
                     uint64_t start, const rl_buffer* q_out, const rl_buffer* k_cache,
-                    const rl_buffer* v_cache, uint64_t max_seq) {
+                    const rl_buffer* v_cache, uint64_t max_seq, bool repeat = false,
+                    uint64_t n_rep = 0, const rl_buffer* k_rep = nullptr,
+                    const rl_buffer* v_rep = nullptr) {
     const char* write_name = sizeof(T) == 4 ? "kv_cache_write_f32" : "kv_cache_write_f16";
     for (int v = 0; v < 2; ++v) {  // Q, then K: RotaryEmbedding::forward_encode
         const rl_buffer* src = v == 0 ? q_src : k_src;
@@ -674,6 +702,18 @@ rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
     if (rl_status st = validate_kv_write(write_name, v_cache, max_seq, v_src, v_dims, v_strides,
                                          4, start, sizeof(T), false))
         return st;
+    const uint64_t total = start + k_dims[2];  // cache length after the append
+    if (repeat) {
+        if (n_rep == 0)
+            return fail(RL_ERR_MODEL_FORMAT, "repeat_kv repeats must be greater than zero");
+        if (k_dims[1] > UINT64_MAX / n_rep)
+            return fail(RL_ERR_MODEL_FORMAT, "repeat_kv head count overflow");
+        if (n_rep > UINT32_MAX || k_dims[1] * n_rep > UINT32_MAX || total > UINT32_MAX)
+            return fail(RL_ERR_INVALID_SHAPE, "repeat_kv dimension exceeds u32");
+        const uint64_t rep_numel = k_dims[0] * k_dims[1] * n_rep * total * k_dims[3];
+        if (rl_status st = check_output(k_rep, rep_numel, sizeof(T), "repeat_kv")) return st;
+        if (rl_status st = check_output(v_rep, rep_numel, sizeof(T), "repeat_kv")) return st;
+    }
     if (rl_status st = require_context(ctx)) return st;
     if (rl_status st = activate(ctx)) return st;
 
@@ -684,16 +724,36 @@ rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
     void* dsts[3] = {q_out->data, k_cache->data, v_cache->data};
     const uint64_t* dims[3] = {q_dims, k_dims, v_dims};
     const uint64_t* strides[3] = {q_strides, k_strides, v_strides};
+    // Jobs 3 and 4 (with a repeat after a non-empty prefix): cache rows
+    // 0 .. start of K and V, a [1, KVH, start, D] view of the cache.
+    const int n_jobs = repeat && start > 0 ? 5 : 3;
+    const uint64_t kvh = k_dims[1], hd = k_dims[3];
+    const uint64_t prefix_dims[4] = {1, kvh, start, hd};
+    const uint64_t prefix_strides[4] = {kvh * max_seq * hd, max_seq * hd, hd, 1};
+    auto set_rep = [&](auto& job, int t) {
+        if (!repeat || t == 0) return;
+        job.rep = (t % 2 == 1 ? k_rep : v_rep)->data;
+        job.n_rep = uint32_t(n_rep);
+        job.rep_rows = uint32_t(total);
+        job.rep_first = t < 3 ? uint32_t(start) : 0u;
+    };
     if (const int lanes = row_lanes<T>(q_dims[3]);
-        lanes && aligned_to(cs, 64 / sizeof(T)) && aligned_to(sn, 64 / sizeof(T))) {
+        lanes && aligned_to(cs, 64 / sizeof(T)) && aligned_to(sn, 64 / sizeof(T)) &&
+        (!repeat || (aligned_to(k_rep->data, 16) && aligned_to(v_rep->data, 16)))) {
         RowJobs jobs{};
         bool ok = true;
-        for (int t = 0; t < 3 && ok; ++t)
-            ok = make_job<T>(jobs.job[t], srcs[t], dims[t], strides[t], 4, dsts[t],
-                             t == 0 ? DstRows{uint32_t(dims[t][2]), 0}
-                                    : DstRows{uint32_t(max_seq), uint32_t(start)},
-                             t < 2);
-        if (ok && launch_jobs<T>(ctx, jobs, 3, lanes, cs, sn, start))
+        for (int t = 0; t < n_jobs && ok; ++t) {
+            if (t < 3)
+                ok = make_job<T>(jobs.job[t], srcs[t], dims[t], strides[t], 4, dsts[t],
+                                 t == 0 ? DstRows{uint32_t(dims[t][2]), 0}
+                                        : DstRows{uint32_t(max_seq), uint32_t(start)},
+                                 t < 2);
+            else
+                ok = make_job<T>(jobs.job[t], t == 3 ? k_cache->data : v_cache->data,
+                                 prefix_dims, prefix_strides, 4, nullptr, DstRows{0, 0}, false);
+            set_rep(jobs.job[t], t);
+        }
+        if (ok && launch_jobs<T>(ctx, jobs, n_jobs, lanes, cs, sn, start))
             return after_launch(ctx, name);
     }
     int n = 16 / int(sizeof(T));
@@ -703,24 +763,33 @@ rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
             ok = aligned_to(srcs[t], n * sizeof(T)) && aligned_to(dsts[t], n * sizeof(T));
             for (uint32_t d = 0; d < 3 && ok; ++d) ok = strides[t][d] % n == 0;
         }
+        if (repeat && ok)
+            ok = aligned_to(k_rep->data, n * sizeof(T)) && aligned_to(v_rep->data, n * sizeof(T));
         if (ok) break;
         n >>= 1;
     }
     constexpr int U = 1;
     RowTasks tasks{};
     uint64_t blocks = 0;
-    for (int t = 0; t < 3; ++t) {
+    for (int t = 0; t < kMaxJobs; ++t) {
         RowTask& task = tasks.task[t];
-        task.src = srcs[t];
-        task.dst = dsts[t];
-        task.rd = make_row_dims(dims[t], strides[t], 4);
+        if (t >= n_jobs) {
+            task.first_block = UINT32_MAX;
+            continue;
+        }
+        const uint64_t* td = t < 3 ? dims[t] : prefix_dims;
+        const uint64_t* ts = t < 3 ? strides[t] : prefix_strides;
+        task.src = t < 3 ? srcs[t] : (t == 3 ? k_cache->data : v_cache->data);
+        task.dst = t < 3 ? dsts[t] : nullptr;
+        task.rd = make_row_dims<3>(td, ts, 4);
         task.packs_per_row = FastDiv(uint32_t(half / n));
-        task.dst_rows = t == 0 ? DstRows{uint32_t(dims[t][2]), 0}
+        task.dst_rows = t == 0 ? DstRows{uint32_t(td[2]), 0}
                                : DstRows{uint32_t(max_seq), uint32_t(start)};
-        const uint64_t rows = dims[t][0] * dims[t][1] * dims[t][2];
+        const uint64_t rows = td[0] * td[1] * td[2];
         task.n_items = uint32_t(rows * (half / n));
         task.first_block = uint32_t(blocks);
         task.rotate = t < 2 ? 1u : 0u;
+        set_rep(task, t);
         blocks += ceil_div(task.n_items, uint64_t(kThreads) * U);
     }
     if (blocks > (1u << 30)) return fail(RL_ERR_INVALID_SHAPE, "%s: work exceeds one launch", name);
@@ -776,6 +845,34 @@ rl_status rl_qkv_rope_kv_append_f16(rl_context* ctx, const rl_buffer* q_src,
     return qkv_entry<half_t>(ctx, "qkv_rope_kv_append_f16", q_src, q_dims, q_strides, k_src,
                              k_dims, k_strides, v_src, v_dims, v_strides, cos_table, sin_table,
                              table_rows, start_pos, q_out, k_cache, v_cache, max_seq);
+}
+
+rl_status rl_qkv_rope_kv_append_repeat_f32(
+    rl_context* ctx, const rl_buffer* q_src, const uint64_t* q_dims, const uint64_t* q_strides,
+    const rl_buffer* k_src, const uint64_t* k_dims, const uint64_t* k_strides,
+    const rl_buffer* v_src, const uint64_t* v_dims, const uint64_t* v_strides,
+    const rl_buffer* cos_table, const rl_buffer* sin_table, uint64_t table_rows,
+    uint64_t start_pos, const rl_buffer* q_out, const rl_buffer* k_cache,
+    const rl_buffer* v_cache, uint64_t max_seq, uint64_t n_rep, const rl_buffer* k_rep,
+    const rl_buffer* v_rep) {
+    return qkv_entry<float>(ctx, "qkv_rope_kv_append_repeat_f32", q_src, q_dims, q_strides,
+                            k_src, k_dims, k_strides, v_src, v_dims, v_strides, cos_table,
+                            sin_table, table_rows, start_pos, q_out, k_cache, v_cache, max_seq,
+                            true, n_rep, k_rep, v_rep);
+}
+
+rl_status rl_qkv_rope_kv_append_repeat_f16(
+    rl_context* ctx, const rl_buffer* q_src, const uint64_t* q_dims, const uint64_t* q_strides,
+    const rl_buffer* k_src, const uint64_t* k_dims, const uint64_t* k_strides,
+    const rl_buffer* v_src, const uint64_t* v_dims, const uint64_t* v_strides,
+    const rl_buffer* cos_table, const rl_buffer* sin_table, uint64_t table_rows,
+    uint64_t start_pos, const rl_buffer* q_out, const rl_buffer* k_cache,
+    const rl_buffer* v_cache, uint64_t max_seq, uint64_t n_rep, const rl_buffer* k_rep,
+    const rl_buffer* v_rep) {
+    return qkv_entry<half_t>(ctx, "qkv_rope_kv_append_repeat_f16", q_src, q_dims, q_strides,
+                             k_src, k_dims, k_strides, v_src, v_dims, v_strides, cos_table,
+                             sin_table, table_rows, start_pos, q_out, k_cache, v_cache, max_seq,
+                             true, n_rep, k_rep, v_rep);
 }
 
 rl_status rl_rope_kv_cache_write_f32(rl_context* ctx, const rl_buffer* src, const uint64_t* dims,

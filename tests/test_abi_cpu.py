@@ -402,6 +402,38 @@ def test_qkv_rope_kv_append_validation():
     assert st == POS
 
 
+def test_qkv_rope_kv_append_repeat_validation():
+    # the append's checks first (same as rl_qkv_rope_kv_append_f16), then
+    # repeat_kv's (src/tensor/repeat_kv.rs:21-25, :42-44), then the outputs
+    f = "rl_qkv_rope_kv_append_repeat_f16"
+    tab = buf(8 * 2, 4)
+    qd, qs = u64s(1, 3, 2, 4), u64s(24, 4, 12, 1)
+    kd, ks = u64s(1, 1, 2, 4), u64s(8, 4, 4, 1)
+
+    def go(start=0, n_rep=3, k_rep=None, v_rep=None, max_seq=8, kcache=None):
+        rep = 1 * 1 * n_rep * (start + 2) * 4
+        return call(f, buf(24, 2), qd, qs, buf(8, 2), kd, ks, buf(8, 2), kd, ks, tab, tab, 8,
+                    start, buf(24, 2), kcache or buf(32, 2), buf(32, 2), max_seq, n_rep,
+                    k_rep or buf(rep, 2), v_rep or buf(rep, 2))
+
+    assert go()[0] == DEVICE
+    assert go(start=3)[0] == DEVICE
+    st, msg = go(n_rep=0)
+    assert st == FORMAT and "repeat_kv repeats must be greater than zero" in msg
+    st, msg = go(n_rep=0, kcache=buf(32, 4))  # the cache write's check comes first
+    assert st == DTYPE and "kv_cache_write_f16" in msg
+    st, msg = go(n_rep=1 << 63)  # 1 head x 2^63 fits u64, not u32
+    assert st == SHAPE and "exceeds u32" in msg
+    kd2, ks2 = u64s(1, 2, 2, 4), u64s(16, 4, 8, 1)  # 2 KV heads: 2 x 2^63 overflows
+    st, msg = call(f, buf(24, 2), qd, qs, buf(16, 2), kd2, ks2, buf(16, 2), kd2, ks2, tab, tab,
+                   8, 0, buf(24, 2), buf(64, 2), buf(64, 2), 8, 1 << 63, buf(64, 2), buf(64, 2))
+    assert st == FORMAT and "head count overflow" in msg
+    st, msg = go(start=3, k_rep=buf(3 * 5 * 4 - 1, 2))
+    assert st == SHAPE and "repeat_kv" in msg
+    st, msg = go(start=3, v_rep=buf(3 * 5 * 4, 4))
+    assert st == SHAPE and "repeat_kv" in msg
+
+
 def test_attention_noalloc_rejects_decode_shapes_beyond_its_scratch():
     # rl_attention_f16_noalloc: the checks of rl_attention_f16, then the decode
     # path's needs against the static scratch (8 MiB - 16 KiB of partials,

@@ -622,6 +622,48 @@ def test_qkv_rope_kv_append_one_launch(ctx, dtype, qh, kvh, seq, hd, start, max_
     assert_bitexact(dvc.numpy(), v_ref, "V cache")
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("qh,kvh,seq,hd,start,max_seq", [(15, 5, 4096, 64, 0, 4096),
+                                                         (15, 5, 1, 64, 100, 4096),
+                                                         (6, 2, 77, 32, 9, 90),
+                                                         (4, 4, 40, 16, 3, 50),
+                                                         (3, 1, 19, 128, 2, 30),
+                                                         (4, 2, 7, 6, 3, 12)])
+def test_qkv_rope_kv_append_repeat_one_launch(ctx, dtype, qh, kvh, seq, hd, start, max_seq):
+    """The QKV launch with repeat_kv of both caches' prefixes after the append
+    equals rope (Q, K), kv_cache_write (K, V), then repeat_kv of the first
+    start + S cache rows made contiguous (tensor/repeat_kv.rs:31-35)."""
+    n_rep = qh // kvh
+    c, s = o.rope_table(hd, max_seq, 10000.0)
+    qp = norm(("qkvr", "q"), (1, seq, qh, hd), dtype)
+    kp = norm(("qkvr", "k"), (1, seq, kvh, hd), dtype)
+    vp = norm(("qkvr", "v"), (1, seq, kvh, hd), dtype)
+    kc0 = norm(("qkvr", "kc"), (1, kvh, max_seq, hd), dtype)
+    vc0 = norm(("qkvr", "vc"), (1, kvh, max_seq, hd), dtype)
+
+    def view(h):
+        return [1, h, seq, hd], [seq * h * hd, hd, h * hd, 1]
+
+    qd, qs = view(qh)
+    kd, ks = view(kvh)
+    dkc, dvc = ctx.upload(kc0), ctx.upload(vc0)
+    dcos, dsin = ctx.upload(c), ctx.upload(s)
+    q_out, k_rep, v_rep = run(ctx, lambda: ctx.qkv_rope_kv_append_repeat(
+        (ctx.upload(qp), qd, qs), (ctx.upload(kp), kd, ks), (ctx.upload(vp), kd, ks),
+        dcos, dsin, start, dkc, dvc, n_rep))
+    q_ref = o.rope(o.contiguous(qp.ravel(), qd, qs), c, s, start)
+    k_ref = o.kv_cache_write(kc0, o.rope(o.contiguous(kp.ravel(), kd, ks), c, s, start), start)
+    v_ref = o.kv_cache_write(vc0, o.contiguous(vp.ravel(), kd, ks), start)
+    total = start + seq
+    assert_bitexact(q_out.numpy(), q_ref, "Q")
+    assert_bitexact(dkc.numpy(), k_ref, "K cache")
+    assert_bitexact(dvc.numpy(), v_ref, "V cache")
+    assert_bitexact(k_rep.numpy(), o.repeat_kv(np.ascontiguousarray(k_ref[:, :, :total]), n_rep),
+                    "repeated K")
+    assert_bitexact(v_rep.numpy(), o.repeat_kv(np.ascontiguousarray(v_ref[:, :, :total]), n_rep),
+                    "repeated V")
+
+
 def test_kv_cache_appends_reference_kat(ctx):
     """src/model/kv_cache.rs:213-258: two one-token f16 appends into a
     [1, 2, 8, 4] cache, then the narrowed [1, 2, 2, 4] prefix made
