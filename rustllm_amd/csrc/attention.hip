@@ -827,36 +827,64 @@ __global__ __launch_bounds__(64) void k_attention_rows(const T* __restrict__ q,
 
 // ------------------------------------------------- split keys (decode)
 
-// One wave merges one query row's `splits` partials (the maxima and sums
-// read by all lanes at once, the weights kept in `w`, this wave's LDS).
+// The merge of one KV head's partials by the workgroup that finishes its
+// last split: thread (r, d) merges output element d of row r over every
+// split, loading kMergeChunk splits' (max, sum, value) at once -- indices
+// past the last split are clamped and masked -- and folding them into a
+// running max, sum and value.  With up to kMergeChunk splits (4096 keys at
+// 256 keys per split) the merge is one memory round trip.
 constexpr uint32_t kMaxSplits = 1024;
+constexpr int kMergeChunk = 16;
+
+// Agent-coherent store and load of a partial (relaxed atomics at agent
+// scope: global_store / global_load with sc1, which write through and read
+// past the XCD's own L2).
+__device__ inline void publish(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float observe(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 template <typename T>
-__device__ inline void merge_splits(const float* src, T* dst, uint32_t splits,
-                                    uint32_t head_dim, float* w) {
-    const uint32_t lane = threadIdx.x % 64;
-    const uint32_t stride = head_dim + 2;
-    float mt = -INFINITY;
-    for (uint32_t s = lane; s < splits; s += 64) mt = fmaxf(mt, src[s * stride]);
-    mt = wave_max_dpp(mt);
-    float lt = 0.0f;
-    for (uint32_t s = lane; s < splits; s += 64) {
-        const float ms = src[s * stride];
-        const float ws = ms == -INFINITY ? 0.0f : exp_fast(ms - mt);
-        w[s] = ws;
-        lt += src[s * stride + 1] * ws;
-    }
-    lt = wave_sum_dpp(lt);
-    // the weights other lanes wrote
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const float inv = 1.0f / lt;
-    for (uint32_t d = lane; d < head_dim; d += 64) {
-        float acc = 0.0f;
-#pragma unroll 8
-        for (uint32_t s = 0; s < splits; ++s) acc += src[s * stride + 2 + d] * w[s];
-        dst[d] = from_float<T>(acc * inv);
+__device__ inline void merge_head(const float* part, T* __restrict__ out,
+                                  const AttnParams& p, uint32_t b, uint32_t first_head,
+                                  uint32_t R, uint32_t splits) {
+    const uint32_t D = p.head_dim;
+    const uint32_t stride = D + 2;
+    for (uint32_t i = threadIdx.x; i < R * D; i += blockDim.x) {
+        const uint32_t r = i / D, d = i % D;
+        const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
+                             r % p.q_len;
+        const float* src = part + row * splits * stride;
+        float mt = -INFINITY, lt = 0.0f, acc = 0.0f;
+        for (uint32_t s0 = 0; s0 < splits; s0 += kMergeChunk) {
+            float mv[kMergeChunk], lv[kMergeChunk], ov[kMergeChunk];
+#pragma unroll
+            for (int j = 0; j < kMergeChunk; ++j) {
+                const uint32_t sp = min(s0 + j, splits - 1);
+                mv[j] = observe(src + sp * stride);
+                lv[j] = observe(src + sp * stride + 1);
+                ov[j] = observe(src + sp * stride + 2 + d);
+            }
+            float mc = mt;
+#pragma unroll
+            for (int j = 0; j < kMergeChunk; ++j)
+                if (s0 + j < splits) mc = fmaxf(mc, mv[j]);
+            if (mc == -INFINITY) continue;  // no key seen yet
+            const float keep = mt == -INFINITY ? 0.0f : exp_fast(mt - mc);
+            lt *= keep;
+            acc *= keep;
+#pragma unroll
+            for (int j = 0; j < kMergeChunk; ++j) {
+                const bool use = s0 + j < splits && mv[j] != -INFINITY;
+                const float w = use ? exp_fast(mv[j] - mc) : 0.0f;
+                lt += lv[j] * w;
+                acc += ov[j] * w;
+            }
+            mt = mc;
+        }
+        out[row * D + d] = from_float<T>(acc * (1.0f / lt));
     }
 }
 
@@ -902,10 +930,33 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
     const uint32_t base = split * kSplitKeys + wave * 64;
     const uint32_t n = p.kv_len > base ? min(64u, p.kv_len - base) : 0u;  // this wave's keys
     const uint32_t key = base + lane;
+    // This thread's query elements first (row r = g * q_len + qi is query qi
+    // of head first_head + g), so that their round trip is the key and
+    // value loads' one rather than a second one after them.
+    constexpr int QPT = (RM * DMAX + 64 * kSplitWaves - 1) / (64 * kSplitWaves);
+    T qreg[QPT];
+#pragma unroll
+    for (int j = 0; j < QPT; ++j) {
+        const uint32_t i = threadIdx.x + uint32_t(j) * 64 * kSplitWaves;
+        const uint32_t r = i / DMAX, d = i % DMAX;
+        T x = T(0.0f);
+        if (i < uint32_t(RM * DMAX) && r < R && d < D) {
+            const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
+                                 r % p.q_len;
+            x = q[row * D + d];
+        }
+        qreg[j] = x;
+    }
     // value rows to LDS when 64 of them fit the stage, else read in place
     const bool staged = vec_rows && 64 * D * sizeof(T) <= kStageBytes;
     if (staged) {
         const uint32_t chunks = n * D * sizeof(T) / 16;  // 16-byte pieces of the n rows
+        // rows n .. 63 (a wave past the last key): zeros, so that the value
+        // reads below need no bounds; written before the copies into rows
+        // 0 .. n are issued, which they do not overlap
+        const uint32_t all = 64 * D * sizeof(T) / 16;
+        for (uint32_t c = chunks + lane; c < all; c += 64)
+            *reinterpret_cast<uint4*>(vstage[wave] + c * 16) = uint4{0, 0, 0, 0};
         const unsigned char* src = reinterpret_cast<const unsigned char*>(vh + uint64_t(base) * D);
         for (uint32_t c0 = 0; c0 < chunks; c0 += 64) {
             if (c0 + lane < chunks)
@@ -913,32 +964,28 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
                     src + uint64_t(c0 + lane) * 16,
                     (__attribute__((address_space(3))) void*)(vstage[wave] + c0 * 16), 16, 0, 0);
         }
-        // rows n .. 63 (a wave past the last key): zeros, so that the value
-        // reads below need no bounds
-        const uint32_t all = 64 * D * sizeof(T) / 16;
-        for (uint32_t c = chunks + lane; c < all; c += 64)
-            *reinterpret_cast<uint4*>(vstage[wave] + c * 16) = uint4{0, 0, 0, 0};
     }
-    // key rows (lane = key), every load before the first use; packs past
-    // the head size are zero
+    // key rows (lane = key), every load issued here, before the barrier:
+    // unconditional, from a valid row (a lane past the wave's keys reads the
+    // last key and its scores are masked below) and a valid pack (packs past
+    // the head size read pack 0 and are zeroed), since loads under a branch
+    // would be sunk past the barrier into a second round trip
     constexpr int PACKS = DMAX / N;
     V kv[PACKS];
-    if (vec_rows && lane < n) {
-        const T* krow = kh + uint64_t(key) * D;
+    if (vec_rows) {
+        const uint32_t krow_i = lane < n ? key : (p.kv_len > 0 ? p.kv_len - 1 : 0);
+        const T* krow = kh + uint64_t(krow_i) * D;
 #pragma unroll
-        for (int i = 0; i < PACKS; ++i)
-            kv[i] = uint32_t(i * N) < D ? *reinterpret_cast<const V*>(krow + i * N) : V{};
-    }
-    // row r = g * q_len + qi is query qi of head first_head + g
-    for (uint32_t i = threadIdx.x; i < RM * DMAX; i += 64 * kSplitWaves) {
-        const uint32_t r = i / DMAX, d = i % DMAX;
-        T x = T(0.0f);
-        if (r < R && d < D) {
-            const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
-                                 r % p.q_len;
-            x = q[row * D + d];
+        for (int i = 0; i < PACKS; ++i) {
+            const bool in = uint32_t(i * N) < D;
+            const V x = *reinterpret_cast<const V*>(krow + (in ? i * N : 0));
+            kv[i] = in ? x : V{};
         }
-        qs[i] = x;
+    }
+#pragma unroll
+    for (int j = 0; j < QPT; ++j) {
+        const uint32_t i = threadIdx.x + uint32_t(j) * 64 * kSplitWaves;
+        if (i < uint32_t(RM * DMAX)) qs[i] = qreg[j];
     }
     __syncthreads();
 
@@ -1077,39 +1124,33 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
         for (uint32_t d = lane; d < D; d += 64) {
             float acc = 0.0f;
             for (int w = 0; w < kSplitWaves; ++w) acc += merge_o[w][r][d] * scale_w[w];
-            dst[2 + d] = acc;
+            publish(dst + 2 + d, acc);
         }
         if (lane == 0) {
-            dst[0] = mt;
-            dst[1] = lt;
+            publish(dst, mt);
+            publish(dst + 1, lt);
         }
     }
 
     // Hand-off: the workgroup that completes a KV head's last split merges
-    // that head's rows (one wave per row), so a decode step is one launch.
-    // Every wave waits for its partial stores to complete (vmcnt), the
-    // barrier orders them before the thread that draws the ticket, and that
-    // thread's device-scope release publishes them (one L2 write-back per
-    // workgroup -- the XCDs' L2s are not coherent); the last workgroup reads
-    // after an acquire and puts the ticket back to zero for the next launch.
+    // that head's rows, so a decode step is one launch.  The partials were
+    // stored agent-coherent (publish: written through the XCD's L2), every
+    // wave waits for those stores to complete (vmcnt) before the barrier, and
+    // only then does one thread draw the ticket -- no L2 write-back, which
+    // an agent-scope release fence would make every workgroup pay in turn.
+    // The last workgroup reads the partials agent-coherent as well and puts
+    // the ticket back to zero for the next launch.
     __shared__ uint32_t ticket;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (threadIdx.x == 0)
         ticket = __hip_atomic_fetch_add(&tickets[kvb], 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
-    }
     __syncthreads();
     if (ticket != splits - 1) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (threadIdx.x == 0) tickets[kvb] = 0;
-    float* w = reinterpret_cast<float*>(vstage[wave]);  // the stage is free now
-    for (uint32_t r = wave; r < R; r += kSplitWaves) {
-        const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
-                             r % p.q_len;
-        merge_splits<T>(part + row * splits * stride, out + row * D, splits, D, w);
-    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&tickets[kvb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    merge_head<T>(part, out, p, b, first_head, R, splits);
 }
 
 // ------------------------------------------------------------ validation
@@ -1353,7 +1394,7 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
     const uint64_t dpl = ceil_div(s.head_dim, 64);
     const uint64_t rm = R <= 4 ? 4 : R <= 8 ? 8 : R <= 16 ? 16 : 32;
     const uint64_t needed = std::min<uint64_t>(s.kv_len, start + s.q_len);  // keys any row sees
-    const uint64_t splits = ceil_div(needed, kSplitKeys);
+    const uint64_t splits = ceil_div(needed, uint64_t(kSplitKeys));
     const bool split_shape = R <= 32 && s.head_dim <= 256 && rm * dpl <= 32 && needed >= 512 &&
                              splits <= kMaxSplits;
     const uint64_t part_bytes = rows * splits * (s.head_dim + 2) * sizeof(float);
