@@ -14,7 +14,8 @@
 //    workgroup's 128 key rows are loaded whole into LDS in the order that
 //    swaps bits 2 and 3 of the key index, so every lane ends up holding runs
 //    of 8 consecutive keys of one query row; each wave stages its score tile
-//    in LDS and writes whole 256-byte row segments per 16 lanes.
+//    in LDS and writes 256-byte row segments per 16 lanes.  All key tiles of
+//    one (head, query tile) run on one XCD.
 //  * PV computes O^T = V^T P^T in steps of 128 keys: each wave stages its
 //    32 x 128 probabilities in LDS (whole 256-byte row segments per 16
 //    lanes), V goes through LDS row-major and its transposed operand comes
@@ -36,17 +37,19 @@ struct GqaParams {
     uint32_t k_tiles;         // 128-key tiles per query tile (QK^T MFMA kernels)
     uint32_t k_per_block;     // key tiles one f32 QK^T workgroup computes in turn
     uint32_t k_groups;        // f32 QK^T workgroups per query tile
+    uint32_t qk_groups;       // (head, query tile) groups of the f16 QK^T kernel
 };
 
 // 16-byte store / load of f16 scores, streamed past the caches (STREAM,
-// non-temporal) or plain.  Measured on [15, 4096, kv_len] scores: QK^T rows
-// that are whole 128-byte lines stream (4096 keys: 99 us, plain 176), rows
-// on the 16-byte grid but not the line grid store plainly so the L2 merges
-// the lines they share (1000 keys: 36 us, streamed 52), ragged rows stream
-// (224 us, plain 259); PV reads ragged rows and rows off the line grid
-// plainly (142 us, streamed 165; 1000 keys 24.6 us, streamed 27.1).
-// A template parameter, not a flag: the compiler merges the two stores of
-// a run-time choice into one plain store.
+// non-temporal) or plain.  Measured on [15, 4096, kv_len] scores with the
+// QK^T key tiles of a query tile on one XCD: QK^T rows that are whole
+// 128-byte lines stream (4096 keys: 99 us, plain 122); rows off the line
+// grid -- 1000 keys, or 4093 keys, whose rows start off the 16-byte grid --
+// store plainly, so the XCD's L2 merges the lines neighbouring key tiles
+// share before they reach HBM (1000 keys: 11.7 us; 4093 keys: 126 us,
+// streamed 182).  PV reads rows off the line grid plainly (1000 keys 24.6 us,
+// streamed 27.1; 4093 keys 124 us).  A template parameter, not a flag: the
+// compiler merges the two stores of a run-time choice into one plain store.
 template <bool STREAM>
 __device__ inline void put_scores(h8* dst, h8 w) {
     if constexpr (STREAM)
@@ -62,6 +65,27 @@ __device__ inline h8 get_scores(const h8* src) {
         return *src;
 }
 
+// The same for 8 scores at any 2-byte alignment: a row of kv_len % 8 != 0
+// scores starts (row x kv_len) mod 8 elements past a 16-byte boundary.
+// gfx950 runs global memory in unaligned mode, so this is still one 16-byte
+// access (split by the hardware where it crosses a line).
+typedef half_t h8u __attribute__((ext_vector_type(8), aligned(2)));
+template <bool STREAM>
+__device__ inline void put_scores_u(half_t* dst, h8 w) {
+    const h8u v = w;
+    if constexpr (STREAM)
+        __builtin_nontemporal_store(v, reinterpret_cast<h8u*>(dst));
+    else
+        *reinterpret_cast<h8u*>(dst) = v;
+}
+template <bool STREAM>
+__device__ inline h8 get_scores_u(const half_t* src) {
+    if constexpr (STREAM)
+        return __builtin_nontemporal_load(reinterpret_cast<const h8u*>(src));
+    else
+        return *reinterpret_cast<const h8u*>(src);
+}
+
 __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
     const uint32_t kv_heads = p.q_heads / p.group;
     return (bh / p.q_heads) * kv_heads + (bh % p.q_heads) / p.group;
@@ -69,16 +93,10 @@ __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
 
 // ------------------------------------------------------------ QK^T, MFMA
 
-// SHIFT: kv_len is not a multiple of 8, so a score row starts `lead`
-// elements past a 16-byte boundary (the output buffer itself is 16-byte
-// aligned).  A tile then owns the 16-byte chunks of its rows that start at
-// keys kbase - lead .. kbase + 127 - lead: it also scores the (up to 7) keys
-// before kbase, with v_dot2 on the vector ALUs, and leaves its last `lead`
-// keys to the next tile, so every chunk is one whole store.  In LDS a row
-// sits `lead` columns to the right (LDS column y = key kbase - lead + y).
-// Only a row's first chunk (tile 0) and last chunk (the last tile) reach
-// past the row; those are stored element by element.
-template <int NT, bool SHIFT, bool STREAM>
+// Rows of kv_len % 8 != 0 scores start off the 16-byte grid; their 8-score
+// chunks go out as unaligned 16-byte stores (put_scores_u), and a row's last
+// partial chunk element by element.
+template <int NT, bool STREAM>
 __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ q,
                                                      const half_t* __restrict__ k,
                                                      half_t* __restrict__ out, GqaParams p) {
@@ -88,14 +106,23 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     constexpr int KS = D + 8;    // LDS row stride (halves) of the key tile
     constexpr int ROW_CHUNKS = D / 8;
     __shared__ __align__(16) half_t tile[4][32 * TS];
-    __shared__ __align__(16) half_t ks[(128 + (SHIFT ? 8 : 0)) * KS];  // SHIFT: + 8 rows before
+    __shared__ __align__(16) half_t ks[128 * KS];
     const uint32_t wave = threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t col = lane % 32;
     const uint32_t hs = lane / 32;
-    // block = (head, 128-query tile, 128-key tile); wave = 32 queries x 128 keys
-    const uint32_t kt_blk = blockIdx.x % p.k_tiles;
-    const uint32_t rest = blockIdx.x / p.k_tiles;
+    // block = (head, 128-query tile, 128-key tile); wave = 32 queries x 128 keys.
+    // Hardware block b runs on XCD b mod 8: the key tiles of one (head, query
+    // tile) group all go to the XCD of the group's index mod 8, so the cache
+    // lines that neighbouring key tiles share (rows off the line grid) are
+    // merged in one L2 and the group's queries meet there too.  The grid is
+    // padded to whole groups per XCD.
+    const uint32_t xcd = blockIdx.x % 8, xi = blockIdx.x / 8;
+    const uint32_t group = (xi / p.k_tiles) * 8 + xcd;
+    if (group >= p.qk_groups) return;  // padding (the whole block)
+    const uint32_t lb = group * p.k_tiles + xi % p.k_tiles;
+    const uint32_t kt_blk = lb % p.k_tiles;
+    const uint32_t rest = lb / p.k_tiles;
     const uint32_t qt = rest % p.q_tiles;
     const uint32_t bh = rest / p.q_tiles;
     const uint32_t q0 = qt * 128 + wave * 32;
@@ -121,28 +148,9 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
         *reinterpret_cast<h8*>(ks + perm32(j) * KS + d0) =
             *reinterpret_cast<const h8*>(kh + uint64_t(key) * D + d0);
     }
-    if constexpr (SHIFT) {
-        // key rows kbase - 8 .. kbase - 1 (tile 0 has none: rows 0.. then,
-        // whose scores are not used)
-        half_t* kpre = ks + 128 * KS;
-        for (uint32_t chunk = threadIdx.x; chunk < 8 * ROW_CHUNKS; chunk += 256) {
-            const uint32_t j = chunk / ROW_CHUNKS;
-            const uint32_t d0 = (chunk % ROW_CHUNKS) * 8;
-            const uint32_t key = kbase >= 8 ? kbase - 8 + j : min(j, p.kv_len - 1);
-            *reinterpret_cast<h8*>(kpre + j * KS + d0) =
-                *reinterpret_cast<const h8*>(kh + uint64_t(key) * D + d0);
-        }
-    }
     __syncthreads();
     if (q0 >= p.q_len) return;  // (no barrier below)
     half_t* my = tile[wave];
-    // elements between a row's first score of this tile and the 16-byte
-    // boundary at or before it: (row index x kv_len) mod 8, exact in 32-bit
-    // arithmetic (kbase is a multiple of 128)
-    auto lead_of = [&](uint32_t r) -> uint32_t {
-        return ((bh * p.q_len + q0 + r) * p.kv_len) & 7u;
-    };
-    const uint32_t my_lead = SHIFT ? lead_of(col) : 0u;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {  // four 32-key tiles
         const uint32_t k0 = kbase + t * 32;
@@ -161,40 +169,7 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
             h8 w;
 #pragma unroll
             for (int e = 0; e < 8; ++e) w[e] = half_t(s[8 * half + e]);
-            half_t* dst = my + col * TS + t * 32 + 16 * half + 8 * hs;
-            if constexpr (SHIFT) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) dst[my_lead + e] = w[e];
-            } else {
-                *reinterpret_cast<h8*>(dst) = w;
-            }
-        }
-    }
-    if constexpr (SHIFT) {
-        if (kbase > 0) {
-            // the scores of keys kbase - 8 + j of this lane's query: its half
-            // of the head (v_dot2, f32 sums), plus the other half's
-            const half_t* kpre = ks + 128 * KS + 8 * hs;
-            float ex[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float a = 0.0f;
-#pragma unroll
-                for (int c = 0; c < DC; ++c) {
-                    const h8 kk = *reinterpret_cast<const h8*>(kpre + j * KS + 16 * c);
-#pragma unroll
-                    for (int e = 0; e < 8; e += 2)
-                        a = __builtin_amdgcn_fdot2(h2{qf[c][e], qf[c][e + 1]},
-                                                   h2{kk[e], kk[e + 1]}, a, false);
-                }
-                ex[j] = a + __shfl_xor(a, 32, 64);
-            }
-            // LDS columns 0 .. lead - 1: keys kbase - lead .. kbase - 1
-            if (hs == 0) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (j + my_lead >= 8) my[col * TS + (j + my_lead - 8)] = half_t(ex[j]);
-            }
+            *reinterpret_cast<h8*>(my + col * TS + t * 32 + 16 * half + 8 * hs) = w;
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -202,50 +177,7 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // rows of the tile to memory: 16 lanes per 256-byte row segment
     const uint32_t keys_here = min(128u, p.kv_len - kbase);
-    if constexpr (SHIFT) {
-        // Chunk c of row r: LDS columns 8c .. 8c + 7, the row's keys
-        // kbase - lead + 8c ..  The tile owns keys [own_lo, own_hi) of the row:
-        // from kbase - lead (0 in tile 0) to kbase + 128 - lead (kv_len in the
-        // last tile).  Whole chunks: 32 rows x 17 slots over the lanes.
-        const bool last_tile = kbase + 128 >= p.kv_len;
-#pragma unroll
-        for (int i = 0; i < 9; ++i) {
-            const uint32_t slot = i * 64 + lane;
-            const uint32_t r = slot / 17, lo = 8 * (slot % 17);
-            if (slot >= 32 * 17 || q0 + r >= p.q_len) continue;
-            const uint32_t lead = lead_of(r);
-            // owned LDS columns [y_lo, y_hi)
-            const uint32_t y_lo = kbase == 0 ? lead : 0u;
-            const uint32_t y_hi = last_tile ? lead + keys_here : 128u;
-            if (lo < y_lo || lo + 8 > y_hi) continue;  // not a whole owned chunk
-            const h8 w = *reinterpret_cast<const h8*>(my + r * TS + lo);
-            const uint64_t first = (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase;
-            put_scores<STREAM>(reinterpret_cast<h8*>(out + (first - lead + lo)), w);
-        }
-        // A row's first chunk (tile 0, lead > 0) and last chunk (last tile)
-        // reach past the row: lane 2r + 0 stores the one, 2r + 1 the other,
-        // element by element.
-        const uint32_t r = lane / 2;
-        if (q0 + r < p.q_len) {
-            const uint32_t lead = lead_of(r);
-            const uint32_t y_lo = kbase == 0 ? lead : 0u;
-            const uint32_t y_hi = last_tile ? lead + keys_here : 128u;
-            const uint32_t last = (y_hi - 1) / 8;
-            const bool first_edge = y_lo > 0 || y_hi < 8;
-            const bool last_edge = last > 0 && y_hi % 8 != 0;
-            if (lane % 2 == 0 ? first_edge : last_edge) {
-                const uint32_t lo = lane % 2 == 0 ? 0u : 8 * last;
-                const uint64_t first = (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase;
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (lo + e >= y_lo && lo + e < y_hi)
-                        out[first - lead + (lo + e)] = my[r * TS + lo + e];
-            }
-        }
-        return;
-    }
-    const bool vec_store = p.kv_len % 8 == 0;
-    if (vec_store && keys_here == 128 && q0 + 31 < p.q_len) {
+    if (keys_here == 128 && q0 + 31 < p.q_len) {
         // A whole tile (the common case): every LDS read, then every store,
         // with no branch between them (under per-store branches the compiler
         // waited for each read before its store).
@@ -258,7 +190,7 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
             const uint32_t r = i * 4 + lane / 16;
             half_t* dst = out + (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase +
                           (lane % 16) * 8;
-            put_scores<STREAM>(reinterpret_cast<h8*>(dst), w[i]);
+            put_scores_u<STREAM>(dst, w[i]);
         }
         return;
     }
@@ -269,8 +201,8 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
         if (q0 + r >= p.q_len || c8 >= keys_here) continue;
         const h8 w = *reinterpret_cast<const h8*>(my + r * TS + c8);
         half_t* dst = out + (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase + c8;
-        if (vec_store && c8 + 8 <= keys_here) {
-            put_scores<STREAM>(reinterpret_cast<h8*>(dst), w);
+        if (c8 + 8 <= keys_here) {
+            put_scores_u<STREAM>(dst, w);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e)
@@ -281,13 +213,10 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
 
 // -------------------------------------------------------------- P V, MFMA
 
-// SHIFT: kv_len is not a multiple of 8 (probs 16-byte aligned).  A row's
-// 128 probabilities of a step are read as the 17 16-byte chunks from the
-// boundary at or before its first one (the 15 inner chunks whole, the two
-// shared with neighbouring steps or rows element by element, one per lane)
-// and kept on that chunk grid in LDS; the products read the row's columns
-// from its lead on, 2 bytes at a time.
-template <int NT, bool SHIFT, bool STREAM>
+// Rows of kv_len % 8 != 0 probabilities start off the 16-byte grid; their
+// chunks are read as unaligned 16-byte loads (get_scores_u), a row's last
+// partial chunk element by element.
+template <int NT, bool STREAM>
 __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ probs,
                                                      const half_t* __restrict__ v,
                                                      half_t* __restrict__ out, GqaParams p) {
@@ -309,73 +238,20 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
     const uint32_t q0 = qt * 128 + wave * 32;
     const half_t* vh = v + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
     const half_t* pbase = probs + uint64_t(bh) * p.q_len * p.kv_len;
-    const bool vec_p = p.kv_len % 8 == 0;
     const uint32_t tr_off = (8 * (lane / 32) + (lane % 16) / 4) * VS + 16 * ((lane / 16) % 2) +
                             4 * (lane % 4);
     half_t* my = pt[wave];
-    constexpr int P_LOADS = SHIFT ? 10 : 8;
-    // a row's lead, (row index x kv_len) mod 8 (the same for every step: a
-    // step is 128 keys)
-    auto lead_of = [&](uint32_t r) -> uint32_t {
-        return ((bh * p.q_len + q0 + r) * p.kv_len) & 7u;
-    };
-
+    constexpr int P_LOADS = 8;
     // this wave's 32 x 128 probabilities of step blk, whole 256-byte row
     // segments per 16 lanes (rows past q_len and keys past kv_len as zeros)
     auto load_p = [&](uint32_t blk, h8 (&pr)[P_LOADS]) {
-        if constexpr (SHIFT) {
-            const uint32_t n = min(uint32_t(BN), p.kv_len - blk * BN);  // keys of this step
-            // whole chunks: 32 rows x 17 slots over the lanes
-#pragma unroll
-            for (int i = 0; i < 9; ++i) {
-                const uint32_t slot = i * 64 + lane;
-                const uint32_t r = slot / 17, lo = 8 * (slot % 17);
-                const h8 zero = {};
-                pr[i] = zero;
-                if (slot >= 32 * 17 || q0 + r >= p.q_len) continue;
-                const uint32_t lead = lead_of(r);
-                if (lo < lead || lo + 8 > lead + n) continue;
-                // the row's first probability of the step
-                const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + blk * BN;
-                pr[i] = get_scores<STREAM>(reinterpret_cast<const h8*>(src + lo - lead));
-            }
-            // the chunks shared with the neighbours, one per lane (as in QK^T)
-            const uint32_t r = lane / 2;
-            const h8 zero = {};
-            pr[9] = zero;
-            if (q0 + r < p.q_len) {
-                const uint32_t lead = lead_of(r);
-                const uint32_t last = (lead + n - 1) / 8;
-                const uint32_t lo = lane % 2 == 0 ? 0u : 8 * last;
-                const bool edge = lane % 2 == 0 ? (lead > 0 || lead + n < 8)
-                                                : (last > 0 && (lead + n) % 8 != 0);
-                if (edge) {
-                    // read whole where the chunk lies in the buffer (its other
-                    // elements masked off), element-wise past the buffer's end
-                    const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + blk * BN;
-                    const uint64_t total = uint64_t(gridDim.x / p.q_tiles) * p.q_len * p.kv_len;
-                    const uint64_t chunk = uint64_t(src - probs) - lead + lo;  // first element
-                    if (chunk + 8 <= total) {
-                        const h8 w = get_scores<STREAM>(reinterpret_cast<const h8*>(probs + chunk));
-#pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            pr[9][e] = (lo + e >= lead && lo + e < lead + n) ? w[e] : half_t(0.0f);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            if (lo + e >= lead && lo + e < lead + n) pr[9][e] = src[lo + e - lead];
-                    }
-                }
-            }
-            return;
-        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t r = i * 4 + lane / 16;
             const uint32_t kb = blk * BN + (lane % 16) * 8;
             const half_t* src = pbase + uint64_t(q0 + r) * p.kv_len + kb;
-            if (q0 + r < p.q_len && vec_p && kb + 8 <= p.kv_len) {
-                pr[i] = get_scores<STREAM>(reinterpret_cast<const h8*>(src));
+            if (q0 + r < p.q_len && kb + 8 <= p.kv_len) {
+                pr[i] = get_scores_u<STREAM>(src);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
@@ -384,27 +260,6 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
         }
     };
     auto store_p = [&](uint32_t blk, const h8 (&pr)[P_LOADS]) {
-        if constexpr (SHIFT) {
-            // LDS row r holds its step on the memory's chunk grid: column x is
-            // the row's key x - lead of the step (the products read columns
-            // lead .. lead + 127).  Slots carry whole chunks or zeros; the
-            // shared chunks are written last, over the slots' zeros.
-            const uint32_t n = min(uint32_t(BN), p.kv_len - blk * BN);
-#pragma unroll
-            for (int i = 0; i < 9; ++i) {
-                const uint32_t slot = i * 64 + lane;
-                if (slot < 32 * 17)
-                    *reinterpret_cast<h8*>(my + (slot / 17) * PS + 8 * (slot % 17)) = pr[i];
-            }
-            const uint32_t r = lane / 2;
-            const uint32_t lead = lead_of(r);
-            const uint32_t last = (lead + n - 1) / 8;
-            const uint32_t lo = lane % 2 == 0 ? 0u : 8 * last;
-            const bool edge = lane % 2 == 0 ? (lead > 0 || lead + n < 8)
-                                            : (last > 0 && (lead + n) % 8 != 0);
-            if (edge && q0 + r < p.q_len) *reinterpret_cast<h8*>(my + r * PS + lo) = pr[9];
-            return;
-        }
         (void)blk;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -437,7 +292,6 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
         for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
 
     const uint32_t blocks = (p.kv_len + BN - 1) / BN;
-    const half_t* prow = my + col * PS + (SHIFT ? lead_of(col) : 0u) + 8 * hs;
     h8 pnext[P_LOADS], vnext[LOADS];
     load_p(0, pnext);
     load_v(0, vnext);
@@ -452,15 +306,8 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
         }
 #pragma unroll
         for (int c = 0; c < PC; ++c) {
-            // P^T operand: keys 16 c + 8 hs + 0..7 of query row col (with
-            // SHIFT at columns shifted by the row's lead: 2-byte reads)
-            h8 pb;
-            if constexpr (SHIFT) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) pb[e] = prow[16 * c + e];
-            } else {
-                pb = *reinterpret_cast<const h8*>(my + col * PS + 16 * c + 8 * hs);
-            }
+            // P^T operand: keys 16 c + 8 hs + 0..7 of query row col
+            const h8 pb = *reinterpret_cast<const h8*>(my + col * PS + 16 * c + 8 * hs);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const half_t* vsrc = vs + tr_off + 16 * c * VS + 32 * t;
@@ -866,19 +713,19 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
         if (use_mfma<T>(s, qd, kd, od)) {
             p.q_tiles = uint32_t(ceil_div(s.q_len, 128));
             p.k_tiles = uint32_t(ceil_div(s.kv_len, 128));
-            const uint64_t grid = heads * p.q_tiles * p.k_tiles;
-            if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
-            const dim3 g(static_cast<unsigned>(grid)), b(256);
-            const bool shift = s.kv_len % 8 != 0;
+            // one XCD per (head, query tile) group, the grid padded to 8 groups
+            const uint64_t groups = heads * p.q_tiles;
+            const uint64_t xgrid = ceil_div(groups, 8) * 8 * p.k_tiles;
+            if (xgrid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
+            p.qk_groups = uint32_t(groups);
+            const dim3 g(static_cast<unsigned>(xgrid)), b(256);
             const bool lines = s.kv_len % 64 == 0;  // score rows are whole 128-byte lines
 #define RL_QK(NT)                                                                      \
     do {                                                                               \
-        if (shift)                                                                     \
-            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, true, true>), g, b, qd, kd, od, p);      \
-        else if (lines)                                                                \
-            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, false, true>), g, b, qd, kd, od, p);     \
+        if (lines)                                                                     \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, true>), g, b, qd, kd, od, p);            \
         else                                                                           \
-            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, false, false>), g, b, qd, kd, od, p);    \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma<NT, false>), g, b, qd, kd, od, p);           \
     } while (0)
             switch (s.head_dim / 32) {
                 case 1: RL_QK(1); break;
@@ -959,16 +806,13 @@ rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, co
             const uint64_t grid = heads * p.q_tiles;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA PV grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
-            const bool shift = s.kv_len % 8 != 0;
             const bool lines = s.kv_len % 64 == 0;  // probability rows are whole 128-byte lines
 #define RL_PV(NT)                                                                      \
     do {                                                                               \
-        if (shift)                                                                     \
-            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true, false>), g, b, pd, vd, od, p);     \
-        else if (lines)                                                                \
-            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false, true>), g, b, pd, vd, od, p);     \
+        if (lines)                                                                     \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true>), g, b, pd, vd, od, p);            \
         else                                                                           \
-            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false, false>), g, b, pd, vd, od, p);    \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false>), g, b, pd, vd, od, p);           \
     } while (0)
             switch (s.head_dim / 32) {
                 case 1: RL_PV(1); break;

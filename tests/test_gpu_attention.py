@@ -234,13 +234,15 @@ def test_gqa_small_integers_match_the_oracle_bit_for_bit(ctx, dtype):
         assert np.array_equal(pv.numpy(), o.gqa_pv((o.gqa_qk(q, k) / 64).astype(dtype), k))
 
 
-@pytest.mark.parametrize("hd,ql,kl", [(64, 2000, 1000), (128, 2048, 512), (32, 2048, 1032)])
+@pytest.mark.parametrize("hd,ql,kl", [(64, 2000, 1000), (128, 2048, 512), (32, 2048, 1032),
+                                      (64, 200, 4093)])
 def test_gqa_qk_large_grids_bit_for_bit(ctx, hd, ql, kl):
-    """Grids of thousands of score tiles (16 heads x 16 query tiles x 4-9 key
-    tiles): small-integer operands make every sum exact, so the library and
-    the oracle agree exactly -- with a partial last query tile, key counts
-    off the 128-key tile (1000, 1032) and off the 128-byte line (1000: rows
-    stored plainly), and whole lines (512)."""
+    """Grids of thousands of score tiles (16 heads x 2-16 query tiles x 4-32
+    key tiles): small-integer operands make every sum exact, so the library
+    and the oracle agree exactly -- with a partial last query tile, key counts
+    off the 128-key tile (1000, 1032, 4093) and off the 128-byte line (1000:
+    rows stored plainly; 4093: rows off the 16-byte grid, unaligned stores),
+    and whole lines (512)."""
     q = (np.arange(1 * 16 * ql * hd) % 7 - 3).reshape(1, 16, ql, hd).astype(np.float16)
     k = (np.arange(1 * 4 * kl * hd) % 5 - 2).reshape(1, 4, kl, hd).astype(np.float16)
     ctx.begin()
