@@ -259,6 +259,15 @@ struct VecOf {
     typedef T type __attribute__((ext_vector_type(N)));
 };
 
+// N elements of T at the alignment of one element: a row of a width that is
+// not a multiple of N starts off the 16-byte grid.  gfx950 runs global memory
+// in unaligned mode, so a load or store of this type is still one 16-byte
+// access (split by the hardware where it crosses a cache line).
+template <typename T, int N>
+struct VecOfU {
+    typedef T type __attribute__((ext_vector_type(N), aligned(sizeof(T))));
+};
+
 // One 16-byte pack of T.
 template <typename T>
 struct Pack16 {

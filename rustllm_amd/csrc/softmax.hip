@@ -116,18 +116,20 @@ __device__ inline float group_sum(float v, float* lds) {
 // Threads of a group past the last row take part in the barriers with no
 // memory accesses.  (One group per block, no grid-stride loop: the loop
 // doubled the VGPR count of the masked f16 variant.)
-// RAGGED: the width is not a multiple of N, so a row starts `lead` elements
-// past a 16-byte boundary.  Its packs stay on the buffer's 16-byte grid: pack
-// p holds the row's elements p * N - lead ..; a pack wholly inside the row
-// moves as one 16-byte access, the two packs it shares with its neighbours
-// move element by element (only this row's elements), so no access leaves
-// the row.
+// RAGGED: the width is not a multiple of N, so a row starts off the 16-byte
+// grid.  Pack p still holds the row's elements p * N .. p * N + N - 1, read
+// and written as unaligned 16-byte accesses (VecOfU); a row's partial last
+// pack reads on into the next row (masked) and is written element by
+// element.  Only the buffer's last pack can reach past its end: that load
+// is moved back inside the buffer and the pack reloaded element by element.
+// The buffer holds at least N elements (smaller ones take k_softmax_stream).
 template <typename T, int N, int NV, int TPR, bool MASK, bool RAGGED>
 __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__ in,
                                                            T* __restrict__ out, uint32_t row_base,
                                                            uint32_t rows, uint32_t width,
                                                            MaskParams mp) {
     typedef typename VecOf<T, N>::type V;
+    typedef typename VecOfU<T, N>::type U;
     constexpr int RPB = kThreads / TPR;
     __shared__ float lds_m[kThreads / kWave];
     __shared__ float lds_s[kThreads / kWave];
@@ -138,15 +140,14 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
         const bool active = row64 < rows;
         const uint32_t row = uint32_t(row64);
         const uint64_t e0 = uint64_t(active ? row : 0) * width;  // the row's first element
-        const uint32_t lead = RAGGED ? uint32_t(e0 % N) : 0u;
-        const uint32_t n_packs = RAGGED ? (lead + width + N - 1) / N : w_packs;
-        const V* src = reinterpret_cast<const V*>(in + (e0 - lead));
-        V* dst = reinterpret_cast<V*>(out + (e0 - lead));
+        const uint32_t n_packs = RAGGED ? (width + N - 1) / N : w_packs;
+        const V* src = reinterpret_cast<const V*>(in + e0);
+        V* dst = reinterpret_cast<V*>(out + e0);
         const uint32_t kept = !active ? 0u : MASK ? kept_keys(row, width, mp) : width;
 
         float v[NV][N];
         float m = -INFINITY;
-        if constexpr (!RAGGED) {
+        {
             // Every lane issues all its loads before using any: a pack past
             // the row's last kept key (or past the row) reloads that last
             // kept pack -- a line the wave reads anyway -- and its elements
@@ -154,13 +155,34 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
             // waited for each load before issuing the next.
             const uint32_t live = (kept + N - 1) / N;  // packs holding a kept key
             const uint32_t last = live > 0 ? live - 1 : 0u;
+            const uint64_t total = uint64_t(rows) * width;
             V raw[NV];
+            bool moved[NV];
 #pragma unroll
             for (int k = 0; k < NV; ++k) {
                 const uint32_t p = lane + k * TPR;
-                raw[k] = load_stream(src + (p < last ? p : last));
+                const uint32_t q = p < last ? p : last;
+                if constexpr (RAGGED) {
+                    const uint64_t off = e0 + uint64_t(q) * N;
+                    moved[k] = off + N > total;  // the buffer's last pack
+                    raw[k] = load_stream(reinterpret_cast<const U*>(in + (moved[k] ? total - N : off)));
+                } else {
+                    raw[k] = load_stream(src + q);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the arithmetic
+            if constexpr (RAGGED) {
+#pragma unroll
+                for (int k = 0; k < NV; ++k) {
+                    if (moved[k]) {
+                        const uint32_t p = lane + k * TPR;
+                        const uint32_t q = p < last ? p : last;
+#pragma unroll
+                        for (int j = 0; j < N; ++j)
+                            raw[k][j] = q * N + j < width ? in[e0 + q * N + j] : T(0.0f);
+                    }
+                }
+            }
 #pragma unroll
             for (int k = 0; k < NV; ++k) {
                 const uint32_t p = lane + k * TPR;
@@ -172,58 +194,6 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
                 }
             }
         }
-#pragma unroll
-        for (int k = 0; k < NV && RAGGED; ++k) {
-            const uint32_t p = lane + k * TPR;
-            // row index of the pack's first element (negative only in a
-            // ragged row's first pack)
-            const int x0 = int(p * N) - int(lead);
-            if (RAGGED && p < n_packs && x0 < int(kept) && (x0 < 0 || x0 + N > int(kept))) {
-                // A pack shared with a neighbouring row (or holding the last
-                // kept key) is read whole -- its other elements lie in the
-                // buffer and are masked off here -- unless it runs past the
-                // buffer's end (the last row's last pack): then element-wise.
-                V raw = {};
-                if (e0 - lead + uint64_t(p + 1) * N <= uint64_t(rows) * width) {
-                    raw = load_stream(src + p);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < N; ++j)
-                        if (x0 + j >= 0 && x0 + j < int(width)) raw[j] = in[e0 + uint32_t(x0 + j)];
-                }
-#pragma unroll
-                for (int j = 0; j < N; ++j) {
-                    const int x = x0 + j;
-                    const float f = (x >= 0 && x < int(kept))
-                                        ? (MASK ? scaled_score(raw[j], mp.scale) : to_float(raw[j]))
-                                        : -INFINITY;
-                    v[k][j] = f;
-                    m = fmaxf(m, f);
-                }
-            } else if (p < n_packs && p * N < kept + lead) {
-                V raw = load_stream(src + p);
-                // (a ragged row's partial packs took the branch above)
-                if (RAGGED || !MASK || (p + 1) * N <= kept) {  // the whole pack is kept
-#pragma unroll
-                    for (int j = 0; j < N; ++j) {
-                        const float f = MASK ? scaled_score(raw[j], mp.scale) : to_float(raw[j]);
-                        v[k][j] = f;
-                        m = fmaxf(m, f);
-                    }
-                } else {  // the pack holding the row's last kept key
-#pragma unroll
-                    for (int j = 0; j < N; ++j) {
-                        const float f =
-                            (p * N + j < kept) ? scaled_score(raw[j], mp.scale) : -INFINITY;
-                        v[k][j] = f;
-                        m = fmaxf(m, f);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < N; ++j) v[k][j] = -INFINITY;
-            }
-        }
         m = group_max<TPR>(m, lds_m);
         // softmax.metal:166-173: an f16 row whose max is -inf is all zeros.
         const bool zero_row = is_f16<T>() && m == -INFINITY;
@@ -231,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const uint32_t p = lane + k * TPR;
-            if (!zero_row && p < n_packs && p * N < kept + lead) {
+            if (!zero_row && p < n_packs && p * N < kept) {
 #pragma unroll
                 for (int j = 0; j < N; ++j) {
                     float e = exp_row<T>(v[k][j] - m);
@@ -248,18 +218,19 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const uint32_t p = lane + k * TPR;
-            const int x0 = int(p * N) - int(lead);
-            if (RAGGED && active && p < n_packs && (x0 < 0 || x0 + N > int(width))) {
+            if (!active || p >= n_packs) continue;
+            V o;
 #pragma unroll
-                for (int j = 0; j < N; ++j) {
-                    const int x = x0 + j;
-                    if (x >= 0 && x < int(width))
-                        out[e0 + uint32_t(x)] = from_float<T>(v[k][j] * inv);
+            for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
+            if constexpr (RAGGED) {
+                if (p * N + N <= width) {
+                    store_stream(reinterpret_cast<U*>(out + e0 + uint64_t(p) * N), U(o));
+                } else {  // the row's partial last pack
+#pragma unroll
+                    for (int j = 0; j < N; ++j)
+                        if (p * N + j < width) out[e0 + p * N + j] = o[j];
                 }
-            } else if (active && p < n_packs) {
-                V o;
-#pragma unroll
-                for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
+            } else {
                 store_stream(dst + p, o);
             }
         }
@@ -414,7 +385,10 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
     // Rows on the buffer's 16-byte pack grid; a width that is not a multiple
     // of the pack takes the ragged variant, whose rows span at most one pack
     // more (one more per thread).
-    const bool packs_ok = aligned_to(in, 16) && aligned_to(out, 16);
+    // Ragged rows (a width that is not a multiple of the pack) take the
+    // same pack counts with unaligned packs; a buffer of fewer than N
+    // elements streams.
+    const bool packs_ok = aligned_to(in, 16) && aligned_to(out, 16) && rows * width >= uint64_t(N);
     const bool ragged = width % N != 0;
     const uint64_t w_packs = ceil_div(width, N);
     const dim3 block(kThreads);
@@ -428,25 +402,21 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
                       block, in, out, uint32_t(base), r32, w32, mp);                             \
         }                                                                                        \
     } while (0)
-    // (NV, TPR) for aligned rows, (NVR, TPRR) with room for the extra pack
-    // for ragged ones: rows of 257..512 packs spread over more threads, as
-    // five packs per thread cost the f16 rows half their occupancy.
-#define RL_SOFTMAX_ROWS2(NV, TPR, NVR, TPRR)        \
+#define RL_SOFTMAX_ROWS(NV, TPR)                    \
     do {                                            \
         if (ragged)                                 \
-            RL_SOFTMAX_ROWS_R(NVR, TPRR, true);     \
+            RL_SOFTMAX_ROWS_R(NV, TPR, true);       \
         else                                        \
             RL_SOFTMAX_ROWS_R(NV, TPR, false);      \
     } while (0)
-#define RL_SOFTMAX_ROWS(NV, TPR) RL_SOFTMAX_ROWS2(NV, TPR, NV + 1, TPR)
     if (packs_ok && w_packs <= 64)
         RL_SOFTMAX_ROWS(1, 64);
     else if (packs_ok && w_packs <= 128)
         RL_SOFTMAX_ROWS(2, 64);
     else if (packs_ok && w_packs <= 256)
-        RL_SOFTMAX_ROWS2(4, 64, 3, 128);
+        RL_SOFTMAX_ROWS(4, 64);
     else if (packs_ok && w_packs <= 512)
-        RL_SOFTMAX_ROWS2(4, 128, 3, 256);
+        RL_SOFTMAX_ROWS(4, 128);
     else if (packs_ok && w_packs <= 1024)
         RL_SOFTMAX_ROWS(4, 256);
     else if (packs_ok && w_packs <= 2048)
@@ -457,7 +427,6 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
         RL_LAUNCH(ctx, (k_softmax_stream<T, MASK>), dim3(row_grid(rows)), block, in, out, r32,
                   w32, mp);
 #undef RL_SOFTMAX_ROWS
-#undef RL_SOFTMAX_ROWS2
 #undef RL_SOFTMAX_ROWS_R
     return after_launch(ctx, name);
 }
