@@ -991,6 +991,17 @@ def probe(ctx, host, ops):
     scores = ctx.empty((1, 15, tok, tok), F16)
     attn_io = (2 * 15 + 2 * 5) * tok * 64 * 2
     n_scores = 15 * tok * tok
+    # ragged scores (4093 keys: rows off the 16-byte grid)
+    q_r = ctx.upload(synth.normal(11, (1, 15, 4093, 64), 0, 1, F16))
+    k_r = ctx.upload(synth.normal(12, (1, 5, 4093, 64), 0, 1, F16))
+    scores_r = ctx.empty((1, 15, 4093, 4093), F16)
+    # the one-launch prologue: Q, K, V views of [1, S, H, D] projections
+    qp = ctx.upload(synth.normal(13, (1, tok, 15, 64), 0, 1, F16))
+    qd, qs = [1, 15, tok, 64], [tok * 15 * 64, 64, 15 * 64, 1]
+    vcache = ctx.empty((1, 5, tok, 64), F16)
+    krep, vrep = ctx.empty((1, 15, tok, 64), F16), ctx.empty((1, 15, tok, 64), F16)
+    # one decode step over a 4096-row cache
+    q1, o1 = ctx.upload(synth.normal(14, (1, 15, 1, 64), 0, 1, F16)), ctx.empty((1, 15, 1, 64), F16)
     for name, nbytes, fn in [
         ("attention_f16 fused [1,15,4096,64] causal (inputs + output)", attn_io,
          lambda: ctx.attention(q, ka, va, 0.125, 0, None, qo)),
@@ -1009,6 +1020,15 @@ def probe(ctx, host, ops):
          lambda: ctx.rope(q, dc, ds, 0, qo)),
         ("attention_softmax_f32 [9,2048,2048]", 9 * (2048 * 2049 // 2) * 4 + 9 * 2048 * 2048 * 4,
          lambda: ctx.attention_softmax(sc, 0.125, 0, so)),
+        ("gqa_qk_f16 ragged [1,15,4093,4093]", (15 + 5) * 4093 * 64 * 2 + 15 * 4093 * 4093 * 2,
+         lambda: ctx.gqa_qk(q_r, k_r, None, scores_r)),
+        ("qkv + KV append + repeat_kv f16 [1,25,4096,64]",
+         2 * 15 * tok * 64 * 2 + 2 * 5 * tok * 64 * (1 + 1 + 3) * 2 + 2 * tok * 32 * 4,
+         lambda: ctx.qkv_rope_kv_append_repeat((qp, qd, qs), (kproj, kdims, kstrides),
+                                               (kproj, kdims, kstrides), dc, ds, 0, kcache,
+                                               vcache, 3, qo, krep, vrep)),
+        ("decode attention_f16 [1,15,1,64] over 4096 rows", 2 * 15 * 64 * 2 + 2 * 5 * tok * 64 * 2,
+         lambda: ctx.attention_noalloc(q1, ka, va, 0.125, tok - 1, None, o1)),
     ]:
         for _ in range(3):
             ctx.begin()

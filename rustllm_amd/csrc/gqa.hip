@@ -112,13 +112,15 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     const uint32_t col = lane % 32;
     const uint32_t hs = lane / 32;
     // block = (head, 128-query tile, 128-key tile); wave = 32 queries x 128 keys.
-    // Hardware block b runs on XCD b mod 8: the key tiles of one (head, query
-    // tile) group all go to the XCD of the group's index mod 8, so the cache
-    // lines that neighbouring key tiles share (rows off the line grid) are
-    // merged in one L2 and the group's queries meet there too.  The grid is
-    // padded to whole groups per XCD.
+    // Hardware block b runs on XCD b mod 8.  XCD x takes a contiguous run of
+    // (head, query tile) groups -- consecutive heads, which share KV heads --
+    // with all their key tiles: the cache lines that neighbouring key tiles
+    // share (rows off the line grid) are merged in one L2, a group's queries
+    // and a KV head's keys are fetched into few L2s.  The grid is padded to
+    // whole runs per XCD.
     const uint32_t xcd = blockIdx.x % 8, xi = blockIdx.x / 8;
-    const uint32_t group = (xi / p.k_tiles) * 8 + xcd;
+    const uint32_t per_xcd = (p.qk_groups + 7) / 8;
+    const uint32_t group = xcd * per_xcd + xi / p.k_tiles;
     if (group >= p.qk_groups) return;  // padding (the whole block)
     const uint32_t lb = group * p.k_tiles + xi % p.k_tiles;
     const uint32_t kt_blk = lb % p.k_tiles;
@@ -713,7 +715,7 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
         if (use_mfma<T>(s, qd, kd, od)) {
             p.q_tiles = uint32_t(ceil_div(s.q_len, 128));
             p.k_tiles = uint32_t(ceil_div(s.kv_len, 128));
-            // one XCD per (head, query tile) group, the grid padded to 8 groups
+            // one XCD per (head, query tile) group, the grid padded to 8 runs
             const uint64_t groups = heads * p.q_tiles;
             const uint64_t xgrid = ceil_div(groups, 8) * 8 * p.k_tiles;
             if (xgrid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
