@@ -46,6 +46,7 @@ namespace rl {
 namespace {
 
 constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kLn2 = 0.693147180559945309417f;
 
 struct AttnParams {
     uint32_t q_heads;      // query heads per batch entry
@@ -888,6 +889,71 @@ __device__ inline void merge_head(const float* part, T* __restrict__ out,
     }
 }
 
+// A split-key decode workgroup: four waves of 64 keys each.
+constexpr int kSplitWaves = 4;
+constexpr int kSplitKeys = 64 * kSplitWaves;   // keys per workgroup
+constexpr int kStageBytes = 64 * 256;          // LDS per wave for staged value rows
+
+// The end of a split-key workgroup: its four waves' states (per wave and
+// row: max, sum and output row, in LDS) -> one partial per row, stored
+// agent-coherent; the workgroup that completes a KV head's last split then
+// merges that head's rows.
+template <typename T, int RM, int DMAX>
+__device__ inline void finish_split(const float (&merge_m)[kSplitWaves][RM],
+                                    const float (&merge_l)[kSplitWaves][RM],
+                                    const float (&merge_o)[kSplitWaves][RM][DMAX],
+                                    float* __restrict__ part, uint32_t* __restrict__ tickets,
+                                    T* __restrict__ out, const AttnParams& p, uint32_t b,
+                                    uint32_t first_head, uint32_t R, uint32_t kvb,
+                                    uint32_t split, uint32_t splits) {
+    const uint32_t wave = threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t D = p.head_dim;
+    __syncthreads();  // every wave's state is in LDS
+    const uint32_t stride = D + 2;
+    for (uint32_t r = wave; r < R; r += kSplitWaves) {
+        float mt = -INFINITY;
+        for (int w = 0; w < kSplitWaves; ++w) mt = fmaxf(mt, merge_m[w][r]);
+        float scale_w[kSplitWaves];
+        float lt = 0.0f;
+        for (int w = 0; w < kSplitWaves; ++w) {
+            scale_w[w] = merge_m[w][r] == -INFINITY ? 0.0f : exp_fast(merge_m[w][r] - mt);
+            lt += merge_l[w][r] * scale_w[w];
+        }
+        const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
+                             r % p.q_len;
+        float* dst = part + (row * splits + split) * stride;
+        for (uint32_t d = lane; d < D; d += 64) {
+            float acc = 0.0f;
+            for (int w = 0; w < kSplitWaves; ++w) acc += merge_o[w][r][d] * scale_w[w];
+            publish(dst + 2 + d, acc);
+        }
+        if (lane == 0) {
+            publish(dst, mt);
+            publish(dst + 1, lt);
+        }
+    }
+
+    // Hand-off: the workgroup that completes a KV head's last split merges
+    // that head's rows, so a decode step is one launch.  The partials were
+    // stored agent-coherent (publish: written through the XCD's L2), every
+    // wave waits for those stores to complete (vmcnt) before the barrier, and
+    // only then does one thread draw the ticket -- no L2 write-back, which
+    // an agent-scope release fence would make every workgroup pay in turn.
+    // The last workgroup reads the partials agent-coherent as well and puts
+    // the ticket back to zero for the next launch.
+    __shared__ uint32_t ticket;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        ticket = __hip_atomic_fetch_add(&tickets[kvb], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != splits - 1) return;
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&tickets[kvb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    merge_head<T>(part, out, p, b, first_head, R, splits);
+}
 
 // Few query rows per KV head (a decode step: R = group * q_len rows): the
 // rows of one KV head share every K and V row read.  Workgroup (kv head,
@@ -898,9 +964,6 @@ __device__ inline void merge_head(const float* part, T* __restrict__ out,
 // straight to LDS (global_load_lds), its key rows to registers -- so a split
 // costs one memory round trip.  RM bounds the rows, DPL the head elements
 // per lane (D <= 64 DPL).
-constexpr int kSplitWaves = 4;
-constexpr int kSplitKeys = 64 * kSplitWaves;   // keys per workgroup
-constexpr int kStageBytes = 64 * 256;          // LDS per wave for staged value rows
 
 template <typename T, int RM, int DPL>
 __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
@@ -1107,50 +1170,185 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
 #pragma unroll
         for (int e = 0; e < DPL; ++e) merge_o[wave][r][lane * DPL + e] = o[r][e];
     }
-    __syncthreads();
-    const uint32_t stride = D + 2;
-    for (uint32_t r = wave; r < R; r += kSplitWaves) {
-        float mt = -INFINITY;
-        for (int w = 0; w < kSplitWaves; ++w) mt = fmaxf(mt, merge_m[w][r]);
-        float scale_w[kSplitWaves];
-        float lt = 0.0f;
-        for (int w = 0; w < kSplitWaves; ++w) {
-            scale_w[w] = merge_m[w][r] == -INFINITY ? 0.0f : exp_fast(merge_m[w][r] - mt);
-            lt += merge_l[w][r] * scale_w[w];
+    finish_split<T>(merge_m, merge_l, merge_o, part, tickets, out, p, b, first_head, R, kvb,
+                    split, splits);
+}
+
+// The split-key decode step on the matrix cores (f16, R <= 16 rows per KV
+// head, head size D = 64 or 128).  Per wave of 64 keys: S^T = K Q^T as four
+// 16-key tiles of v_mfma_f32_16x16x32_f16 (A = key rows loaded straight
+// from memory, B = the query rows, zero past R), then O = P V in two 32-key
+// steps (A = P from the score registers, B = value columns read from the
+// wave's LDS stage by transpose reads).  Row a of score tile m holds key
+// key16(m, a), so that lane l's registers of tiles 2t and 2t + 1 hold keys
+// 32 t + 8 (l / 16) + 0..7 of query row l % 16: the P operand of step t as
+// they stand.  No barrier before the products (every wave reads only its
+// own stage and registers); the end is finish_split's, as for
+// k_attention_split.
+__device__ inline uint32_t key16(uint32_t m, uint32_t a) {
+    return 32 * (m / 2) + 8 * (a / 4) + 4 * (m % 2) + a % 4;
+}
+
+// max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row's four
+// lane groups).  A swap returns {lower lane's value, upper lane's value} in
+// both lanes of a pair, so both compute the same result bit for bit.
+__device__ inline float rows4_max(float v) {
+    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                              false);
+    v = fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ inline float rows4_sum(float v) {
+    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                              false);
+    v = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split_mfma(
+    const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
+    float* __restrict__ part, uint32_t* __restrict__ tickets, half_t* __restrict__ out,
+    AttnParams p, uint32_t splits) {
+    static_assert(D == 64 || D == 128, "head size 64 or 128");
+    constexpr int RM = 16;
+    constexpr int KS = D / 32;  // 32-element steps of the scores
+    constexpr int NT = D / 16;  // 16-element tiles of the output
+    __shared__ __align__(16) half_t vstage[kSplitWaves][64 * D];
+    __shared__ float merge_m[kSplitWaves][RM];
+    __shared__ float merge_l[kSplitWaves][RM];
+    __shared__ float merge_o[kSplitWaves][RM][D];
+    const uint32_t wave = threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t lr = lane % 16;  // query row of the scores and P, column of the outputs
+    const uint32_t g = lane / 16;
+    const uint32_t kvb = blockIdx.x / splits;  // b * kv_heads + kv head
+    const uint32_t split = blockIdx.x % splits;
+    const uint32_t kv_heads = p.q_heads / p.group;
+    const uint32_t b = kvb / kv_heads;
+    const uint32_t first_head = (kvb % kv_heads) * p.group;
+    const uint32_t R = p.group * p.q_len;
+    const half_t* kh = k + uint64_t(kvb) * p.kv_head_stride;
+    const half_t* vh = v + uint64_t(kvb) * p.kv_head_stride;
+    const uint32_t base = split * kSplitKeys + wave * 64;
+    const uint32_t n = p.kv_len > base ? min(64u, p.kv_len - base) : 0u;  // this wave's keys
+
+    // every load issued before the first use, unconditional (clamped rows,
+    // masked afterwards) so that none waits behind a branch or a select: the
+    // query row lr (row r = g' * q_len + qi is query qi of head
+    // first_head + g'; a row past R reads row 0, its scores are masked),
+    // elements 32 s + 8 g .. + 7
+    const bool row_live = lr < R;
+    const uint32_t qr = row_live ? lr : 0u;
+    const uint64_t qrow = (uint64_t(b) * p.q_heads + first_head + qr / p.q_len) * p.q_len +
+                          qr % p.q_len;
+    h8 qf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const h8*>(q + qrow * D + 32 * s + 8 * g);
+    // key rows: tile m, row lr holds key base + key16(m, lr) (a row past the
+    // last key reads the last key; its scores are masked below)
+    h8 kf[4][KS];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const uint32_t key = min(base + key16(m, lr), p.kv_len - 1);
+        const half_t* krow = kh + uint64_t(key) * D;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kf[m][s] = *reinterpret_cast<const h8*>(krow + 32 * s + 8 * g);
+    }
+    // then the 64 value rows (needed last), 16 bytes a lane, to registers:
+    // loads of one kind only, so that the products wait for the key rows
+    // alone (vmcnt counts in order); rows past the last key copy the last
+    // key's row, whose probability is zero
+    h8 vf[D / 8];
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+        const uint32_t c = 64 * i + lane;  // 16-byte piece c of the 64 rows
+        const uint32_t key = min(base + c / (D / 8), p.kv_len - 1);
+        vf[i] = *reinterpret_cast<const h8*>(vh + uint64_t(key) * D + (c % (D / 8)) * 8);
+    }
+    // all of them issued before the first wait (the scheduler would
+    // otherwise place value loads behind the products' waits for key rows)
+    __builtin_amdgcn_sched_barrier(0);
+
+    // S^T: lane l holds query row lr's scores of keys key16(m, 4 g + r)
+    f32x4 sc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        sc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            sc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[m][s], qf[s], sc[m], 0, 0, 0);
+    }
+    // the row's max over its 64 keys (16 per lane, four lanes per row) in
+    // log2 units, probabilities rounded to f16 as the P operand, and their
+    // sum.  Row lr sees the wave's keys below min(n, limit + 1 - base) (none
+    // past R); key16(m, 4 g + r) - 8 g is a constant, compared with that
+    // count less 8 g.
+    const uint32_t limit = p.start + lr % p.q_len;  // last key row lr sees
+    const uint32_t causal = limit + 1 > base ? limit + 1 - base : 0u;
+    const int seen = row_live ? int(min(n, causal)) - int(8 * g) : 0;
+    float x[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int kc = 32 * (m / 2) + 4 * (m % 2) + r;
+            x[m][r] = kc < seen ? sc[m][r] * p.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, x[m][r]);
         }
-        const uint64_t row = (uint64_t(b) * p.q_heads + first_head + r / p.q_len) * p.q_len +
-                             r % p.q_len;
-        float* dst = part + (row * splits + split) * stride;
-        for (uint32_t d = lane; d < D; d += 64) {
-            float acc = 0.0f;
-            for (int w = 0; w < kSplitWaves; ++w) acc += merge_o[w][r][d] * scale_w[w];
-            publish(dst + 2 + d, acc);
+    mx = rows4_max(mx);
+    // 2^(x - mx), 0 for masked keys (x = -inf; mx = -inf only if every key is);
+    // results below 2^-126 flush to zero, as they round to zero in f16
+    const float ms = mx == -INFINITY ? 0.0f : mx;
+    half_t ph[4][4];
+    float lsum = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ph[m][r] = static_cast<half_t>(__builtin_amdgcn_exp2f(x[m][r] - ms));
+            lsum += static_cast<float>(ph[m][r]);
         }
-        if (lane == 0) {
-            publish(dst, mt);
-            publish(dst + 1, lt);
+    lsum = rows4_sum(lsum);
+
+    // P V: lane 16 g + 4 j + a reads 4 elements of value rows 32 t + 8 g + j
+    // and + 4, columns 16 nt + 4 a; the transpose hands lane 16 g + i column
+    // 16 nt + i of those eight rows
+    // the value rows to the wave's LDS stage (read by this wave only: no barrier)
+    half_t* stage = vstage[wave];
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) *reinterpret_cast<h8*>(stage + (64 * i + lane) * 8) = vf[i];
+    f32x4 o[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) o[nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const half_t* tr = stage + (8 * g + lr / 4) * D + 4 * (lr % 4);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const h8 a = {ph[2 * t][0],     ph[2 * t][1],     ph[2 * t][2],     ph[2 * t][3],
+                      ph[2 * t + 1][0], ph[2 * t + 1][1], ph[2 * t + 1][2], ph[2 * t + 1][3]};
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const half_t* src = tr + 32 * t * D + 16 * nt;
+            const h4 lo = lds_read_transposed(src);
+            const h4 hi = lds_read_transposed(src + 4 * D);
+            const h8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, o[nt], 0, 0, 0);
         }
     }
-
-    // Hand-off: the workgroup that completes a KV head's last split merges
-    // that head's rows, so a decode step is one launch.  The partials were
-    // stored agent-coherent (publish: written through the XCD's L2), every
-    // wave waits for those stores to complete (vmcnt) before the barrier, and
-    // only then does one thread draw the ticket -- no L2 write-back, which
-    // an agent-scope release fence would make every workgroup pay in turn.
-    // The last workgroup reads the partials agent-coherent as well and puts
-    // the ticket back to zero for the next launch.
-    __shared__ uint32_t ticket;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        ticket = __hip_atomic_fetch_add(&tickets[kvb], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (ticket != splits - 1) return;
-    if (threadIdx.x == 0)
-        __hip_atomic_store(&tickets[kvb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_head<T>(part, out, p, b, first_head, R, splits);
+    // lane l holds rows 4 g + r, column 16 nt + lr of the wave's output
+    if (g == 0) {
+        merge_m[wave][lr] = mx * kLn2;  // natural units, as finish_split takes them
+        merge_l[wave][lr] = lsum;
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) merge_o[wave][4 * g + r][16 * nt + lr] = o[nt][r];
+    finish_split<half_t>(merge_m, merge_l, merge_o, part, tickets, out, p, b, first_head, R,
+                         kvb, split, splits);
 }
 
 // ------------------------------------------------------------ validation
@@ -1445,18 +1643,31 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
         const dim3 gs(static_cast<unsigned>(s.batch * s.kv_heads * splits)), bs(64 * kSplitWaves);
         float* pf = static_cast<float*>(part);
         const uint32_t sp = uint32_t(splits);
+        // f16 with at most 16 rows per KV head and head size 64 or 128: the
+        // matrix-core kernel
+        bool on_mfma = false;
+        if constexpr (std::is_same<T, half_t>::value) {
+            on_mfma = vec_rows && R <= 16 && (s.head_dim == 64 || s.head_dim == 128) &&
+                      aligned_to(qd, 16);
+            if (on_mfma && s.head_dim == 64)
+                RL_LAUNCH(ctx, k_attention_split_mfma<64>, gs, bs, qd, kd, vd, pf, tk, od, p, sp);
+            else if (on_mfma)
+                RL_LAUNCH(ctx, k_attention_split_mfma<128>, gs, bs, qd, kd, vd, pf, tk, od, p, sp);
+        }
 #define RL_SPLIT(RMV, DPLV)                                                                    \
     RL_LAUNCH(ctx, (k_attention_split<T, RMV, DPLV>), gs, bs, qd, kd, vd, pf, tk, od, p, sp,   \
               vec_rows)
-        if (rm == 4 && dpl == 1) RL_SPLIT(4, 1);
-        else if (rm == 4 && dpl == 2) RL_SPLIT(4, 2);
-        else if (rm == 4) RL_SPLIT(4, 4);
-        else if (rm == 8 && dpl == 1) RL_SPLIT(8, 1);
-        else if (rm == 8 && dpl == 2) RL_SPLIT(8, 2);
-        else if (rm == 8) RL_SPLIT(8, 4);
-        else if (rm == 16 && dpl == 1) RL_SPLIT(16, 1);
-        else if (rm == 16) RL_SPLIT(16, 2);
-        else RL_SPLIT(32, 1);
+        if (!on_mfma) {
+            if (rm == 4 && dpl == 1) RL_SPLIT(4, 1);
+            else if (rm == 4 && dpl == 2) RL_SPLIT(4, 2);
+            else if (rm == 4) RL_SPLIT(4, 4);
+            else if (rm == 8 && dpl == 1) RL_SPLIT(8, 1);
+            else if (rm == 8 && dpl == 2) RL_SPLIT(8, 2);
+            else if (rm == 8) RL_SPLIT(8, 4);
+            else if (rm == 16 && dpl == 1) RL_SPLIT(16, 1);
+            else if (rm == 16) RL_SPLIT(16, 2);
+            else RL_SPLIT(32, 1);
+        }
 #undef RL_SPLIT
         const rl_status st = after_launch(ctx, name);
         if (mode == DecodeScratch::kPool)

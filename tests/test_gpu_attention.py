@@ -77,6 +77,9 @@ DECODE_SHAPES = [
     (1, 4, 4, 1, 3000, 3000, 256, 2999),   # plain heads, D 256
     (1, 32, 4, 4, 600, 600, 64, 596),      # 32 rows per KV head
     (1, 3, 1, 1, 513, 520, 96, 512),       # just past the split threshold, D 96
+    (1, 15, 5, 1, 4093, 4096, 64, 4092),   # ragged last wave (4093 keys)
+    (1, 8, 8, 1, 1500, 1536, 128, 1400),   # one row per KV head, keys past the causal limit
+    (1, 12, 3, 3, 2100, 2100, 64, 2097),   # 12 rows per KV head, three new tokens
 ]
 
 
