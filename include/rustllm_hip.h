@@ -469,11 +469,11 @@ rl_status rl_attention_f16(rl_context* ctx, const rl_buffer* q, const rl_buffer*
  * harnesses that forbid hipMalloc): same arguments, checks and results, but
  * the decode path (few query rows per KV head, >= 512 visible keys) keeps
  * its per-split partials and hand-off counters in a file-scope device array
- * of 8 MiB (16 KiB of counters, the rest partials) that each GPU holds from
+ * of 8 MiB (256 KiB of counters, the rest partials) that each GPU holds from
  * the library's load until the process ends, instead of a pool block and
  * the context's counters; the other paths allocate nothing anyway.  A decode
  * shape needing more -- batch*q_heads*q_len * ceil(keys/256) * (head_dim+2)
- * floats above 8 MiB - 16 KiB, or more than 4096 batch*kv_heads counters --
+ * floats above 8 MiB - 256 KiB, or more than 1024 batch*kv_heads counters --
  * is RL_ERR_INVALID_SHAPE.  Every call on one GPU shares that array: calls
  * that overlap on one GPU (other streams, other threads) race.  Allowed
  * while recording a graph. */

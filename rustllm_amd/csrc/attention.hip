@@ -889,8 +889,12 @@ __device__ inline void merge_head(const float* part, T* __restrict__ out,
     }
 }
 
-// A split-key decode workgroup: four waves of 64 keys each.
+// A split-key decode workgroup: four waves of 64 keys each.  The hand-off
+// counter of KV head i is word i * kTicketStride of the counter array: one
+// per 256 bytes, so that the atomics of different heads do not queue on one
+// line (the 80 workgroups of a 5-head, 4096-key step: 7.5 -> 7.05 us).
 constexpr int kSplitWaves = 4;
+constexpr uint32_t kTicketStride = 64;
 constexpr int kSplitKeys = 64 * kSplitWaves;   // keys per workgroup
 constexpr int kStageBytes = 64 * 256;          // LDS per wave for staged value rows
 
@@ -946,12 +950,13 @@ __device__ inline void finish_split(const float (&merge_m)[kSplitWaves][RM],
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0)
-        ticket = __hip_atomic_fetch_add(&tickets[kvb], 1u, __ATOMIC_RELAXED,
+        ticket = __hip_atomic_fetch_add(&tickets[kvb * kTicketStride], 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (ticket != splits - 1) return;
     if (threadIdx.x == 0)
-        __hip_atomic_store(&tickets[kvb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&tickets[kvb * kTicketStride], 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     merge_head<T>(part, out, p, b, first_head, R, splits);
 }
 
@@ -1505,8 +1510,9 @@ bool use_flash(const AttnShape& s, const void* q, const void* k, const void* v, 
 // array, so calls that overlap on one GPU (other streams, other threads)
 // race; calls on one stream are ordered.
 constexpr uint64_t kScratchBytes = uint64_t(8) << 20;
-constexpr uint64_t kScratchTicketBytes = uint64_t(16) << 10;
-constexpr uint64_t kScratchTickets = kScratchTicketBytes / sizeof(uint32_t);
+constexpr uint64_t kScratchTicketBytes = uint64_t(256) << 10;
+constexpr uint64_t kScratchTicketWords = kScratchTicketBytes / sizeof(uint32_t);
+constexpr uint64_t kScratchTickets = kScratchTicketWords / kTicketStride;  // 1024 counters
 constexpr uint64_t kScratchPartialBytes = kScratchBytes - kScratchTicketBytes;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -1534,9 +1540,9 @@ rl_status scratch_on_device(rl_context* ctx, void** out) {
         void* ptr = nullptr;
         hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (err == hipSuccess) {
-            hipLaunchKernelGGL(k_zero_u32, dim3(unsigned(kScratchTickets / 256)), dim3(256), 0,
+            hipLaunchKernelGGL(k_zero_u32, dim3(unsigned(kScratchTicketWords / 256)), dim3(256), 0,
                                ctx->stream, static_cast<uint32_t*>(ptr),
-                               uint32_t(kScratchTickets));
+                               uint32_t(kScratchTicketWords));
             err = hipGetLastError();
         }
         slot.err = err;
@@ -1548,11 +1554,13 @@ rl_status scratch_on_device(rl_context* ctx, void** out) {
     return RL_OK;
 }
 
-// The decode hand-off counters: at least n of them, all zero.  Growing
-// waits for the stream (a launch in flight may hold the old array).
+// The decode hand-off counters: at least n of them (n * kTicketStride
+// words), all zero.  Growing waits for the stream (a launch in flight may
+// hold the old array).
 rl_status ensure_tickets(rl_context* ctx, uint64_t n) {
-    if (ctx->ticket_count >= n) return RL_OK;
-    const uint64_t count = std::max<uint64_t>(n, 256);
+    const uint64_t words = n * kTicketStride;
+    if (ctx->ticket_count >= words) return RL_OK;
+    const uint64_t count = std::max<uint64_t>(words, 256 * kTicketStride);
     hipError_t err = hipStreamSynchronize(ctx->stream);
     if (err == hipSuccess && ctx->tickets != nullptr) err = hipFree(ctx->tickets);
     if (err != hipSuccess) return fail(RL_ERR_DEVICE, "ticket array: %s", hipGetErrorString(err));

@@ -79,8 +79,9 @@ struct rl_context {
     bool staging_pending = false;
 
     // One counter per (batch, KV head) for the decode attention's split
-    // hand-off: zero between launches (the workgroup that draws the last
-    // ticket puts it back).  Grown on demand, freed with the context.
+    // hand-off, one per 256 bytes: zero between launches (the workgroup that
+    // draws the last ticket puts it back).  Grown on demand, freed with the
+    // context.  ticket_count is in 32-bit words.
     uint32_t* tickets = nullptr;
     uint64_t ticket_count = 0;
 };

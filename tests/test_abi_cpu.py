@@ -436,8 +436,8 @@ def test_qkv_rope_kv_append_repeat_validation():
 
 def test_attention_noalloc_rejects_decode_shapes_beyond_its_scratch():
     # rl_attention_f16_noalloc: the checks of rl_attention_f16, then the decode
-    # path's needs against the static scratch (8 MiB - 16 KiB of partials,
-    # 4096 counters), all before any device call
+    # path's needs against the static scratch (8 MiB - 256 KiB of partials,
+    # 1024 counters), all before any device call
     def go(f, b, qh, kvh, kl, hd=64):
         cap = kl
         return call(f, buf(b * qh * hd, 2), buf(b * kvh * cap * hd, 2),
@@ -447,11 +447,11 @@ def test_attention_noalloc_rejects_decode_shapes_beyond_its_scratch():
     f = "rl_attention_f16_noalloc"
     assert go(f, 1, 15, 5, 4096)[0] == DEVICE           # SmolLM2 decode: 63 KB of partials
     assert go(f, 64, 32, 1, 32768)[0] == SHAPE          # 2048 rows x 128 splits x 66 floats
-    assert "allocation-free entry holds 8372224 bytes" in abi.last_error()
+    assert "allocation-free entry holds 8126464 bytes" in abi.last_error()
     assert go("rl_attention_f16", 64, 32, 1, 32768)[0] == DEVICE  # the pooled entry takes it
-    assert go(f, 5000, 1, 1, 512, 32)[0] == SHAPE       # 5000 hand-off counters > 4096
-    assert "5000 counters" in abi.last_error()
-    assert go(f, 4096, 1, 1, 512, 32)[0] == DEVICE
+    assert go(f, 1025, 1, 1, 512, 32)[0] == SHAPE       # 1025 hand-off counters > 1024
+    assert "1025 counters" in abi.last_error()
+    assert go(f, 1024, 1, 1, 512, 32)[0] == DEVICE
     assert go(f, 64, 32, 1, 300)[0] == DEVICE           # < 512 keys: not the split path
 
 
