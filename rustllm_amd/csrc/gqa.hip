@@ -70,6 +70,7 @@ __device__ inline h8 get_scores(const h8* src) {
 // gfx950 runs global memory in unaligned mode, so this is still one 16-byte
 // access (split by the hardware where it crosses a line).
 typedef half_t h8u __attribute__((ext_vector_type(8), aligned(2)));
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));  // f32 rows off the grid
 template <bool STREAM>
 __device__ inline void put_scores_u(half_t* dst, h8 w) {
     const h8u v = w;
@@ -351,8 +352,10 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
 // (tile t + 1 loads while tile t is multiplied), in key order at a stride of
 // 2 mod 64 floats (every operand read on its own bank).  Each lane stores
 // its result registers directly, four consecutive keys per 16-byte store: a
-// row receives 32-byte pieces that the L2 merges into whole lines.
-template <int NT>
+// row receives 32-byte pieces that the L2 merges into whole lines.  VEC:
+// score rows on the 16-byte grid (kv_len % 4 == 0); otherwise the stores
+// are unaligned 16-byte stores, a row's last partial group element-wise.
+template <int NT, bool VEC>
 __global__ __launch_bounds__(256) void k_gqa_qk_mfma_f32(const float* __restrict__ q,
                                                          const float* __restrict__ k,
                                                          float* __restrict__ out, GqaParams p) {
@@ -406,7 +409,6 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma_f32(const float* __restrict
     store_tile(ks[0]);
     __syncthreads();
 
-    const bool vec_store = p.kv_len % 4 == 0;
     float* orow = out + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * p.kv_len;
     for (uint32_t t = t_first; t < t_end; ++t) {
         const uint32_t buf = (t - t_first) % 2;
@@ -423,13 +425,17 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma_f32(const float* __restrict
                 for (int j = 0; j < DS; ++j)
                     s = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[2 * j], qf[j], s, 0, 0, 0);
                 if (!q_valid) continue;
-                // register 4g + e holds key k0 + 8g + 4hs + e
+                // register 4g + e holds key k0 + 8g + 4hs + e; rows of
+                // kv_len % 4 != 0 scores start off the 16-byte grid and take
+                // unaligned 16-byte stores
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const uint32_t key = k0 + 8 * g + 4 * hs;
-                    if (vec_store && key + 4 <= p.kv_len) {
-                        *reinterpret_cast<float4*>(orow + key) =
-                            float4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
+                    const f32x4 w = {s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
+                    if constexpr (VEC) {  // kv_len % 4 == 0: a group is whole or past the end
+                        if (key < p.kv_len) *reinterpret_cast<f32x4*>(orow + key) = w;
+                    } else if (key + 4 <= p.kv_len) {
+                        *reinterpret_cast<f32x4u*>(orow + key) = w;
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
@@ -448,8 +454,10 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma_f32(const float* __restrict
 // per 16 lanes) at a row stride of 2 mod 64, so that lane (col, hs) reads the
 // probability of key 2s + hs of its query -- the B operand of the step over
 // keys 2s, 2s + 1 -- on its own bank; V rows at 32 mod 64 floats.  The next
-// step's operands are in flight during this step's products.
-template <int NT>
+// step's operands are in flight during this step's products.  VEC:
+// probability rows on the 16-byte grid (streamed loads); otherwise plain
+// unaligned 16-byte loads, a row's last partial group element-wise.
+template <int NT, bool VEC>
 __global__ __launch_bounds__(256) void k_gqa_pv_mfma_f32(const float* __restrict__ probs,
                                                          const float* __restrict__ v,
                                                          float* __restrict__ out, GqaParams p) {
@@ -470,7 +478,6 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma_f32(const float* __restrict
     const uint32_t q0 = qt * 128 + wave * 32;
     const float* vh = v + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
     const float* pbase = probs + uint64_t(bh) * p.q_len * p.kv_len;
-    const bool vec_p = p.kv_len % 4 == 0;
     float* my = pt[wave];
 
     // rows past q_len and keys past kv_len as zeros
@@ -480,8 +487,13 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma_f32(const float* __restrict
             const uint32_t r = i * 4 + lane / 16;
             const uint32_t kb = blk * BN + (lane % 16) * 4;
             const float* src = pbase + uint64_t(q0 + r) * p.kv_len + kb;
-            if (q0 + r < p.q_len && vec_p && kb + 4 <= p.kv_len) {
-                pr[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src));
+            if constexpr (VEC) {  // kv_len % 4 == 0: a group is whole or past the end
+                if (q0 + r < p.q_len && kb < p.kv_len)
+                    pr[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src));
+                else
+                    pr[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            } else if (q0 + r < p.q_len && kb + 4 <= p.kv_len) {
+                pr[i] = *reinterpret_cast<const f32x4u*>(src);  // a row off the 16-byte grid
             } else {
                 const bool row = q0 + r < p.q_len;
                 pr[i] = f32x4{row && kb < p.kv_len ? src[0] : 0.0f,
@@ -754,12 +766,22 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
             const uint64_t grid = base * p.k_groups;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
+            // score rows on the 16-byte grid (kv_len % 4 == 0) or off it
+            const bool vec = s.kv_len % 4 == 0;
+#define RL_QK32(NT)                                                                    \
+    do {                                                                               \
+        if (vec)                                                                       \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<NT, true>), g, b, qd, kd, od, p);        \
+        else                                                                           \
+            RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<NT, false>), g, b, qd, kd, od, p);       \
+    } while (0)
             switch (s.head_dim / 32) {
-                case 1: RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<1>), g, b, qd, kd, od, p); break;
-                case 2: RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<2>), g, b, qd, kd, od, p); break;
-                case 3: RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<3>), g, b, qd, kd, od, p); break;
-                default: RL_LAUNCH(ctx, (k_gqa_qk_mfma_f32<4>), g, b, qd, kd, od, p); break;
+                case 1: RL_QK32(1); break;
+                case 2: RL_QK32(2); break;
+                case 3: RL_QK32(3); break;
+                default: RL_QK32(4); break;
             }
+#undef RL_QK32
             return after_launch(ctx, name);
         }
     }
@@ -831,12 +853,22 @@ rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, co
             const uint64_t grid = heads * p.q_tiles;
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA PV grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
+            // probability rows on the 16-byte grid (kv_len % 4 == 0) or off it
+            const bool vec = s.kv_len % 4 == 0;
+#define RL_PV32(NT)                                                                    \
+    do {                                                                               \
+        if (vec)                                                                       \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<NT, true>), g, b, pd, vd, od, p);        \
+        else                                                                           \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<NT, false>), g, b, pd, vd, od, p);       \
+    } while (0)
             switch (s.head_dim / 32) {
-                case 1: RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<1>), g, b, pd, vd, od, p); break;
-                case 2: RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<2>), g, b, pd, vd, od, p); break;
-                case 3: RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<3>), g, b, pd, vd, od, p); break;
-                default: RL_LAUNCH(ctx, (k_gqa_pv_mfma_f32<4>), g, b, pd, vd, od, p); break;
+                case 1: RL_PV32(1); break;
+                case 2: RL_PV32(2); break;
+                case 3: RL_PV32(3); break;
+                default: RL_PV32(4); break;
             }
+#undef RL_PV32
             return after_launch(ctx, name);
         }
     }

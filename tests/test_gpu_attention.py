@@ -237,17 +237,19 @@ def test_gqa_small_integers_match_the_oracle_bit_for_bit(ctx, dtype):
         assert np.array_equal(pv.numpy(), o.gqa_pv((o.gqa_qk(q, k) / 64).astype(dtype), k))
 
 
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
 @pytest.mark.parametrize("hd,ql,kl", [(64, 2000, 1000), (128, 2048, 512), (32, 2048, 1032),
                                       (64, 200, 4093)])
-def test_gqa_qk_large_grids_bit_for_bit(ctx, hd, ql, kl):
+def test_gqa_qk_large_grids_bit_for_bit(ctx, hd, ql, kl, dtype):
     """Grids of thousands of score tiles (16 heads x 2-16 query tiles x 4-32
     key tiles): small-integer operands make every sum exact, so the library
     and the oracle agree exactly -- with a partial last query tile, key counts
     off the 128-key tile (1000, 1032, 4093) and off the 128-byte line (1000:
     rows stored plainly; 4093: rows off the 16-byte grid, unaligned stores),
-    and whole lines (512)."""
-    q = (np.arange(1 * 16 * ql * hd) % 7 - 3).reshape(1, 16, ql, hd).astype(np.float16)
-    k = (np.arange(1 * 4 * kl * hd) % 5 - 2).reshape(1, 4, kl, hd).astype(np.float16)
+    and whole lines (512); in f32 the 4093-key rows are off the 16-byte grid
+    too (unaligned 16-byte stores)."""
+    q = (np.arange(1 * 16 * ql * hd) % 7 - 3).reshape(1, 16, ql, hd).astype(dtype)
+    k = (np.arange(1 * 4 * kl * hd) % 5 - 2).reshape(1, 4, kl, hd).astype(dtype)
     ctx.begin()
     s = ctx.gqa_qk(ctx.upload(q), ctx.upload(k))
     ctx.finish()
