@@ -64,6 +64,14 @@ struct AttnParams {
 
 // ------------------------------------------------------------- MFMA kernel
 
+// max over lanes l and l ^ 32 without an LDS permute: v_permlane32_swap
+// returns {lower lane's value, upper lane's value} in both lanes.
+__device__ inline float max_halves(float v) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
 // max(a, b, c) in one v_max3_f32.  (fmaxf on a value the compiler cannot
 // prove canonical, such as an MFMA result, costs an extra v_max_f32 x, x.)
 __device__ inline float max3(float a, float b, float c) {
@@ -378,7 +386,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                         my = max3(my, s[kt][r + 2], s[kt][r + 3]);
                     }
                 mx = fmaxf(mx, my);
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                mx = max_halves(mx);
                 const float mx_log2 = mx * p.scale_log2;
                 if (__any(mx_log2 > m + kRescaleSlack)) {
                     const float m_new = fmaxf(m, mx_log2);
@@ -646,7 +654,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention_f32(
                         my = max3(my, s[kt][r + 2], s[kt][r + 3]);
                     }
                 mx = fmaxf(mx, my);
-                const float mx_log2 = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mx_log2 = max_halves(mx);
                 if (__any(mx_log2 > m + kRescaleSlack)) {
                     const float m_new = fmaxf(m, mx_log2);
                     const float alpha = m_new > m ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
