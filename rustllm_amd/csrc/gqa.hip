@@ -178,8 +178,14 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // rows of the tile to memory: 16 lanes per 256-byte row segment
+    // rows of the tile to memory: 16 lanes per 256-byte row segment.  A
+    // 16-byte LDS read serves 32 lanes at once over 128 dword banks, so the
+    // two rows lanes 0-31 (and 32-63) read must lie 64 dwords apart modulo
+    // 128: at a row stride of 68 dwords (136 halves, which keeps the MFMA
+    // layout writes above conflict-free) that is rows 16 apart.  Instruction
+    // i reads rows 2i, 2i + 16 (lanes 0-31) and 2i + 1, 2i + 17 (lanes 32-63).
     const uint32_t keys_here = min(128u, p.kv_len - kbase);
+    const uint32_t rlane = (lane / 32) + 16 * ((lane / 16) % 2);
     if (keys_here == 128 && q0 + 31 < p.q_len) {
         // A whole tile (the common case): every LDS read, then every store,
         // with no branch between them (under per-store branches the compiler
@@ -187,10 +193,10 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
         h8 w[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            w[i] = *reinterpret_cast<const h8*>(my + (i * 4 + lane / 16) * TS + (lane % 16) * 8);
+            w[i] = *reinterpret_cast<const h8*>(my + (2 * i + rlane) * TS + (lane % 16) * 8);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t r = i * 4 + lane / 16;
+            const uint32_t r = 2 * i + rlane;
             half_t* dst = out + (uint64_t(bh) * p.q_len + q0 + r) * p.kv_len + kbase +
                           (lane % 16) * 8;
             put_scores_u<STREAM>(dst, w[i]);
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint32_t r = i * 4 + lane / 16;  // tile row (query q0 + r)
+        const uint32_t r = 2 * i + rlane;  // tile row (query q0 + r)
         const uint32_t c8 = (lane % 16) * 8;   // first key of this lane's 8
         if (q0 + r >= p.q_len || c8 >= keys_here) continue;
         const h8 w = *reinterpret_cast<const h8*>(my + r * TS + c8);
