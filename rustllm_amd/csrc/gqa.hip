@@ -10,12 +10,14 @@
 // or read once; Q, K and V are small), in f32 by the f32 matrix cores.  A
 // head size of 32..128 in steps of 32 takes the matrix cores
 // (v_mfma_f32_32x32x16_f16 for f16):
-//  * QK^T computes S^T = K Q^T per wave (32 queries x 128 keys): the
-//    workgroup's 128 key rows are loaded whole into LDS in the order that
-//    swaps bits 2 and 3 of the key index, so every lane ends up holding runs
-//    of 8 consecutive keys of one query row; each wave stages its score tile
-//    in LDS and writes 256-byte row segments per 16 lanes.  All key tiles of
-//    one (head, query tile) run on one XCD.
+//  * QK^T computes S^T = K Q^T per wave (32 queries x 128 keys; a
+//    workgroup takes 128 queries x 256 keys): the workgroup's 256 key rows are
+//    loaded whole into LDS in the order that swaps bits 2 and 3 of the key
+//    index, so every lane ends up holding runs of 8 consecutive keys of one
+//    query row; each wave stages its score tile in LDS (reusing the key
+//    tile's space) and writes 256-byte row segments per 16 lanes, 512 bytes
+//    a row per workgroup.  All key tiles of one (head, query tile) run on
+//    one XCD.
 //  * PV computes O^T = V^T P^T in steps of 128 keys: each wave stages its
 //    32 x 128 probabilities in LDS (whole 256-byte row segments per 16
 //    lanes), V goes through LDS row-major and its transposed operand comes
@@ -33,8 +35,8 @@ namespace {
 struct GqaParams {
     uint32_t q_heads, group, q_len, kv_len, head_dim;
     uint64_t kv_head_stride;  // elements between KV heads (kv_capacity * head_dim)
-    uint32_t q_tiles;         // query tiles per head (MFMA kernels)
-    uint32_t k_tiles;         // 128-key tiles per query tile (QK^T MFMA kernels)
+    uint32_t q_tiles;         // 128-query tiles per head (MFMA kernels)
+    uint32_t k_tiles;         // key tiles per query tile (QK^T: 256 keys in f16, 128 in f32)
     uint32_t k_per_block;     // key tiles one f32 QK^T workgroup computes in turn
     uint32_t k_groups;        // f32 QK^T workgroups per query tile
     uint32_t qk_groups;       // (head, query tile) groups of the f16 QK^T kernel
@@ -94,11 +96,18 @@ __device__ inline uint32_t kv_head_of(uint32_t bh, const GqaParams& p) {
 
 // ------------------------------------------------------------ QK^T, MFMA
 
+// Workgroup = 128 queries x 256 keys of one head; wave w = queries 32 (w % 4)
+// .. + 31 x keys 128 (w / 4) .. + 127.  The workgroup writes 128 rows x 512
+// bytes of scores: HBM takes the [15, 4096, 4096] tensor in that pattern at
+// ~83 us, against ~90 us as 128 rows x 256 bytes (a write-pattern probe of
+// the same shapes).  The 256 key rows go to LDS once for the four query
+// quarters; after the products the waves stage their score tiles in the
+// same LDS (a barrier between), which keeps a workgroup at 70 KB.
 // Rows of kv_len % 8 != 0 scores start off the 16-byte grid; their 8-score
 // chunks go out as unaligned 16-byte stores (put_scores_u), and a row's last
 // partial chunk element by element.
 template <int NT, bool STREAM>
-__global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ q,
+__global__ __launch_bounds__(512) void k_gqa_qk_mfma(const half_t* __restrict__ q,
                                                      const half_t* __restrict__ k,
                                                      half_t* __restrict__ out, GqaParams p) {
     constexpr int D = 32 * NT;
@@ -106,31 +115,31 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     constexpr int TS = 128 + 8;  // LDS row stride (halves) of a wave's 32 x 128 score tile
     constexpr int KS = D + 8;    // LDS row stride (halves) of the key tile
     constexpr int ROW_CHUNKS = D / 8;
-    __shared__ __align__(16) half_t tile[4][32 * TS];
-    __shared__ __align__(16) half_t ks[128 * KS];
+    constexpr int KEY_HALVES = 256 * KS;
+    constexpr int LDS_HALVES = KEY_HALVES > 8 * 32 * TS ? KEY_HALVES : 8 * 32 * TS;
+    __shared__ __align__(16) half_t lds[LDS_HALVES];
+    half_t* const ks = lds;  // the key tile, then (after a barrier) the eight score tiles
     const uint32_t wave = threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t col = lane % 32;
     const uint32_t hs = lane / 32;
-    // block = (head, 128-query tile, 128-key tile); wave = 32 queries x 128 keys.
-    // Hardware block b runs on XCD b mod 8.  XCD x takes a contiguous run of
-    // (head, query tile) groups -- consecutive heads, which share KV heads --
-    // with all their key tiles: the cache lines that neighbouring key tiles
-    // share (rows off the line grid) are merged in one L2, a group's queries
-    // and a KV head's keys are fetched into few L2s.  The grid is padded to
-    // whole runs per XCD.
+    // block = (head, 128-query tile, 256-key tile).  Hardware block b runs on
+    // XCD b mod 8.  XCD x takes a contiguous run of (head, query tile) groups
+    // -- consecutive heads, which share KV heads -- with all their key tiles:
+    // the cache lines that neighbouring key tiles share (rows off the line
+    // grid) are merged in one L2, a group's queries and a KV head's keys are
+    // fetched into few L2s.  The grid is padded to whole runs per XCD.
     const uint32_t xcd = blockIdx.x % 8, xi = blockIdx.x / 8;
     const uint32_t per_xcd = (p.qk_groups + 7) / 8;
     const uint32_t group = xcd * per_xcd + xi / p.k_tiles;
     if (group >= p.qk_groups) return;  // padding (the whole block)
-    const uint32_t lb = group * p.k_tiles + xi % p.k_tiles;
-    const uint32_t kt_blk = lb % p.k_tiles;
-    const uint32_t rest = lb / p.k_tiles;
-    const uint32_t qt = rest % p.q_tiles;
-    const uint32_t bh = rest / p.q_tiles;
-    const uint32_t q0 = qt * 128 + wave * 32;
+    const uint32_t kt_blk = xi % p.k_tiles;
+    const uint32_t qt = group % p.q_tiles;
+    const uint32_t bh = group / p.q_tiles;
+    const uint32_t q0 = qt * 128 + (wave % 4) * 32;
     const half_t* kh = k + uint64_t(kv_head_of(bh, p)) * p.kv_head_stride;
-    const uint32_t kbase = kt_blk * 128;
+    const uint32_t kblock = kt_blk * 256;
+    const uint32_t kbase = kblock + (wave / 4) * 128;  // this wave's first key
     // this wave's queries first, so their loads overlap the key tile's; a
     // query past q_len reads row 0 (its scores are not stored)
     const uint32_t qi = q0 + col;
@@ -139,42 +148,50 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     const half_t* qrow = q + (uint64_t(bh) * p.q_len + (q_valid ? qi : 0)) * D + 8 * hs;
 #pragma unroll
     for (int c = 0; c < DC; ++c) qf[c] = *reinterpret_cast<const h8*>(qrow + 16 * c);
-    // the block's 128 key rows -> LDS, whole rows per 8 (D 64) lanes; key row
-    // j goes to LDS row perm32(j) so that the S^T operand of lane i is row i.
-    // Keys past kv_len read row kv_len - 1 (their scores are not stored).
+    // the block's 256 key rows -> LDS, whole rows per ROW_CHUNKS lanes; key
+    // row j goes to LDS row perm32(j) of its 32-row group, so that the S^T
+    // operand of lane i is row i.  Keys past kv_len read row kv_len - 1
+    // (their scores are not stored).
 #pragma unroll
-    for (int li = 0; li < 128 * ROW_CHUNKS / 256; ++li) {
-        const uint32_t chunk = threadIdx.x + 256 * li;
+    for (int li = 0; li < 256 * ROW_CHUNKS / 512; ++li) {
+        const uint32_t chunk = threadIdx.x + 512 * li;
         const uint32_t j = chunk / ROW_CHUNKS;
         const uint32_t d0 = (chunk % ROW_CHUNKS) * 8;
-        const uint32_t key = min(kbase + j, p.kv_len - 1);
-        *reinterpret_cast<h8*>(ks + perm32(j) * KS + d0) =
+        const uint32_t key = min(kblock + j, p.kv_len - 1);
+        *reinterpret_cast<h8*>(ks + ((j & ~31u) | perm32(j & 31u)) * KS + d0) =
             *reinterpret_cast<const h8*>(kh + uint64_t(key) * D + d0);
     }
     __syncthreads();
-    if (q0 >= p.q_len) return;  // (no barrier below)
-    half_t* my = tile[wave];
+    const bool active = q0 < p.q_len && kbase < p.kv_len;
+    const uint32_t keys_here = kbase < p.kv_len ? min(128u, p.kv_len - kbase) : 0u;
+    // the scores, rounded to f16 as each 32-key tile completes: lane (query
+    // col, hs) holds keys 32 t + 16 half + 8 hs + 0..7 in sh[t][half]
+    h8 sh[4][2];
+    if (active) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {  // four 32-key tiles
-        const uint32_t k0 = kbase + t * 32;
-        if (k0 >= p.kv_len) break;
-        const half_t* krow = ks + (t * 32 + col) * KS + 8 * hs;
-        f32x16 s;
+        for (int t = 0; t < 4; ++t) {  // four 32-key tiles
+            const half_t* krow = ks + ((wave / 4) * 128 + t * 32 + col) * KS + 8 * hs;
+            f32x16 sc;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+            for (int r = 0; r < 16; ++r) sc[r] = 0.0f;
 #pragma unroll
-        for (int c = 0; c < DC; ++c)
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(krow + 16 * c),
-                                                       qf[c], s, 0, 0, 0);
-        // lane (query col, hs) holds keys k0 + 16 half + 8 hs + 0..7
+            for (int c = 0; c < DC; ++c)
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    *reinterpret_cast<const h8*>(krow + 16 * c), qf[c], sc, 0, 0, 0);
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            h8 w;
+            for (int half = 0; half < 2; ++half)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) w[e] = half_t(s[8 * half + e]);
-            *reinterpret_cast<h8*>(my + col * TS + t * 32 + 16 * half + 8 * hs) = w;
+                for (int e = 0; e < 8; ++e) sh[t][half][e] = half_t(sc[8 * half + e]);
         }
     }
+    __syncthreads();  // every wave's key reads are done: the LDS takes the score tiles
+    if (!active) return;  // (no barrier below)
+    half_t* my = lds + wave * 32 * TS;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+            *reinterpret_cast<h8*>(my + col * TS + t * 32 + 16 * half + 8 * hs) = sh[t][half];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -184,7 +201,6 @@ __global__ __launch_bounds__(256) void k_gqa_qk_mfma(const half_t* __restrict__ 
     // 128: at a row stride of 68 dwords (136 halves, which keeps the MFMA
     // layout writes above conflict-free) that is rows 16 apart.  Instruction
     // i reads rows 2i, 2i + 16 (lanes 0-31) and 2i + 1, 2i + 17 (lanes 32-63).
-    const uint32_t keys_here = min(128u, p.kv_len - kbase);
     const uint32_t rlane = (lane / 32) + 16 * ((lane / 16) % 2);
     if (keys_here == 128 && q0 + 31 < p.q_len) {
         // A whole tile (the common case): every LDS read, then every store,
@@ -731,14 +747,15 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
     const uint64_t heads = s.batch * s.q_heads;
     if constexpr (std::is_same<T, half_t>::value) {
         if (use_mfma<T>(s, qd, kd, od)) {
+            // 128-query x 256-key workgroups; one XCD per (head, query tile)
+            // group, the grid padded to 8 runs
             p.q_tiles = uint32_t(ceil_div(s.q_len, 128));
-            p.k_tiles = uint32_t(ceil_div(s.kv_len, 128));
-            // one XCD per (head, query tile) group, the grid padded to 8 runs
+            p.k_tiles = uint32_t(ceil_div(s.kv_len, 256));
             const uint64_t groups = heads * p.q_tiles;
             const uint64_t xgrid = ceil_div(groups, 8) * 8 * p.k_tiles;
             if (xgrid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA QK grid exceeds u32");
             p.qk_groups = uint32_t(groups);
-            const dim3 g(static_cast<unsigned>(xgrid)), b(256);
+            const dim3 g(static_cast<unsigned>(xgrid)), b(512);
             const bool lines = s.kv_len % 64 == 0;  // score rows are whole 128-byte lines
 #define RL_QK(NT)                                                                      \
     do {                                                                               \
