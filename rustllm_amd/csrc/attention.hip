@@ -1190,7 +1190,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split(
 // The split-key decode step on the matrix cores (f16, R <= 16 rows per KV
 // head, head size D = 64 or 128).  Per wave of 64 keys: S^T = K Q^T as four
 // 16-key tiles of v_mfma_f32_16x16x32_f16 (A = key rows loaded straight
-// from memory, B = the query rows, zero past R), then O = P V in two 32-key
+// from memory, B = the query rows; a row past R reads row 0 and is masked),
+// then O = P V in two 32-key
 // steps (A = P from the score registers, B = value columns read from the
 // wave's LDS stage by transpose reads).  Row a of score tile m holds key
 // key16(m, a), so that lane l's registers of tiles 2t and 2t + 1 hold keys
@@ -1232,7 +1233,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split_mfma(
     __shared__ __align__(16) half_t vstage[kSplitWaves][64 * D];
     __shared__ float merge_m[kSplitWaves][RM];
     __shared__ float merge_l[kSplitWaves][RM];
-    __shared__ float merge_o[kSplitWaves][RM][D];
+    // rows padded by 4 floats: the 64 lanes' writes below (rows 4 g + r,
+    // columns 16 nt + lane % 16) then fall on 64 distinct banks
+    __shared__ float merge_o[kSplitWaves][RM][D + 4];
     const uint32_t wave = threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t lr = lane % 16;  // query row of the scores and P, column of the outputs
@@ -1327,13 +1330,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split_mfma(
         }
     lsum = rows4_sum(lsum);
 
-    // P V: lane 16 g + 4 j + a reads 4 elements of value rows 32 t + 8 g + j
-    // and + 4, columns 16 nt + 4 a; the transpose hands lane 16 g + i column
-    // 16 nt + i of those eight rows
     // the value rows to the wave's LDS stage (read by this wave only: no barrier)
     half_t* stage = vstage[wave];
 #pragma unroll
     for (int i = 0; i < D / 8; ++i) *reinterpret_cast<h8*>(stage + (64 * i + lane) * 8) = vf[i];
+    // P V: lane 16 g + 4 j + a reads 4 elements of value rows 32 t + 8 g + j
+    // and + 4, columns 16 nt + 4 a; the transpose hands lane 16 g + i column
+    // 16 nt + i of those eight rows
     f32x4 o[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) o[nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
