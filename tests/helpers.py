@@ -1,4 +1,6 @@
-"""Comparison helpers shared by the tests (tolerances as the north star states them)."""
+"""Comparison helpers shared by the tests: the reference's known-answer vectors, bit-exact
+comparison, relative error above a magnitude floor, f16 ulp distance, and float64 attention
+with forward error bounds for the attention products."""
 
 from __future__ import annotations
 

@@ -20,7 +20,7 @@ takes views of its own tensors where a projection would sit (Q/K/V are
 slices of xn; the down projection's output is a slice of act); the FFN's
 gate/up projections are the one place with no such view, so SwiGLU reads
 seeded N(0, 1) gate/up tensors.  Every stage is compared with the oracle
-applied to that stage's actual GPU inputs, at the north-star bars:
+applied to that stage's actual GPU inputs, at the parity bars of the ops:
 bit-exact RoPE, repeat_kv, gathers and adds; f16 RMSNorm, softmax and SwiGLU
 within 2 ulp (masked probabilities exactly 0); the two products within the
 float64 forward error bounds the attention tests use.
