@@ -674,6 +674,17 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
                        kernel_times_us(ctx, [lambda: ctx.attention(qd, s0[1], s0[2], 0.125,
                                                                    tok - 1, None, od)], reps,
                                        batch=False)))
+    # the same step through the allocation-free entry (same kernel, no pool
+    # block, so a graph can record it): also the sustained figure, over
+    # rotated copies of the cache (>= 1 GiB in all, so that every replay
+    # reads K and V from HBM)
+    n_dec = int(max(4, -(-(1 << 30) // (2 * k.size * 2))))
+    dsets = [(ctx.upload(k), ctx.upload(v)) for _ in range(n_dec)]
+    rows.append(op_row("decode attention_f16, allocation-free entry (1 token, 4096-row cache)",
+                       "f16", [1, qh, 1, hd], dec_bytes,
+                       kernel_times_us(ctx, [lambda s=s: ctx.attention_noalloc(
+                           qd, s[0], s[1], 0.125, tok - 1, None, od) for s in dsets], reps)))
+    del dsets
     return rows
 
 
