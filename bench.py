@@ -293,7 +293,8 @@ def kernel_times_us(ctx, launches, reps, batch=True):
     us = [ctx.elapsed_ms(start, stop) * 1e3 for start, stop in evs]
     for e in [e for pair in evs for e in pair]:
         ctx.destroy_event(e)
-    return us, (graph_batch_us(ctx, launches) if GRAPH_BATCH and batch else None)
+    return us, (graph_batch_us(ctx, launches) if GRAPH_BATCH and batch else None), \
+        len(launches) + reps
 
 
 # Sustained figures: each op also timed as back-to-back launches recorded in
@@ -329,7 +330,7 @@ def graph_batch_us(ctx, launches, min_per_graph=32, replays=8):
 
 
 def op_row(name, dtype, shape, nbytes, timing):
-    us_list, batch_us = timing
+    us_list, batch_us = timing[0], timing[1]
     us = float(np.mean(us_list))
     gbs = nbytes / (us * 1e-6) / 1e9
     batch = "   n/a" if batch_us is None else f"{batch_us:7.2f}"
@@ -339,6 +340,9 @@ def op_row(name, dtype, shape, nbytes, timing):
            "us_min": round(float(np.min(us_list)), 3),
            "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
            "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None}
+    if len(timing) > 2:  # kernel dispatches of the one-launch timing: warm-up, then timed
+        row["dispatches"] = timing[2]
+        row["timed"] = len(us_list)
     if batch_us is not None:
         gb = nbytes / (batch_us * 1e-6) / 1e9
         row.update({"us_graph_batch": round(batch_us, 3), "GB/s_graph_batch": round(gb, 1),
