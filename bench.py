@@ -310,8 +310,10 @@ _LIVE_GRAPHS = []
 def graph_batch_us(ctx, launches, min_per_graph=32, replays=8):
     """us per launch of back-to-back launches replayed as a graph: one launch
     on each of the op's buffer sets (>= 1 GiB in total, so a replay streams
-    from HBM, not from the 256 MB Infinity Cache), at least `min_per_graph`."""
+    from HBM, not from the 256 MB Infinity Cache), at least `min_per_graph`.
+    One kernel per launch: the fusion of recorded streaming ops is off here."""
     per_graph = max(min_per_graph, len(launches))
+    ctx.set_fusion(False)
     ctx.capture_begin()
     failed = False
     try:
@@ -321,6 +323,7 @@ def graph_batch_us(ctx, launches, min_per_graph=32, replays=8):
         failed = True
     finally:
         graph = ctx.capture_end()
+        ctx.set_fusion(True)
     _LIVE_GRAPHS.append(graph)
     if failed:
         return None
@@ -1140,6 +1143,14 @@ def main():
     if aux:
         log(f"step on 1 stream: {ms_seq * 1e3:.1f} us, {seq_value:.1f} GB/s "
             f"({100 * seq_value / PEAK_GBS:.1f}% of peak)")
+    # the same step recorded with one kernel per op (no fusion of the
+    # independent streaming ops), for comparison
+    ctx.set_fusion(False)
+    ms_unfused = time_step(ctx, [], ops, sets, args.steps, args.warmup)
+    ctx.set_fusion(True)
+    unfused_value = step_bytes / (ms_unfused * 1e-3) / 1e9
+    log(f"step with one kernel per op: {ms_unfused * 1e3:.1f} us, {unfused_value:.1f} GB/s "
+        f"({100 * unfused_value / PEAK_GBS:.1f}% of peak)")
     for a in aux:
         a.close()
 
@@ -1205,7 +1216,10 @@ def main():
                    "buffer_sets": args.sets, "footprint_gib": round(footprint / 2**30, 2),
                    "streams": args.streams,
                    "one_stream_GBps": round(seq_value, 1),
-                   "one_stream_ms_per_step": round(ms_seq, 5)},
+                   "one_stream_ms_per_step": round(ms_seq, 5),
+                   "recorded_streaming_ops_fused": True,
+                   "one_kernel_per_op_GBps": round(unfused_value, 1),
+                   "one_kernel_per_op_ms_per_step": round(ms_unfused, 5)},
         "pct_of_peak": round(100 * value / PEAK_GBS, 1),
         "roofline": roofline,
         "cpu_baseline": cpu,

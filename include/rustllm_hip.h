@@ -163,8 +163,16 @@ rl_status rl_execution_finish(rl_context* ctx);
 
 /* Records the ops enqueued between begin and end as a replayable graph (the
  * HIP counterpart of re-encoding one command buffer).  Buffers used while
- * recording must stay allocated while the graph is replayed. */
+ * recording must stay allocated while the graph is replayed.  While
+ * recording, consecutive streaming ops (add, mul, SiLU, SwiGLU, casts, bias
+ * add) that touch disjoint bytes or only read the same ones are recorded as
+ * one kernel (each computing exactly what its own launch does), as the
+ * encoders of one Metal command buffer may overlap. */
 rl_status rl_graph_capture_begin(rl_context* ctx);
+/* No counterpart in the reference: turns that fusion of recorded streaming
+ * ops off (enabled = 0) or on (the default), for callers that time or
+ * inspect the ops of a graph one by one. */
+rl_status rl_context_set_fusion(rl_context* ctx, int32_t enabled);
 rl_status rl_graph_capture_end(rl_context* ctx, rl_graph** out);
 rl_status rl_graph_launch(rl_context* ctx, rl_graph* graph);
 void rl_graph_destroy(rl_graph* graph);

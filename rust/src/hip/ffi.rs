@@ -129,6 +129,7 @@ extern "C" {
     pub fn rl_execution_begin(ctx: *mut rl_context) -> rl_status;
     pub fn rl_execution_finish(ctx: *mut rl_context) -> rl_status;
     pub fn rl_graph_capture_begin(ctx: *mut rl_context) -> rl_status;
+    pub fn rl_context_set_fusion(ctx: *mut rl_context, enabled: i32) -> rl_status;
     pub fn rl_graph_capture_end(ctx: *mut rl_context, out: *mut *mut rl_graph) -> rl_status;
     pub fn rl_graph_launch(ctx: *mut rl_context, graph: *mut rl_graph) -> rl_status;
     pub fn rl_graph_destroy(graph: *mut rl_graph);

@@ -100,6 +100,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "rl_execution_begin": ([_P], _I32),
     "rl_execution_finish": ([_P], _I32),
     "rl_graph_capture_begin": ([_P], _I32),
+    "rl_context_set_fusion": ([_P, _I32], _I32),
     "rl_graph_capture_end": ([_P, ctypes.POINTER(_P)], _I32),
     "rl_graph_launch": ([_P, _P], _I32),
     "rl_graph_destroy": ([_P], None),
@@ -304,6 +305,11 @@ class Context:
                                       buf.byte_len))
         return out
 
+    def copy(self, src: DeviceBuffer, dst: DeviceBuffer) -> None:
+        """Stream-ordered device copy of src's bytes into dst."""
+        check(self.lib.rl_buffer_copy(self.handle, ctypes.byref(src.raw), ctypes.byref(dst.raw),
+                                      src.byte_len))
+
     def upload(self, array) -> DeviceBuffer:
         a = np.ascontiguousarray(array)
         if a.dtype not in _DTYPES and a.dtype != np.uint32:
@@ -359,6 +365,10 @@ class Context:
 
     def capture_begin(self) -> None:
         check(self.lib.rl_graph_capture_begin(self.handle))
+
+    def set_fusion(self, enabled: bool) -> None:
+        """Whether streaming ops recorded into a graph share fused launches."""
+        check(self.lib.rl_context_set_fusion(self.handle, 1 if enabled else 0))
 
     def capture_end(self):
         g = ctypes.c_void_p()

@@ -1550,6 +1550,7 @@ rl_status scratch_on_device(rl_context* ctx, void** out) {
     std::call_once(slot.once, [&] {
         void* ptr = nullptr;
         hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err == hipSuccess) err = flush_fused(ctx) == RL_OK ? hipSuccess : hipErrorLaunchFailure;
         if (err == hipSuccess) {
             hipLaunchKernelGGL(k_zero_u32, dim3(unsigned(kScratchTicketWords / 256)), dim3(256), 0,
                                ctx->stream, static_cast<uint32_t*>(ptr),

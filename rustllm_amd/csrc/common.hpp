@@ -49,6 +49,39 @@ struct BufferPool {
     ~BufferPool();
 };
 
+// A streaming op deferred while a graph is recorded: independent ones are
+// launched together as one kernel (elementwise.hip: flush_fused).  `kind`
+// names the op's body, `blocks` its share of the grid; the byte ranges it
+// reads and writes decide which ops may share a launch.
+struct FusedOp {
+    uint32_t kind = 0;
+    uint32_t blocks = 0;
+    const void* a = nullptr;
+    const void* b = nullptr;
+    void* out = nullptr;
+    uint64_t n_packs = 0;
+    uint32_t tail = 0;       // map: elements after the last pack
+    uint32_t div = 1;        // packs per row (bias add, row gather) or per head (repeat_kv)
+    uint64_t head_packs = 0;  // repeat_kv
+    uint32_t repeats = 0;
+    bool small_index = false;
+    uint32_t outer_rank = 0;  // row gather: outer dims, innermost first
+    uint32_t outer_dim[4] = {1, 1, 1, 1};
+    uint32_t outer_stride[4] = {0, 0, 0, 0};
+    uintptr_t read[2][2] = {{0, 0}, {0, 0}};  // [begin, end) of each input
+    uintptr_t write[2] = {0, 0};
+};
+constexpr uint32_t kMaxFused = 16;
+constexpr uint32_t kMaxFusedOuterRank = 4;
+// Fused kinds (elementwise.hip launches them): maps, bias adds, row
+// gathers and repeat_kv.
+enum FusedKind : uint32_t {
+    kFusedAddF32 = 1, kFusedMulF32, kFusedSiluF32, kFusedSwigluF32,
+    kFusedAddF16, kFusedMulF16, kFusedSiluF16, kFusedSwigluF16,
+    kFusedCastF32F16, kFusedCastF16F32, kFusedBiasF32, kFusedBiasF16,
+    kFusedGatherF32, kFusedGatherF16, kFusedRepeatF32, kFusedRepeatF16,
+};
+
 }  // namespace rl
 
 struct rl_context {
@@ -84,13 +117,36 @@ struct rl_context {
     // context.  ticket_count is in 32-bit words.
     uint32_t* tickets = nullptr;
     uint64_t ticket_count = 0;
+
+    // Streaming ops recorded into a graph but not yet launched (at most
+    // kMaxFused, no two touching the same bytes unless both only read them).
+    rl::FusedOp fused[rl::kMaxFused];
+    uint32_t fused_count = 0;
+    bool fuse_recorded = true;  // rl_context_set_fusion
 };
+
+
+namespace rl {
+// Launches the deferred streaming ops as one kernel (nothing if there are
+// none).  Every other stream operation of a recording context calls it
+// first, so the recorded order is the call order.
+rl_status flush_fused(rl_context* ctx);
+// Adds an op to the deferred ones, launching those first if the op writes
+// bytes one of them touches, reads bytes one of them writes, or the batch
+// is full.
+rl_status defer_fused(rl_context* ctx, const FusedOp& f);
+// Whether an op launched now on `ctx` is deferred for a fused launch.
+inline bool fusing(const rl_context* ctx) {
+    return ctx->capturing && ctx->fuse_recorded && ctx->timed_start == nullptr;
+}
+}  // namespace rl
 
 // Every kernel launch of the library: on the context's stream, and, when
 // armed by rl_event_time_next_kernel, with the kernel's own start/end
 // timestamps recorded (hipExtLaunchKernelGGL).
 #define RL_LAUNCH(ctx, kernel, grid, block, ...)                                              \
     do {                                                                                      \
+        if ((ctx)->fused_count != 0) (void)rl::flush_fused(ctx);                              \
         if ((ctx)->timed_start != nullptr) {                                                  \
             hipExtLaunchKernelGGL(kernel, grid, block, 0, (ctx)->stream, (ctx)->timed_start,  \
                                   (ctx)->timed_stop, 0, __VA_ARGS__);                         \

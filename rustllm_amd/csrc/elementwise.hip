@@ -13,6 +13,9 @@
 // and a 300 MB one 80%, non-temporal loads being worth about 8 points.  The
 // few elements past the last whole pack are handled by block 0.
 #include "common.hpp"
+#include "movement_bodies.hpp"
+
+#include <type_traits>
 
 namespace rl {
 namespace {
@@ -121,21 +124,29 @@ struct MapShape<CopyOp, float, half_t> {
     static constexpr bool nt_store = false;
 };
 
-// out[i] = op(a[i], b[i]) for ARITY 2, op(a[i]) for ARITY 1.  Block b covers
-// packs [b * 256 * UNROLL, (b + 1) * 256 * UNROLL): the grid spans the whole
-// array (at most 2^32 elements, so at most 2^22 blocks), with no loop.
+// Pack size of a map: 16-byte packs; the widening cast uses 4-element packs
+// so its stores stay 16 B per lane and contiguous across the wave (8-element
+// f32 packs would be two strided 16-byte stores, which costs extra HBM
+// writes).
+template <typename TIn, typename TOut>
+constexpr int map_pack() {
+    return (sizeof(TIn) == 4 && sizeof(TOut) == 4) ? 4 : (sizeof(TOut) == 4 ? 4 : 8);
+}
+
+// out[i] = op(a[i], b[i]) for ARITY 2, op(a[i]) for ARITY 1.  Block blk covers
+// packs [blk * 256 * UNROLL, (blk + 1) * 256 * UNROLL): the grid spans the
+// whole array (at most 2^32 elements, so at most 2^22 blocks), with no loop.
 template <typename TIn, typename TOut, int N, int UNROLL, int ARITY, bool NTS, bool PHASED,
           typename Op>
-__global__ __launch_bounds__(kThreads) void k_map(const TIn* __restrict__ a,
-                                                  const TIn* __restrict__ b,
-                                                  TOut* __restrict__ out, uint64_t n_packs,
-                                                  uint32_t tail, Op op) {
+__device__ inline void map_body(const TIn* __restrict__ a, const TIn* __restrict__ b,
+                                TOut* __restrict__ out, uint64_t n_packs, uint32_t tail, Op op,
+                                uint32_t blk) {
     typedef typename VecOf<TIn, N>::type VI;
     typedef typename VecOf<TOut, N>::type VO;
     const VI* va = reinterpret_cast<const VI*>(a);
     const VI* vb = reinterpret_cast<const VI*>(b);
     VO* vo = reinterpret_cast<VO*>(out);
-    const uint64_t base = uint64_t(blockIdx.x) * kThreads * UNROLL + threadIdx.x;
+    const uint64_t base = uint64_t(blk) * kThreads * UNROLL + threadIdx.x;
     if constexpr (PHASED) {
         // Three phases: every pack's loads (at indices clamped into the
         // array), every result, then every store (a clamped pack rewrites the
@@ -200,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void k_map(const TIn* __restrict__ a,
             }
         }
     }
-    if (blockIdx.x == 0 && threadIdx.x < tail) {
+    if (blk == 0 && threadIdx.x < tail) {
         uint64_t i = n_packs * N + threadIdx.x;
         float y = 0.0f;
         if constexpr (ARITY == 2) y = to_float(b[i]);
@@ -208,20 +219,29 @@ __global__ __launch_bounds__(kThreads) void k_map(const TIn* __restrict__ a,
     }
 }
 
-// out[r, c] = x[r, c] + bias[c] on packs; col_packs = cols / N.
+template <typename TIn, typename TOut, int N, int UNROLL, int ARITY, bool NTS, bool PHASED,
+          typename Op>
+__global__ __launch_bounds__(kThreads) void k_map(const TIn* __restrict__ a,
+                                                  const TIn* __restrict__ b,
+                                                  TOut* __restrict__ out, uint64_t n_packs,
+                                                  uint32_t tail, Op op) {
+    map_body<TIn, TOut, N, UNROLL, ARITY, NTS, PHASED, Op>(a, b, out, n_packs, tail, op,
+                                                            blockIdx.x);
+}
+
+// out[r, c] = x[r, c] + bias[c] on packs; col_packs = cols / N.  Block blk
+// of nblk strides over the packs.
 template <typename T, int N, int UNROLL>
-__global__ __launch_bounds__(kThreads) void k_add_broadcast(const T* __restrict__ x,
-                                                            const T* __restrict__ bias,
-                                                            T* __restrict__ out,
-                                                            uint64_t n_packs, FastDiv col_packs) {
+__device__ inline void broadcast_body(const T* __restrict__ x, const T* __restrict__ bias,
+                                      T* __restrict__ out, uint64_t n_packs, FastDiv col_packs,
+                                      uint32_t blk, uint32_t nblk) {
     typedef typename VecOf<T, N>::type V;
     const V* vx = reinterpret_cast<const V*>(x);
     const V* vbias = reinterpret_cast<const V*>(bias);
     V* vo = reinterpret_cast<V*>(out);
     const uint64_t tile = uint64_t(kThreads) * UNROLL;
-    const uint64_t step = uint64_t(gridDim.x) * tile;
-    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_packs;
-         base += step) {
+    const uint64_t step = uint64_t(nblk) * tile;
+    for (uint64_t base = uint64_t(blk) * tile + threadIdx.x; base < n_packs; base += step) {
         V rx[UNROLL], rb[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
@@ -245,6 +265,14 @@ __global__ __launch_bounds__(kThreads) void k_add_broadcast(const T* __restrict_
             }
         }
     }
+}
+
+template <typename T, int N, int UNROLL>
+__global__ __launch_bounds__(kThreads) void k_add_broadcast(const T* __restrict__ x,
+                                                            const T* __restrict__ bias,
+                                                            T* __restrict__ out,
+                                                            uint64_t n_packs, FastDiv col_packs) {
+    broadcast_body<T, N, UNROLL>(x, bias, out, n_packs, col_packs, blockIdx.x, gridDim.x);
 }
 
 // out[r, c] = x[r, c] + bias[c] for rows of at most 1024 packs: thread t of
@@ -299,15 +327,131 @@ inline unsigned grid_for(uint64_t items, uint64_t per_block) {
     return unsigned(blocks);
 }
 
+// ----------------------------------------------- streaming ops in one launch
+
+// While a graph is recorded, the maps and bias adds below and the row
+// gathers and repeat_kv of movement.hip are not launched one by one: runs of
+// them that touch disjoint bytes (or only read the same bytes) are recorded
+// as one kernel whose blocks are split among the ops,
+// each op's blocks running that op's body on its own share of the grid.
+// Successive kernels of one stream run one after another here, each with a
+// ramp-up and a drain of ~1.5-2 us; one kernel for a batch of independent
+// ops (the reference's ops encoded into one command buffer, which the GPU
+// may overlap) streams them as one.  Each op computes exactly what its own
+// launch computes (the same body and pack shape).
+typedef OuterDimsT<kMaxFusedOuterRank, uint32_t> FusedDims;
+
+struct FusedSeg {
+    uint32_t kind;
+    uint32_t tail;  // map
+    const void* a;
+    const void* b;
+    void* out;
+    uint64_t n_packs;
+    uint64_t head_packs;  // repeat_kv
+    FastDiv div;          // packs per row (bias add, row gather) or per head (repeat_kv)
+    uint32_t repeats;     // repeat_kv
+    uint32_t small_index;
+    FusedDims outer;      // row gather
+};
+struct FusedTable {
+    uint32_t first[kMaxFused];  // each op's first block in the fused grid (ascending)
+    uint32_t count;
+    FusedSeg seg[kMaxFused];
+};
+
+constexpr int kBroadcastUnroll = 4;  // packs per thread of the bias add
+
+// The fused kind of a map (0: launched on its own).
+template <typename TIn, typename TOut, typename Op>
+constexpr uint32_t fused_kind() {
+    constexpr bool f32 = sizeof(TIn) == 4 && sizeof(TOut) == 4;
+    constexpr bool f16 = sizeof(TIn) == 2 && sizeof(TOut) == 2;
+    if constexpr (std::is_same<Op, AddOp>::value) return f32 ? kFusedAddF32 : f16 ? kFusedAddF16 : 0;
+    if constexpr (std::is_same<Op, MulOp>::value) return f32 ? kFusedMulF32 : f16 ? kFusedMulF16 : 0;
+    if constexpr (std::is_same<Op, SiluF32Op>::value) return f32 ? kFusedSiluF32 : 0;
+    if constexpr (std::is_same<Op, SiluF16Op>::value) return f16 ? kFusedSiluF16 : 0;
+    if constexpr (std::is_same<Op, SwigluF32Op>::value) return f32 ? kFusedSwigluF32 : 0;
+    if constexpr (std::is_same<Op, SwigluF16Op>::value) return f16 ? kFusedSwigluF16 : 0;
+    if constexpr (std::is_same<Op, CopyOp>::value)
+        return sizeof(TIn) == 4 && sizeof(TOut) == 2   ? kFusedCastF32F16
+               : sizeof(TIn) == 2 && sizeof(TOut) == 4 ? kFusedCastF16F32
+                                                       : 0;
+    return 0;
+}
+
+template <typename TIn, typename TOut, int ARITY, typename Op>
+__device__ inline void fused_map(const FusedSeg& s, uint32_t blk) {
+    typedef MapShape<Op, TIn, TOut> M;
+    map_body<TIn, TOut, map_pack<TIn, TOut>(), M::unroll, ARITY, M::nt_store, M::phased, Op>(
+        static_cast<const TIn*>(s.a), static_cast<const TIn*>(s.b), static_cast<TOut*>(s.out),
+        s.n_packs, s.tail, Op{}, blk);
+}
+
+template <typename T>
+__device__ inline void fused_bias(const FusedSeg& s, uint32_t blk, uint32_t nblk) {
+    broadcast_body<T, 16 / sizeof(T), kBroadcastUnroll>(
+        static_cast<const T*>(s.a), static_cast<const T*>(s.b), static_cast<T*>(s.out),
+        s.n_packs, s.div, blk, nblk);
+}
+
+constexpr int kMoveUnroll = 2;  // packs per thread of the row gather and repeat_kv
+
+template <typename T>
+__device__ inline void fused_gather(const FusedSeg& s, uint32_t blk, uint32_t nblk) {
+    gather_rows_body<T, 16 / sizeof(T), kMoveUnroll>(static_cast<const T*>(s.a),
+                                                     static_cast<T*>(s.out), uint32_t(s.n_packs),
+                                                     s.div, s.outer, blk, nblk);
+}
+
+template <typename T>
+__device__ inline void fused_repeat(const FusedSeg& s, uint32_t blk, uint32_t nblk) {
+    repeat_kv_body<T, 16 / sizeof(T), kMoveUnroll>(static_cast<const T*>(s.a),
+                                                   static_cast<T*>(s.out), s.n_packs, s.head_packs,
+                                                   s.div, s.repeats, s.small_index != 0, blk, nblk);
+}
+
+__global__ __launch_bounds__(kThreads) void k_fused(FusedTable t) {
+    // the op of this block: the last whose first block is not past it (the
+    // firsts are read at once and compared, no dependent loads)
+    uint32_t i = 0;
+#pragma unroll
+    for (uint32_t j = 1; j < kMaxFused; ++j) i += (j < t.count && blockIdx.x >= t.first[j]) ? 1u : 0u;
+    const FusedSeg& s = t.seg[i];  // read in place from the kernel arguments
+    const uint32_t first = t.first[i];
+    const uint32_t blk = blockIdx.x - first;
+    const uint32_t nblk = (i + 1 < t.count ? t.first[i + 1] : gridDim.x) - first;
+    switch (s.kind) {
+        case kFusedAddF32: fused_map<float, float, 2, AddOp>(s, blk); break;
+        case kFusedMulF32: fused_map<float, float, 2, MulOp>(s, blk); break;
+        case kFusedSiluF32: fused_map<float, float, 1, SiluF32Op>(s, blk); break;
+        case kFusedSwigluF32: fused_map<float, float, 2, SwigluF32Op>(s, blk); break;
+        case kFusedAddF16: fused_map<half_t, half_t, 2, AddOp>(s, blk); break;
+        case kFusedMulF16: fused_map<half_t, half_t, 2, MulOp>(s, blk); break;
+        case kFusedSiluF16: fused_map<half_t, half_t, 1, SiluF16Op>(s, blk); break;
+        case kFusedSwigluF16: fused_map<half_t, half_t, 2, SwigluF16Op>(s, blk); break;
+        case kFusedCastF32F16: fused_map<float, half_t, 1, CopyOp>(s, blk); break;
+        case kFusedCastF16F32: fused_map<half_t, float, 1, CopyOp>(s, blk); break;
+        case kFusedBiasF32: fused_bias<float>(s, blk, nblk); break;
+        case kFusedBiasF16: fused_bias<half_t>(s, blk, nblk); break;
+        case kFusedGatherF32: fused_gather<float>(s, blk, nblk); break;
+        case kFusedGatherF16: fused_gather<half_t>(s, blk, nblk); break;
+        case kFusedRepeatF32: fused_repeat<float>(s, blk, nblk); break;
+        case kFusedRepeatF16: fused_repeat<half_t>(s, blk, nblk); break;
+        default: break;
+    }
+}
+
+inline bool overlaps(const uintptr_t (&r)[2], uintptr_t begin, uintptr_t end) {
+    return r[0] < end && begin < r[1];
+}
+
 template <typename TIn, typename TOut, int ARITY, typename Op>
 rl_status launch_map(rl_context* ctx, const char* name, const void* a, const void* b, void* out,
                      uint64_t n, Op op) {
     if (n == 0) return RL_OK;
     if (rl_status st = activate(ctx)) return st;
-    // 16-byte packs; the widening cast uses 4-element packs so its stores
-    // stay 16 B per lane and contiguous across the wave (8-element f32 packs
-    // would be two strided 16-byte stores, which costs extra HBM writes).
-    constexpr int N = (sizeof(TIn) == 4 && sizeof(TOut) == 4) ? 4 : (sizeof(TOut) == 4 ? 4 : 8);
+    constexpr int N = map_pack<TIn, TOut>();
     constexpr int UNROLL = MapShape<Op, TIn, TOut>::unroll;
     constexpr bool NTS = MapShape<Op, TIn, TOut>::nt_store;
     constexpr bool PHASED = MapShape<Op, TIn, TOut>::phased;
@@ -324,7 +468,29 @@ rl_status launch_map(rl_context* ctx, const char* name, const void* a, const voi
     if (vec) {
         uint64_t n_packs = n / N;
         uint32_t tail = uint32_t(n - n_packs * N);
-        RL_LAUNCH(ctx, (k_map<TIn, TOut, N, UNROLL, ARITY, NTS, PHASED, Op>), dim3(grid_for(n_packs, uint64_t(kThreads) * UNROLL)), dim3(kThreads), pa, pb, po, n_packs, tail, op);
+        const unsigned grid = grid_for(n_packs, uint64_t(kThreads) * UNROLL);
+        constexpr uint32_t kind = fused_kind<TIn, TOut, Op>();
+        if (kind != 0 && fusing(ctx)) {
+            FusedOp f;
+            f.kind = kind;
+            f.blocks = grid;
+            f.a = pa;
+            f.b = pb;
+            f.out = po;
+            f.n_packs = n_packs;
+            f.tail = tail;
+            f.read[0][0] = uintptr_t(pa);
+            f.read[0][1] = uintptr_t(pa) + n * sizeof(TIn);
+            if (ARITY == 2) {
+                f.read[1][0] = uintptr_t(pb);
+                f.read[1][1] = uintptr_t(pb) + n * sizeof(TIn);
+            }
+            f.write[0] = uintptr_t(po);
+            f.write[1] = uintptr_t(po) + n * sizeof(TOut);
+            if (rl_status st = defer_fused(ctx, f)) return st;
+            return after_launch(ctx, name);
+        }
+        RL_LAUNCH(ctx, (k_map<TIn, TOut, N, UNROLL, ARITY, NTS, PHASED, Op>), dim3(grid), dim3(kThreads), pa, pb, po, n_packs, tail, op);
     } else {
         RL_LAUNCH(ctx, (k_map<TIn, TOut, 1, UNROLL, ARITY, NTS, PHASED, Op>), dim3(grid_for(n, uint64_t(kThreads) * UNROLL)), dim3(kThreads), pa, pb, po, n, 0u, op);
     }
@@ -341,13 +507,32 @@ rl_status launch_add_broadcast(rl_context* ctx, const char* name, const rl_buffe
     constexpr int N = 16 / sizeof(T);
     // Four packs per thread: f16 53% -> 56% of peak on [4096, 1536] (same
     // sweep as MapShape).
-    constexpr int UNROLL = 4;
+    constexpr int UNROLL = kBroadcastUnroll;
     const T* px = static_cast<const T*>(x->data);
     const T* pbias = static_cast<const T*>(bias->data);
     T* po = static_cast<T*>(out->data);
     const bool vec = cols % N == 0 && aligned_to(px, 16) && aligned_to(pbias, 16) &&
                      aligned_to(po, 16) && n / N <= UINT32_MAX;
     const uint64_t col_packs = cols / N;
+    if (vec && fusing(ctx)) {
+        const uint64_t n_packs = n / N;
+        FusedOp f;
+        f.kind = sizeof(T) == 4 ? kFusedBiasF32 : kFusedBiasF16;
+        f.blocks = grid_for(n_packs, uint64_t(kThreads) * kBroadcastUnroll);
+        f.a = px;
+        f.b = pbias;
+        f.out = po;
+        f.n_packs = n_packs;
+        f.div = uint32_t(col_packs);
+        f.read[0][0] = uintptr_t(px);
+        f.read[0][1] = uintptr_t(px) + n * sizeof(T);
+        f.read[1][0] = uintptr_t(pbias);
+        f.read[1][1] = uintptr_t(pbias) + cols * sizeof(T);
+        f.write[0] = uintptr_t(po);
+        f.write[1] = uintptr_t(po) + n * sizeof(T);
+        if (rl_status st = defer_fused(ctx, f)) return st;
+        return after_launch(ctx, name);
+    }
     if (vec && sizeof(T) == 4 && col_packs <= 1024 && rows <= UINT32_MAX) {
         // f32 rows of up to 1024 packs: a block per 8 rows, a thread per
         // column pack (threads rounded up to whole waves).  [4096, 1536]:
@@ -379,6 +564,59 @@ rl_status check_input(const rl_buffer* b, uint64_t element_size, const char* wha
 }
 
 }  // namespace
+
+rl_status defer_fused(rl_context* ctx, const FusedOp& f) {
+    bool clash = ctx->fused_count == kMaxFused;
+    uint64_t blocks = f.blocks;
+    for (uint32_t i = 0; i < ctx->fused_count && !clash; ++i) {
+        const FusedOp& p = ctx->fused[i];
+        blocks += p.blocks;
+        clash = overlaps(p.write, f.write[0], f.write[1]) ||
+                overlaps(p.read[0], f.write[0], f.write[1]) ||
+                overlaps(p.read[1], f.write[0], f.write[1]) ||
+                overlaps(p.write, f.read[0][0], f.read[0][1]) ||
+                overlaps(p.write, f.read[1][0], f.read[1][1]);
+    }
+    if (clash || blocks > (1u << 30))
+        if (rl_status st = flush_fused(ctx)) return st;
+    ctx->fused[ctx->fused_count++] = f;
+    return RL_OK;
+}
+
+rl_status flush_fused(rl_context* ctx) {
+    if (ctx->fused_count == 0) return RL_OK;
+    FusedTable t{};
+    uint32_t first = 0;
+    for (uint32_t i = 0; i < ctx->fused_count; ++i) {
+        const FusedOp& f = ctx->fused[i];
+        t.first[i] = first;
+        FusedSeg& g = t.seg[i];
+        g.kind = f.kind;
+        g.tail = f.tail;
+        g.a = f.a;
+        g.b = f.b;
+        g.out = f.out;
+        g.n_packs = f.n_packs;
+        g.head_packs = f.head_packs;
+        g.div = FastDiv(f.div ? f.div : 1u);
+        g.repeats = f.repeats;
+        g.small_index = f.small_index ? 1u : 0u;
+        g.outer.rank = f.outer_rank;
+        for (uint32_t d = 0; d < kMaxFusedOuterRank; ++d) {
+            g.outer.dim[d] = FastDiv(f.outer_dim[d] ? f.outer_dim[d] : 1u);
+            g.outer.stride[d] = f.outer_stride[d];
+        }
+        first += f.blocks;
+    }
+    t.count = ctx->fused_count;
+    ctx->fused_count = 0;
+    hipLaunchKernelGGL(k_fused, dim3(first), dim3(kThreads), 0, ctx->stream, t);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(RL_ERR_DEVICE, "fused streaming ops: %s", hipGetErrorString(err));
+    return RL_OK;
+}
+
 }  // namespace rl
 
 using namespace rl;

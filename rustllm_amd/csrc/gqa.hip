@@ -815,6 +815,7 @@ rl_status qk_entry(rl_context* ctx, const char* name, const rl_buffer* q, const 
     {
         const dim3 g(static_cast<unsigned>(grid)), b(256);
         const size_t lds = s.head_dim * sizeof(float);
+        if (rl_status st = flush_fused(ctx)) return st;
         if (ctx->timed_start != nullptr) {
             hipExtLaunchKernelGGL((k_gqa_qk_rows<T>), g, b, lds, ctx->stream, ctx->timed_start,
                                   ctx->timed_stop, 0, qd, kd, od, p, uint32_t(key_blocks));

@@ -15,60 +15,20 @@
 #include <vector>
 
 #include "common.hpp"
+#include "movement_bodies.hpp"
 
 namespace rl {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = kMoveThreads;
 constexpr int kMaxRank = 16;
+typedef OuterDimsT<kMaxRank> OuterDims;
 
-// Outer dimensions of a view, innermost first.
-struct OuterDims {
-    uint32_t rank;
-    FastDiv dim[kMaxRank];
-    uint64_t stride[kMaxRank];
-
-    __device__ inline uint64_t offset(uint32_t index) const {
-        uint64_t off = 0;
-#pragma unroll 4
-        for (uint32_t d = 0; d < rank; ++d) {
-            uint32_t q, r;
-            dim[d].divmod(index, q, r);
-            off += uint64_t(r) * stride[d];
-            index = q;
-        }
-        return off;
-    }
-};
-
-// dst[i] = src[offset(row) + pack], rows of `row_packs` packs of N elements.
 template <typename T, int N, int UNROLL>
 __global__ __launch_bounds__(kThreads) void k_gather_rows(const T* __restrict__ src,
                                                           T* __restrict__ dst, uint32_t n_packs,
                                                           FastDiv row_packs, OuterDims outer) {
-    typedef typename VecOf<T, N>::type V;
-    V* vdst = reinterpret_cast<V*>(dst);
-    const uint64_t tile = uint64_t(kThreads) * UNROLL;
-    const uint64_t step = uint64_t(gridDim.x) * tile;
-    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_packs;
-         base += step) {
-        V r[UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            uint64_t i = base + uint64_t(u) * kThreads;
-            if (i < n_packs) {
-                uint32_t row, p;
-                row_packs.divmod(uint32_t(i), row, p);
-                uint64_t off = outer.offset(row) + uint64_t(p) * N;
-                r[u] = *reinterpret_cast<const V*>(src + off);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            uint64_t i = base + uint64_t(u) * kThreads;
-            if (i < n_packs) store_stream(vdst + i, r[u]);
-        }
-    }
+    gather_rows_body<T, N, UNROLL>(src, dst, n_packs, row_packs, outer, blockIdx.x, gridDim.x);
 }
 
 // Per-element gather over all dims (innermost first in `dims`).
@@ -81,45 +41,13 @@ __global__ __launch_bounds__(kThreads) void k_gather_elems(const T* __restrict__
         dst[i] = src[dims.offset(uint32_t(i))];
 }
 
-// out[(head * repeats + r) * head_packs + p] = in[head * head_packs + p],
-// head = b * kv_heads + kv_head.
 template <typename T, int N, int UNROLL>
 __global__ __launch_bounds__(kThreads) void k_repeat_kv(const T* __restrict__ in,
                                                         T* __restrict__ out, uint64_t n_packs,
                                                         uint64_t head_packs, FastDiv head_div,
                                                         uint32_t repeats, bool small_index) {
-    typedef typename VecOf<T, N>::type V;
-    const V* vin = reinterpret_cast<const V*>(in);
-    V* vout = reinterpret_cast<V*>(out);
-    const uint64_t tile = uint64_t(kThreads) * UNROLL;
-    const uint64_t step = uint64_t(gridDim.x) * tile;
-    for (uint64_t base = uint64_t(blockIdx.x) * tile + threadIdx.x; base < n_packs;
-         base += step) {
-        V r[UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            uint64_t i = base + uint64_t(u) * kThreads;
-            if (i < n_packs) r[u] = load_stream(vin + i);
-        }
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            uint64_t i = base + uint64_t(u) * kThreads;
-            if (i < n_packs) {
-                uint64_t head, p;
-                if (small_index) {
-                    uint32_t q, rem;
-                    head_div.divmod(uint32_t(i), q, rem);
-                    head = q;
-                    p = rem;
-                } else {
-                    head = i / head_packs;
-                    p = i - head * head_packs;
-                }
-                V* dst = vout + head * repeats * head_packs + p;
-                for (uint32_t k = 0; k < repeats; ++k) store_stream(dst + k * head_packs, r[u]);
-            }
-        }
-    }
+    repeat_kv_body<T, N, UNROLL>(in, out, n_packs, head_packs, head_div, repeats, small_index,
+                                 blockIdx.x, gridDim.x);
 }
 
 inline unsigned grid_for(uint64_t items, uint64_t per_block) {
@@ -184,6 +112,29 @@ rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* 
         // time than with four (fewer, longer waves) and match one.
         constexpr int U = 2;
         const dim3 grid(grid_for(n_packs, uint64_t(kThreads) * U)), block(kThreads);
+        if (n == 16 / int(sizeof(T)) && rank - 1 <= kMaxFusedOuterRank && fusing(ctx)) {
+            // recorded into a graph: one of the fused streaming ops
+            FusedOp f;
+            f.kind = sizeof(T) == 4 ? kFusedGatherF32 : kFusedGatherF16;
+            f.blocks = grid.x;
+            f.a = src;
+            f.out = dst;
+            f.n_packs = n_packs;
+            f.div = uint32_t(inner / n);
+            f.outer_rank = rank - 1;
+            uint64_t last = v.dims[rank - 1] - 1;  // the view's last element in the source
+            for (uint32_t d = 0; d + 1 < rank; ++d) {
+                f.outer_dim[d] = uint32_t(v.dims[rank - 2 - d]);
+                f.outer_stride[d] = uint32_t(v.strides[rank - 2 - d]);
+                last += (v.dims[rank - 2 - d] - 1) * v.strides[rank - 2 - d];
+            }
+            f.read[0][0] = uintptr_t(src);
+            f.read[0][1] = uintptr_t(src + last + 1);
+            f.write[0] = uintptr_t(dst);
+            f.write[1] = uintptr_t(dst + numel);
+            if (rl_status st = defer_fused(ctx, f)) return st;
+            return after_launch(ctx, name);
+        }
         switch (n) {
             case 8:
                 RL_LAUNCH(ctx, (k_gather_rows<T, 8, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
@@ -291,20 +242,41 @@ rl_status repeat_kv_impl(rl_context* ctx, const char* name, const rl_buffer* in,
         const uint64_t head_packs = head / N;
         const uint64_t n_packs = in_numel / N;
         const bool small = n_packs <= UINT32_MAX && head_packs <= UINT32_MAX;
+        if (N * sizeof(T) == 16 && fusing(ctx)) {
+            // recorded into a graph: one of the fused streaming ops
+            FusedOp f;
+            f.kind = sizeof(T) == 4 ? kFusedRepeatF32 : kFusedRepeatF16;
+            f.blocks = grid_for(n_packs, kThreads * U);
+            f.a = src;
+            f.out = dst;
+            f.n_packs = n_packs;
+            f.head_packs = head_packs;
+            f.div = small ? uint32_t(head_packs) : 1u;
+            f.repeats = uint32_t(repeats);
+            f.small_index = small;
+            f.read[0][0] = uintptr_t(src);
+            f.read[0][1] = uintptr_t(src) + in_numel * sizeof(T);
+            f.write[0] = uintptr_t(dst);
+            f.write[1] = uintptr_t(dst) + in_numel * repeats * sizeof(T);
+            return rl_status(defer_fused(ctx, f));
+        }
         RL_LAUNCH(ctx, (k_repeat_kv<T, N, U>), dim3(grid_for(n_packs, kThreads * U)), dim3(kThreads), static_cast<const T*>(src), static_cast<T*>(dst), n_packs, head_packs, FastDiv(small ? uint32_t(head_packs) : 1u), uint32_t(repeats), small);
+        return rl_status(RL_OK);
     };
     const bool aligned16 = aligned_to(src, 16) && aligned_to(dst, 16);
+    rl_status st = RL_OK;
     if (es == 4) {
         if (head % 4 == 0 && aligned16)
-            launch(float(), std::integral_constant<int, 4>());
+            st = launch(float(), std::integral_constant<int, 4>());
         else
-            launch(float(), std::integral_constant<int, 1>());
+            st = launch(float(), std::integral_constant<int, 1>());
     } else {
         if (head % 8 == 0 && aligned16)
-            launch(half_t(), std::integral_constant<int, 8>());
+            st = launch(half_t(), std::integral_constant<int, 8>());
         else
-            launch(half_t(), std::integral_constant<int, 1>());
+            st = launch(half_t(), std::integral_constant<int, 1>());
     }
+    if (st != RL_OK) return st;
     return after_launch(ctx, name);
 }
 

@@ -375,6 +375,7 @@ rl_status rl_buffer_copy(rl_context* ctx, const rl_buffer* src, const rl_buffer*
     if (rl_status st = require_context(ctx)) return st;
     if (rl_status st = activate(ctx)) return st;
     if (byte_len == 0) return RL_OK;
+    if (rl_status st = flush_fused(ctx)) return st;
     RL_HIP(hipMemcpyAsync(dst->data, src->data, byte_len, hipMemcpyDeviceToDevice, ctx->stream),
            "device copy");
     return RL_OK;
@@ -426,16 +427,29 @@ rl_status rl_graph_capture_begin(rl_context* ctx) {
     return RL_OK;
 }
 
+rl_status rl_context_set_fusion(rl_context* ctx, int32_t enabled) {
+    if (rl_status st = require_context(ctx)) return st;
+    if (rl_status st = activate(ctx)) return st;
+    if (rl_status st = flush_fused(ctx)) return st;  // ops deferred so far keep their batch
+    ctx->fuse_recorded = enabled != 0;
+    return RL_OK;
+}
+
 rl_status rl_graph_capture_end(rl_context* ctx, rl_graph** out) {
     if (out == nullptr) return fail(RL_ERR_INVALID_ARGUMENT, "output pointer is null");
     *out = nullptr;
     if (rl_status st = require_context(ctx)) return st;
     if (!ctx->capturing) return fail(RL_ERR_DEVICE, "no graph is being recorded");
-    ctx->capturing = false;
     if (rl_status st = activate(ctx)) return st;
+    const rl_status flushed = flush_fused(ctx);  // the recording ends even if this fails
+    ctx->capturing = false;
     hipGraph_t graph = nullptr;
     RL_HIP(hipStreamEndCapture(ctx->stream, &graph), "hipStreamEndCapture");
     hipGraphExec_t exec = nullptr;
+    if (flushed != RL_OK) {
+        (void)hipGraphDestroy(graph);
+        return flushed;
+    }
     hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     if (err != hipSuccess) {
         (void)hipGraphDestroy(graph);
@@ -482,6 +496,7 @@ rl_status rl_event_record(rl_context* ctx, rl_event* event) {
     if (event == nullptr) return fail(RL_ERR_INVALID_ARGUMENT, "event is null");
     if (rl_status st = require_context(ctx)) return st;
     if (rl_status st = activate(ctx)) return st;
+    if (rl_status st = flush_fused(ctx)) return st;
     RL_HIP(hipEventRecord(event->event, ctx->stream), "hipEventRecord");
     return RL_OK;
 }
@@ -490,6 +505,7 @@ rl_status rl_event_wait(rl_context* ctx, rl_event* event) {
     if (event == nullptr) return fail(RL_ERR_INVALID_ARGUMENT, "event is null");
     if (rl_status st = require_context(ctx)) return st;
     if (rl_status st = activate(ctx)) return st;
+    if (rl_status st = flush_fused(ctx)) return st;
     RL_HIP(hipStreamWaitEvent(ctx->stream, event->event, 0), "hipStreamWaitEvent");
     return RL_OK;
 }
