@@ -4,11 +4,13 @@
 A step is one pass of the elementwise/broadcast batch on [4096, 1536]:
 add, mul, SiLU, fused SwiGLU, stride-0 bias add and cast, in
 f32 and f16, plus contiguous of a [1, 9, 4096, 64] transposed view and
-repeat_kv 3 -> 9 heads -- 16 kernel launches.  Inputs are resident in HBM
-before timing.  Each step uses the next of several buffer sets (>= 1 GiB in
-total, four times the 256 MB Infinity Cache) so that reads come from HBM,
-not from the cache.  Steps are replayed as recorded graphs and timed with
-stream events.
+repeat_kv 3 -> 9 heads -- 16 ops.  Inputs are resident in HBM before timing.
+Each step uses the next of several buffer sets (>= 1 GiB in total, four
+times the 256 MB Infinity Cache) so that reads come from HBM, not from the
+cache.  Steps are recorded into graphs (a step per buffer set in one graph),
+where the library runs a step's 16 independent ops as one fused launch, and
+timed with stream events around the replays; the same step with one kernel
+per op is reported beside it.
 
 GB/s = algorithmic bytes (inputs read once + outputs written once) / time.
 The JSON line's `value` is the whole step's aggregate; `per_op` lists each
