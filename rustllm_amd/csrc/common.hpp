@@ -123,6 +123,9 @@ struct rl_context {
     rl::FusedOp fused[rl::kMaxFused];
     uint32_t fused_count = 0;
     bool fuse_recorded = true;  // rl_context_set_fusion
+    // A fused launch that failed where no status could be returned (inside
+    // RL_LAUNCH): reported by the next after_launch.
+    hipError_t fused_error = hipSuccess;
 };
 
 
@@ -146,7 +149,8 @@ inline bool fusing(const rl_context* ctx) {
 // timestamps recorded (hipExtLaunchKernelGGL).
 #define RL_LAUNCH(ctx, kernel, grid, block, ...)                                              \
     do {                                                                                      \
-        if ((ctx)->fused_count != 0) (void)rl::flush_fused(ctx);                              \
+        if ((ctx)->fused_count != 0 && rl::flush_fused(ctx) != RL_OK)                         \
+            (ctx)->fused_error = hipErrorLaunchFailure; /* reported by after_launch */        \
         if ((ctx)->timed_start != nullptr) {                                                  \
             hipExtLaunchKernelGGL(kernel, grid, block, 0, (ctx)->stream, (ctx)->timed_start,  \
                                   (ctx)->timed_stop, 0, __VA_ARGS__);                         \

@@ -141,6 +141,11 @@ rl_status activate(rl_context* ctx) {
 }
 
 rl_status after_launch(rl_context* ctx, const char* kernel_name) {
+    if (ctx->fused_error != hipSuccess) {  // a fused launch this op flushed failed
+        const hipError_t fe = ctx->fused_error;
+        ctx->fused_error = hipSuccess;
+        return hip_fail(fe, "fused streaming ops");
+    }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, kernel_name);
     if (ctx->profiling) {
