@@ -245,6 +245,8 @@ def test_buffer_calls_without_context():
     assert lib.rl_buffer_empty(NULL, 4, 4, ctypes.byref(raw)) == DEVICE
     assert lib.rl_execution_finish(NULL) == DEVICE
     assert lib.rl_profile_take(NULL, None) == 0
+    assert lib.rl_context_set_fusion(NULL, 0) == DEVICE
+    assert lib.rl_graph_capture_begin(NULL) == DEVICE
 
 
 def _fastdiv(d):
