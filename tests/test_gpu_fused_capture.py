@@ -173,6 +173,37 @@ def test_more_ops_than_one_launch_holds(ctx):
         assert_bitexact(x, o.add(a, b), "add")
 
 
+def test_ragged_sizes_in_one_launch(ctx):
+    """Sizes that end inside a block and inside a pack: each op's last block
+    is partly past its array and the elements after the last whole pack are
+    its tail, in both dtypes, beside a bias add over 1,000 columns."""
+    shape, bshape = (333, 1001), (333, 1000)
+    host, outs, ops = [], [], []
+    for dt in (F32, F16):
+        a, b = norm("ra", shape, dt), norm("rb", shape, dt)
+        x, bias = norm("rx", bshape, dt), norm("rbias", (1000,), dt)
+        da, db, dx, dbias = ctx.upload(a), ctx.upload(b), ctx.upload(x), ctx.upload(bias)
+        bufs = [ctx.empty(shape, dt) for _ in range(4)] + [ctx.empty(bshape, dt)]
+        host.append((a, b, x, bias))
+        outs += bufs
+        ops += [lambda da=da, db=db, y=bufs[0]: ctx.add(da, db, y),
+                lambda da=da, db=db, y=bufs[1]: ctx.mul(da, db, y),
+                lambda da=da, y=bufs[2]: ctx.silu(da, y),
+                lambda da=da, db=db, y=bufs[3]: ctx.swiglu(da, db, y),
+                lambda dx=dx, dbias=dbias, y=bufs[4]: ctx.add_broadcast(dx, dbias, y)]
+
+    def record():
+        for op in ops:
+            op()
+
+    eager = replay_and_compare(ctx, record, outs)
+    for k, (a, b, x, bias) in enumerate(host):
+        e = eager[5 * k:5 * k + 5]
+        assert_bitexact(e[0], o.add(a, b), "add")
+        assert_bitexact(e[1], o.mul(a, b), "mul")
+        assert_bitexact(e[4], o.add_broadcast(x, bias), "bias add")
+
+
 def test_other_kernels_between_fused_ops(ctx):
     """An op outside the fused set (RMSNorm) reading a deferred op's output,
     and a deferred op reading the RMSNorm's, in one recording."""
