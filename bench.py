@@ -1,22 +1,26 @@
 #!/usr/bin/env python3
-"""Per-op HBM bandwidth of the gfx950 tensor-op library on one MI355X.
+"""HBM bandwidth of the gfx950 tensor-op library on one MI355X.
 
-A step is one pass of the elementwise/broadcast batch on [4096, 1536]:
-add, mul, SiLU, fused SwiGLU, stride-0 bias add and cast, in
-f32 and f16, plus contiguous of a [1, 9, 4096, 64] transposed view and
-repeat_kv 3 -> 9 heads -- 16 ops.  Inputs are resident in HBM before timing.
-Each step uses the next of several buffer sets (>= 1 GiB in total, four
-times the 256 MB Infinity Cache) so that reads come from HBM, not from the
-cache.  Steps are recorded into graphs (a step per buffer set in one graph),
-where the library runs a step's 16 independent ops as one fused launch, and
-timed with stream events around the replays; the same step with one kernel
-per op is reported beside it.
+A step is one pass of the non-GEMM chain of a SmolLM2-360M decoder layer in
+f16 at a 4096-token prefill (LayerChain): RMSNorm [4096, 960]; RoPE of Q
+and K with the KV-cache append and repeat_kv 5 -> 15 heads, one launch;
+causal scale/mask + softmax on [15, 4096, 4096] scores; SwiGLU [4096, 2560];
+residual add -- 5 launches.  Inputs are resident in HBM before timing.  Step
+i runs on buffer set i mod R (1.1 GB each, so every set is four times the
+256 MB Infinity Cache); K steps are launched back to back on one stream with
+events around them, after W warm-up steps.  GB/s = the step's algorithmic
+bytes (each launch's inputs read once and outputs written once) / time per
+step.  The softmax -- 3/4 of the step's time -- records its own start and
+end in every timed step; its mean launch duration gives the roofline
+fraction.  The CPU oracle runs the same chain on set 0's inputs (one core,
+then every core), and every stage of the GPU's outputs is checked against
+it.
 
-GB/s = algorithmic bytes (inputs read once + outputs written once) / time.
-The JSON line's `value` is the whole step's aggregate; `per_op` lists each
-op, and the RMSNorm grid, the attention-score softmax shapes and the
-SmolLM2-360M decoder-layer chain are timed the same way as extra lines in
-`per_op`.
+The JSON line (stdout, one line) carries the headline, the roofline, the CPU
+baseline, the [4096, 1536] batch step and a summary of the per-op table;
+the full per-op table -- each op alone on rotated buffer copies, one launch
+and sustained, at every configuration's shapes -- goes to stderr and to
+--per-op-out.
 
     python bench.py [--steps K] [--warmup W] [--sets R] [--no-cpu] [--quick]
 """
@@ -134,6 +138,16 @@ def set_bytes(b) -> int:
     return sum(v.byte_len for v in b.values())
 
 
+# Graph-replayed figures: the sustained time of each op (back-to-back
+# launches recorded in one graph and replayed), the chain and the batch step
+# recorded as graphs.  On by default; `--no-graph-batch` leaves them out.
+# Under `rocprofv3 --kernel-trace` a run that created, replayed and destroyed
+# one graph per op once ended in a SIGSEGV inside hipGraphLaunch, so every
+# graph is kept until the process exits rather than destroyed after use.
+GRAPH_BATCH = True
+_LIVE_GRAPHS = []
+
+
 def time_graphs(ctx, graphs, launches_per_graph, reps, warmup=2):
     """Replays `graphs` round-robin `reps` times; returns ms per launch."""
     for i in range(warmup):
@@ -164,135 +178,24 @@ def capture(ctx, fn):
     return g
 
 
-def capture_step(ctx, aux, ops, s, events):
-    """One step as a graph.  With aux contexts the independent ops are spread
-    round-robin over their streams, forked from and joined back into ctx's
-    stream, so the recorded graph has parallel branches and one kernel's
-    ramp-down overlaps the next one's ramp-up."""
-    fork, joins = events
+def time_step(ctx, ops, sets, steps, warmup):
+    """ms per step of the [4096, 1536] batch: the steps over the buffer sets
+    recorded in turn into one graph (a step per set, so a replay is
+    len(sets) steps; `steps` is a multiple of the set count), replayed
+    after `warmup` steps, events around the timed replays."""
+    assert steps % len(sets) == 0
     ctx.capture_begin()
     try:
-        if aux:
-            ctx.record(fork)
-            for a in aux:
-                a.wait(fork)
-        streams = [ctx] + aux
-        for i, op in enumerate(ops):
-            op.launch(streams[i % len(streams)], s)
-        for a, e in zip(aux, joins):
-            a.record(e)
-            ctx.wait(e)
+        for s in sets:
+            for op in ops:
+                op.launch(ctx, s)
     finally:
-        g = ctx.capture_end()
-    return g
-
-
-def time_step(ctx, aux, ops, sets, steps, warmup):
-    """ms per step.  On one stream the steps over the buffer sets are recorded
-    in turn into one graph (a step per set, so a replay is len(sets) steps and
-    the host's cost of launching a graph is spread over them) when `steps` is
-    a multiple of the set count; otherwise, and with aux streams, one recorded
-    step graph per buffer set."""
-    per_graph = len(sets) if not aux and steps % len(sets) == 0 else 1
-    events = [(ctx.event(), [ctx.event() for _ in aux]) for _ in sets]
-    if per_graph > 1:
-        ctx.capture_begin()
-        try:
-            for s in sets:
-                for op in ops:
-                    op.launch(ctx, s)
-        finally:
-            graphs = [ctx.capture_end()]
-    else:
-        graphs = [capture_step(ctx, aux, ops, s, ev) for s, ev in zip(sets, events)]
-    for i in range(-(-warmup // per_graph)):
-        ctx.graph_launch(graphs[i % len(graphs)])
+        graph = ctx.capture_end()
+    _LIVE_GRAPHS.append(graph)
+    ms = time_graphs(ctx, [graph], len(sets), steps // len(sets),
+                     warmup=max(1, -(-warmup // len(sets))))
     ctx.finish()
-    start, end = ctx.event(), ctx.event()
-    ctx.record(start)
-    for i in range(steps // per_graph):
-        ctx.graph_launch(graphs[i % len(graphs)])
-    ctx.record(end)
-    ms = ctx.elapsed_ms(start, end)
-    ctx.finish()
-    for g in graphs:
-        ctx.graph_destroy(g)
-    for fork, joins in events:
-        for e in [fork] + joins:
-            ctx.destroy_event(e)
-    ctx.destroy_event(start)
-    ctx.destroy_event(end)
-    return ms / steps
-
-
-def split_by_bytes(ops, n):
-    """Greedy split of the ops over n streams, largest first, balancing bytes;
-    each stream keeps the step's op order."""
-    load = [0] * n
-    owner = {}
-    for i in sorted(range(len(ops)), key=lambda i: -ops[i].nbytes):
-        k = load.index(min(load))
-        owner[i] = k
-        load[k] += ops[i].nbytes
-    return [[op for i, op in enumerate(ops) if owner[i] == k] for k in range(n)]
-
-
-def time_step_streams(ctx, aux, ops, sets, steps, warmup):
-    """ms per step with the step's independent ops spread over several
-    streams: each stream replays its own recorded graph (its share of the
-    ops), forked from and joined back into ctx's stream with events every
-    step.  Kernels on different streams may run concurrently, so one
-    kernel's ramp-down overlaps another's ramp-up."""
-    streams = [ctx] + aux
-    shares = split_by_bytes(ops, len(streams))
-    graphs = []
-    for s in sets:
-        row = []
-        for c, share in zip(streams, shares):
-            c.capture_begin()
-            try:
-                for op in share:
-                    op.launch(c, s)
-            finally:
-                row.append(c.capture_end())
-        graphs.append(row)
-    fork = [ctx.event() for _ in range(2)]
-    joins = [[a.event() for a in aux] for _ in range(2)]
-
-    def one_step(i):
-        f, js = fork[i % 2], joins[i % 2]
-        ctx.record(f)
-        for a in aux:
-            a.wait(f)
-        row = graphs[i % len(graphs)]
-        for c, g in zip(streams, row):
-            c.graph_launch(g)
-        for a, e in zip(aux, js):
-            a.record(e)
-            ctx.wait(e)
-
-    for i in range(warmup):
-        one_step(i)
-    ctx.finish()
-    for a in aux:
-        a.finish()
-    start, end = ctx.event(), ctx.event()
-    ctx.record(start)
-    for i in range(steps):
-        one_step(i)
-    ctx.record(end)
-    ms = ctx.elapsed_ms(start, end)
-    ctx.finish()
-    for a in aux:
-        a.finish()
-    for row in graphs:
-        for c, g in zip(streams, row):
-            c.graph_destroy(g)
-    for e in fork + [e for js in joins for e in js]:
-        ctx.destroy_event(e)
-    ctx.destroy_event(start)
-    ctx.destroy_event(end)
-    return ms / steps
+    return ms
 
 
 def kernel_times_us(ctx, launches, reps, batch=True):
@@ -316,16 +219,6 @@ def kernel_times_us(ctx, launches, reps, batch=True):
         ctx.destroy_event(e)
     return us, (graph_batch_us(ctx, launches) if GRAPH_BATCH and batch else None), \
         len(launches) + reps
-
-
-# Sustained figures: each op also timed as back-to-back launches recorded in
-# one graph and replayed.  On by default; `--no-graph-batch` leaves them out
-# (the traced profile command passes it: under `rocprofv3 --kernel-trace` a
-# run that created, replayed and destroyed one such graph per op ended in a
-# SIGSEGV inside hipGraphLaunch).  The graphs are kept until the process
-# exits rather than destroyed after their op.
-GRAPH_BATCH = True
-_LIVE_GRAPHS = []
 
 
 def graph_batch_us(ctx, launches, min_per_graph=32, replays=8):
@@ -415,8 +308,8 @@ def per_op_rows(ctx, ops, sets, reps):
 
 def extra_rows(ctx, reps, quick):
     """RMSNorm over hidden {576, 768, 960} x tokens, scale/mask + softmax on
-    [9, 2048, 2048] scores and the SmolLM2-360M decoder-layer chain -- same
-    method, rotated buffer sets."""
+    [9, 2048, 2048] scores and each op of the SmolLM2-360M decoder layer
+    alone -- same method, rotated buffer sets."""
     rows = []
 
     def measure(name, dtype, shape, nbytes, make_set, launch):
@@ -554,9 +447,6 @@ def extra_rows(ctx, reps, quick):
             lambda s: ctx.add(s[0], s[1], s[2]))
     rows.extend(attention_rows(ctx, qh, kvh, hd, tok, reps))
     if not quick:
-        rows.append(layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds))
-        rows.append(layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds,
-                                    fused_prologue=True))
         rows.append(fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds))
     # [64, 768] f32 (the reference's CPU-runnable case), fused add + RMSNorm
     # (writes the sum and the norm)
@@ -766,148 +656,222 @@ def fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
             "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None}
 
 
-def layer_chain_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20,
-                    fused_prologue=False):
-    """The whole non-GEMM chain of one SmolLM2-360M layer in order -- RMSNorm,
-    RoPE of Q and K (read straight from the [1, H, S, D] views of the
-    normalised rows that the Q and K projections would produce), repeat_kv of
-    the rotated K and of V, causal scale/mask + softmax, SwiGLU, residual add:
-    8 launches recorded as one graph per buffer set and replayed.  Where a
-    GEMM sits between two stages (V, the scores, gate/up, the down
-    projection) the stage reads a seeded stand-in.  Bytes are the sum of the
-    launches' algorithmic bytes.  After timing, every output of the first
-    set is compared with the oracle on that set's inputs.
+# ------------------------------------------- the headline: one layer's chain
 
-    fused_prologue: RoPE of Q and K, the KV-cache append of K and V
-    (start 0, a cache of tok rows) and repeat_kv of both caches as one launch
-    (rl_qkv_rope_kv_append_repeat_f16), 5 launches in all; the cache writes
-    add their bytes."""
-    rng_key = ("chain",)
-    qdims, qstrides = [1, qh, tok, hd], [tok * hid, hd, hid, 1]
-    kdims, kstrides = [1, kvh, tok, hd], [tok * hid, hd, hid, 1]
-    vdims, vstrides = [1, kvh, tok, hd], [kvh * tok * hd, tok * hd, hd, 1]
-    unmasked = qh * (tok * (tok + 1) // 2)
-    nbytes = (tok * hid * 4 + hid * 2                                   # RMSNorm
-              + 2 * (qh + kvh) * tok * hd * 2 + 2 * 2 * tok * (hd // 2) * 4  # RoPE Q, K
-              + 2 * (kvh + qh) * tok * hd * 2                           # repeat_kv K, V
-              + unmasked * 2 + qh * tok * tok * 2                       # scale/mask + softmax
-              + 3 * tok * ffn * 2                                       # SwiGLU
-              + 3 * tok * hid * 2)                                      # residual add
-    if fused_prologue:
-        # one pass: Q and K read once, rotated K to the cache and repeated;
-        # V read once, to the cache and repeated
-        nbytes -= 2 * (qh + kvh) * tok * hd * 2 + 2 * (kvh + qh) * tok * hd * 2
-        nbytes += (2 * qh * tok * hd * 2                                # Q in, out
-                   + 2 * (kvh + kvh + qh) * tok * hd * 2)               # K, V in, cache, repeat
-    label = ("layer chain, prologue in one launch (5 launches)" if fused_prologue
-             else "layer chain (8 launches, one graph)")
+class LayerChain:
+    """The non-GEMM chain of one SmolLM2-360M decoder layer (hidden 960, 15 Q
+    heads, 5 KV heads, head size 64, FFN 2560) in f16 at a 4096-token
+    prefill, in the order of TransformerBlock::forward_with_cache_encode
+    (nn/transformer_block.rs:128-158):
 
-    scores = np.random.default_rng(7).standard_normal((qh, tok, tok), dtype=np.float32)
-    scores = scores.astype(F16)
-    host = {}
+      1. RMSNorm [4096, 960] (eps 1e-5)                               x -> xn
+      2. RoPE (theta 1e4, positions 0..4095) of Q [1, 15, 4096, 64] and
+         K [1, 5, 4096, 64], read straight from strided views of xn (the
+         rows the Q/K projections would produce), K and V appended to
+         [1, 5, 4096, 64] caches, both caches repeated to 15 heads
+      3. causal scale/mask (1/8) + softmax on [15, 4096, 4096]  scores -> p
+      4. SwiGLU [4096, 2560]                                      g, u -> h
+      5. residual add [4096, 960]                                xn, r -> o
 
-    def make(i):
-        h = {"x": synth.normal(synth.seed_for(*rng_key, "x", i), (tok, hid), 0, 1, F16),
-             "v": synth.normal(synth.seed_for(*rng_key, "v", i), (1, kvh, tok, hd), 0, 1, F16),
-             "g": synth.normal(synth.seed_for(*rng_key, "g", i), (tok, ffn), 0, 1, F16),
-             "u": synth.normal(synth.seed_for(*rng_key, "u", i), (tok, ffn), 0, 1, F16),
-             "r": synth.normal(synth.seed_for(*rng_key, "r", i), (tok, hid), 0, 1, F16)}
-        if i == 0:
-            host.update(h)
-        b = {k: ctx.upload(v) for k, v in h.items()}
-        b["s"] = ctx.upload(scores)
-        b.update({"xn": ctx.empty((tok, hid), F16), "qr": ctx.empty(qdims, F16),
-                  "kr": ctx.empty(kdims, F16), "kq": ctx.empty(qdims, F16),
-                  "vq": ctx.empty(qdims, F16), "p": ctx.empty((qh, tok, tok), F16),
-                  "h": ctx.empty((tok, ffn), F16), "o": ctx.empty((tok, hid), F16),
-                  "vc": ctx.empty(kdims, F16)})
+    `prologue="one"`: stage 2 is one launch (rl_qkv_rope_kv_append_repeat_f16),
+    5 launches in all.  `prologue="split"`: rope Q, rope K (into the K
+    cache), repeat_kv of K and of V, 8 launches; V is then the cache itself.
+    Where a GEMM sits between two stages (V, the scores, gate/up) the stage
+    reads a seeded stand-in.  Bytes are the sum of the launches' algorithmic
+    bytes (inputs read once, outputs written once; the masked scores are
+    not read; the RoPE tables counted once per rotation)."""
+
+    HID, QH, KVH, HD, FFN, TOK = 960, 15, 5, 64, 2560, 4096
+    WORKLOAD = "SmolLM2-360M layer non-GEMM chain, f16, 4096 tokens"
+
+    def __init__(self, ctx, prologue="one"):
+        self.ctx = ctx
+        self.fused = prologue == "one"
+        hid, qh, kvh, hd, ffn, tok = (self.HID, self.QH, self.KVH, self.HD, self.FFN, self.TOK)
+        self.qdims, self.qstrides = [1, qh, tok, hd], [tok * hid, hd, hid, 1]
+        self.kdims, self.kstrides = [1, kvh, tok, hd], [tok * hid, hd, hid, 1]
+        self.vdims, self.vstrides = [1, kvh, tok, hd], [kvh * tok * hd, tok * hd, hd, 1]
+        self.cos, self.sin = _rope_table(hd, tok)
+        self.dc, self.ds = ctx.upload(self.cos), ctx.upload(self.sin)
+        self.w = synth.uniform_range(synth.seed_for("c5", "norm-w"), (hid,), 0.5, 1.5, F16)
+        self.dw = ctx.upload(self.w)
+        self.launches = 5 if self.fused else 8
+        n_scores = qh * tok * tok
+        unmasked = qh * (tok * (tok + 1) // 2)
+        self.softmax_bytes = unmasked * 2 + n_scores * 2
+        table = 2 * tok * (hd // 2) * 4
+        stage = {
+            "rmsnorm": tok * hid * 4 + hid * 2,
+            "softmax": self.softmax_bytes,
+            "swiglu": 3 * tok * ffn * 2,
+            "residual_add": 3 * tok * hid * 2,
+        }
+        if self.fused:
+            # Q in and out; K and V in, to the caches, repeated to 15 heads
+            stage["prologue"] = (2 * qh * tok * hd * 2 + 2 * (kvh + kvh + qh) * tok * hd * 2
+                                 + table)
+        else:
+            stage["rope_q"] = 2 * qh * tok * hd * 2 + table
+            stage["rope_k"] = 2 * kvh * tok * hd * 2 + table
+            stage["repeat_kv_k"] = (kvh + qh) * tok * hd * 2
+            stage["repeat_kv_v"] = (kvh + qh) * tok * hd * 2
+        self.stage_bytes = stage
+        self.nbytes = sum(stage.values())
+        self._scores = None
+
+    def scores(self):
+        """The stand-in for the QK^T output: N(0, 1) f16 scores, one array
+        shared by every buffer set (each set holds its own device copy)."""
+        if self._scores is None:
+            rng = np.random.default_rng(synth.seed_for("c5", "scores") & 0xFFFFFFFF)
+            s = rng.standard_normal((self.QH, self.TOK, self.TOK), dtype=np.float32)
+            self._scores = s.astype(F16)
+        return self._scores
+
+    def host_inputs(self, i):
+        hid, kvh, hd, ffn, tok = self.HID, self.KVH, self.HD, self.FFN, self.TOK
+        key = ("c5-chain", i)
+        return {"x": synth.normal(synth.seed_for(*key, "x"), (tok, hid), 0, 1, F16),
+                "v": synth.normal(synth.seed_for(*key, "v"), (1, kvh, tok, hd), 0, 1, F16),
+                "g": synth.normal(synth.seed_for(*key, "g"), (tok, ffn), 0, 1, F16),
+                "u": synth.normal(synth.seed_for(*key, "u"), (tok, ffn), 0, 1, F16),
+                "r": synth.normal(synth.seed_for(*key, "r"), (tok, hid), 0, 1, F16),
+                "s": self.scores()}
+
+    def device_set(self, host):
+        ctx = self.ctx
+        hid, qh, ffn, tok = self.HID, self.QH, self.FFN, self.TOK
+        b = {k: ctx.upload(v) for k, v in host.items()}
+        b.update({"xn": ctx.empty((tok, hid), F16), "qr": ctx.empty(self.qdims, F16),
+                  "kc": ctx.empty(self.kdims, F16), "vc": ctx.empty(self.kdims, F16),
+                  "kq": ctx.empty(self.qdims, F16), "vq": ctx.empty(self.qdims, F16),
+                  "p": ctx.empty((qh, tok, tok), F16), "h": ctx.empty((tok, ffn), F16),
+                  "o": ctx.empty((tok, hid), F16)})
         return b
 
-    def chain(b):
-        ctx.rmsnorm(b["x"], wn, 1e-5, b["xn"])
-        if fused_prologue:  # "kr" and "vc" are the caches
-            ctx.qkv_rope_kv_append_repeat((b["xn"], qdims, qstrides), (b["xn"], kdims, kstrides),
-                                          (b["v"], vdims, vstrides), dc, ds, 0, b["kr"], b["vc"],
-                                          qh // kvh, b["qr"], b["kq"], b["vq"])
-        else:
-            ctx.rope_strided(b["xn"], qdims, qstrides, dc, ds, 0, b["qr"])
-            ctx.rope_strided(b["xn"], kdims, kstrides, dc, ds, 0, b["kr"])
-            ctx.repeat_kv(b["kr"], qh // kvh, b["kq"])
-            ctx.repeat_kv(b["v"], qh // kvh, b["vq"])
+    def launch(self, b, stamp=None):
+        """Enqueues the chain on `b`; `stamp` = (start, stop) events that the
+        softmax launch records its own start and end in."""
+        ctx = self.ctx
+        ctx.rmsnorm(b["x"], self.dw, 1e-5, b["xn"])
+        self.launch_prologue(b)
+        if stamp is not None:
+            ctx.time_next_kernel(*stamp)
         ctx.attention_softmax(b["s"], 0.125, 0, b["p"])
         ctx.swiglu(b["g"], b["u"], b["h"])
         ctx.add(b["xn"], b["r"], b["o"])
 
-    bufs = [make(i) for i in range(sets)]
-    graphs = [capture(ctx, lambda b=b: chain(b)) for b in bufs]
-    ms = time_graphs(ctx, graphs, 1, reps)
+    def launch_prologue(self, b):
+        """Stage 2: RoPE of Q and K, the KV append, repeat_kv of both."""
+        ctx, rep = self.ctx, self.QH // self.KVH
+        if self.fused:
+            ctx.qkv_rope_kv_append_repeat((b["xn"], self.qdims, self.qstrides),
+                                          (b["xn"], self.kdims, self.kstrides),
+                                          (b["v"], self.vdims, self.vstrides), self.dc, self.ds,
+                                          0, b["kc"], b["vc"], rep, b["qr"], b["kq"], b["vq"])
+        else:
+            ctx.rope_strided(b["xn"], self.qdims, self.qstrides, self.dc, self.ds, 0, b["qr"])
+            ctx.rope_strided(b["xn"], self.kdims, self.kstrides, self.dc, self.ds, 0, b["kc"])
+            ctx.repeat_kv(b["kc"], rep, b["kq"])
+            ctx.repeat_kv(b["v"], rep, b["vq"])
+
+
+def time_chain(ctx, chain, sets, steps, warmup):
+    """K chain steps launched back to back on the context's stream, step i
+    on buffer set i mod len(sets), bracketed by stream events (after a
+    synchronize).  Each step's softmax launch records its own start and end
+    (the per-dispatch duration a kernel trace reports).  Returns ms per
+    step and the softmax launches' durations in us."""
+    for i in range(warmup):
+        chain.launch(sets[i % len(sets)])
     ctx.finish()
-    for g in graphs:
-        ctx.graph_destroy(g)
-    us = ms * 1e3
-    gbs = nbytes / (us * 1e-6) / 1e9
-    log(f"  {label:34s} {us:9.2f} us {gbs:8.1f} GB/s ({100 * gbs / PEAK_GBS:5.1f}%)")
-    bad = check_chain(bufs[0], host, scores, wn.numpy(), dc.numpy(), ds.numpy(), qh, kvh, hd, tok)
-    if fused_prologue and not np.array_equal(bufs[0]["vc"].numpy().view(np.uint16),
-                                             host["v"].view(np.uint16)):
-        bad.append("V_cache")
-    if bad:
-        log(f"  {label}: MISMATCH against the oracle in {bad}")
-    else:
-        log(f"  {label}: every stage matches the oracle")
-    return {"op": label, "dtype": "f16",
-            "shape": [tok, hid], "bytes": nbytes, "us": round(us, 3), "us_min": None,
-            "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
-            "us_graph_batch": round(us, 3), "GB/s_graph_batch": round(gbs, 1),
-            "pct_peak_graph_batch": round(100 * gbs / PEAK_GBS, 1),
-            "outputs_match_oracle": not bad, "mismatched_stages": bad}
+    stamps = [(ctx.event(), ctx.event()) for _ in range(steps)]
+    start, end = ctx.event(), ctx.event()
+    ctx.finish()
+    ctx.record(start)
+    for i in range(steps):
+        chain.launch(sets[i % len(sets)], stamp=stamps[i])
+    ctx.record(end)
+    ctx.finish()
+    ms = ctx.elapsed_ms(start, end)
+    sm_us = [ctx.elapsed_ms(a, b) * 1e3 for a, b in stamps]
+    for e in [start, end] + [e for pair in stamps for e in pair]:
+        ctx.destroy_event(e)
+    return ms / steps, sm_us
 
 
-def check_chain(b, host, scores, wn, cos, sin, qh, kvh, hd, tok) -> list[str]:
-    """The layer chain's outputs against the oracle on the same inputs:
-    bit-exact RoPE, repeat_kv and add; f16 RMSNorm, softmax and SwiGLU
-    within 2 ulp.  Returns the stages that differ."""
-    from oracle import oracle as o
+def time_chain_graphs(ctx, chain, sets, steps, warmup):
+    """ms per step with each set's chain recorded as a graph (recorded
+    streaming ops fused, the library's default) and the graphs replayed
+    round-robin.  The graphs stay alive until the process ends."""
+    graphs = []
+    for b in sets:
+        ctx.capture_begin()
+        try:
+            chain.launch(b)
+        finally:
+            graphs.append(ctx.capture_end())
+    _LIVE_GRAPHS.extend(graphs)
+    ms = time_graphs(ctx, graphs, 1, steps, warmup=warmup)
+    ctx.finish()
+    return ms
 
-    o.set_threads(cpu_threads())
+
+def oracle_chain(o, chain, host):
+    """The chain on the CPU oracle (same stages, same order, f16 storage).
+    V's cache is V itself (the append copies it)."""
+    hid, qh, kvh, hd, tok = chain.HID, chain.QH, chain.KVH, chain.HD, chain.TOK
+    rep = qh // kvh
+    out = {"xn": o.rmsnorm(host["x"], chain.w, 1e-5)}
+    out.update(oracle_after_norm(o, chain, host, out["xn"]))
+    out["p"] = o.attention_softmax(host["s"], 0.125, 0)
+    out["h"] = o.swiglu(host["g"], host["u"])
+    return out
+
+
+def oracle_after_norm(o, chain, host, xn):
+    """The chain's stages that read xn (RoPE of its Q/K views, repeat_kv,
+    the residual add), on the oracle."""
+    qh, kvh, rep = chain.QH, chain.KVH, chain.QH // chain.KVH
+    flat = xn.ravel()
+    q = o.contiguous(flat, chain.qdims, chain.qstrides).reshape(chain.qdims)
+    k = o.contiguous(flat, chain.kdims, chain.kstrides).reshape(chain.kdims)
+    kc = o.rope(k, chain.cos, chain.sin, 0)
+    return {"qr": o.rope(q, chain.cos, chain.sin, 0), "kc": kc,
+            "kq": o.repeat_kv(kc, rep), "vq": o.repeat_kv(host["v"], rep),
+            "o": o.add(xn, host["r"])}
+
+
+def _ulp16(got, ref) -> int:
+    gi = got.view(np.int16).astype(np.int32)
+    ri = ref.view(np.int16).astype(np.int32)
+    gi = np.where(gi < 0, -(gi & 0x7FFF), gi)
+    ri = np.where(ri < 0, -(ri & 0x7FFF), ri)
+    return int(np.max(np.abs(gi - ri)))
+
+
+def check_chain(o, chain, b, host, ref) -> list[str]:
+    """The GPU chain's outputs on buffer set `b` against the oracle's `ref`
+    on the same inputs: f16 RMSNorm, softmax and SwiGLU within 2 ulp; the
+    stages that read xn (RoPE, repeat_kv, residual add, the V cache)
+    bit-exact against the oracle applied to the GPU's own xn.  Returns the
+    stages that differ."""
     bad = []
-
-    def ulp(got, ref):
-        gi = got.view(np.int16).astype(np.int32)
-        ri = ref.view(np.int16).astype(np.int32)
-        gi = np.where(gi < 0, -(gi & 0x7FFF), gi)
-        ri = np.where(ri < 0, -(ri & 0x7FFF), ri)
-        return int(np.max(np.abs(gi - ri)))
-
     xn = b["xn"].numpy()
-    if ulp(xn, o.rmsnorm(host["x"], wn, 1e-5)) > 2:
+    if _ulp16(xn, ref["xn"]) > 2:
         bad.append("rmsnorm")
-    hid = xn.shape[1]
-    q_view = np.ascontiguousarray(xn.reshape(1, tok, qh, hd).transpose(0, 2, 1, 3))
-    k_view = np.ascontiguousarray(xn[:, :kvh * hd].reshape(1, tok, kvh, hd).transpose(0, 2, 1, 3))
-    kr = b["kr"].numpy()
-    if not np.array_equal(b["qr"].numpy().view(np.uint16),
-                          o.rope(q_view, cos, sin, 0).view(np.uint16)):
-        bad.append("rope_Q")
-    if not np.array_equal(kr.view(np.uint16), o.rope(k_view, cos, sin, 0).view(np.uint16)):
-        bad.append("rope_K")
-    if not np.array_equal(b["kq"].numpy().view(np.uint16),
-                          o.repeat_kv(kr, qh // kvh).view(np.uint16)):
-        bad.append("repeat_kv_K")
-    if not np.array_equal(b["vq"].numpy().view(np.uint16),
-                          o.repeat_kv(host["v"], qh // kvh).view(np.uint16)):
-        bad.append("repeat_kv_V")
-    p = b["p"].numpy()
-    ref = o.attention_softmax(scores, 0.125, 0)
-    if ulp(p, ref) > 2:
+    if _ulp16(b["p"].numpy(), ref["p"]) > 2:
         bad.append("attention_softmax")
-    del p, ref
-    if ulp(b["h"].numpy(), o.swiglu(host["g"], host["u"])) > 2:
+    if _ulp16(b["h"].numpy(), ref["h"]) > 2:
         bad.append("swiglu")
-    if not np.array_equal(b["o"].numpy().view(np.uint16),
-                          o.add(xn, host["r"]).view(np.uint16)):
-        bad.append("residual_add")
-    assert hid == qh * hd
+    exact = (oracle_after_norm(o, chain, host, xn) if not np.array_equal(xn, ref["xn"])
+             else ref)
+    for name in ("qr", "kc", "kq", "vq", "o"):
+        if not np.array_equal(b[name].numpy().view(np.uint16), exact[name].view(np.uint16)):
+            bad.append(name)
+    if chain.fused and not np.array_equal(b["vc"].numpy().view(np.uint16),
+                                          host["v"].view(np.uint16)):
+        bad.append("v_cache")
     return bad
 
 
@@ -930,38 +894,46 @@ def cpu_threads() -> int:
     return max(1, min(n, int(cap))) if cap.isdigit() and int(cap) > 0 else n
 
 
-def cpu_baseline(host, budget_s: float, threads: int = 1):
-    """The oracle (scalar C restatement of the reference ops; `threads` > 1
-    splits each op's rows/elements over OpenMP threads) on whole batch steps
-    until `budget_s` seconds have run."""
+def _oracle():
     sys.path.insert(0, ROOT)
     from oracle import oracle as o
+    return o
 
+
+def cpu_chain(chain, host, budget_s: float, threads: int = 1):
+    """The oracle (scalar C restatement of the reference ops; `threads` > 1
+    splits each op's rows/elements over OpenMP threads) on whole passes of
+    the layer chain over one buffer set's inputs, at least one pass and
+    until `budget_s` seconds have run.  Returns passes, seconds, outputs."""
+    o = _oracle()
+    o.set_threads(threads)
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        outs = oracle_chain(o, chain, host)
+        passes += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    return passes, time.perf_counter() - t0, outs
+
+
+def oracle_batch_step(host, threads):
+    """One step of the [4096, 1536] batch on the oracle (its outputs)."""
+    o = _oracle()
     o.set_threads(threads)
     a32, b32, a16, b16 = host["a_float32"], host["b_float32"], host["a_float16"], host["b_float16"]
     outs = {}
-
-    def step():
-        for t, a, b in (("float32", a32, b32), ("float16", a16, b16)):
-            outs[f"add_{t}"] = o.add(a, b)
-            outs[f"mul_{t}"] = o.mul(a, b)
-            outs[f"silu_{t}"] = o.silu(a)
-            outs[f"swiglu_{t}"] = o.swiglu(a, b)
-            outs[f"bias_{t}"] = o.add_broadcast(a, host[f"bias_{t}"])
-            outs[f"view_{t}"] = o.contiguous(host[f"view_{t}"].ravel(), VIEW_DIMS, VIEW_STRIDES)
-            outs[f"kv_{t}"] = o.repeat_kv(host[f"kv_{t}"], 3)
-        outs["cast_h"] = o.cast(a32, F16)
-        outs["cast_f"] = o.cast(a16, F32)
-
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
-        step()
-        steps += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    elapsed = time.perf_counter() - t0
-    return steps, elapsed, outs
+    for t, a, b in (("float32", a32, b32), ("float16", a16, b16)):
+        outs[f"add_{t}"] = o.add(a, b)
+        outs[f"mul_{t}"] = o.mul(a, b)
+        outs[f"silu_{t}"] = o.silu(a)
+        outs[f"swiglu_{t}"] = o.swiglu(a, b)
+        outs[f"bias_{t}"] = o.add_broadcast(a, host[f"bias_{t}"])
+        outs[f"view_{t}"] = o.contiguous(host[f"view_{t}"].ravel(), VIEW_DIMS, VIEW_STRIDES)
+        outs[f"kv_{t}"] = o.repeat_kv(host[f"kv_{t}"], 3)
+    outs["cast_h"] = o.cast(a32, F16)
+    outs["cast_f"] = o.cast(a16, F32)
+    return outs
 
 
 def check_outputs(ctx, dev, outs) -> list[str]:
@@ -1054,6 +1026,25 @@ def probe(ctx, host, ops):
     krep, vrep = ctx.empty((1, 15, tok, 64), F16), ctx.empty((1, 15, tok, 64), F16)
     # one decode step over a 4096-row cache
     q1, o1 = ctx.upload(synth.normal(14, (1, 15, 1, 64), 0, 1, F16)), ctx.empty((1, 15, 1, 64), F16)
+    # the layer chain's other kernels at its shapes (LayerChain): the f16
+    # scores' causal scale/mask + softmax, SwiGLU [4096, 2560], residual add
+    chain = LayerChain(ctx)
+    cb = chain.device_set(chain.host_inputs(0))
+    for name, nbytes, fn in [
+        ("attention_softmax_f16 [15,4096,4096] causal", chain.softmax_bytes,
+         lambda: ctx.attention_softmax(cb["s"], 0.125, 0, cb["p"])),
+        ("swiglu_f16 [4096,2560]", chain.stage_bytes["swiglu"],
+         lambda: ctx.swiglu(cb["g"], cb["u"], cb["h"])),
+        ("add_f16 [4096,960]", chain.stage_bytes["residual_add"],
+         lambda: ctx.add(cb["x"], cb["r"], cb["o"])),
+        ("chain prologue: qkv rope + KV append + repeat_kv f16", chain.stage_bytes["prologue"],
+         lambda: chain.launch_prologue(cb)),
+    ]:
+        for _ in range(3):
+            ctx.begin()
+            fn()
+            ctx.finish()
+        log(f"probe {name}: {nbytes} algorithmic bytes per launch")
     for name, nbytes, fn in [
         ("attention_f16 fused [1,15,4096,64] causal (inputs + output)", attn_io,
          lambda: ctx.attention(q, ka, va, 0.125, 0, None, qo)),
@@ -1119,26 +1110,71 @@ def measured_traffic(op_name):
 
 # ------------------------------------------------------------------ main
 
+# The per-op rows the JSON line carries (the full table goes to stderr and
+# to the --per-op-out file): the metric's four ops at the layer's shapes,
+# the largest RMSNorm rows, the [9, 2048, 2048] softmax and the SwiGLU rows.
+SUMMARY_ROWS = [
+    ("layer.1 rmsnorm_f16", [4096, 960]),
+    ("layer.2 rope_Q_f16 (fused gather)", [1, 15, 4096, 64]),
+    ("layer.2 rope_K_f16 (fused gather)", [1, 5, 4096, 64]),
+    ("layer.2 QKV + KV append + repeat_kv (one launch)", [1, 25, 4096, 64]),
+    ("layer.4 attention_softmax_f16", [15, 4096, 4096]),
+    ("layer.5 swiglu_f16", [4096, 2560]),
+    ("layer.6 residual add_f16", [4096, 960]),
+    ("rmsnorm_f16", [16384, 960]),
+    ("rmsnorm_f32", [16384, 960]),
+    ("attention_softmax_f32", [9, 2048, 2048]),
+    ("softmax_f32", [9, 2048, 2048]),
+    ("swiglu_f16", [4096, 1536]),
+    ("swiglu_f32", [4096, 1536]),
+    ("add_rmsnorm_f32", [64, 768]),
+]
+
+
+def summary(rows):
+    """{"op shape": [us, GB/s, % of peak, sustained % of peak]} for SUMMARY_ROWS."""
+    out = {}
+    for op, shape in SUMMARY_ROWS:
+        for r in rows:
+            if r["op"] == op and r["shape"] == shape:
+                out[f"{op} {shape}"] = [r["us"], r["GB/s"], r["pct_peak"],
+                                        r.get("pct_peak_graph_batch")]
+                break
+    return out
+
+
+def write_side_file(path, payload):
+    try:
+        os.makedirs(os.path.dirname(path), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump(payload, f, indent=1)
+        return os.path.relpath(path, ROOT)
+    except OSError as e:
+        log(f"could not write {path}: {e}")
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--sets", type=int, default=4, help="buffer sets rotated across steps")
-    ap.add_argument("--streams", type=int, default=1,
-                    help="streams the step's independent ops are spread over")
-    ap.add_argument("--forked-graph", action="store_true",
-                    help="with --streams > 1: one recorded graph with parallel branches "
-                         "instead of one graph per stream")
+    ap.add_argument("--sets", type=int, default=2,
+                    help="buffer sets of the layer chain rotated across steps (1.1 GB each)")
     ap.add_argument("--op-reps", type=int, default=100, help="timed launches per op line")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU leg: at least one chain pass on one core, then passes on all "
+                         "cores for half this long")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
-    ap.add_argument("--quick", action="store_true", help="fewer extra shapes")
+    ap.add_argument("--no-extra", action="store_true", help="skip the per-op lines")
+    ap.add_argument("--quick", action="store_true", help="fewer per-op shapes")
     ap.add_argument("--no-graph-batch", action="store_true",
-                    help="leave out the sustained (back-to-back, graph-replayed) time of each op")
+                    help="leave out the graph-replayed figures (sustained per-op times, the "
+                         "chain and the batch step as graphs)")
+    ap.add_argument("--per-op-out", default=os.path.join(ROOT, "gpurun_out", "bench_per_op.json"),
+                    help="file the full per-op table is written to")
     ap.add_argument("--probe", action="store_true",
-                    help="no timing: run each batch op 3 times on one buffer set, then a "
+                    help="no timing: run each op 3 times on one buffer set, then a "
                          "256 MiB device-to-device copy 3 times (for hardware-counter runs)")
     args = ap.parse_args()
     global GRAPH_BATCH
@@ -1151,85 +1187,109 @@ def main():
         sys.exit(2)
 
     ctx = abi.Context(0)
-    host = batch_inputs("bench")
-    ops = batch_ops()
     if args.probe:
-        probe(ctx, host, ops)
+        probe(ctx, batch_inputs("bench"), batch_ops())
         return
-    log(f"uploading {args.sets} buffer sets")
-    sets = [batch_set(ctx, host) for _ in range(args.sets)]
-    footprint = sum(set_bytes(s) for s in sets)
-    step_bytes = sum(op.nbytes for op in ops)
-    log(f"footprint {footprint / 2**30:.2f} GiB, {step_bytes / 1e6:.1f} MB per step")
 
-    aux = [abi.Context(0) for _ in range(max(0, args.streams - 1))]
-    if aux and args.forked_graph:
-        ms_step = time_step(ctx, aux, ops, sets, args.steps, args.warmup)
-    elif aux:
-        ms_step = time_step_streams(ctx, aux, ops, sets, args.steps, args.warmup)
-    else:
-        ms_step = time_step(ctx, [], ops, sets, args.steps, args.warmup)
-    value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"step on {args.streams} streams: {ms_step * 1e3:.1f} us, {value:.1f} GB/s "
-        f"({100 * value / PEAK_GBS:.1f}% of peak)")
-    ms_seq = ms_step if not aux else time_step(ctx, [], ops, sets, args.steps, args.warmup)
-    seq_value = step_bytes / (ms_seq * 1e-3) / 1e9
-    if aux:
-        log(f"step on 1 stream: {ms_seq * 1e3:.1f} us, {seq_value:.1f} GB/s "
-            f"({100 * seq_value / PEAK_GBS:.1f}% of peak)")
-    # the same step recorded with one kernel per op (no fusion of the
-    # independent streaming ops), for comparison
-    ctx.set_fusion(False)
-    ms_unfused = time_step(ctx, [], ops, sets, args.steps, args.warmup)
-    ctx.set_fusion(True)
-    unfused_value = step_bytes / (ms_unfused * 1e-3) / 1e9
-    log(f"step with one kernel per op: {ms_unfused * 1e3:.1f} us, {unfused_value:.1f} GB/s "
-        f"({100 * unfused_value / PEAK_GBS:.1f}% of peak)")
-    for a in aux:
-        a.close()
+    # ---- the headline: the layer chain, 5 launches, over rotated buffer sets
+    chain = LayerChain(ctx, "one")
+    log(f"layer chain: {args.sets} buffer sets")
+    host0 = chain.host_inputs(0)
+    csets = [chain.device_set(host0)] + [chain.device_set(chain.host_inputs(i))
+                                         for i in range(1, args.sets)]
+    footprint = sum(set_bytes(s) for s in csets)
+    ms_step, sm_us = time_chain(ctx, chain, csets, args.steps, args.warmup)
+    value = chain.nbytes / (ms_step * 1e-3) / 1e9
+    sm_mean = float(np.mean(sm_us))
+    sm_gbs = chain.softmax_bytes / (sm_mean * 1e-6) / 1e9
+    log(f"layer chain ({chain.launches} launches): {ms_step * 1e3:.2f} us per step, "
+        f"{value:.1f} GB/s ({100 * value / PEAK_GBS:.1f}% of peak), footprint "
+        f"{footprint / 2**30:.2f} GiB")
+    log(f"  its softmax launches: {sm_mean:.2f} us mean ({len(sm_us)} launches), "
+        f"{sm_gbs:.1f} GB/s ({100 * sm_gbs / PEAK_GBS:.1f}%)")
+    ms_graph = (time_chain_graphs(ctx, chain, csets, max(args.steps, 20), args.warmup)
+                if GRAPH_BATCH else None)
+    if ms_graph is not None:
+        log(f"  the same chain recorded as graphs: {ms_graph * 1e3:.2f} us per step")
+    split = LayerChain(ctx, "split")
+    ms_split, _ = time_chain(ctx, split, csets, args.steps, args.warmup)
+    log(f"layer chain, prologue as 4 launches ({split.launches} launches): "
+        f"{ms_split * 1e3:.2f} us per step, {split.nbytes / (ms_split * 1e-3) / 1e9:.1f} GB/s")
+    chain.launch(csets[0])  # set 0 holds the 5-launch chain's outputs again
+    ctx.finish()
 
-    log("per op ([4096, 1536] batch):")
-    rows = per_op_rows(ctx, ops, sets, args.op_reps)
-    # The step's kernel: recorded into a graph, a step's 16 independent ops
-    # run as one fused launch (a replay holds one such launch per buffer
-    # set), so the kernel's duration is the step's, from the events around
-    # the timed replays (the gaps between launches included).
-    roofline = {"bound": "hbm", "kernel": "fused step", "achieved": round(value, 1),
-                "peak": PEAK_GBS, "unit": "GB/s", "frac": round(value / PEAK_GBS, 4),
-                "bytes_per_launch": step_bytes, "us_per_launch": round(ms_step * 1e3, 3),
-                "traffic": measured_traffic("fused step")}
-
+    threads = cpu_threads()
+    o = _oracle()
     cpu = None
     if not args.no_cpu:
-        log(f"cpu baseline: oracle, 1 thread, ~{args.cpu_seconds:.0f} s of whole steps")
-        steps, elapsed, outs = cpu_baseline(host, args.cpu_seconds)
-        bad = check_outputs(ctx, sets[0], outs)
-        cpu_gbs = step_bytes * steps / elapsed / 1e9
-        cpu = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{steps} whole batch steps (16 ops on [4096,1536] and the "
-                         f"view/KV shapes) in {elapsed:.1f} s",
-               "gpu_outputs_match_oracle": not bad}
-        if bad:
-            log(f"MISMATCH against the oracle: {bad}")
-        log(f"cpu: {cpu_gbs:.2f} GB/s over {steps} steps")
-        threads = cpu_threads()
-        cpu["host_cores_available"] = threads
-        if threads == 1:
-            cpu["all_cores"] = None
-            cpu["note"] = ("this process could use one core of the host (its affinity set / "
-                           "OMP_NUM_THREADS), so no multi-core figure was taken")
+        log(f"cpu baseline: oracle, 1 thread, >= 1 chain pass (~{args.cpu_seconds:.0f} s)")
+        passes, elapsed, ref = cpu_chain(chain, host0, args.cpu_seconds, 1)
+        cpu_gbs = chain.nbytes * passes / elapsed / 1e9
+        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{passes} whole pass(es) of the layer chain on buffer set 0's inputs "
+                         f"in {elapsed:.1f} s ({1e3 * elapsed / passes:.0f} ms a pass)"}
+        log(f"cpu (1 thread): {cpu_gbs:.3f} GB/s, {passes} pass(es) in {elapsed:.1f} s")
         if threads > 1:
-            secs = args.cpu_seconds / 2
-            log(f"cpu baseline: oracle, {threads} threads, ~{secs:.0f} s of whole steps")
-            steps_n, elapsed_n, _ = cpu_baseline(host, secs, threads)
-            gbs_n = step_bytes * steps_n / elapsed_n / 1e9
-            cpu["all_cores"] = {"value": round(gbs_n, 2), "unit": "GB/s", "cores": threads,
-                                "sample": f"{steps_n} whole batch steps in {elapsed_n:.1f} s"}
-            log(f"cpu ({threads} threads): {gbs_n:.2f} GB/s over {steps_n} steps")
+            passes_n, elapsed_n, _ = cpu_chain(chain, host0, args.cpu_seconds / 2, threads)
+            gbs_n = chain.nbytes * passes_n / elapsed_n / 1e9
+            cpu["all_cores"] = {"value": round(gbs_n, 3), "cores": threads,
+                                "sample": f"{passes_n} passes in {elapsed_n:.1f} s"}
+            log(f"cpu ({threads} threads): {gbs_n:.3f} GB/s, {passes_n} passes in "
+                f"{elapsed_n:.1f} s")
+        else:
+            cpu["all_cores"] = None
+            cpu["note"] = "this process may use one core (affinity / OMP_NUM_THREADS)"
+    else:
+        o.set_threads(threads)
+        ref = oracle_chain(o, chain, host0)
+    bad = check_chain(o, chain, csets[0], host0, ref)
+    log("layer chain: every stage matches the oracle" if not bad
+        else f"layer chain: MISMATCH against the oracle in {bad}")
+    if cpu is not None:
+        cpu["gpu_outputs_match_oracle"] = not bad
+    del csets, ref
+    chain._scores = None
 
-    extra = [] if args.no_extra else extra_rows(ctx, args.op_reps, args.quick)
-    del sets
+    # ---- the [4096, 1536] batch step (secondary): 16 ops over rotated sets
+    host = batch_inputs("bench")
+    ops = batch_ops()
+    sets = [batch_set(ctx, host) for _ in range(4)]
+    distinct = set_bytes(sets[0])  # every input and output of a step, each once
+    c2_steps = 4 * max(1, -(-max(args.steps, 20) // 4))
+    ms_c2 = time_step(ctx, ops, sets, c2_steps, args.warmup) if GRAPH_BATCH else None
+    ctx.set_fusion(False)
+    ms_c2_unfused = time_step(ctx, ops, sets, c2_steps, args.warmup) if GRAPH_BATCH else None
+    ctx.set_fusion(True)
+    c2_bad = check_outputs(ctx, sets[0], oracle_batch_step(host, threads))
+    c2 = {"workload": "elementwise+broadcast batch [4096,1536], f32 and f16 (16 ops)",
+          "distinct_bytes_per_step": distinct, "outputs_match_oracle": not c2_bad}
+    if ms_c2 is not None:
+        c2.update({"us_per_step_fused_launch": round(ms_c2 * 1e3, 2),
+                   "GB/s_fused_launch": round(distinct / (ms_c2 * 1e-3) / 1e9, 1),
+                   "us_per_step_kernel_per_op": round(ms_c2_unfused * 1e3, 2),
+                   "GB/s_kernel_per_op": round(distinct / (ms_c2_unfused * 1e-3) / 1e9, 1)})
+        log(f"batch step [4096,1536]: {ms_c2 * 1e3:.1f} us fused, {ms_c2_unfused * 1e3:.1f} us "
+            f"one kernel per op ({distinct / 1e6:.1f} MB distinct bytes)")
+    if c2_bad:
+        log(f"batch step: MISMATCH against the oracle: {c2_bad}")
 
+    rows = []
+    if not args.no_extra:
+        log("per op ([4096, 1536] batch):")
+        rows = per_op_rows(ctx, ops, sets, args.op_reps)
+        del sets
+        rows += extra_rows(ctx, args.op_reps, args.quick)
+    else:
+        del sets
+    side = write_side_file(args.per_op_out, {"per_op": rows})
+
+    sm_traffic = measured_traffic("attention_softmax_f16 [15,4096,4096] causal")
+    roofline = {"bound": "hbm", "kernel": "k_softmax_rows<half, 8, 4, 128, true, false>",
+                "op": "causal scale/mask + softmax f16 [15,4096,4096]",
+                "achieved": round(sm_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(sm_gbs / PEAK_GBS, 4), "traffic": sm_traffic,
+                "bytes_per_launch": chain.softmax_bytes, "us_per_launch": round(sm_mean, 3),
+                "launches_timed": len(sm_us), "share_of_step": round(sm_mean / (ms_step * 1e3), 3)}
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -1241,26 +1301,32 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32/f16",
+        "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": "elementwise+broadcast batch [4096,1536], f32 and "
-                               "f16 storage (add, mul, silu, swiglu, bias add, casts, "
-                               "contiguous [1,9,4096,64] view, repeat_kv 3->9)",
-                   "ops_per_step": len(ops), "bytes_per_step": step_bytes,
+        "config": {"workload": LayerChain.WORKLOAD,
+                   "stages": "rmsnorm [4096,960] -> rope Q/K + KV append + repeat_kv 5->15 "
+                             "(one launch) -> causal scale/mask+softmax [15,4096,4096] -> "
+                             "swiglu [4096,2560] -> residual add [4096,960]",
+                   "launches_per_step": chain.launches, "bytes_per_step": chain.nbytes,
                    "buffer_sets": args.sets, "footprint_gib": round(footprint / 2**30, 2),
-                   "streams": args.streams,
-                   "one_stream_GBps": round(seq_value, 1),
-                   "one_stream_ms_per_step": round(ms_seq, 5),
-                   "recorded_streaming_ops_fused": True,
-                   "one_kernel_per_op_GBps": round(unfused_value, 1),
-                   "one_kernel_per_op_ms_per_step": round(ms_unfused, 5)},
+                   "timing": "eager launches on one stream, events around the K steps",
+                   "graph_replay_ms_per_step": None if ms_graph is None else round(ms_graph, 5),
+                   "eight_launch_ms_per_step": round(ms_split, 5),
+                   "outputs_match_oracle": not bad},
         "pct_of_peak": round(100 * value / PEAK_GBS, 1),
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "per_op": rows + extra,
+        "per_op_summary": {"columns": ["us", "GB/s", "pct_peak", "pct_peak_sustained"],
+                           **summary(rows)},
+        "per_op_file": side,
+        "batch_step": c2,
     }
     ctx.close()
-    print(json.dumps(line), flush=True)
+    text = json.dumps(line, separators=(",", ":"))
+    if len(text) > 7500:  # keep the line short enough for the driver to parse
+        line.pop("per_op_summary")
+        text = json.dumps(line, separators=(",", ":"))
+    print(text, flush=True)
 
 
 if __name__ == "__main__":

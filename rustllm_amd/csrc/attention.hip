@@ -952,8 +952,13 @@ __device__ inline void finish_split(const float (&merge_m)[kSplitWaves][RM],
     // wave waits for those stores to complete (vmcnt) before the barrier, and
     // only then does one thread draw the ticket -- no L2 write-back, which
     // an agent-scope release fence would make every workgroup pay in turn.
-    // The last workgroup reads the partials agent-coherent as well and puts
-    // the ticket back to zero for the next launch.
+    // This release side rests on the hardware, not on the memory model: the
+    // stores are relaxed atomics that gfx950 has completed at the point of
+    // coherence (vmcnt 0) before the relaxed fetch_add is issued, which the
+    // C++/HIP model alone does not order.  The merging workgroup (one per KV
+    // head) takes an agent-scope acquire fence after its ticket, reads the
+    // partials agent-coherent as well and puts the ticket back to zero for
+    // the next launch.  The back-to-back decode tests guard the hand-off.
     __shared__ uint32_t ticket;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -962,6 +967,7 @@ __device__ inline void finish_split(const float (&merge_m)[kSplitWaves][RM],
                                         __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (ticket != splits - 1) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (threadIdx.x == 0)
         __hip_atomic_store(&tickets[kvb * kTicketStride], 0u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);

@@ -356,6 +356,24 @@ __device__ inline void store_stream(V* p, V v) {
     __builtin_nontemporal_store(v, p);
 }
 
+// The same for N elements of T at the alignment of one element (VecOfU), for
+// packs that start off the 16-byte grid.  The builtins see the pointer as
+// spelled here, so the access keeps the element alignment; passed through
+// load_stream / store_stream the deduced V would drop VecOfU's alignment
+// attribute and claim 16.
+template <typename T, int N>
+__device__ inline typename VecOf<T, N>::type load_stream_u(const T* p) {
+    typedef typename VecOfU<T, N>::type U;
+    return __builtin_nontemporal_load(reinterpret_cast<const U*>(p));
+}
+
+template <typename T, int N>
+__device__ inline void store_stream_u(T* p, typename VecOf<T, N>::type v) {
+    typedef typename VecOfU<T, N>::type U;
+    const U u = v;
+    __builtin_nontemporal_store(u, reinterpret_cast<U*>(p));
+}
+
 // e^x as 2^(x * log2 e) on the hardware exp2 (v_exp_f32), which returns
 // 0 for -inf, inf for +inf and NaN for NaN by itself.  The only error beyond
 // the instruction's own ~1 ulp is the rounding of t = x * log2 e, which

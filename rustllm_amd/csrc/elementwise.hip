@@ -163,9 +163,12 @@ __device__ inline void map_body(const TIn* __restrict__ a, const TIn* __restrict
     const uint64_t base = uint64_t(blk) * kThreads * UNROLL + threadIdx.x;
     if constexpr (PHASED) {
         // Three phases: every pack's loads (at indices clamped into the
-        // array), every result, then every store (a clamped pack rewrites the
-        // last pack's own value).  With per-pack branches the compiler issued
-        // pack u + 1's loads only after pack u's store.
+        // array, so no load waits on a branch), every result, then the
+        // stores of the packs that are this lane's own.  A clamped lane
+        // stores nothing: with out == a (in place) the last pack may already
+        // hold its owner's result when a clamped lane reads it.  With
+        // per-pack branches around the loads the compiler issued pack
+        // u + 1's loads only after pack u's store.
         if (n_packs > 0) {
             VI ra[UNROLL], rb[UNROLL];
             VO r[UNROLL];
@@ -189,11 +192,11 @@ __device__ inline void map_body(const TIn* __restrict__ a, const TIn* __restrict
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) {
                 const uint64_t i = base + uint64_t(u) * kThreads;
-                const uint64_t ic = i < n_packs ? i : n_packs - 1;
+                if (i >= n_packs) continue;
                 if constexpr (NTS)
-                    store_stream(vo + ic, r[u]);
+                    store_stream(vo + i, r[u]);
                 else
-                    vo[ic] = r[u];
+                    vo[i] = r[u];
             }
         }
     } else {

@@ -118,7 +118,8 @@ __device__ inline float group_sum(float v, float* lds) {
 // doubled the VGPR count of the masked f16 variant.)
 // RAGGED: the width is not a multiple of N, so a row starts off the 16-byte
 // grid.  Pack p still holds the row's elements p * N .. p * N + N - 1, read
-// and written as unaligned 16-byte accesses (VecOfU); a row's partial last
+// and written as unaligned 16-byte accesses (load_stream_u / store_stream_u,
+// VecOfU: the element alignment the pointers have); a row's partial last
 // pack reads on into the next row (masked) and is written element by
 // element.  Only the buffer's last pack can reach past its end: that load
 // is moved back inside the buffer and the pack reloaded element by element.
@@ -129,7 +130,6 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
                                                            uint32_t rows, uint32_t width,
                                                            MaskParams mp) {
     typedef typename VecOf<T, N>::type V;
-    typedef typename VecOfU<T, N>::type U;
     constexpr int RPB = kThreads / TPR;
     __shared__ float lds_m[kThreads / kWave];
     __shared__ float lds_s[kThreads / kWave];
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
                 if constexpr (RAGGED) {
                     const uint64_t off = e0 + uint64_t(q) * N;
                     moved[k] = off + N > total;  // the buffer's last pack
-                    raw[k] = load_stream(reinterpret_cast<const U*>(in + (moved[k] ? total - N : off)));
+                    raw[k] = load_stream_u<T, N>(in + (moved[k] ? total - N : off));
                 } else {
                     raw[k] = load_stream(src + q);
                 }
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
             for (int j = 0; j < N; ++j) o[j] = from_float<T>(v[k][j] * inv);
             if constexpr (RAGGED) {
                 if (p * N + N <= width) {
-                    store_stream(reinterpret_cast<U*>(out + e0 + uint64_t(p) * N), U(o));
+                    store_stream_u<T, N>(out + e0 + uint64_t(p) * N, o);
                 } else {  // the row's partial last pack
 #pragma unroll
                     for (int j = 0; j < N; ++j)

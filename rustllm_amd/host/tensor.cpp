@@ -1325,14 +1325,21 @@ Tensor SwiGlu::forward(const Context& ctx, const Tensor& gate, const Tensor& up)
     return gate.silu(ctx).mul(ctx, up);
 }
 
-// src/nn/swiglu.rs:15-37: the fused kernel for contiguous equal shapes
-// (F16 as in the reference; F32 fused is bit-identical to silu -> mul).
+// src/nn/swiglu.rs:15-37: an F16 gate with contiguous inputs of equal shape
+// takes the fused kernel, whose buffer check rejects an up that is not F16
+// (InvalidShape "SwiGLU requires equal F16 buffers", ops/swiglu.rs:14-19).
+// Otherwise silu then mul; for two contiguous F32 tensors of equal shape
+// that pair runs as one launch (swiglu_f32: silu_f32(g) * u, the same
+// values as the two ops).
 Tensor SwiGlu::forward_encode(const Context& ctx, const Tensor& gate, const Tensor& up) {
-    if (gate.dtype() == up.dtype() && gate.is_contiguous() && up.is_contiguous() &&
-        gate.shape() == up.shape()) {
-        Buffer out = gate.dtype() == DType::F16 ? ops::swiglu_f16_encode(ctx, gate.buffer(), up.buffer())
-                                                : ops::swiglu_f32_encode(ctx, gate.buffer(), up.buffer());
-        return Tensor::from_buffer(std::move(out), gate.shape().dims(), gate.dtype());
+    const bool fusable = gate.is_contiguous() && up.is_contiguous() && gate.shape() == up.shape();
+    if (gate.dtype() == DType::F16 && fusable) {
+        Buffer out = ops::swiglu_f16_encode(ctx, gate.buffer(), up.buffer());
+        return Tensor::from_buffer(std::move(out), gate.shape().dims(), DType::F16);
+    }
+    if (gate.dtype() == DType::F32 && up.dtype() == DType::F32 && fusable) {
+        Buffer out = ops::swiglu_f32_encode(ctx, gate.buffer(), up.buffer());
+        return Tensor::from_buffer(std::move(out), gate.shape().dims(), DType::F32);
     }
     return gate.silu_encode(ctx).mul_encode(ctx, up);
 }

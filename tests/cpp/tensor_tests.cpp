@@ -235,6 +235,42 @@ TEST(batches_silu_then_mul_in_one_command_buffer) {
     CHECK(std::fabs(values[1] + 0.8068242f) < 0.02f);
 }
 
+// nn/swiglu.rs:15-37 with ops/swiglu.rs:14-19: an F16 gate with contiguous
+// equal-shape inputs takes the fused F16 kernel, whose buffer check rejects
+// an F32 up; an F32 gate falls through to silu then mul, which rejects the
+// dtype pair there.
+TEST(swiglu_encode_dispatch_follows_the_gate_dtype) {
+    auto gate16 = Tensor::from_f16_slice(context, to_f16({1.0, -1.0}), {2});
+    auto up16 = Tensor::from_f16_slice(context, to_f16({2.0, 3.0}), {2});
+    auto gate32 = Tensor::from_f32_slice(context, {1.0f, -1.0f}, {2});
+    auto up32 = Tensor::from_f32_slice(context, {2.0f, 3.0f}, {2});
+    {
+        TinyError e = catch_error([&] {
+            Execution execution(context);
+            nn::SwiGlu::forward_encode(context, gate16, up32);
+            execution.finish();
+        });
+        CHECK(e.kind() == TinyError::Kind::InvalidShape);
+        CHECK(std::string(e.what()).find("SwiGLU requires equal F16 buffers") != std::string::npos);
+    }
+    CHECK(expect_error([&] {
+              Execution execution(context);
+              nn::SwiGlu::forward_encode(context, gate32, up16);
+              execution.finish();
+          }) == TinyError::Kind::UnsupportedDType);
+    Execution execution(context);
+    Tensor fused = nn::SwiGlu::forward_encode(context, gate16, up16);
+    Tensor fused32 = nn::SwiGlu::forward_encode(context, gate32, up32);
+    execution.finish();
+    CHECK(fused.dtype() == DType::F16 && fused32.dtype() == DType::F32);
+    auto values = fused.to_f32_vec();
+    CHECK(std::fabs(values[0] - 1.4621172f) < 0.02f);
+    CHECK(std::fabs(values[1] + 0.8068242f) < 0.02f);
+    auto values32 = fused32.to_f32_vec();
+    CHECK(std::fabs(values32[0] - 1.4621172f) < 1e-5f);
+    CHECK(std::fabs(values32[1] + 0.8068242f) < 1e-5f);
+}
+
 // ops/rmsnorm.rs:286-319: the reference test's own CPU implementation.
 std::vector<float> cpu_rmsnorm(const std::vector<float>& input, const std::vector<float>& weight,
                                size_t rows, size_t hidden_size, float epsilon) {

@@ -109,6 +109,31 @@ def test_silu_extremes(ctx):
     assert f16_ulp_distance(got, o.silu(xh)) <= F16_ULP
 
 
+@pytest.mark.parametrize("n", [1000, 100_003, 4096 * 1536 + 8 * 100 + 5])
+def test_silu_f16_in_place(ctx, n):
+    """SiLU f16 written over its own input (out == input, which the ABI
+    accepts) at sizes whose last block of packs is partial: every pack is
+    stored only by the lane that owns it, so the result is the oracle's SiLU
+    of the original input (within 2 ulp) -- eagerly, and recorded into a
+    graph (the fused launch of recorded ops) and replayed twice, each time
+    onto a fresh copy of the input."""
+    x = norm(("silu-inplace",), (n,), np.float16, 0.0, 3.0)
+    ref = o.silu(x)
+    d = ctx.upload(x)
+    run(ctx, lambda: ctx.silu(d, d))
+    check_float(d.numpy(), ref, f"in-place silu n={n}")
+    src, d2 = ctx.upload(x), ctx.upload(x)
+    ctx.capture_begin()
+    ctx.silu(d2, d2)
+    graph = ctx.capture_end()
+    for i in range(2):
+        ctx.copy(src, d2)
+        ctx.graph_launch(graph)
+        ctx.finish()
+        check_float(d2.numpy(), ref, f"in-place silu n={n}, graph replay {i}")
+    ctx.graph_destroy(graph)
+
+
 def test_silu_swiglu_f16_every_half(ctx):
     """SiLU over all 65,536 halves (incl. +-inf, NaN, subnormals and the range
     where the sigmoid's reciprocal is subnormal), and SwiGLU with every half as

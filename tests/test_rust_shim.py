@@ -81,17 +81,28 @@ def test_status_constants_match_the_header():
 
 
 def struct_fields(text, name, c_style):
+    """[(field, Rust type)] of a struct, in order; C array fields T x[N]
+    become [T'; N]."""
     if c_style:
         body = re.search(r"typedef struct %s \{(.*?)\}" % name, text, flags=re.S).group(1)
-        return re.findall(r"([A-Za-z_][A-Za-z0-9_]*)(?:\[[A-Z_]+\])?;", body)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        out = []
+        for ctype, field, dim in re.findall(
+                r"([A-Za-z_][A-Za-z0-9_ ]*?\**)\s*([A-Za-z_][A-Za-z0-9_]*)(?:\[([A-Z_0-9]+)\])?;",
+                body):
+            t = c_to_rust(ctype)
+            out.append((field, f"[{t}; {dim}]" if dim else t))
+        return out
     body = re.search(r"pub struct %s \{(.*?)\n\}" % name, text, flags=re.S).group(1)
-    return re.findall(r"pub ([a-z_]+):", body)
+    return [(f, " ".join(t.split())) for f, t in re.findall(r"pub ([a-z_]+): ([^,]+),", body)]
 
 
-def test_repr_c_structs_follow_the_header_field_order():
+def test_repr_c_structs_follow_the_header_field_order_and_types():
     h, r = open(HEADER).read(), open(FFI).read()
     for name in ("rl_buffer", "rl_profile", "rl_error_payload"):
         assert struct_fields(h, name, True) == struct_fields(r, name, False), name
+        assert f"#[repr(C)]\npub struct {name}" in r.replace("#[derive", "\n#[derive") or \
+            re.search(r"#\[repr\(C\)\][^{]*pub struct %s \{" % name, r), name
     assert "#define RL_ERROR_MAX_RANK 16" in h and "RL_ERROR_MAX_RANK: usize = 16" in r
 
 
@@ -110,6 +121,9 @@ def test_check_maps_every_status_to_its_tinyerror_variant():
         assert re.search(r"%s(?: if has_payload)? => TinyError::%s" % (code, re.escape(variant)),
                          body), code
     assert "rl_last_error_payload" in body
+    # RL_ERR_DEVICE (and a data-carrying code without its payload) is the
+    # reference's Metal variant: the device error
+    assert re.search(r"_ => TinyError::Metal\(message\)", body)
     for field in ("left", "right", "start_pos", "seq_len", "max_seq_len", "token_id",
                   "vocab_size"):
         assert f"{field}:" in body, field
