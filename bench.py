@@ -30,6 +30,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -1173,6 +1174,9 @@ def main():
                          "chain and the batch step as graphs)")
     ap.add_argument("--per-op-out", default=os.path.join(ROOT, "gpurun_out", "bench_per_op.json"),
                     help="file the full per-op table is written to")
+    ap.add_argument("--per-op-only", action="store_true",
+                    help="only the per-op table, written to --per-op-out (the child process "
+                         "of a default run)")
     ap.add_argument("--probe", action="store_true",
                     help="no timing: run each op 3 times on one buffer set, then a "
                          "256 MiB device-to-device copy 3 times (for hardware-counter runs)")
@@ -1189,6 +1193,16 @@ def main():
     ctx = abi.Context(0)
     if args.probe:
         probe(ctx, batch_inputs("bench"), batch_ops())
+        return
+    if args.per_op_only:
+        host = batch_inputs("bench")
+        sets = [batch_set(ctx, host) for _ in range(4)]
+        log("per op ([4096, 1536] batch):")
+        rows = per_op_rows(ctx, batch_ops(), sets, args.op_reps)
+        del sets
+        rows += extra_rows(ctx, args.op_reps, args.quick)
+        write_side_file(args.per_op_out, {"per_op": rows})
+        ctx.close()
         return
 
     # ---- the headline: the layer chain, 5 launches, over rotated buffer sets
@@ -1273,18 +1287,34 @@ def main():
     if c2_bad:
         log(f"batch step: MISMATCH against the oracle: {c2_bad}")
 
-    rows = []
+    del sets
+    rows, per_op_status = [], "not run (--no-extra)"
     if not args.no_extra:
-        log("per op ([4096, 1536] batch):")
-        rows = per_op_rows(ctx, ops, sets, args.op_reps)
-        del sets
-        rows += extra_rows(ctx, args.op_reps, args.quick)
-    else:
-        del sets
-    side = write_side_file(args.per_op_out, {"per_op": rows})
+        # The per-op table runs in a child process (the same script with
+        # --per-op-only), after this process has returned its buffers: a
+        # failure there costs the table, not the headline.
+        ctx.lib.rl_context_trim(ctx.handle)
+        cmd = [sys.executable, os.path.abspath(__file__), "--per-op-only", "--op-reps",
+               str(args.op_reps), "--per-op-out", args.per_op_out]
+        cmd += ["--quick"] if args.quick else []
+        cmd += ["--no-graph-batch"] if args.no_graph_batch else []
+        try:
+            os.remove(args.per_op_out)
+        except OSError:
+            pass
+        rc = subprocess.run(cmd).returncode
+        try:
+            with open(args.per_op_out) as f:
+                rows = json.load(f)["per_op"]
+        except (OSError, ValueError, KeyError):
+            rows = []
+        per_op_status = "ok" if rc == 0 else f"per-op process exited with status {rc}"
+        if rc != 0:
+            log(f"per-op table: {per_op_status}")
+    side = os.path.relpath(args.per_op_out, ROOT) if rows else None
 
     sm_traffic = measured_traffic("attention_softmax_f16 [15,4096,4096] causal")
-    roofline = {"bound": "hbm", "kernel": "k_softmax_rows<half, 8, 4, 128, true, false>",
+    roofline = {"bound": "hbm", "kernel": "k_softmax_rows_h2<4, 128, true, false>",
                 "op": "causal scale/mask + softmax f16 [15,4096,4096]",
                 "achieved": round(sm_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(sm_gbs / PEAK_GBS, 4), "traffic": sm_traffic,
@@ -1319,6 +1349,7 @@ def main():
         "per_op_summary": {"columns": ["us", "GB/s", "pct_peak", "pct_peak_sustained"],
                            **summary(rows)},
         "per_op_file": side,
+        "per_op_status": per_op_status,
         "batch_step": c2,
     }
     ctx.close()

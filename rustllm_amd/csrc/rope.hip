@@ -165,7 +165,10 @@ __device__ inline void decode_job_row(const RowDimsN<kMaxJobRank>& rd, uint32_t 
     }
 }
 
-template <typename T, int L>
+// U rows per lane group: the group takes rows first + u * kRows (u < U) of
+// its block's kRows * U and issues every row's loads before any arithmetic,
+// so a wave has U rows' loads in flight.
+template <typename T, int L, int U>
 __global__ __launch_bounds__(kThreads) void k_rope_blocks(RowJobs jobs,
                                                           const float* __restrict__ cos_table,
                                                           const float* __restrict__ sin_table,
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void k_rope_blocks(RowJobs jobs,
     constexpr int N = 16 / int(sizeof(T));  // elements per lane
     constexpr uint32_t D = uint32_t(L * N);
     constexpr uint32_t kHalf = D / 2;
-    constexpr uint32_t kRows = kThreads / L;  // rows per block
+    constexpr uint32_t kRows = kThreads / L;  // rows per block and row slot
     typedef typename VecOf<T, N>::type V;
     typedef typename VecOf<float, N>::type VF;
     uint32_t k = 0;
@@ -181,52 +184,65 @@ __global__ __launch_bounds__(kThreads) void k_rope_blocks(RowJobs jobs,
     for (int t = 1; t < kMaxJobs; ++t) k += blockIdx.x >= jobs.job[t].first_block ? 1u : 0u;
     const RowJob& job = jobs.job[k];
     const bool rotate = job.rotate != 0;
-    uint32_t row = (blockIdx.x - job.first_block) * kRows + threadIdx.x / L;
-    const bool live = row < job.n_rows;
-    if (!live) row = job.n_rows - 1;  // a valid row: every lane takes part in the DPP moves
-    uint64_t src_off;
-    uint32_t pos, group;
-    decode_job_row(job.rows, row, src_off, pos, group);
+    const uint32_t first = (blockIdx.x - job.first_block) * kRows * U + threadIdx.x / L;
     const uint32_t lane = threadIdx.x % L;
     const uint32_t pack = (L == 8 && lane >= 4) ? 11 - lane : lane;
     const uint32_t pair = (pack % (L / 2)) * N;
-    // The three loads go out back to back.  A copy job reads table row 0
-    // (valid for every job here) and ignores it, which keeps them branch-free.
-    const uint64_t t = rotate ? uint64_t(start + pos) * kHalf + pair : pair;
-    const VF c = *reinterpret_cast<const VF*>(cos_table + t);
-    const VF s = *reinterpret_cast<const VF*>(sin_table + t);
-    const V x = load_stream(reinterpret_cast<const V*>(static_cast<const T*>(job.src) + src_off +
-                                                       pack * N));
-    // The rotation is computed for copy jobs too and then not used: a branch
-    // around it would let the compiler sink the table loads into it, behind
-    // a wait for x.
-    int w[4], m[4];
-    __builtin_memcpy(w, &x, 16);
+    V x[U];
+    VF c[U], s[U];
+    uint32_t pos[U], group[U];
+    bool live[U];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) m[i] = partner_dword<L>(w[i]);
-    V other;
-    __builtin_memcpy(&other, m, 16);
-    // First half: first*c - second*s; second half: second*c + first*s.
-    // Negating the partner is exact, so each result keeps the reference's
-    // two rounded products and one rounded sum.
+    for (int u = 0; u < U; ++u) {
+        uint32_t row = first + uint32_t(u) * kRows;
+        live[u] = row < job.n_rows;
+        if (!live[u]) row = job.n_rows - 1;  // a valid row: every lane takes part in the DPP moves
+        uint64_t src_off;
+        decode_job_row(job.rows, row, src_off, pos[u], group[u]);
+        // The three loads go out back to back.  A copy job reads table row 0
+        // (valid for every job here) and ignores it, which keeps them
+        // branch-free.
+        const uint64_t t = rotate ? uint64_t(start + pos[u]) * kHalf + pair : pair;
+        c[u] = *reinterpret_cast<const VF*>(cos_table + t);
+        s[u] = *reinterpret_cast<const VF*>(sin_table + t);
+        x[u] = load_stream(reinterpret_cast<const V*>(static_cast<const T*>(job.src) + src_off +
+                                                      pack * N));
+    }
     const bool first_half = pack < uint32_t(L / 2);
-    V o;
 #pragma unroll
-    for (int j = 0; j < N; ++j) {
-        const float own = to_float(x[j]);
-        const float partner = first_half ? -to_float(other[j]) : to_float(other[j]);
-        o[j] = rotate ? from_float<T>(own * c[j] + partner * s[j]) : x[j];
-    }
-    if (!live) return;
-    if (job.dst) {
-        const uint64_t r =
-            uint64_t(group) * job.dst_rows.group_rows + job.dst_rows.first_row + pos;
-        store_stream(reinterpret_cast<V*>(static_cast<T*>(job.dst) + r * D + pack * N), o);
-    }
-    if (job.rep) {
-        for (uint32_t i = 0; i < job.n_rep; ++i) {
-            const uint64_t r = (uint64_t(group) * job.n_rep + i) * job.rep_rows + job.rep_first + pos;
-            store_stream(reinterpret_cast<V*>(static_cast<T*>(job.rep) + r * D + pack * N), o);
+    for (int u = 0; u < U; ++u) {
+        // The rotation is computed for copy jobs too and then not used: a
+        // branch around it would let the compiler sink the table loads into
+        // it, behind a wait for x.
+        int w[4], m[4];
+        __builtin_memcpy(w, &x[u], 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m[i] = partner_dword<L>(w[i]);
+        V other;
+        __builtin_memcpy(&other, m, 16);
+        // First half: first*c - second*s; second half: second*c + first*s.
+        // Negating the partner is exact, so each result keeps the
+        // reference's two rounded products and one rounded sum.
+        V o;
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const float own = to_float(x[u][j]);
+            const float partner = first_half ? -to_float(other[j]) : to_float(other[j]);
+            o[j] = rotate ? from_float<T>(own * c[u][j] + partner * s[u][j]) : x[u][j];
+        }
+        if (!live[u]) continue;
+        if (job.dst) {
+            const uint64_t r =
+                uint64_t(group[u]) * job.dst_rows.group_rows + job.dst_rows.first_row + pos[u];
+            store_stream(reinterpret_cast<V*>(static_cast<T*>(job.dst) + r * D + pack * N), o);
+        }
+        if (job.rep) {
+            for (uint32_t i = 0; i < job.n_rep; ++i) {
+                const uint64_t r =
+                    (uint64_t(group[u]) * job.n_rep + i) * job.rep_rows + job.rep_first + pos[u];
+                store_stream(reinterpret_cast<V*>(static_cast<T*>(job.rep) + r * D + pack * N),
+                             o);
+            }
         }
     }
 }
@@ -269,12 +285,35 @@ bool make_job(RowJob& job, const void* src, const uint64_t* dims, const uint64_t
     return true;
 }
 
+// Rows per lane group of a launch of `total_rows` rows of `lanes` lanes
+// each: 2 when one row per group would need more waves than the chip holds
+// at once (8 per SIMD), so that every wave is resident from the start with
+// two rows' loads in flight; else 1.
+inline int rows_per_group(const rl_context* ctx, uint64_t total_rows, int lanes) {
+    const uint64_t waves = ceil_div(total_rows * uint64_t(lanes), 64);
+    return waves > uint64_t(8) * 4 * uint64_t(ctx->num_cus) ? 2 : 1;
+}
+
+template <typename T, int L>
+void launch_rows(rl_context* ctx, int unroll, dim3 grid, const RowJobs& jobs,
+                 const float* cos_table, const float* sin_table, uint32_t start) {
+    if (unroll == 2)
+        RL_LAUNCH(ctx, (k_rope_blocks<T, L, 2>), grid, dim3(kThreads), jobs, cos_table,
+                  sin_table, start);
+    else
+        RL_LAUNCH(ctx, (k_rope_blocks<T, L, 1>), grid, dim3(kThreads), jobs, cos_table,
+                  sin_table, start);
+}
+
 // Assigns first blocks to jobs[0 .. n) (jobs with no rows get none) and
 // launches; false when the grid would be too large.
 template <typename T>
 bool launch_jobs(rl_context* ctx, RowJobs& jobs, int n, int lanes, const float* cos_table,
                  const float* sin_table, uint64_t start) {
-    const uint64_t rows_per_block = uint64_t(kThreads) / lanes;
+    uint64_t total_rows = 0;
+    for (int t = 0; t < n; ++t) total_rows += jobs.job[t].n_rows;
+    const int unroll = rows_per_group(ctx, total_rows, lanes);
+    const uint64_t rows_per_block = uint64_t(kThreads) / lanes * unroll;
     uint64_t blocks = 0;
     for (int t = 0; t < kMaxJobs; ++t) {
         RowJob& job = jobs.job[t];
@@ -287,21 +326,13 @@ bool launch_jobs(rl_context* ctx, RowJobs& jobs, int n, int lanes, const float* 
         if (blocks >= (1u << 30)) return false;
     }
     if (blocks == 0) return true;
-    const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+    const dim3 grid(static_cast<unsigned>(blocks));
     const uint32_t s32 = uint32_t(start);
     switch (lanes) {
-        case 2:
-            RL_LAUNCH(ctx, (k_rope_blocks<T, 2>), grid, block, jobs, cos_table, sin_table, s32);
-            break;
-        case 4:
-            RL_LAUNCH(ctx, (k_rope_blocks<T, 4>), grid, block, jobs, cos_table, sin_table, s32);
-            break;
-        case 8:
-            RL_LAUNCH(ctx, (k_rope_blocks<T, 8>), grid, block, jobs, cos_table, sin_table, s32);
-            break;
-        default:
-            RL_LAUNCH(ctx, (k_rope_blocks<T, 16>), grid, block, jobs, cos_table, sin_table, s32);
-            break;
+        case 2: launch_rows<T, 2>(ctx, unroll, grid, jobs, cos_table, sin_table, s32); break;
+        case 4: launch_rows<T, 4>(ctx, unroll, grid, jobs, cos_table, sin_table, s32); break;
+        case 8: launch_rows<T, 8>(ctx, unroll, grid, jobs, cos_table, sin_table, s32); break;
+        default: launch_rows<T, 16>(ctx, unroll, grid, jobs, cos_table, sin_table, s32); break;
     }
     return true;
 }

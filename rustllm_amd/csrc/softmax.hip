@@ -43,10 +43,21 @@ struct MaskParams {
     uint32_t start;
 };
 
+// The scale/mask op's output for a kept score: the f32 product, rounded to
+// T.  For f16 the empty asm keeps the product in a register: without it the
+// compiler folds the multiply and the rounding into one v_fma_mixlo_f16
+// with a +0 addend, which turns the -0 product of a -0 score into +0.
+template <typename T>
+__device__ inline T scale_to(T raw, float scale) {
+    float p = to_float(raw) * scale;
+    if constexpr (sizeof(T) == 2) asm volatile("" : "+v"(p));
+    return from_float<T>(p);
+}
+
 // Score as the scale/mask op would store it, widened back to float.
 template <typename T>
 __device__ inline float scaled_score(T raw, float scale) {
-    return to_float(from_float<T>(to_float(raw) * scale));
+    return to_float(scale_to<T>(raw, scale));
 }
 
 template <typename T>
@@ -237,6 +248,184 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(const T* __restrict__
     }
 }
 
+// ----------------------- f16 rows, the first pass on pairs of halves
+
+// k_softmax_rows for f16 rows whose scale is itself an f16 value (the fused
+// scale/mask at 1/8, 1/sqrt(64), ...; 1 for the plain softmax).  On the
+// [15, 4096, 4096] causal scores k_softmax_rows keeps the SIMDs' vector ALUs
+// ~93% busy (counters: 14 VALU instructions per element), almost all of it
+// in the first pass, which widens, scales, rounds, indexes, compares and
+// selects every element of every row.  Here that pass works on pairs of
+// halves (v_pk_mul_f16, v_pk_max_f16) and masks whole packs:
+//  * the scaled score is one f16 multiply: x * scale with x and scale f16
+//    values is exact in f32 (11 + 11 significant bits), so rounding it once
+//    to f16 gives the scale/mask op's f16 output (f32 product, then RNE);
+//  * a pack past the row's last kept key becomes -inf by one select per
+//    pair; the one pack of a row that holds its last kept key masks its
+//    remaining elements in a branch that only that row's lane takes;
+//  * the row max is a max of pairs (NaN scores are ignored, as fmaxf does),
+//    widened once.
+// exp(x - max) is exp2(x * log2 e - max * log2 e), one FMA with the pair
+// element widened in the FMA, where |max| <= 256: the rounding of
+// max * log2 e adds at most |max| * 6e-8 relative error (<= 1.6e-5, 0.03 ulp
+// of f16); larger maxima take (x - max) * log2 e.  A pack past the row's
+// last kept key stores 0 * (1 / sum), computed once per row: +0, or NaN
+// where a NaN score made the sum NaN, as in the two-op composition.
+typedef half_t h2v __attribute__((ext_vector_type(2)));
+
+template <bool NEAR>
+__device__ inline float exp_arg(float x, float m, float mL) {
+    constexpr float kLog2e = 1.44269504088896340736f;
+    if constexpr (NEAR)
+        return fmaf(x, kLog2e, -mL);
+    else
+        return (x - m) * kLog2e;
+}
+
+// exp of the kept packs' scores (ev), and their sum; packs past the last
+// kept key are left unset (the store writes them without ev).
+template <int NV, bool NEAR>
+__device__ inline float exp_packs(const h2v (&s)[NV][4], float (&ev)[NV][8], float m,
+                                  uint32_t lane, uint32_t tpr, uint32_t kept) {
+    const float mL = m * 1.44269504088896340736f;
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        if ((lane + k * tpr) * 8 < kept) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = static_cast<float>(s[k][e / 2][e % 2]);
+                ev[k][e] = __builtin_amdgcn_exp2f(exp_arg<NEAR>(x, m, mL));
+                sum += ev[k][e];
+            }
+        }
+    }
+    return sum;
+}
+
+template <int NV, int TPR, bool MASK, bool RAGGED>
+__global__ __launch_bounds__(kThreads) void k_softmax_rows_h2(const half_t* __restrict__ in,
+                                                              half_t* __restrict__ out,
+                                                              uint32_t row_base, uint32_t rows,
+                                                              uint32_t width, MaskParams mp,
+                                                              h2v scale2) {
+    constexpr int N = 8;
+    typedef typename VecOf<half_t, N>::type V;
+    constexpr int RPB = kThreads / TPR;
+    __shared__ float lds_m[kThreads / kWave];
+    __shared__ float lds_s[kThreads / kWave];
+    const uint32_t lane = threadIdx.x % TPR;
+    const uint64_t row64 = uint64_t(row_base) + uint64_t(blockIdx.x) * RPB + threadIdx.x / TPR;
+    const bool active = row64 < rows;
+    const uint32_t row = uint32_t(row64);
+    const uint64_t e0 = uint64_t(active ? row : 0) * width;
+    const uint32_t n_packs = RAGGED ? (width + N - 1) / N : width / N;
+    const V* src = reinterpret_cast<const V*>(in + e0);
+    V* dst = reinterpret_cast<V*>(out + e0);
+    const uint32_t kept = !active ? 0u : MASK ? kept_keys(row, width, mp) : width;
+
+    // Loads as in k_softmax_rows: all issued first, packs past the last
+    // kept one reloading it (their values are replaced by -inf below).
+    V raw[NV];
+    {
+        const uint32_t live = (kept + N - 1) / N;
+        const uint32_t last = live > 0 ? live - 1 : 0u;
+        const uint64_t total = uint64_t(rows) * width;
+        bool moved[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const uint32_t p = lane + k * TPR;
+            const uint32_t q = p < last ? p : last;
+            if constexpr (RAGGED) {
+                const uint64_t off = e0 + uint64_t(q) * N;
+                moved[k] = off + N > total;  // the buffer's last pack
+                raw[k] = load_stream_u<half_t, N>(in + (moved[k] ? total - N : off));
+            } else {
+                raw[k] = load_stream(src + q);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (RAGGED) {
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                if (moved[k]) {
+                    const uint32_t p = lane + k * TPR;
+                    const uint32_t q = p < last ? p : last;
+#pragma unroll
+                    for (int j = 0; j < N; ++j)
+                        raw[k][j] = q * N + j < width ? in[e0 + q * N + j] : half_t(0.0f);
+                }
+            }
+        }
+    }
+
+    // Masked halves become -inf before the multiply (-inf * scale = -inf),
+    // so every operand of the max is a multiply's result: canonical, which
+    // spares the max its canonicalising of each operand.
+    const h2v ninf2 = {half_t(-INFINITY), half_t(-INFINITY)};
+    h2v s[NV][4];
+    h2v mx = ninf2;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t b = (lane + k * TPR) * N;  // the pack's first key
+        const bool none = b >= kept;
+        h2v r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = none ? ninf2 : h2v{raw[k][2 * j], raw[k][2 * j + 1]};
+        if (!none && b + N > kept) {  // the pack holding the row's last kept key
+#pragma unroll
+            for (int e = 0; e < N; ++e)
+                if (b + e >= kept) r[e / 2][e % 2] = half_t(-INFINITY);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s[k][j] = r[j] * scale2;
+            mx = __builtin_elementwise_max(mx, s[k][j]);
+        }
+    }
+    float m = fmaxf(static_cast<float>(mx[0]), static_cast<float>(mx[1]));
+    m = group_max<TPR>(m, lds_m);
+    // softmax.metal:166-173: an f16 row whose max is -inf is all zeros.
+    const bool zero_row = m == -INFINITY;
+    float ev[NV][8];
+    float sum = 0.0f;
+    if (!zero_row) {
+        if (fabsf(m) <= 256.0f)
+            sum = exp_packs<NV, true>(s, ev, m, lane, TPR, kept);
+        else
+            sum = exp_packs<NV, false>(s, ev, m, lane, TPR, kept);
+    }
+    sum = group_sum<TPR>(sum, lds_s);
+    const float inv = zero_row ? 0.0f : 1.0f / sum;
+    // A pack past the last kept key (or any pack of an all-zero row) holds
+    // 0 * (1 / sum) in every element: +0, or NaN where the sum is NaN or 0.
+    const half_t fill = from_float<half_t>(0.0f * inv);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const uint32_t p = lane + k * TPR;
+        if (!active || p >= n_packs) continue;
+        V o;
+        if (zero_row || p * N >= kept) {
+#pragma unroll
+            for (int e = 0; e < N; ++e) o[e] = fill;
+        } else {
+#pragma unroll
+            for (int e = 0; e < N; ++e) o[e] = from_float<half_t>(ev[k][e] * inv);
+        }
+        if constexpr (RAGGED) {
+            if (p * N + N <= width) {
+                store_stream_u<half_t, N>(out + e0 + uint64_t(p) * N, o);
+            } else {  // the row's partial last pack
+#pragma unroll
+                for (int e = 0; e < N; ++e)
+                    if (p * N + e < width) out[e0 + p * N + e] = o[e];
+            }
+        } else {
+            store_stream(dst + p, o);
+        }
+    }
+}
+
 // ------------------------------------- streaming rows of any width (2 reads)
 
 // Online merge of (max, sum of exp(x - max)) pairs.
@@ -348,7 +537,7 @@ __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ i
                     const uint32_t pj = p * N + j;
                     if (pj < lead || pj >= lead + width) continue;
                     const uint32_t x = pj - lead;
-                    out[e0 + x] = x < kept ? from_float<T>(to_float(raw[j]) * mp.scale)
+                    out[e0 + x] = x < kept ? scale_to<T>(raw[j], mp.scale)
                                            : from_float<T>(-INFINITY);
                 }
                 continue;
@@ -358,7 +547,7 @@ __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ i
                 V raw = load_stream(src + p);
 #pragma unroll
                 for (int j = 0; j < N; ++j)
-                    o[j] = (p * N + j < kept + lead) ? from_float<T>(to_float(raw[j]) * mp.scale)
+                    o[j] = (p * N + j < kept + lead) ? scale_to<T>(raw[j], mp.scale)
                                                      : from_float<T>(-INFINITY);
             } else {
 #pragma unroll
@@ -392,14 +581,30 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
     const bool ragged = width % N != 0;
     const uint64_t w_packs = ceil_div(width, N);
     const dim3 block(kThreads);
+    // f16 rows whose scale is an f16 value take the first pass on pairs
+    // (k_softmax_rows_h2); the plain softmax's scale is 1.
+    bool pairs = false;
+    h2v scale2 = {half_t(1.0f), half_t(1.0f)};
+    if constexpr (sizeof(T) == 2) {
+        const half_t hs = static_cast<half_t>(mp.scale);
+        pairs = static_cast<float>(hs) == mp.scale;
+        scale2 = h2v{hs, hs};
+    }
     // Row chunks of at most 2^30 blocks each (one launch for any real shape).
 #define RL_SOFTMAX_ROWS_R(NV, TPR, R)                                                            \
     do {                                                                                         \
         for (uint64_t base = 0; base < rows; base += (uint64_t(1) << 30) * (kThreads / TPR)) { \
             const uint64_t left = ceil_div(rows - base, kThreads / TPR);                         \
-            RL_LAUNCH(ctx, (k_softmax_rows<T, N, NV, TPR, MASK, R>),                             \
-                      dim3(unsigned(left < (uint64_t(1) << 30) ? left : (uint64_t(1) << 30))),   \
-                      block, in, out, uint32_t(base), r32, w32, mp);                             \
+            const dim3 grid(unsigned(left < (uint64_t(1) << 30) ? left : (uint64_t(1) << 30)));  \
+            if constexpr (sizeof(T) == 2) {                                                      \
+                if (pairs) {                                                                     \
+                    RL_LAUNCH(ctx, (k_softmax_rows_h2<NV, TPR, MASK, R>), grid, block, in, out,  \
+                              uint32_t(base), r32, w32, mp, scale2);                             \
+                    continue;                                                                    \
+                }                                                                                \
+            }                                                                                    \
+            RL_LAUNCH(ctx, (k_softmax_rows<T, N, NV, TPR, MASK, R>), grid, block, in, out,       \
+                      uint32_t(base), r32, w32, mp);                                             \
         }                                                                                        \
     } while (0)
 #define RL_SOFTMAX_ROWS(NV, TPR)                    \

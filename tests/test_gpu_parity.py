@@ -422,6 +422,48 @@ def test_scale_mask_and_fused_softmax(ctx, dtype, shape, start):
     check_float(got2, ref, f"unfused {shape}")
 
 
+SCALES = [0.125, 1.0 / np.sqrt(80.0), 0.3, 1.0 / 3.0, 2.0, 1.0]
+
+
+@pytest.mark.parametrize("scale", SCALES)
+def test_scale_mask_f16_every_half(ctx, scale):
+    """f16 scale/mask over all 65,536 halves (+-0, subnormals, +-inf, NaN) in
+    one decode row (every key kept), bit-exact against the oracle's f32
+    product rounded to f16 -- for scales that are f16 values (1/8, 2, 1) and
+    scales that are not (1/sqrt(80), 0.3, 1/3), where the f32 product's own
+    rounding matters."""
+    xh = np.arange(65536, dtype=np.uint16).view(np.float16).reshape(1, 1, 65536)
+    d = ctx.upload(xh)
+    got = run(ctx, lambda: ctx.scale_mask(d, float(np.float32(scale)), 65535)).numpy()
+    assert_bitexact(got, o.scale_mask(xh, float(np.float32(scale)), 65535), f"scale {scale}")
+
+
+@pytest.mark.parametrize("scale", SCALES)
+@pytest.mark.parametrize("shape,start", [((4, 64, 1000), 936), ((15, 256, 4096), 3840),
+                                         ((3, 33, 4093), 100), ((2, 16, 512), 0)])
+def test_fused_softmax_f16_scales(ctx, scale, shape, start):
+    """Fused causal scale/mask + softmax in f16 at scales that are f16 values
+    (the launch that scales pairs of halves) and scales that are not (the
+    element-wise launch), on N(0, 2) scores with -0.0, +-inf and NaN planted
+    in a few rows: within 2 ulp of the oracle, masked entries exactly 0, NaN
+    and zero rows where the oracle has them."""
+    x = norm(("fused-scales", start), shape, np.float16, 0.0, 2.0)
+    flat = x.reshape(-1, shape[-1])
+    flat[1, :7] = -0.0
+    flat[2, 3] = np.inf
+    flat[3, 0] = np.nan
+    flat[4, :] = -np.inf
+    flat[5, 2] = -np.inf
+    s = float(np.float32(scale))
+    got = run(ctx, lambda: ctx.attention_softmax(ctx.upload(x), s, start)).numpy()
+    ref = o.attention_softmax(x, s, start)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan), "NaN positions"
+    assert np.array_equal(got[~nan] == 0, ref[~nan] == 0), "zero positions"
+    check_float(np.where(nan, 0, got).astype(np.float16), np.where(nan, 0, ref).astype(np.float16),
+                f"fused softmax f16 scale {scale} {shape}")
+
+
 def test_scale_mask_reference_kats(ctx):
     kat = K["scale_mask_prefill"]
     x = np.array(kat["input"], np.float32).reshape(kat["shape"])
