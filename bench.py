@@ -718,6 +718,15 @@ class LayerChain:
             stage["repeat_kv_v"] = (kvh + qh) * tok * hd * 2
         self.stage_bytes = stage
         self.nbytes = sum(stage.values())
+        # (bytes read, bytes written) of each launch of the 5-launch chain
+        q, kv = qh * tok * hd * 2, kvh * tok * hd * 2
+        self.stage_rw = {
+            "rmsnorm": (tok * hid * 2 + hid * 2, tok * hid * 2),
+            "prologue": (q + 2 * kv + table, q + 2 * kv + 2 * (qh // kvh) * kv),
+            "softmax": (unmasked * 2, n_scores * 2),
+            "swiglu": (2 * tok * ffn * 2, tok * ffn * 2),
+            "residual_add": (2 * tok * hid * 2, tok * hid * 2),
+        }
         self._scores = None
 
     def scores(self):
@@ -816,6 +825,28 @@ def time_chain_graphs(ctx, chain, sets, steps, warmup):
     ms = time_graphs(ctx, graphs, 1, steps, warmup=warmup)
     ctx.finish()
     return ms
+
+
+PROBE = os.path.join(ROOT, "rustllm_amd", "hbm_probe")
+
+
+def probe_streams(pairs, timeout=120):
+    """Back-to-back us per launch of a plain streaming kernel moving each
+    (read, write) byte pair (rustllm_amd/hbm_probe, a process of its own),
+    or None if the probe is missing or fails."""
+    if not os.path.exists(PROBE):
+        log(f"{PROBE} is missing (python -m rustllm_amd.build builds it)")
+        return None
+    try:
+        res = subprocess.run([PROBE] + [f"{r}:{w}" for r, w in pairs], capture_output=True,
+                             text=True, timeout=timeout)
+    except subprocess.TimeoutExpired:
+        log("hbm_probe timed out")
+        return None
+    if res.returncode != 0:
+        log(f"hbm_probe failed ({res.returncode}): {res.stderr.strip()[-300:]}")
+        return None
+    return [c["us"] for c in json.loads(res.stdout)["cases"]]
 
 
 def oracle_chain(o, chain, host):
@@ -1232,6 +1263,15 @@ def main():
     chain.launch(csets[0])  # set 0 holds the 5-launch chain's outputs again
     ctx.finish()
 
+    # What HBM allows for the same bytes: a plain streaming kernel per stage
+    probe_us = probe_streams(list(chain.stage_rw.values()))
+    attain = None
+    if probe_us is not None:
+        attain = dict(zip(chain.stage_rw, probe_us))
+        log("  a plain streaming kernel moving each stage's bytes (back to back): " +
+            ", ".join(f"{k} {v:.2f} us" for k, v in attain.items()) +
+            f"; {sum(probe_us):.2f} us in all")
+
     threads = cpu_threads()
     o = _oracle()
     cpu = None
@@ -1320,6 +1360,12 @@ def main():
                 "frac": round(sm_gbs / PEAK_GBS, 4), "traffic": sm_traffic,
                 "bytes_per_launch": chain.softmax_bytes, "us_per_launch": round(sm_mean, 3),
                 "launches_timed": len(sm_us), "share_of_step": round(sm_mean / (ms_step * 1e3), 3)}
+    if attain is not None:
+        # the same bytes moved by a plain streaming kernel, back to back
+        roofline["attainable_us"] = round(attain["softmax"], 3)
+        roofline["attainable_GBps"] = round(chain.softmax_bytes / (attain["softmax"] * 1e-6) / 1e9,
+                                            1)
+        roofline["frac_of_attainable"] = round(attain["softmax"] / sm_mean, 4)
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -1342,6 +1388,10 @@ def main():
                    "timing": "eager launches on one stream, events around the K steps",
                    "graph_replay_ms_per_step": None if ms_graph is None else round(ms_graph, 5),
                    "eight_launch_ms_per_step": round(ms_split, 5),
+                   "attainable_ms_per_step": (None if attain is None
+                                              else round(sum(attain.values()) * 1e-3, 5)),
+                   "attainable_by_stage_us": (None if attain is None else
+                                              {k: round(v, 2) for k, v in attain.items()}),
                    "outputs_match_oracle": not bad},
         "pct_of_peak": round(100 * value / PEAK_GBS, 1),
         "roofline": roofline,

@@ -24,6 +24,7 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "librustllm_hip.so")
 HOST_LIB = os.path.join(PKG, "librustllm_tensor.so")
 CPP_TESTS = os.path.join(ROOT, "tests", "cpp", "tensor_tests.bin")
+PROBE = os.path.join(PKG, "hbm_probe")
 
 ARCH = "gfx950"
 HIP_SOURCES = ["runtime.hip", "elementwise.hip", "movement.hip", "rmsnorm.hip", "softmax.hip",
@@ -97,9 +98,19 @@ def build_host() -> str | None:
     return HOST_LIB
 
 
+def build_probe() -> str:
+    """The HBM streaming probe the bench compares each kernel with
+    (rustllm_amd/hbm_probe, a plain executable: no library, no Python)."""
+    tmp = PROBE + ".tmp"
+    _run([hipcc(), *hip_flags(), "-o", tmp, os.path.join(CSRC, "hbm_probe.hip")])
+    os.replace(tmp, PROBE)
+    return PROBE
+
+
 def build_all() -> None:
     build_hip()
     build_host()
+    build_probe()
 
 
 if __name__ == "__main__":
