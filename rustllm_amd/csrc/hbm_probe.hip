@@ -2,17 +2,20 @@
 //
 //     hbm_probe READ_BYTES:WRITE_BYTES [...]
 //
-// For each pair, one plain streaming kernel that reads READ_BYTES (one
-// stream, non-temporal 16-byte loads) and writes WRITE_BYTES (one stream,
-// non-temporal 16-byte stores).  Both streams are spread evenly over the
-// grid: block b reads and writes its proportional, contiguous share of each
-// stream (as a row kernel does), with up to four 16-byte packs per thread
-// and stream, every load issued before the first store.  It is timed as 40
-// back-to-back launches over windows of a 4 GiB pool (so that no launch
-// reuses what the 256 MB Infinity Cache holds from the previous ones), best
-// of 3, and as single launches bracketed by events.  Prints one JSON object:
-// {"cases": [{"read": R, "write": W, "us": back-to-back us per launch,
-// "us_one": one launch}, ...]}.
+// For each pair, plain streaming kernels that read READ_BYTES (one stream,
+// non-temporal 16-byte loads) and write WRITE_BYTES (one stream,
+// non-temporal 16-byte stores), four 16-byte packs per thread and stream,
+// every load issued before the first store, in two layouts:
+//  * phased: thread pack i is loaded if i < reads and stored if i < writes,
+//    so the blocks past the shorter stream's end move one stream only;
+//  * interleaved: block b moves its proportional, contiguous share of each
+//    stream (as a row kernel does).
+// Each is timed as 40 back-to-back launches over windows of a 4 GiB pool
+// (so that no launch reuses what the 256 MB Infinity Cache holds from the
+// previous ones), best of 3, and as single launches bracketed by events.
+// Prints one JSON object: {"cases": [{"read": R, "write": W, "us": the
+// faster layout's back-to-back us per launch, "us_phased": ..,
+// "us_interleaved": .., "us_one": one launch of the faster}, ...]}.
 //
 // The bench compares each kernel of the layer chain with this probe at the
 // kernel's own read and write bytes: the probe does no arithmetic and no
@@ -32,26 +35,46 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kUnroll = 4;
 
-// Block b of nb covers slots [b * S, (b + 1) * S) of the longer stream
-// (S = kThreads * kUnroll) and the matching share of the other:
-// packs [first(b), first(b + 1)) with first(b) = b * S * n / n_max.
-__device__ inline uint64_t share_first(uint64_t b, uint64_t n, uint64_t n_max) {
-    return (b * kThreads * kUnroll * n) / n_max;
-}
-
-__global__ __launch_bounds__(kThreads) void k_stream(const f4* __restrict__ src,
+__global__ __launch_bounds__(kThreads) void k_phased(const f4* __restrict__ src,
                                                      f4* __restrict__ dst, uint64_t n_read,
                                                      uint64_t n_write) {
-    const uint64_t n_max = n_read > n_write ? n_read : n_write;
+    const uint64_t base = uint64_t(blockIdx.x) * kThreads * kUnroll + threadIdx.x;
+    f4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint64_t i = base + uint64_t(u) * kThreads;
+        v[u] = i < n_read ? __builtin_nontemporal_load(src + i) : f4{1.0f, 2.0f, 3.0f, 4.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint64_t i = base + uint64_t(u) * kThreads;
+        if (i < n_write) __builtin_nontemporal_store(v[u], dst + i);
+    }
+}
+
+// Block b covers slots [b * S, (b + 1) * S) of the longer stream
+// (S = kThreads * kUnroll) and packs [first(b), first(b + 1)) of each stream
+// of n packs, first(b) = floor(b * S * (n / n_max)) (the ratio in double,
+// the last block ending at n); a share is at most S packs.
+__device__ inline uint64_t share_first(uint64_t b, double ratio, uint64_t n) {
+    if (b >= gridDim.x) return n;
+    const uint64_t f = uint64_t(double(b * kThreads * kUnroll) * ratio);
+    return f < n ? f : n;
+}
+
+__global__ __launch_bounds__(kThreads) void k_interleaved(const f4* __restrict__ src,
+                                                          f4* __restrict__ dst, uint64_t n_read,
+                                                          uint64_t n_write, double r_ratio,
+                                                          double w_ratio) {
     const uint64_t b = blockIdx.x;
-    const uint64_t r0 = share_first(b, n_read, n_max), r1 = share_first(b + 1, n_read, n_max);
-    const uint64_t w0 = share_first(b, n_write, n_max), w1 = share_first(b + 1, n_write, n_max);
-    const uint64_t r_end = r1 < n_read ? r1 : n_read, w_end = w1 < n_write ? w1 : n_write;
+    const uint64_t r0 = share_first(b, r_ratio, n_read), r1 = share_first(b + 1, r_ratio, n_read);
+    const uint64_t w0 = share_first(b, w_ratio, n_write);
+    const uint64_t w1 = share_first(b + 1, w_ratio, n_write);
     f4 v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
         const uint64_t i = r0 + uint64_t(u) * kThreads + threadIdx.x;
-        v[u] = i < r_end ? __builtin_nontemporal_load(src + i) : f4{1.0f, 2.0f, 3.0f, 4.0f};
+        v[u] = i < r1 ? __builtin_nontemporal_load(src + i) : f4{1.0f, 2.0f, 3.0f, 4.0f};
     }
     f4 acc = v[0];
 #pragma unroll
@@ -59,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void k_stream(const f4* __restrict__ src,
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
         const uint64_t i = w0 + uint64_t(u) * kThreads + threadIdx.x;
-        if (i < w_end) __builtin_nontemporal_store(acc + float(u), dst + i);
+        if (i < w1) __builtin_nontemporal_store(acc + float(u), dst + i);
     }
 }
 
@@ -74,7 +97,7 @@ bool ok(hipError_t e, const char* what) {
 int main(int argc, char** argv) {
     struct Case {
         uint64_t read, write;
-        double us = 0, us_one = 0;
+        double us = 0, us_one = 0, us_phased = 0, us_interleaved = 0;
     };
     std::vector<Case> cases;
     for (int a = 1; a < argc; ++a) {
@@ -112,43 +135,57 @@ int main(int argc, char** argv) {
         if (windows > 64) windows = 64;
         const unsigned grid = unsigned((n + uint64_t(kThreads) * kUnroll - 1) /
                                        (uint64_t(kThreads) * kUnroll));
-        auto launch = [&](uint64_t i) {
-            char* w = pool + (i % windows) * window;
-            hipLaunchKernelGGL(k_stream, dim3(grid), dim3(kThreads), 0, 0,
-                               reinterpret_cast<const f4*>(w), reinterpret_cast<f4*>(w + rbytes),
-                               n_read, n_write);
-        };
-        for (uint64_t i = 0; i < windows; ++i) launch(i);
-        if (!ok(hipDeviceSynchronize(), "warm-up")) return 1;
-        float best = 1e30f;
-        constexpr int kReps = 40;
-        for (int rep = 0; rep < 3; ++rep) {
-            if (!ok(hipEventRecord(e0, 0), "event")) return 1;
-            for (int i = 0; i < kReps; ++i) launch(uint64_t(rep) * kReps + i);
-            if (!ok(hipEventRecord(e1, 0), "event") || !ok(hipEventSynchronize(e1), "timing"))
-                return 1;
-            float ms = 0;
-            if (!ok(hipEventElapsedTime(&ms, e0, e1), "elapsed")) return 1;
-            best = ms < best ? ms : best;
+        const double r_ratio = double(n_read) / double(n), w_ratio = double(n_write) / double(n);
+        for (int layout = 0; layout < 2; ++layout) {
+            auto launch = [&](uint64_t i) {
+                char* w = pool + (i % windows) * window;
+                const f4* src = reinterpret_cast<const f4*>(w);
+                f4* dst = reinterpret_cast<f4*>(w + rbytes);
+                if (layout == 0)
+                    hipLaunchKernelGGL(k_phased, dim3(grid), dim3(kThreads), 0, 0, src, dst,
+                                       n_read, n_write);
+                else
+                    hipLaunchKernelGGL(k_interleaved, dim3(grid), dim3(kThreads), 0, 0, src, dst,
+                                       n_read, n_write, r_ratio, w_ratio);
+            };
+            for (uint64_t i = 0; i < windows; ++i) launch(i);
+            if (!ok(hipDeviceSynchronize(), "warm-up")) return 1;
+            float best = 1e30f;
+            constexpr int kReps = 40;
+            for (int rep = 0; rep < 3; ++rep) {
+                if (!ok(hipEventRecord(e0, 0), "event")) return 1;
+                for (int i = 0; i < kReps; ++i) launch(uint64_t(rep) * kReps + i);
+                if (!ok(hipEventRecord(e1, 0), "event") || !ok(hipEventSynchronize(e1), "timing"))
+                    return 1;
+                float ms = 0;
+                if (!ok(hipEventElapsedTime(&ms, e0, e1), "elapsed")) return 1;
+                best = ms < best ? ms : best;
+            }
+            double one = 0;
+            for (int i = 0; i < 10; ++i) {
+                if (!ok(hipEventRecord(e0, 0), "event")) return 1;
+                launch(uint64_t(i) * 7);
+                if (!ok(hipEventRecord(e1, 0), "event") || !ok(hipEventSynchronize(e1), "timing"))
+                    return 1;
+                float ms = 0;
+                if (!ok(hipEventElapsedTime(&ms, e0, e1), "elapsed")) return 1;
+                one += ms * 1e3 / 10;
+            }
+            const double us = best * 1e3 / kReps;
+            (layout == 0 ? c.us_phased : c.us_interleaved) = us;
+            if (layout == 0 || us < c.us) {
+                c.us = us;
+                c.us_one = one;
+            }
         }
-        c.us = best * 1e3 / kReps;
-        double one = 0;
-        for (int i = 0; i < 10; ++i) {
-            if (!ok(hipEventRecord(e0, 0), "event")) return 1;
-            launch(uint64_t(i) * 7);
-            if (!ok(hipEventRecord(e1, 0), "event") || !ok(hipEventSynchronize(e1), "timing"))
-                return 1;
-            float ms = 0;
-            if (!ok(hipEventElapsedTime(&ms, e0, e1), "elapsed")) return 1;
-            one += ms * 1e3 / 10;
-        }
-        c.us_one = one;
     }
     printf("{\"cases\": [");
     for (size_t i = 0; i < cases.size(); ++i)
-        printf("%s{\"read\": %llu, \"write\": %llu, \"us\": %.3f, \"us_one\": %.3f}", i ? ", " : "",
-               (unsigned long long)cases[i].read, (unsigned long long)cases[i].write, cases[i].us,
-               cases[i].us_one);
+        printf("%s{\"read\": %llu, \"write\": %llu, \"us\": %.3f, \"us_phased\": %.3f, "
+               "\"us_interleaved\": %.3f, \"us_one\": %.3f}",
+               i ? ", " : "", (unsigned long long)cases[i].read,
+               (unsigned long long)cases[i].write, cases[i].us, cases[i].us_phased,
+               cases[i].us_interleaved, cases[i].us_one);
     printf("]}\n");
     return ok(hipFree(pool), "hipFree") ? 0 : 1;
 }

@@ -145,17 +145,19 @@ __device__ inline int partner_dword(int v) {
         return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);  // row_ror:8
 }
 
-// decode_row over all kMaxJobRank dims with no branch, so the scalar loads of
-// every dim go out together.  Dims past rd.rank are make_row_dims' zero
-// initialisation -- divisor 1, stride 0, group multiplier 0 -- and leave the
-// row, the offset and the group as they are.
-__device__ inline void decode_job_row(const RowDimsN<kMaxJobRank>& rd, uint32_t row,
-                                      uint64_t& src_off, uint32_t& position, uint32_t& group) {
+// decode_row over the first R row dims with no branch, so the scalar loads
+// of every dim go out together (the views of a launch have at most R row
+// dims; R = kMaxJobRank decodes any job).  Dims past rd.rank are
+// make_row_dims' zero initialisation -- divisor 1, stride 0, group
+// multiplier 0 -- and leave the row, the offset and the group as they are.
+template <int R>
+__device__ inline void decode_job_row_r(const RowDimsN<kMaxJobRank>& rd, uint32_t row,
+                                        uint64_t& src_off, uint32_t& position, uint32_t& group) {
     src_off = 0;
     position = 0;
     group = 0;
 #pragma unroll
-    for (uint32_t d = 0; d < uint32_t(kMaxJobRank); ++d) {
+    for (uint32_t d = 0; d < uint32_t(R); ++d) {
         uint32_t q, r;
         rd.dim[d].divmod(row, q, r);
         src_off += uint64_t(r) * rd.stride[d];
@@ -167,8 +169,14 @@ __device__ inline void decode_job_row(const RowDimsN<kMaxJobRank>& rd, uint32_t 
 
 // U rows per lane group: the group takes rows first + u * kRows (u < U) of
 // its block's kRows * U and issues every row's loads before any arithmetic,
-// so a wave has U rows' loads in flight.
-template <typename T, int L, int U>
+// so a wave has U rows' loads in flight.  A lane and its rotation partner
+// need the same cos and sin values: the first-half lane loads cos, the
+// second-half lane sin, and each takes the other's over the same DPP move
+// as the data (half the table loads, which on the [1, 25, 4096, 64]
+// prologue outnumbered the data loads four to one).  A block belongs to one
+// job, so a copy job branches around the rotation without divergence.
+// R: row dims decoded (3 when every job of the launch has at most 3).
+template <typename T, int L, int U, int R>
 __global__ __launch_bounds__(kThreads) void k_rope_blocks(RowJobs jobs,
                                                           const float* __restrict__ cos_table,
                                                           const float* __restrict__ sin_table,
@@ -188,8 +196,10 @@ __global__ __launch_bounds__(kThreads) void k_rope_blocks(RowJobs jobs,
     const uint32_t lane = threadIdx.x % L;
     const uint32_t pack = (L == 8 && lane >= 4) ? 11 - lane : lane;
     const uint32_t pair = (pack % (L / 2)) * N;
+    const bool first_half = pack < uint32_t(L / 2);
+    const float* own_table = first_half ? cos_table : sin_table;
     V x[U];
-    VF c[U], s[U];
+    VF tab[U];  // cos (first half) or sin (second half)
     uint32_t pos[U], group[U];
     bool live[U];
 #pragma unroll
@@ -198,37 +208,44 @@ __global__ __launch_bounds__(kThreads) void k_rope_blocks(RowJobs jobs,
         live[u] = row < job.n_rows;
         if (!live[u]) row = job.n_rows - 1;  // a valid row: every lane takes part in the DPP moves
         uint64_t src_off;
-        decode_job_row(job.rows, row, src_off, pos[u], group[u]);
-        // The three loads go out back to back.  A copy job reads table row 0
+        decode_job_row_r<R>(job.rows, row, src_off, pos[u], group[u]);
+        // The loads go out back to back.  A copy job reads table row 0
         // (valid for every job here) and ignores it, which keeps them
         // branch-free.
         const uint64_t t = rotate ? uint64_t(start + pos[u]) * kHalf + pair : pair;
-        c[u] = *reinterpret_cast<const VF*>(cos_table + t);
-        s[u] = *reinterpret_cast<const VF*>(sin_table + t);
+        tab[u] = *reinterpret_cast<const VF*>(own_table + t);
         x[u] = load_stream(reinterpret_cast<const V*>(static_cast<const T*>(job.src) + src_off +
                                                       pack * N));
     }
-    const bool first_half = pack < uint32_t(L / 2);
+    __builtin_amdgcn_sched_barrier(0);  // every load ahead of the first wait
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        // The rotation is computed for copy jobs too and then not used: a
-        // branch around it would let the compiler sink the table loads into
-        // it, behind a wait for x.
-        int w[4], m[4];
-        __builtin_memcpy(w, &x[u], 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) m[i] = partner_dword<L>(w[i]);
-        V other;
-        __builtin_memcpy(&other, m, 16);
-        // First half: first*c - second*s; second half: second*c + first*s.
-        // Negating the partner is exact, so each result keeps the
-        // reference's two rounded products and one rounded sum.
         V o;
+        if (!rotate) {
+            o = x[u];
+        } else {
+            int tv[N], pv[N], w[4], m[4];
+            __builtin_memcpy(tv, &tab[u], sizeof(VF));
 #pragma unroll
-        for (int j = 0; j < N; ++j) {
-            const float own = to_float(x[u][j]);
-            const float partner = first_half ? -to_float(other[j]) : to_float(other[j]);
-            o[j] = rotate ? from_float<T>(own * c[u][j] + partner * s[u][j]) : x[u][j];
+            for (int i = 0; i < N; ++i) pv[i] = partner_dword<L>(tv[i]);
+            __builtin_memcpy(w, &x[u], 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) m[i] = partner_dword<L>(w[i]);
+            VF ptab;
+            V other;
+            __builtin_memcpy(&ptab, pv, sizeof(VF));
+            __builtin_memcpy(&other, m, 16);
+            const VF c = first_half ? tab[u] : ptab;
+            const VF s = first_half ? ptab : tab[u];
+            // First half: first*c - second*s; second half: second*c + first*s.
+            // Negating the partner is exact, so each result keeps the
+            // reference's two rounded products and one rounded sum.
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                const float own = to_float(x[u][j]);
+                const float partner = first_half ? -to_float(other[j]) : to_float(other[j]);
+                o[j] = from_float<T>(own * c[j] + partner * s[j]);
+            }
         }
         if (!live[u]) continue;
         if (job.dst) {
@@ -294,15 +311,24 @@ inline int rows_per_group(const rl_context* ctx, uint64_t total_rows, int lanes)
     return waves > uint64_t(8) * 4 * uint64_t(ctx->num_cus) ? 2 : 1;
 }
 
-template <typename T, int L>
-void launch_rows(rl_context* ctx, int unroll, dim3 grid, const RowJobs& jobs,
-                 const float* cos_table, const float* sin_table, uint32_t start) {
+template <typename T, int L, int R>
+void launch_rows_r(rl_context* ctx, int unroll, dim3 grid, const RowJobs& jobs,
+                   const float* cos_table, const float* sin_table, uint32_t start) {
     if (unroll == 2)
-        RL_LAUNCH(ctx, (k_rope_blocks<T, L, 2>), grid, dim3(kThreads), jobs, cos_table,
+        RL_LAUNCH(ctx, (k_rope_blocks<T, L, 2, R>), grid, dim3(kThreads), jobs, cos_table,
                   sin_table, start);
     else
-        RL_LAUNCH(ctx, (k_rope_blocks<T, L, 1>), grid, dim3(kThreads), jobs, cos_table,
+        RL_LAUNCH(ctx, (k_rope_blocks<T, L, 1, R>), grid, dim3(kThreads), jobs, cos_table,
                   sin_table, start);
+}
+
+template <typename T, int L>
+void launch_rows(rl_context* ctx, int unroll, bool rank3, dim3 grid, const RowJobs& jobs,
+                 const float* cos_table, const float* sin_table, uint32_t start) {
+    if (rank3)
+        launch_rows_r<T, L, 3>(ctx, unroll, grid, jobs, cos_table, sin_table, start);
+    else
+        launch_rows_r<T, L, kMaxJobRank>(ctx, unroll, grid, jobs, cos_table, sin_table, start);
 }
 
 // Assigns first blocks to jobs[0 .. n) (jobs with no rows get none) and
@@ -311,7 +337,11 @@ template <typename T>
 bool launch_jobs(rl_context* ctx, RowJobs& jobs, int n, int lanes, const float* cos_table,
                  const float* sin_table, uint64_t start) {
     uint64_t total_rows = 0;
-    for (int t = 0; t < n; ++t) total_rows += jobs.job[t].n_rows;
+    bool rank3 = true;  // every job's view has at most 3 row dims
+    for (int t = 0; t < n; ++t) {
+        total_rows += jobs.job[t].n_rows;
+        rank3 = rank3 && jobs.job[t].rows.rank <= 3;
+    }
     const int unroll = rows_per_group(ctx, total_rows, lanes);
     const uint64_t rows_per_block = uint64_t(kThreads) / lanes * unroll;
     uint64_t blocks = 0;
@@ -329,10 +359,10 @@ bool launch_jobs(rl_context* ctx, RowJobs& jobs, int n, int lanes, const float* 
     const dim3 grid(static_cast<unsigned>(blocks));
     const uint32_t s32 = uint32_t(start);
     switch (lanes) {
-        case 2: launch_rows<T, 2>(ctx, unroll, grid, jobs, cos_table, sin_table, s32); break;
-        case 4: launch_rows<T, 4>(ctx, unroll, grid, jobs, cos_table, sin_table, s32); break;
-        case 8: launch_rows<T, 8>(ctx, unroll, grid, jobs, cos_table, sin_table, s32); break;
-        default: launch_rows<T, 16>(ctx, unroll, grid, jobs, cos_table, sin_table, s32); break;
+        case 2: launch_rows<T, 2>(ctx, unroll, rank3, grid, jobs, cos_table, sin_table, s32); break;
+        case 4: launch_rows<T, 4>(ctx, unroll, rank3, grid, jobs, cos_table, sin_table, s32); break;
+        case 8: launch_rows<T, 8>(ctx, unroll, rank3, grid, jobs, cos_table, sin_table, s32); break;
+        default: launch_rows<T, 16>(ctx, unroll, rank3, grid, jobs, cos_table, sin_table, s32); break;
     }
     return true;
 }
