@@ -1227,6 +1227,21 @@ __device__ inline float rows4_sum(float v) {
     return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
+// Chunk swizzle of the decode's value stage (rows of D halves, 16-byte
+// chunks): with chunk c of row r at c ^ stage_swizzle<D>(r), the stage
+// writes (16 lanes, 16 bytes each, per LDS cycle) and the transpose reads
+// (32 lanes, 8 bytes each: rows 8 g + j, four lanes a row) fall on 64
+// distinct 4-byte banks; unswizzled, the reads met 4 (D 64) or 8 (D 128)
+// lanes a bank.  Row bits 2 and 5 are not used, so rows + 4 and + 32 share
+// a row's swizzle.
+template <int D>
+__device__ inline uint32_t stage_swizzle(uint32_t r) {
+    if constexpr (D == 64)
+        return (r & 2u) | ((r >> 1) & 4u);
+    else
+        return ((r & 3u) << 1) | (r & 8u);
+}
+
 template <int D>
 __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split_mfma(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
@@ -1336,24 +1351,31 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_attention_split_mfma(
         }
     lsum = rows4_sum(lsum);
 
-    // the value rows to the wave's LDS stage (read by this wave only: no barrier)
+    // the value rows to the wave's LDS stage (read by this wave only: no
+    // barrier), 16-byte chunk c of row r at chunk c ^ stage_swizzle<D>(r)
     half_t* stage = vstage[wave];
 #pragma unroll
-    for (int i = 0; i < D / 8; ++i) *reinterpret_cast<h8*>(stage + (64 * i + lane) * 8) = vf[i];
+    for (int i = 0; i < D / 8; ++i) {
+        const uint32_t c = 64 * i + lane, row = c / (D / 8), ch = c % (D / 8);
+        *reinterpret_cast<h8*>(stage + row * D + (ch ^ stage_swizzle<D>(row)) * 8) = vf[i];
+    }
     // P V: lane 16 g + 4 j + a reads 4 elements of value rows 32 t + 8 g + j
-    // and + 4, columns 16 nt + 4 a; the transpose hands lane 16 g + i column
-    // 16 nt + i of those eight rows
+    // and + 4, columns 16 nt + 4 a (chunk 2 nt + a / 2, swizzled by the row;
+    // rows 32 t + 8 g + j + 4 h share the swizzle of row 8 g + j); the
+    // transpose hands lane 16 g + i column 16 nt + i of those eight rows
     f32x4 o[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) o[nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const half_t* tr = stage + (8 * g + lr / 4) * D + 4 * (lr % 4);
+    const uint32_t vrow = 8 * g + lr / 4;
+    const uint32_t vsw = stage_swizzle<D>(vrow);
+    const half_t* tr = stage + vrow * D + 4 * (lr % 2);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const h8 a = {ph[2 * t][0],     ph[2 * t][1],     ph[2 * t][2],     ph[2 * t][3],
                       ph[2 * t + 1][0], ph[2 * t + 1][1], ph[2 * t + 1][2], ph[2 * t + 1][3]};
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            const half_t* src = tr + 32 * t * D + 16 * nt;
+            const half_t* src = tr + 32 * t * D + ((2 * nt + (lr % 4) / 2) ^ vsw) * 8;
             const h4 lo = lds_read_transposed(src);
             const h4 hi = lds_read_transposed(src + 4 * D);
             const h8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
