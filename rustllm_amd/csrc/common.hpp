@@ -65,7 +65,7 @@ struct FusedOp {
     uint64_t head_packs = 0;  // repeat_kv
     uint32_t repeats = 0;
     bool small_index = false;
-    uint32_t outer_rank = 0;  // row gather: outer dims, innermost first
+    uint32_t outer_rank = 0;  // row gather / scatter: outer dims, innermost first
     uint32_t outer_dim[4] = {1, 1, 1, 1};
     uint32_t outer_stride[4] = {0, 0, 0, 0};
     uintptr_t read[2][2] = {{0, 0}, {0, 0}};  // [begin, end) of each input
@@ -80,6 +80,7 @@ enum FusedKind : uint32_t {
     kFusedAddF16, kFusedMulF16, kFusedSiluF16, kFusedSwigluF16,
     kFusedCastF32F16, kFusedCastF16F32, kFusedBiasF32, kFusedBiasF16,
     kFusedGatherF32, kFusedGatherF16, kFusedRepeatF32, kFusedRepeatF16,
+    kFusedScatterF32, kFusedScatterF16,  // row copies walked in source order
 };
 
 }  // namespace rl

@@ -370,7 +370,7 @@ struct FusedSeg {
     FastDiv div;          // packs per row (bias add, row gather) or per head (repeat_kv)
     uint32_t repeats;     // repeat_kv
     uint32_t small_index;
-    FusedDims outer;      // row gather
+    FusedDims outer;      // row gather / scatter
 };
 struct FusedTable {
     uint32_t first[kMaxFused];  // each op's first block in the fused grid (ascending)
@@ -424,6 +424,13 @@ __device__ inline void fused_gather(const FusedSeg& s, uint32_t blk, uint32_t nb
 }
 
 template <typename T>
+__device__ inline void fused_scatter(const FusedSeg& s, uint32_t blk, uint32_t nblk) {
+    scatter_rows_body<T, 16 / sizeof(T), kMoveUnroll, sizeof(T) == 2>(
+        static_cast<const T*>(s.a), static_cast<T*>(s.out), uint32_t(s.n_packs), s.div, s.outer,
+        blk, nblk);
+}
+
+template <typename T>
 __device__ inline void fused_repeat(const FusedSeg& s, uint32_t blk, uint32_t nblk) {
     repeat_kv_body<T, 16 / sizeof(T), kMoveUnroll>(static_cast<const T*>(s.a),
                                                    static_cast<T*>(s.out), s.n_packs, s.head_packs,
@@ -457,6 +464,8 @@ __global__ __launch_bounds__(kThreads) void k_fused(FusedTable t) {
         case kFusedGatherF16: fused_gather<half_t>(s, blk, nblk); break;
         case kFusedRepeatF32: fused_repeat<float>(s, blk, nblk); break;
         case kFusedRepeatF16: fused_repeat<half_t>(s, blk, nblk); break;
+        case kFusedScatterF32: fused_scatter<float>(s, blk, nblk); break;
+        case kFusedScatterF16: fused_scatter<half_t>(s, blk, nblk); break;
         default: break;
     }
 }

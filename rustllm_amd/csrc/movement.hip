@@ -6,11 +6,15 @@
 // the copy is a gather of rows: each row's source offset is decoded once per
 // 16-byte pack with 32-bit multiply-high division, and rows move as whole
 // packs, so every wave load covers runs of at least one row (256 B for a
-// 64-wide f32 head).  Anything else falls back to a per-element gather.
+// 64-wide f32 head).  A view that permutes a dense tensor (a transpose of
+// head and sequence dims) is walked in source order instead: contiguous
+// loads, each row stored whole at its output position.  Anything else falls
+// back to a per-element gather.
 //
 // repeat_kv: each thread reads one pack of the KV input once and writes it
 // to the `repeats` query heads that share it, so HBM sees the minimum
 // traffic (input once + output once).
+#include <algorithm>
 #include <type_traits>
 #include <vector>
 
@@ -29,6 +33,16 @@ __global__ __launch_bounds__(kThreads) void k_gather_rows(const T* __restrict__ 
                                                           T* __restrict__ dst, uint32_t n_packs,
                                                           FastDiv row_packs, OuterDims outer) {
     gather_rows_body<T, N, UNROLL>(src, dst, n_packs, row_packs, outer, blockIdx.x, gridDim.x);
+}
+
+// The row copy walked in source order (a view that permutes a dense tensor):
+// `outer` = the source's row dims, fastest first, with their output strides.
+template <typename T, int N, int UNROLL, bool NT_STORE>
+__global__ __launch_bounds__(kThreads) void k_scatter_rows(const T* __restrict__ src,
+                                                           T* __restrict__ dst, uint32_t n_packs,
+                                                           FastDiv row_packs, OuterDims outer) {
+    scatter_rows_body<T, N, UNROLL, NT_STORE>(src, dst, n_packs, row_packs, outer, blockIdx.x,
+                                              gridDim.x);
 }
 
 // Per-element gather over all dims (innermost first in `dims`).
@@ -99,11 +113,37 @@ rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* 
             if (ok) break;
             n >>= 1;
         }
+        // A view that permutes a dense tensor -- its outer dims sorted by
+        // stride have strides inner, inner * dim, ... (so it covers source
+        // elements [0, numel) once each) -- is walked in source order; the
+        // output strides of view dim d are the product of the dims after it.
+        std::vector<uint32_t> by_stride;  // outer view dims, ascending stride
+        for (uint32_t d = 0; d + 1 < rank; ++d) by_stride.push_back(d);
+        std::sort(by_stride.begin(), by_stride.end(),
+                  [&](uint32_t a, uint32_t b) { return v.strides[a] < v.strides[b]; });
+        bool dense = rank >= 2;
+        uint64_t expect = inner;
+        for (uint32_t d : by_stride) {
+            if (!dense || v.strides[d] != expect) {
+                dense = false;
+                break;
+            }
+            expect *= v.dims[d];
+        }
         OuterDims outer{};
         outer.rank = rank - 1;
-        for (uint32_t d = 0; d + 1 < rank; ++d) {
-            outer.dim[d] = FastDiv(uint32_t(v.dims[rank - 2 - d]));
-            outer.stride[d] = v.strides[rank - 2 - d];
+        if (dense) {
+            std::vector<uint64_t> out_stride(rank, 1);
+            for (uint32_t d = rank - 1; d-- > 0;) out_stride[d] = out_stride[d + 1] * v.dims[d + 1];
+            for (uint32_t k = 0; k + 1 < rank; ++k) {
+                outer.dim[k] = FastDiv(uint32_t(v.dims[by_stride[k]]));
+                outer.stride[k] = out_stride[by_stride[k]];
+            }
+        } else {
+            for (uint32_t d = 0; d + 1 < rank; ++d) {
+                outer.dim[d] = FastDiv(uint32_t(v.dims[rank - 2 - d]));
+                outer.stride[d] = v.strides[rank - 2 - d];
+            }
         }
         const uint64_t n_packs = numel / n;
         const FastDiv row_packs(uint32_t(inner / n));
@@ -115,7 +155,8 @@ rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* 
         if (n == 16 / int(sizeof(T)) && rank - 1 <= kMaxFusedOuterRank && fusing(ctx)) {
             // recorded into a graph: one of the fused streaming ops
             FusedOp f;
-            f.kind = sizeof(T) == 4 ? kFusedGatherF32 : kFusedGatherF16;
+            f.kind = dense ? (sizeof(T) == 4 ? kFusedScatterF32 : kFusedScatterF16)
+                           : (sizeof(T) == 4 ? kFusedGatherF32 : kFusedGatherF16);
             f.blocks = grid.x;
             f.a = src;
             f.out = dst;
@@ -124,8 +165,8 @@ rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* 
             f.outer_rank = rank - 1;
             uint64_t last = v.dims[rank - 1] - 1;  // the view's last element in the source
             for (uint32_t d = 0; d + 1 < rank; ++d) {
-                f.outer_dim[d] = uint32_t(v.dims[rank - 2 - d]);
-                f.outer_stride[d] = uint32_t(v.strides[rank - 2 - d]);
+                f.outer_dim[d] = outer.dim[d].divisor;
+                f.outer_stride[d] = uint32_t(outer.stride[d]);
                 last += (v.dims[rank - 2 - d] - 1) * v.strides[rank - 2 - d];
             }
             f.read[0][0] = uintptr_t(src);
@@ -135,20 +176,24 @@ rl_status launch_contiguous(rl_context* ctx, const char* name, const T* src, T* 
             if (rl_status st = defer_fused(ctx, f)) return st;
             return after_launch(ctx, name);
         }
+        // f16: streamed stores into the 128-byte rows; f32: plain stores
+        constexpr bool NT = sizeof(T) == 2;
+#define RL_ROWS(N)                                                                                 \
+    do {                                                                                           \
+        if (dense)                                                                                 \
+            RL_LAUNCH(ctx, (k_scatter_rows<T, N, U, NT>), grid, block, src, dst, uint32_t(n_packs), \
+                      row_packs, outer);                                                           \
+        else                                                                                       \
+            RL_LAUNCH(ctx, (k_gather_rows<T, N, U>), grid, block, src, dst, uint32_t(n_packs),    \
+                      row_packs, outer);                                                           \
+    } while (0)
         switch (n) {
-            case 8:
-                RL_LAUNCH(ctx, (k_gather_rows<T, 8, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
-                break;
-            case 4:
-                RL_LAUNCH(ctx, (k_gather_rows<T, 4, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
-                break;
-            case 2:
-                RL_LAUNCH(ctx, (k_gather_rows<T, 2, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
-                break;
-            default:
-                RL_LAUNCH(ctx, (k_gather_rows<T, 1, U>), grid, block, src, dst, uint32_t(n_packs), row_packs, outer);
-                break;
+            case 8: RL_ROWS(8); break;
+            case 4: RL_ROWS(4); break;
+            case 2: RL_ROWS(2); break;
+            default: RL_ROWS(1); break;
         }
+#undef RL_ROWS
     } else {
         OuterDims all{};
         all.rank = rank;

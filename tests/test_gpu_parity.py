@@ -243,6 +243,30 @@ def test_contiguous_random_permutations(ctx, dtype, seed):
     assert_bitexact(got, np.ascontiguousarray(view), f"perm {shape} {perm}")
 
 
+@pytest.mark.parametrize("dtype", DT)
+def test_contiguous_dense_permutations_rowwise(ctx, dtype):
+    """Permutations of dense tensors that keep the stride-1 dim innermost
+    (copied in source order, whole rows) at ranks 3-5 with 16-byte packs and
+    grids of many blocks, and permutes of a narrowed tensor (gaps between the
+    rows: copied in output order) -- all bit-exact against numpy."""
+    cases = [((7, 300, 64), (1, 0, 2)), ((2, 129, 5, 64), (0, 2, 1, 3)),
+             ((3, 4, 50, 32), (2, 0, 1, 3)), ((2, 3, 4, 5, 16), (3, 1, 0, 2, 4)),
+             ((64, 9, 128), (1, 0, 2))]
+    for shape, perm in cases:
+        base = norm(("dperm", shape), shape, dtype)
+        view = base.transpose(perm)
+        got = run(ctx, lambda: ctx.contiguous(ctx.upload(base), list(view.shape),
+                                              _view_strides(view))).numpy()
+        assert_bitexact(got, np.ascontiguousarray(view), f"dense {shape} {perm}")
+    base = norm(("narrowed",), (6, 200, 64), dtype)
+    for view in (base[:, 3:150].transpose(1, 0, 2), base[1:5].transpose(1, 0, 2)):
+        offset = (view.__array_interface__["data"][0] - base.__array_interface__["data"][0]) \
+            // base.itemsize
+        src = ctx.upload(base.ravel()[offset:].copy())
+        got = run(ctx, lambda: ctx.contiguous(src, list(view.shape), _view_strides(view))).numpy()
+        assert_bitexact(got, np.ascontiguousarray(view), f"narrowed {view.shape}")
+
+
 def test_contiguous_special_views(ctx):
     # stride-0 broadcast, transposed inner dims (per-element path), narrowed KV cache
     bias = norm(("b0",), (24,), np.float32)
