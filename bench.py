@@ -54,11 +54,13 @@ def log(msg: str) -> None:
 
 
 class Op:
-    """One kernel launch on one buffer set: `launch(ctx, bufs)` and its bytes."""
+    """One kernel launch on one buffer set: `launch(ctx, bufs)`, its bytes and
+    the part of them it writes."""
 
-    def __init__(self, name, dtype, shape, nbytes, launch):
+    def __init__(self, name, dtype, shape, nbytes, launch, write=None):
         self.name, self.dtype, self.shape, self.nbytes, self.launch = (name, dtype, shape, nbytes,
                                                                        launch)
+        self.write = write
 
 
 def batch_inputs(seed_tag: str):
@@ -93,20 +95,21 @@ def batch_ops():
             return lambda c, b: kind(c, b, tag)
 
         ops.append(Op(f"add_{sfx}", sfx, [T, H], 3 * n * es,
-                      mk(lambda c, b, t: c.add(b[f"a_{t}"], b[f"b_{t}"], b[f"o1_{t}"]))))
+                      mk(lambda c, b, t: c.add(b[f"a_{t}"], b[f"b_{t}"], b[f"o1_{t}"])), n * es))
         ops.append(Op(f"mul_{sfx}", sfx, [T, H], 3 * n * es,
-                      mk(lambda c, b, t: c.mul(b[f"a_{t}"], b[f"b_{t}"], b[f"o2_{t}"]))))
+                      mk(lambda c, b, t: c.mul(b[f"a_{t}"], b[f"b_{t}"], b[f"o2_{t}"])), n * es))
         ops.append(Op(f"silu_{sfx}", sfx, [T, H], 2 * n * es,
-                      mk(lambda c, b, t: c.silu(b[f"a_{t}"], b[f"o3_{t}"]))))
+                      mk(lambda c, b, t: c.silu(b[f"a_{t}"], b[f"o3_{t}"])), n * es))
         ops.append(Op(f"swiglu_{sfx}", sfx, [T, H], 3 * n * es,
-                      mk(lambda c, b, t: c.swiglu(b[f"a_{t}"], b[f"b_{t}"], b[f"o4_{t}"]))))
+                      mk(lambda c, b, t: c.swiglu(b[f"a_{t}"], b[f"b_{t}"], b[f"o4_{t}"])),
+                      n * es))
         ops.append(Op(f"add_broadcast_{sfx}", sfx, [T, H], 2 * n * es + H * es,
                       mk(lambda c, b, t: c.add_broadcast(b[f"a_{t}"], b[f"bias_{t}"],
-                                                         b[f"o5_{t}"]))))
+                                                         b[f"o5_{t}"])), n * es))
     ops.append(Op("cast_f32_to_f16", "f32->f16", [T, H], n * 6,
-                  lambda c, b: c.cast(b["a_float32"], F16, b["cast_h"])))
+                  lambda c, b: c.cast(b["a_float32"], F16, b["cast_h"]), n * 2))
     ops.append(Op("cast_f16_to_f32", "f16->f32", [T, H], n * 6,
-                  lambda c, b: c.cast(b["a_float16"], F32, b["cast_f"])))
+                  lambda c, b: c.cast(b["a_float16"], F32, b["cast_f"]), n * 4))
     nv = 9 * 4096 * 64
     nkv = 3 * 4096 * 64
     for dt in (F32, F16):
@@ -115,9 +118,10 @@ def batch_ops():
         sfx = "f16" if dt == F16 else "f32"
         ops.append(Op(f"contiguous_{sfx}", sfx, VIEW_DIMS, 2 * nv * es,
                       lambda c, b, t=tag: c.contiguous(b[f"view_{t}"], VIEW_DIMS, VIEW_STRIDES,
-                                                       b[f"vo_{t}"])))
+                                                       b[f"vo_{t}"]), nv * es))
         ops.append(Op(f"repeat_kv_{sfx}", sfx, [1, 3, 4096, 64], (nkv + 3 * nkv) * es,
-                      lambda c, b, t=tag: c.repeat_kv(b[f"kv_{t}"], 3, b[f"kvo_{t}"])))
+                      lambda c, b, t=tag: c.repeat_kv(b[f"kv_{t}"], 3, b[f"kvo_{t}"]),
+                      3 * nkv * es))
     return ops
 
 
@@ -247,7 +251,9 @@ def graph_batch_us(ctx, launches, min_per_graph=32, replays=8):
     return ms * 1e3
 
 
-def op_row(name, dtype, shape, nbytes, timing):
+def op_row(name, dtype, shape, nbytes, timing, write=None):
+    """One per-op line; `write` = the bytes of `nbytes` the op writes (None
+    for ops that HBM does not bound: matrix-core and latency-bound rows)."""
     us_list, batch_us = timing[0], timing[1]
     us = float(np.mean(us_list))
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -258,6 +264,8 @@ def op_row(name, dtype, shape, nbytes, timing):
            "us_min": round(float(np.min(us_list)), 3),
            "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
            "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None}
+    if write is not None:
+        row["read_bytes"], row["write_bytes"] = nbytes - write, write
     if len(timing) > 2:  # kernel dispatches of the one-launch timing: warm-up, then timed
         row["dispatches"] = timing[2]
         row["timed"] = len(us_list)
@@ -300,7 +308,7 @@ def per_op_rows(ctx, ops, sets, reps):
                    for i, s in ((i, sets[i % len(sets)]) for i in range(n))]
         launches = [lambda s=s, op=op: op.launch(ctx, s) for s in op_sets]
         rows.append(op_row(op.name, op.dtype, op.shape, op.nbytes,
-                           kernel_times_us(ctx, launches, reps)))
+                           kernel_times_us(ctx, launches, reps), op.write))
         del launches, op_sets
     return rows
 
@@ -313,14 +321,15 @@ def extra_rows(ctx, reps, quick):
     alone -- same method, rotated buffer sets."""
     rows = []
 
-    def measure(name, dtype, shape, nbytes, make_set, launch):
+    def measure(name, dtype, shape, nbytes, make_set, launch, write=None):
         # As many buffer sets as make >= 1 GiB in total (4 .. 256 sets).
         first = make_set(0)
         footprint = sum(b.byte_len for b in first)
         nsets = int(min(256, max(4, -(-(1 << 30) // max(footprint, 1)))))
         sets = [first] + [make_set(i) for i in range(1, nsets)]
         launches = [lambda s=s: launch(s) for s in sets]
-        rows.append(op_row(name, dtype, shape, nbytes, kernel_times_us(ctx, launches, reps)))
+        rows.append(op_row(name, dtype, shape, nbytes, kernel_times_us(ctx, launches, reps),
+                           write))
         del sets, launches, first
 
     tokens_list = [4096, 16384] if quick else [1, 16, 256, 4096, 16384]
@@ -337,7 +346,8 @@ def extra_rows(ctx, reps, quick):
                 measure(f"rmsnorm_{sfx}", sfx, [tokens, hidden], nbytes,
                         lambda i, x=x, tokens=tokens, hidden=hidden, dt=dt:
                         (ctx.upload(x), ctx.empty((tokens, hidden), dt)),
-                        lambda s, w=w: ctx.rmsnorm(s[0], w, 1e-5, s[1]))
+                        lambda s, w=w: ctx.rmsnorm(s[0], w, 1e-5, s[1]),
+                        tokens * hidden * es)
 
     # attention scores: prefill [9, 2048, 2048] causal, scale 1/8; decode [9, 1, 2048]
     def logits(shape, dt=F32):
@@ -357,11 +367,11 @@ def extra_rows(ctx, reps, quick):
         ("softmax_f32", 2 * n * 4, lambda s: ctx.softmax(s[0], s[1])),
     ]:
         measure(name, "f32", [9, 2048, 2048], nbytes,
-                lambda i: (ctx.upload(pre), ctx.empty(pre.shape, F32)), fn)
+                lambda i: (ctx.upload(pre), ctx.empty(pre.shape, F32)), fn, n * 4)
     dec = logits((9, 1, 2048))
     measure("attention_softmax_f32", "f32", [9, 1, 2048], 2 * dec.size * 4,
             lambda i: (ctx.upload(dec), ctx.empty(dec.shape, F32)),
-            lambda s: ctx.attention_softmax(s[0], 0.125, 2047, s[1]))
+            lambda s: ctx.attention_softmax(s[0], 0.125, 2047, s[1]), dec.size * 4)
 
     # SmolLM2-360M decoder layer, f16, 4096 tokens
     hid, qh, kvh, hd, ffn, tok = 960, 15, 5, 64, 2560, 4096
@@ -371,7 +381,7 @@ def extra_rows(ctx, reps, quick):
     x = synth.normal(synth.seed_for("c5", "x"), (tok, hid), 0, 1, F16)
     measure("layer.1 rmsnorm_f16", "f16", [tok, hid], tok * hid * 4 + hid * 2,
             lambda i: (ctx.upload(x), ctx.empty((tok, hid), F16)),
-            lambda s: ctx.rmsnorm(s[0], wn, 1e-5, s[1]))
+            lambda s: ctx.rmsnorm(s[0], wn, 1e-5, s[1]), tok * hid * 2)
     for heads, label in ((qh, "Q"), (kvh, "K")):
         proj = synth.normal(synth.seed_for("c5", label), (1, tok, heads, hd), 0, 1, F16)
         dims, strides = [1, heads, tok, hd], [tok * heads * hd, hd, heads * hd, 1]
@@ -379,21 +389,23 @@ def extra_rows(ctx, reps, quick):
         measure(f"layer.2 rope_{label}_f16 (fused gather)", "f16", dims, nbytes,
                 lambda i, proj=proj, dims=dims: (ctx.upload(proj), ctx.empty(dims, F16)),
                 lambda s, dims=dims, strides=strides: ctx.rope_strided(s[0], dims, strides, dc,
-                                                                        ds, 0, s[1]))
+                                                                        ds, 0, s[1]),
+                proj.size * 2)
         cont = np.ascontiguousarray(proj.transpose(0, 2, 1, 3))
         measure(f"layer.2 rope_{label}_f16", "f16", list(cont.shape), nbytes,
                 lambda i, cont=cont: (ctx.upload(cont), ctx.empty(cont.shape, F16)),
-                lambda s: ctx.rope(s[0], dc, ds, 0, s[1]))
+                lambda s: ctx.rope(s[0], dc, ds, 0, s[1]), proj.size * 2)
     # K rotated straight into a [1, 5, 4096, 64] cache, V gathered into one
     proj_k = synth.normal(synth.seed_for("c5", "Kc"), (1, tok, kvh, hd), 0, 1, F16)
     kdims, kstrides = [1, kvh, tok, hd], [tok * kvh * hd, hd, kvh * hd, 1]
     measure("layer.2 rope_K_f16 -> KV cache (fused)", "f16", kdims,
             2 * proj_k.size * 2 + 2 * tok * (hd // 2) * 4,
             lambda i: (ctx.upload(proj_k), ctx.empty(kdims, F16)),
-            lambda s: ctx.rope_kv_cache_write(s[0], kdims, kstrides, dc, ds, 0, s[1]))
+            lambda s: ctx.rope_kv_cache_write(s[0], kdims, kstrides, dc, ds, 0, s[1]),
+            proj_k.size * 2)
     measure("layer.2 V_f16 -> KV cache (fused gather)", "f16", kdims, 2 * proj_k.size * 2,
             lambda i: (ctx.upload(proj_k), ctx.empty(kdims, F16)),
-            lambda s: ctx.kv_cache_write_strided(s[0], kdims, kstrides, s[1], 0))
+            lambda s: ctx.kv_cache_write_strided(s[0], kdims, kstrides, s[1], 0), proj_k.size * 2)
     # Q and K rotated, K and V appended, as one launch
     proj_q = synth.normal(synth.seed_for("c5", "Qc"), (1, tok, qh, hd), 0, 1, F16)
     qdims, qstrides = [1, qh, tok, hd], [tok * qh * hd, hd, qh * hd, 1]
@@ -403,7 +415,8 @@ def extra_rows(ctx, reps, quick):
                        ctx.empty(qdims, F16), ctx.empty(kdims, F16), ctx.empty(kdims, F16)),
             lambda s: ctx.qkv_rope_kv_append((s[0], qdims, qstrides), (s[1], kdims, kstrides),
                                              (s[2], kdims, kstrides), dc, ds, 0, s[4], s[5],
-                                             s[3]))
+                                             s[3]),
+            (proj_q.size + 2 * proj_k.size) * 2)
     # ... and repeat_kv of both caches (5 -> 15 heads) in the same launch
     n_rep = qh // kvh
     measure("layer.2 QKV + KV append + repeat_kv (one launch)", "f16",
@@ -415,7 +428,8 @@ def extra_rows(ctx, reps, quick):
                        ctx.empty(qdims, F16), ctx.empty(qdims, F16)),
             lambda s: ctx.qkv_rope_kv_append_repeat(
                 (s[0], qdims, qstrides), (s[1], kdims, kstrides), (s[2], kdims, kstrides), dc,
-                ds, 0, s[4], s[5], n_rep, s[3], s[6], s[7]))
+                ds, 0, s[4], s[5], n_rep, s[3], s[6], s[7]),
+            (proj_q.size + 2 * proj_k.size * (1 + n_rep)) * 2)
     # token embedding gather: 4096 ids into a [49152, 960] f16 table
     # (each set has its own 94 MB table, so the gathered rows come from HBM)
     vocab = 49152
@@ -423,11 +437,11 @@ def extra_rows(ctx, reps, quick):
     ids = (synth.uniform(synth.seed_for("c5", "ids"), tok) * vocab).astype(np.uint32)
     measure("layer.0 embedding_f16", "f16", [tok, hid], 2 * tok * hid * 2 + tok * 4,
             lambda i: (ctx.upload(emb), ctx.empty((tok, hid), F16)),
-            lambda s: ctx.embedding(s[0], ids, s[1]))
+            lambda s: ctx.embedding(s[0], ids, s[1]), tok * hid * 2)
     kv = synth.normal(synth.seed_for("c5", "kv"), (1, kvh, tok, hd), 0, 1, F16)
     measure("layer.3 repeat_kv_f16", "f16", [1, kvh, tok, hd], (kv.size + 3 * kv.size) * 2,
             lambda i: (ctx.upload(kv), ctx.empty((1, qh, tok, hd), F16)),
-            lambda s: ctx.repeat_kv(s[0], 3, s[1]))
+            lambda s: ctx.repeat_kv(s[0], 3, s[1]), 3 * kv.size * 2)
     if not quick:
         rng = np.random.default_rng(5)
         sc = rng.standard_normal((qh, tok, tok), dtype=np.float32).astype(F16)
@@ -435,17 +449,17 @@ def extra_rows(ctx, reps, quick):
         unm = qh * (tok * (tok + 1) // 2)
         measure("layer.4 attention_softmax_f16", "f16", [qh, tok, tok], unm * 2 + n * 2,
                 lambda i: (ctx.upload(sc), ctx.empty(sc.shape, F16)),
-                lambda s: ctx.attention_softmax(s[0], 0.125, 0, s[1]))
+                lambda s: ctx.attention_softmax(s[0], 0.125, 0, s[1]), n * 2)
         del sc
     g = synth.normal(synth.seed_for("c5", "g"), (tok, ffn), 0, 1, F16)
     u = synth.normal(synth.seed_for("c5", "u"), (tok, ffn), 0, 1, F16)
     measure("layer.5 swiglu_f16", "f16", [tok, ffn], 3 * g.size * 2,
             lambda i: (ctx.upload(g), ctx.upload(u), ctx.empty(g.shape, F16)),
-            lambda s: ctx.swiglu(s[0], s[1], s[2]))
+            lambda s: ctx.swiglu(s[0], s[1], s[2]), g.size * 2)
     r = synth.normal(synth.seed_for("c5", "r"), (tok, hid), 0, 1, F16)
     measure("layer.6 residual add_f16", "f16", [tok, hid], 3 * r.size * 2,
             lambda i: (ctx.upload(x), ctx.upload(r), ctx.empty(r.shape, F16)),
-            lambda s: ctx.add(s[0], s[1], s[2]))
+            lambda s: ctx.add(s[0], s[1], s[2]), r.size * 2)
     rows.extend(attention_rows(ctx, qh, kvh, hd, tok, reps))
     if not quick:
         rows.append(fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds))
@@ -456,7 +470,7 @@ def extra_rows(ctx, reps, quick):
     measure("add_rmsnorm_f32", "f32", [64, 768], 64 * 768 * 4 * 4 + 768 * 4,
             lambda i: (ctx.upload(x0), ctx.upload(x0), ctx.empty(x0.shape, F32),
                        ctx.empty(x0.shape, F32)),
-            lambda s: ctx.add_rmsnorm(s[0], s[1], w0, 1e-5, s[2], s[3]))
+            lambda s: ctx.add_rmsnorm(s[0], s[1], w0, 1e-5, s[2], s[3]), 2 * x0.size * 4)
     return rows
 
 
@@ -512,11 +526,11 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
     qk_bytes = (q.size + k.size + n_scores) * 2
     rows.append(op_row("layer.4 gqa_qk_f16 (scores)", "f16", [1, qh, tok, tok], qk_bytes,
                        kernel_times_us(ctx, [lambda i=i: ctx.gqa_qk(s0[0], s0[1], None, sc[i])
-                                             for i in range(2)], reps)))
+                                             for i in range(2)], reps), n_scores * 2))
     pv_bytes = (n_scores + v.size + q.size) * 2
     rows.append(op_row("layer.4 gqa_pv_f16", "f16", [1, qh, tok, hd], pv_bytes,
                        kernel_times_us(ctx, [lambda i=i: ctx.gqa_pv(pr[i], s0[2], out)
-                                             for i in range(2)], reps)))
+                                             for i in range(2)], reps), q.size * 2))
     # the same two products in f32 (f32 matrix cores; 2 x 32.2 GFLOP over all keys)
     q32, k32, v32 = (ctx.upload(x.astype(np.float32)) for x in (q, k, v))
     sc32 = ctx.empty((1, qh, tok, tok), np.float32)
@@ -569,18 +583,18 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
     pr_r = [ctx.empty((1, qh, rl_tok, rl_tok), F16) for _ in range(2)]
     out_r = ctx.empty((1, qh, rl_tok, hd), F16)
     kv_r = kvh * rl_tok * hd
-    for name, fns, nbytes in (
+    for name, fns, nbytes, write in (
             ("layer.4 ragged gqa_qk_f16 (4093 keys)",
              [lambda i=i: ctx.gqa_qk(q_r, s0[1], rl_tok, sc_r[i]) for i in range(2)],
-             (qh * rl_tok * hd + kv_r + n_r) * 2),
+             (qh * rl_tok * hd + kv_r + n_r) * 2, n_r * 2),
             ("layer.4 ragged attention_softmax_f16 (4093 keys)",
              [lambda i=i: ctx.attention_softmax(sc_r[i], 0.125, 0, pr_r[i]) for i in range(2)],
-             (unmasked_r + n_r) * 2),
+             (unmasked_r + n_r) * 2, n_r * 2),
             ("layer.4 ragged gqa_pv_f16 (4093 keys)",
              [lambda i=i: ctx.gqa_pv(pr_r[i], s0[2], out_r) for i in range(2)],
-             (n_r + kv_r + qh * rl_tok * hd) * 2)):
+             (n_r + kv_r + qh * rl_tok * hd) * 2, qh * rl_tok * hd * 2)):
         shape = [1, qh, rl_tok, rl_tok if "pv" not in name else hd]
-        rows.append(op_row(name, "f16", shape, nbytes, kernel_times_us(ctx, fns, reps)))
+        rows.append(op_row(name, "f16", shape, nbytes, kernel_times_us(ctx, fns, reps), write))
     del sc_r, pr_r, out_r, q_r
     # decode: one new token of 15 heads over a 4096-row KV cache (one launch:
     # key splits whose last workgroup per KV head merges them), kernel-stamped
@@ -830,9 +844,10 @@ def time_chain_graphs(ctx, chain, sets, steps, warmup):
 PROBE = os.path.join(ROOT, "rustllm_amd", "hbm_probe")
 
 
-def probe_streams(pairs, timeout=120):
-    """Back-to-back us per launch of a plain streaming kernel moving each
-    (read, write) byte pair (rustllm_amd/hbm_probe, a process of its own),
+def probe_cases(pairs, timeout=120):
+    """The probe's record of each (read, write) byte pair -- "us": back-to-back
+    us per launch of a plain streaming kernel moving those bytes, "us_one":
+    one launch between events (rustllm_amd/hbm_probe, a process of its own) --
     or None if the probe is missing or fails."""
     if not os.path.exists(PROBE):
         log(f"{PROBE} is missing (python -m rustllm_amd.build builds it)")
@@ -846,7 +861,45 @@ def probe_streams(pairs, timeout=120):
     if res.returncode != 0:
         log(f"hbm_probe failed ({res.returncode}): {res.stderr.strip()[-300:]}")
         return None
-    return [c["us"] for c in json.loads(res.stdout)["cases"]]
+    return json.loads(res.stdout)["cases"]
+
+
+def probe_streams(pairs, timeout=120):
+    """Back-to-back us per launch of each (read, write) pair (probe_cases)."""
+    cases = probe_cases(pairs, timeout)
+    return None if cases is None else [c["us"] for c in cases]
+
+
+def attach_attainable(rows, min_bytes=1 << 20, max_bytes=3 << 30):
+    """Adds to each HBM-bound row (one with a read/write split) the probe's
+    times for the same read and write bytes -- back to back
+    ("attainable_us") and one launch between events ("attainable_one_us") --
+    and the row's times as a percentage of them: sustained (graph batch)
+    against back to back, one launch against one launch (a row with no
+    graph-batch figure is compared one launch to one launch only).  100 = as
+    fast as a plain streaming kernel moving those bytes; below 70 % of 8 TB/s
+    at these sizes that figure, not the peak, says whether a kernel leaves
+    time on the table."""
+    todo = [r for r in rows if "write_bytes" in r and min_bytes <= r["bytes"] <= max_bytes]
+    pairs = sorted({(r["read_bytes"], r["write_bytes"]) for r in todo})
+    if not pairs:
+        return
+    cases = probe_cases(pairs)
+    if cases is None:
+        return
+    b2b = {p: c["us"] for p, c in zip(pairs, cases)}
+    single = {p: c["us_one"] for p, c in zip(pairs, cases)}
+    for r in todo:
+        key = (r["read_bytes"], r["write_bytes"])
+        a, a1 = b2b[key], single[key]
+        r["attainable_us"], r["attainable_one_us"] = round(a, 3), round(a1, 3)
+        r["pct_of_attainable_one_launch"] = round(100 * a1 / r["us"], 1)
+        if r["us_graph_batch"] is not None:
+            r["pct_of_attainable_sustained"] = round(100 * a / r["us_graph_batch"], 1)
+            what = f"sustained at {r['pct_of_attainable_sustained']:5.1f}% of it"
+        else:
+            what = f"one launch at {r['pct_of_attainable_one_launch']:5.1f}% of one launch"
+        log(f"  {r['op']:34s} {str(r['shape']):20s} attainable {a:8.2f} us: {what}")
 
 
 def oracle_chain(o, chain, host):
@@ -1164,13 +1217,15 @@ SUMMARY_ROWS = [
 
 
 def summary(rows):
-    """{"op shape": [us, GB/s, % of peak, sustained % of peak]} for SUMMARY_ROWS."""
+    """{"op shape": [us, GB/s, % of peak, sustained % of peak, sustained % of
+    the probe's time for the same bytes]} for SUMMARY_ROWS."""
     out = {}
     for op, shape in SUMMARY_ROWS:
         for r in rows:
             if r["op"] == op and r["shape"] == shape:
                 out[f"{op} {shape}"] = [r["us"], r["GB/s"], r["pct_peak"],
-                                        r.get("pct_peak_graph_batch")]
+                                        r.get("pct_peak_graph_batch"),
+                                        r.get("pct_of_attainable_sustained")]
                 break
     return out
 
@@ -1232,6 +1287,8 @@ def main():
         rows = per_op_rows(ctx, batch_ops(), sets, args.op_reps)
         del sets
         rows += extra_rows(ctx, args.op_reps, args.quick)
+        log("per op against the HBM probe at the same read and write bytes:")
+        attach_attainable(rows)
         write_side_file(args.per_op_out, {"per_op": rows})
         ctx.close()
         return
@@ -1396,7 +1453,8 @@ def main():
         "pct_of_peak": round(100 * value / PEAK_GBS, 1),
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "per_op_summary": {"columns": ["us", "GB/s", "pct_peak", "pct_peak_sustained"],
+        "per_op_summary": {"columns": ["us", "GB/s", "pct_peak", "pct_peak_sustained",
+                                       "pct_of_attainable_sustained"],
                            **summary(rows)},
         "per_op_file": side,
         "per_op_status": per_op_status,

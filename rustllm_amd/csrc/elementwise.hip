@@ -45,7 +45,11 @@ struct SiluF32Op {  // silu.metal:17-23: x * (1 / (1 + exp(-x)))
 // (x < -87.3) it flushes to zero and the result is -0, and the exact result
 // there (|x e^x| < 1e-35) also rounds to -0 in f16.  x = -inf gives NaN, as
 // -inf / inf does.  Three fewer VALU operations per element make this
-// f16-bandwidth kernel 8% faster.
+// f16-bandwidth kernel 8% faster.  Taking the half x unconverted in both
+// products (v_fma_mix_f32, two instructions fewer per element, the same
+// results bit for bit) measured no faster ([4096, 1536]: 5.91 against 5.89
+// us back to back): the time goes to the exp -> add -> rcp latency, not to
+// the instruction count.
 struct SiluF16Op {
     __device__ float operator()(float x, float) const {
         return x * rcp_fast(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896340736f));
@@ -117,11 +121,16 @@ struct MapShape<CopyOp, half_t, float> {  // widening cast: 8-byte loads
     static constexpr bool phased = false;
     static constexpr bool nt_store = true;
 };
+// Narrowing cast: packs of 4 (16-byte loads, 8-byte stores), four a thread,
+// streamed stores.  With packs of 8 each 16-byte load instruction covers
+// every other 16 bytes of 2 KB (a lane's 32 bytes come in two loads);
+// [4096, 1536] back to back: 7.9 us (8 a pack, 2 a thread, plain stores)
+// -> 7.2 us.
 template <>
 struct MapShape<CopyOp, float, half_t> {
-    static constexpr int unroll = 2;
+    static constexpr int unroll = 4;
     static constexpr bool phased = false;
-    static constexpr bool nt_store = false;
+    static constexpr bool nt_store = true;
 };
 
 // Launch shape of a map inside the fused launch of recorded ops (below):
@@ -138,13 +147,14 @@ struct FusedShape {
     static constexpr bool phased = MapShape<Op, TIn, TOut>::phased;
 };
 
-// Pack size of a map: 16-byte packs; the widening cast uses 4-element packs
-// so its stores stay 16 B per lane and contiguous across the wave (8-element
-// f32 packs would be two strided 16-byte stores, which costs extra HBM
-// writes).
+// Pack size of a map: 16-byte packs; both casts use 4-element packs, so
+// that the f32 side moves 16 B per lane contiguous across the wave (with
+// 8-element packs a lane's 32 f32 bytes would be two 16-byte accesses each
+// covering every other 16 bytes of the wave's span: for the widening cast
+// extra HBM writes, for the narrowing one 9% more time).
 template <typename TIn, typename TOut>
 constexpr int map_pack() {
-    return (sizeof(TIn) == 4 && sizeof(TOut) == 4) ? 4 : (sizeof(TOut) == 4 ? 4 : 8);
+    return (sizeof(TIn) == 4 || sizeof(TOut) == 4) ? 4 : 8;
 }
 
 // out[i] = op(a[i], b[i]) for ARITY 2, op(a[i]) for ARITY 1.  Block blk covers
