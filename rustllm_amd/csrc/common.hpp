@@ -338,6 +338,14 @@ struct Pack16 {
 };
 
 __device__ inline float to_float(float v) { return v; }
+// rope.hip: a plain copy of a [..., S, D] view (unit innermost stride) into
+// rows group * group_rows + first_row + s of dst on the row-block kernel;
+// false (nothing launched) when the view does not fit that kernel.
+template <typename T>
+bool launch_copy_rows(rl_context* ctx, const T* src, const uint64_t* dims,
+                      const uint64_t* strides, uint32_t rank, T* dst, uint32_t group_rows,
+                      uint32_t first_row);
+
 __device__ inline float to_float(half_t v) { return static_cast<float>(v); }
 
 template <typename T>

@@ -9,6 +9,8 @@
 // the [1, S, H*D] projection that LayerKvCache::append_encode first makes
 // contiguous, src/model/kv_cache.rs:123-137): the gather and the write are
 // then one pass, so the projection is read once and the cache written once.
+// Rows of 32-256 bytes go through the RoPE row-block kernel as a copy job
+// (launch_copy_rows); other head sizes and alignments through k_kv_write.
 #include "common.hpp"
 
 namespace rl {
@@ -67,6 +69,13 @@ template <typename T>
 rl_status launch_kv_write(rl_context* ctx, const char* name, const T* src, const uint64_t* dims,
                           const uint64_t* strides, T* cache, uint64_t max_seq, uint64_t start) {
     if (rl_status st = activate(ctx)) return st;
+    // Rows of 32-256 bytes on 16-byte boundaries: the row-block kernel (16
+    // bytes a lane, rows decoded branch-free; the [1, 5, 4096, 64] f16 append
+    // of a [1, 4096, 5, 64] projection view, graph-replayed back to back:
+    // 4.22 us with k_kv_write below, 2.63 us).
+    if (strides[3] == 1 &&
+        launch_copy_rows<T>(ctx, src, dims, strides, 4, cache, uint32_t(max_seq), uint32_t(start)))
+        return after_launch(ctx, name);
     const uint64_t heads = dims[1], seq = dims[2], head_dim = dims[3];
     int n = 16 / int(sizeof(T));
     while (n > 1) {

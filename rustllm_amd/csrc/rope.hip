@@ -874,6 +874,33 @@ rl_status qkv_entry(rl_context* ctx, const char* name, const rl_buffer* q_src,
 }
 
 }  // namespace
+
+// A plain copy of a [..., S, D] view into rows group * group_rows +
+// first_row + s of dst on the row-block kernel (a copy job, as the layer
+// prologue's V append), or false when the view does not fit that kernel.
+// A copy job issues its table loads like a rotating one and ignores the
+// values (branch-free); they read floats [0, D / 2) of the table pointer,
+// i.e. 2D bytes, which the view's first row holds (D elements of >= 2
+// bytes, 16-byte aligned: make_job checks), so the source stands in for the
+// table.
+template <typename T>
+bool launch_copy_rows(rl_context* ctx, const T* src, const uint64_t* dims,
+                      const uint64_t* strides, uint32_t rank, T* dst, uint32_t group_rows,
+                      uint32_t first_row) {
+    const int lanes = row_lanes<T>(dims[rank - 1]);
+    if (lanes == 0) return false;
+    RowJobs jobs{};
+    if (!make_job<T>(jobs.job[0], src, dims, strides, rank, dst, DstRows{group_rows, first_row},
+                     false))
+        return false;
+    const float* table = reinterpret_cast<const float*>(src);
+    return launch_jobs<T>(ctx, jobs, 1, lanes, table, table, 0);
+}
+template bool launch_copy_rows<float>(rl_context*, const float*, const uint64_t*, const uint64_t*,
+                                      uint32_t, float*, uint32_t, uint32_t);
+template bool launch_copy_rows<half_t>(rl_context*, const half_t*, const uint64_t*,
+                                       const uint64_t*, uint32_t, half_t*, uint32_t, uint32_t);
+
 }  // namespace rl
 
 using namespace rl;

@@ -631,6 +631,7 @@ def test_rope_reference_kats(ctx):
 
 # (kv_heads, max_seq, head_dim, seq_len, start)
 KV_CASES = [(5, 4096, 64, 4096, 0), (5, 4096, 64, 1, 4095), (5, 4096, 64, 7, 100),
+            (4, 300, 128, 77, 200), (3, 64, 16, 40, 10),
             (2, 8, 4, 1, 3), (3, 17, 6, 5, 12), (2, 9, 5, 4, 2)]
 
 
