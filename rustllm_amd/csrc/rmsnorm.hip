@@ -186,8 +186,11 @@ RowPlan plan_rows(uint64_t h_packs, uint64_t rows, bool narrow_ties) {
 }
 
 // narrow_ties: between groups of equal lane use, take the narrower one (more
-// packs per lane): f16 [16384, 960] runs 8% faster on 16 lanes x 8 packs than
-// on 32 x 4, while f32 rows keep the wider group on a tie.
+// packs per lane) when its instantiated pack count is exactly what the row
+// needs: f16 [16384, 960] runs 8% faster on 16 lanes x 8 packs than on
+// 32 x 4, while [16384, 768] (96 packs) on 16 x 8 -- two reloads of the last
+// pack a lane -- takes 9.6 us against 8.9 on 32 x 3 (16 x 6: 9.0-9.3).  f32
+// rows keep the wider group on a tie.
 RowPlan plan_by_length(uint64_t h_packs, bool narrow_ties) {
     RowPlan best{0, 0};
     bool best_ok = false;
@@ -201,7 +204,8 @@ RowPlan plan_by_length(uint64_t h_packs, bool narrow_ties) {
         const bool ok = need >= 3 && need <= 12;
         const uint64_t num = h_packs, den = uint64_t(tpr) * need;
         const bool better_use = num * best_den > best_num * den ||
-                                (narrow_ties && num * best_den == best_num * den);
+                                (narrow_ties && num * best_den == best_num * den &&
+                                 uint64_t(nv) == need);
         if (best.tpr == 0 || (ok && !best_ok) || (ok == best_ok && better_use)) {
             best = {tpr, nv};
             best_ok = ok;
