@@ -1111,6 +1111,12 @@ def probe(ctx, host, ops):
     krep, vrep = ctx.empty((1, 15, tok, 64), F16), ctx.empty((1, 15, tok, 64), F16)
     # one decode step over a 4096-row cache
     q1, o1 = ctx.upload(synth.normal(14, (1, 15, 1, 64), 0, 1, F16)), ctx.empty((1, 15, 1, 64), F16)
+    # f32 operands of the same attention core
+    q32 = ctx.upload(synth.normal(15, (1, 15, tok, 64), 0, 1, F32))
+    k32 = ctx.upload(synth.normal(16, (1, 5, tok, 64), 0, 1, F32))
+    v32 = ctx.upload(synth.normal(17, (1, 5, tok, 64), 0, 1, F32))
+    o32 = ctx.empty((1, 15, tok, 64), F32)
+    scores32 = ctx.empty((1, 15, tok, tok), F32)
     # the layer chain's other kernels at its shapes (LayerChain): the f16
     # scores' causal scale/mask + softmax, SwiGLU [4096, 2560], residual add
     chain = LayerChain(ctx)
@@ -1157,6 +1163,13 @@ def probe(ctx, host, ops):
                                                vcache, 3, qo, krep, vrep)),
         ("decode attention_f16 [1,15,1,64] over 4096 rows", 2 * 15 * 64 * 2 + 2 * 5 * tok * 64 * 2,
          lambda: ctx.attention_noalloc(q1, ka, va, 0.125, tok - 1, None, o1)),
+        # the f32 matrix-core kernels at the same shape (Q/K/V as f32, f32 scores)
+        ("gqa_qk_f32 [1,15,4096,4096]", (15 + 5) * tok * 64 * 4 + n_scores * 4,
+         lambda: ctx.gqa_qk(q32, k32, None, scores32)),
+        ("gqa_pv_f32 [1,15,4096,64]", n_scores * 4 + (5 + 15) * tok * 64 * 4,
+         lambda: ctx.gqa_pv(scores32, v32, o32)),
+        ("attention_f32 fused [1,15,4096,64] causal (inputs + output)", attn_io * 2,
+         lambda: ctx.attention(q32, k32, v32, 0.125, 0, None, o32)),
     ]:
         for _ in range(3):
             ctx.begin()
