@@ -22,6 +22,9 @@
 //    32 x 128 probabilities in LDS (whole 256-byte row segments per 16
 //    lanes), V goes through LDS row-major and its transposed operand comes
 //    from ds_read_b64_tr_b16; the next step's loads are in flight meanwhile.
+//    Rows on the line grid are walked from a step that differs per
+//    workgroup (walk_step), so that the workgroups do not all read one
+//    column range at once.
 // f32 takes v_mfma_f32_32x32x2_f32 with the same workgroups (the f32
 // kernels below); other head sizes take row kernels on the vector ALUs.
 #include "common.hpp"
@@ -238,6 +241,25 @@ __global__ __launch_bounds__(512) void k_gqa_qk_mfma(const half_t* __restrict__ 
 
 // -------------------------------------------------------------- P V, MFMA
 
+// Step i of a P V workgroup's walk over its `steps` key steps.  With ROTATE,
+// workgroup b starts at step b mod steps and wraps: in key order every
+// resident workgroup reads the same 256-byte column range of its
+// probability rows at once (rows 8 KB apart at 4096 keys), which some
+// placements of the rows in HBM serve far slower ([15, 4096, 4096] x
+// [5, 4096, 64] f16 on two hipMalloc'd probability tensors: 100 us in key
+// order, 88 us rotated; in key order the same launch has taken 86-107 us
+// from box to box).  Rows off the line grid keep key order (rotated:
+// 4093 keys 134.5 against 122.9 us).  Each output is still one fixed-order
+// f32 sum (its order depends only on the workgroup), so results repeat
+// exactly from run to run; sums of exactly representable products do not
+// depend on the order at all.
+template <bool ROTATE>
+__device__ inline uint32_t walk_step(uint32_t i, uint32_t steps) {
+    if constexpr (!ROTATE) return i;
+    const uint32_t s = i + blockIdx.x % steps;
+    return s >= steps ? s - steps : s;
+}
+
 // Rows of kv_len % 8 != 0 probabilities start off the 16-byte grid; their
 // chunks are read as unaligned 16-byte loads (get_scores_u), a row's last
 // partial chunk element by element.
@@ -318,16 +340,16 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
 
     const uint32_t blocks = (p.kv_len + BN - 1) / BN;
     h8 pnext[P_LOADS], vnext[LOADS];
-    load_p(0, pnext);
-    load_v(0, vnext);
+    load_p(walk_step<STREAM>(0, blocks), pnext);
+    load_v(walk_step<STREAM>(0, blocks), vnext);
     store_p(0, pnext);
     store_v(vnext);
     __syncthreads();
     for (uint32_t blk = 0; blk < blocks; ++blk) {
         const bool more = blk + 1 < blocks;
         if (more) {  // next step's operands in flight during this step's products
-            load_p(blk + 1, pnext);
-            load_v(blk + 1, vnext);
+            load_p(walk_step<STREAM>(blk + 1, blocks), pnext);
+            load_v(walk_step<STREAM>(blk + 1, blocks), vnext);
         }
 #pragma unroll
         for (int c = 0; c < PC; ++c) {
