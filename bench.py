@@ -621,10 +621,13 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
     return rows
 
 
-def fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20):
+def fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20, per_graph=4):
     """One SmolLM2-360M layer's non-projection work with the attention fused:
     RMSNorm, Q/K rotation + K/V append (one launch), the fused attention core,
-    SwiGLU, residual add -- 5 launches as one graph.  Bytes are the launches'
+    SwiGLU, residual add -- 5 launches.  `us`: the layers launched back to
+    back on rotated buffer sets, events around them (as the headline chain);
+    `us_graph_batch`: the same recorded as graphs of `per_graph` layers (one
+    kernel per op), replayed round-robin.  Bytes are the launches'
     algorithmic bytes (the attention counted by its inputs and output)."""
     qdims, qstrides = [1, qh, tok, hd], [tok * qh * hd, hd, qh * hd, 1]
     kdims, kstrides = [1, kvh, tok, hd], [tok * kvh * hd, hd, kvh * hd, 1]
@@ -657,18 +660,31 @@ def fused_layer_row(ctx, hid, qh, kvh, hd, ffn, tok, wn, dc, ds, sets=2, reps=20
         ctx.add(b["xn"], b["r"], b["o"])
 
     bufs = [make(i) for i in range(sets)]
-    graphs = [capture(ctx, lambda b=b: layer(b)) for b in bufs]
-    ms = time_graphs(ctx, graphs, 1, reps)
+    for i in range(2 * sets):  # warm-up
+        layer(bufs[i % sets])
+    ctx.finish()
+    start, end = ctx.event(), ctx.event()
+    ctx.record(start)
+    for i in range(reps):
+        layer(bufs[i % sets])
+    ctx.record(end)
+    us = ctx.elapsed_ms(start, end) * 1e3 / reps
+    ctx.destroy_event(start)
+    ctx.destroy_event(end)
+    graphs = [capture(ctx, lambda g=g: [layer(bufs[(g + j) % sets]) for j in range(per_graph)])
+              for g in range(sets)]
+    us_graph = time_graphs(ctx, graphs, per_graph, max(1, reps // per_graph)) * 1e3
     ctx.finish()
     for g in graphs:
         ctx.graph_destroy(g)
-    us = ms * 1e3
-    log(f"  {'layer with fused attention (5 launches)':34s} {us:9.2f} us")
-    return {"op": "layer with fused attention (5 launches, one graph)", "dtype": "f16",
+    log(f"  {'layer with fused attention (5 launches)':34s} {us:9.2f} us  "
+        f"graphs of {per_graph} layers {us_graph:7.2f} us/layer")
+    gb, gbg = nbytes / (us * 1e-6) / 1e9, nbytes / (us_graph * 1e-6) / 1e9
+    return {"op": "layer with fused attention (5 launches)", "dtype": "f16",
             "shape": [tok, hid], "bytes": nbytes, "us": round(us, 3), "us_min": None,
-            "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_GBS, 1),
-            "us_graph_batch": None, "GB/s_graph_batch": None, "pct_peak_graph_batch": None}
+            "GB/s": round(gb, 1), "pct_peak": round(100 * gb / PEAK_GBS, 1),
+            "us_graph_batch": round(us_graph, 3), "GB/s_graph_batch": round(gbg, 1),
+            "pct_peak_graph_batch": round(100 * gbg / PEAK_GBS, 1)}
 
 
 # ------------------------------------------- the headline: one layer's chain
@@ -824,19 +840,23 @@ def time_chain(ctx, chain, sets, steps, warmup):
     return ms / steps, sm_us
 
 
-def time_chain_graphs(ctx, chain, sets, steps, warmup):
-    """ms per step with each set's chain recorded as a graph (recorded
-    streaming ops fused, the library's default) and the graphs replayed
-    round-robin.  The graphs stay alive until the process ends."""
+def time_chain_graphs(ctx, chain, sets, steps, warmup, per_graph=4):
+    """ms per step with the chain recorded as graphs of `per_graph` steps
+    each (step j of a graph on set j mod len(sets); recorded streaming ops
+    fused, the library's default) and the graphs replayed round-robin.  A
+    graph launch costs ~9 us before its first kernel starts, so one step per
+    graph would add that to every step.  The graphs stay alive until the
+    process ends."""
     graphs = []
-    for b in sets:
+    for g in range(len(sets)):
         ctx.capture_begin()
         try:
-            chain.launch(b)
+            for j in range(per_graph):
+                chain.launch(sets[(g + j) % len(sets)])
         finally:
             graphs.append(ctx.capture_end())
     _LIVE_GRAPHS.extend(graphs)
-    ms = time_graphs(ctx, graphs, 1, steps, warmup=warmup)
+    ms = time_graphs(ctx, graphs, per_graph, max(1, steps // per_graph), warmup=warmup)
     ctx.finish()
     return ms
 
