@@ -169,6 +169,8 @@ GQA_SHAPES = [  # batch, q_heads, kv_heads, q_len, kv_len, capacity, head_dim
     (1, 15, 5, 200, 1001, 1024, 64),  # odd key count: rows off the 16-byte grid, 8 key tiles
     (2, 4, 2, 129, 259, 264, 128),    # batch 2, key count 3 mod 8, ragged query tiles
     (1, 6, 3, 33, 130, 136, 32),      # key count 2 mod 8: a last tile of 2 keys
+    (1, 15, 5, 300, 1024, 1024, 64),  # rows on the line grid: PV walks 8 key steps from a
+    (2, 6, 3, 129, 640, 704, 128),    # per-workgroup start (5 steps here), batch 2
 ]
 
 
@@ -226,7 +228,8 @@ def test_gqa_small_integers_match_the_oracle_bit_for_bit(ctx, dtype):
     """Small-integer operands make every sum exact: the library (matrix cores
     or row kernels) and the oracle agree exactly -- also where the key count
     puts the score rows off the 16-byte grid (every element in its place)."""
-    for hd, ql, kl in ((64, 40, 72), (48, 40, 72), (64, 130, 301), (128, 70, 1003), (32, 5, 9)):
+    for hd, ql, kl in ((64, 40, 72), (48, 40, 72), (64, 130, 301), (128, 70, 1003), (32, 5, 9),
+                       (64, 300, 1024), (128, 130, 384)):  # line-grid rows: rotated PV walks
         q = (np.arange(1 * 6 * ql * hd) % 7 - 3).reshape(1, 6, ql, hd).astype(dtype)
         k = (np.arange(1 * 2 * kl * hd) % 5 - 2).reshape(1, 2, kl, hd).astype(dtype)
         ctx.begin()
