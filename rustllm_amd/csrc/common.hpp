@@ -376,6 +376,13 @@ __device__ inline typename VecOf<T, N>::type load_stream_u(const T* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const U*>(p));
 }
 
+// A plain (cached) load of such a pack.
+template <typename T, int N>
+__device__ inline typename VecOf<T, N>::type load_u(const T* p) {
+    typedef typename VecOfU<T, N>::type U;
+    return *reinterpret_cast<const U*>(p);
+}
+
 template <typename T, int N>
 __device__ inline void store_stream_u(T* p, typename VecOf<T, N>::type v) {
     typedef typename VecOfU<T, N>::type U;
