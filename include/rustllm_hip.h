@@ -26,7 +26,13 @@
  *  - Output buffers are passed in by the caller, allocated with
  *    rl_buffer_empty() exactly where the reference calls MetalBuffer::empty /
  *    empty_with_element_size (src/metal/buffer.rs:111-142).  Each op checks
- *    the output's len and byte_len.
+ *    the output's len and byte_len.  The reference always writes a fresh
+ *    buffer; here an output may also be the very buffer of an input (same
+ *    data pointer and length) for add, mul, SiLU, SwiGLU, the bias add,
+ *    RMSNorm and add + RMSNorm, softmax, scale/mask and the fused scale/mask
+ *    + softmax, and RoPE -- each reads all it writes first.  For every other
+ *    op, and for outputs that overlap an input only in part, the output must
+ *    not overlap the inputs.
  *  - f16 is IEEE binary16.  All arithmetic is float32; f16 results are
  *    rounded to nearest even.
  *  - One context per thread; a context is not thread-safe (MetalContext is

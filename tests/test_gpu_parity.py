@@ -948,3 +948,76 @@ def test_pool_reuses_released_blocks(ctx):
     second = ctx.empty((n,), np.float32)
     assert second.ptr == addr
     del held
+
+
+# ------------------------------------------------------ outputs over inputs
+
+def _in_place_cases(ctx, dtype, rows, width):
+    """(name, fresh-input factory, op on given buffers) for every op whose
+    output may be the very buffer of an input: the element-wise maps, the
+    bias add, and the row ops."""
+    x = norm(("inplace-x",), (rows, width), dtype)
+    y = norm(("inplace-y",), (rows, width), dtype)
+    bias = norm(("inplace-b",), (width,), dtype)
+    w = synth.uniform_range(synth.seed_for("inplace-w", width), (width,), 0.5, 1.5, dtype)
+    s = norm(("inplace-s",), (rows, width), dtype, 0.0, 2.0)
+    up = ctx.upload
+    masks = [] if rows > width else [
+        ("scale/mask", lambda: (up(s),),
+         lambda a, out: ctx.scale_mask(a, 0.125, width - rows, out), 0),
+        ("scale/mask + softmax", lambda: (up(s),),
+         lambda a, out: ctx.attention_softmax(a, 0.125, width - rows, out), 0)]
+    return masks + [
+        ("add, out = a", lambda: (up(x), up(y)), lambda a, b, out: ctx.add(a, b, out), 0),
+        ("add, out = b", lambda: (up(x), up(y)), lambda a, b, out: ctx.add(a, b, out), 1),
+        ("mul, out = a", lambda: (up(x), up(y)), lambda a, b, out: ctx.mul(a, b, out), 0),
+        ("SwiGLU, out = gate", lambda: (up(x), up(y)), lambda a, b, out: ctx.swiglu(a, b, out), 0),
+        ("SwiGLU, out = up", lambda: (up(x), up(y)), lambda a, b, out: ctx.swiglu(a, b, out), 1),
+        ("SiLU", lambda: (up(x),), lambda a, out: ctx.silu(a, out), 0),
+        ("bias add", lambda: (up(x), up(bias)), lambda a, b, out: ctx.add_broadcast(a, b, out), 0),
+        ("RMSNorm", lambda: (up(x), up(w)), lambda a, b, out: ctx.rmsnorm(a, b, 1e-5, out), 0),
+        ("softmax", lambda: (up(s),), lambda a, out: ctx.softmax(a, out), 0),
+    ]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("rows,width", [(33, 1001), (16, 4096), (3, 9003), (4096, 1536)])
+def test_outputs_over_inputs(ctx, dtype, rows, width):
+    """An output passed as the very buffer of one of its inputs (out == a,
+    which the ABI accepts for these ops) gives the same bits as a separate
+    output: each lane group reads everything it writes before writing it
+    (rows held in registers, packs stored by the lane that loaded them).
+    Ragged widths, partial last blocks and the streaming softmax (9003 f32
+    columns) included."""
+    for name, make, op, which in _in_place_cases(ctx, dtype, rows, width):
+        ins = make()
+        ref = run(ctx, lambda: op(*ins, ctx.empty(ins[which].shape, dtype))).numpy()
+        ins = make()
+        run(ctx, lambda: op(*ins, ins[which]))
+        assert_bitexact(ins[which].numpy(), ref, f"{name} in place, {dtype.__name__} [{rows}, {width}]")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("shape", [(1, 15, 4096, 64), (2, 3, 7, 6), (1, 2, 33, 128)])
+def test_rope_and_add_rmsnorm_over_inputs(ctx, dtype, shape):
+    """RoPE written over its input, and add + RMSNorm writing the sum over x
+    and the normalised rows over the residual: the same bits as separate
+    outputs."""
+    c, s = o.rope_table(shape[-1], shape[-2] + 8, 10000.0)
+    dc, ds = ctx.upload(c), ctx.upload(s)
+    x = norm(("inplace-rope",), shape, dtype)
+    ref = run(ctx, lambda: ctx.rope(ctx.upload(x), dc, ds, 3)).numpy()
+    d = ctx.upload(x)
+    run(ctx, lambda: ctx.rope(d, dc, ds, 3, d))
+    assert_bitexact(d.numpy(), ref, f"rope in place {shape}")
+    h = shape[-1]
+    rows = int(np.prod(shape[:-1]))
+    a = norm(("inplace-ar-x",), (rows, h), dtype)
+    r = norm(("inplace-ar-r",), (rows, h), dtype)
+    wt = ctx.upload(synth.uniform_range(synth.seed_for("inplace-ar-w", h), (h,), 0.5, 1.5, dtype))
+    s_ref, y_ref = run(ctx, lambda: ctx.add_rmsnorm(ctx.upload(a), ctx.upload(r), wt, 1e-5))
+    s_ref, y_ref = s_ref.numpy(), y_ref.numpy()
+    da, dr = ctx.upload(a), ctx.upload(r)
+    run(ctx, lambda: ctx.add_rmsnorm(da, dr, wt, 1e-5, sum_out=da, norm_out=dr))
+    assert_bitexact(da.numpy(), s_ref, f"add + rmsnorm sum over x {shape}")
+    assert_bitexact(dr.numpy(), y_ref, f"add + rmsnorm rows over the residual {shape}")
