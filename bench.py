@@ -1296,7 +1296,7 @@ def main():
     ap.add_argument("--no-graph-batch", action="store_true",
                     help="leave out the graph-replayed figures (sustained per-op times, the "
                          "chain and the batch step as graphs)")
-    ap.add_argument("--per-op-out", default=os.path.join(ROOT, "gpurun_out", "bench_per_op.json"),
+    ap.add_argument("--per-op-out", default=os.path.join(ROOT, "bench_out", "bench_per_op.json"),
                     help="file the full per-op table is written to")
     ap.add_argument("--per-op-only", action="store_true",
                     help="only the per-op table, written to --per-op-out (the child process "
