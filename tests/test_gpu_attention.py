@@ -259,6 +259,23 @@ def test_gqa_qk_large_grids_bit_for_bit(ctx, hd, ql, kl, dtype):
     assert np.array_equal(s.numpy(), o.gqa_qk(q, k))
 
 
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_gqa_qk_every_key_residue_bit_for_bit(ctx, hd):
+    """f16 score rows of every key count residue mod 8 (a row then starts r
+    scores past the 16-byte grid for r = row kv_len mod 8): each row segment
+    goes out in the buffer's aligned chunks, the chunks it shares with the
+    neighbouring segment element by element -- every score in its place and
+    no neighbour overwritten, at partial query and key tiles."""
+    for kl in (1024, 1025, 1026, 1027, 1028, 1029, 1030, 1031, 129, 250, 7):
+        ql = 97 if kl > 200 else 40
+        q = (np.arange(1 * 6 * ql * hd) % 7 - 3).reshape(1, 6, ql, hd).astype(np.float16)
+        k = (np.arange(1 * 2 * kl * hd) % 5 - 2).reshape(1, 2, kl, hd).astype(np.float16)
+        ctx.begin()
+        s = ctx.gqa_qk(ctx.upload(q), ctx.upload(k))
+        ctx.finish()
+        assert np.array_equal(s.numpy(), o.gqa_qk(q, k)), f"hd {hd}, {kl} keys"
+
+
 def test_unfused_chain_f16_within_the_reference_bound(ctx):
     """The reference's four calls on the library (gqa_qk, scale/mask +
     softmax, gqa_pv) with the reference's rounding points stay within the
