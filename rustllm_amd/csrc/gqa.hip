@@ -244,15 +244,15 @@ __global__ __launch_bounds__(512) void k_gqa_qk_mfma(const half_t* __restrict__ 
 // Step i of a P V workgroup's walk over its `steps` key steps.  With ROTATE,
 // workgroup b starts at step b mod steps and wraps: in key order every
 // resident workgroup reads the same 256-byte column range of its
-// probability rows at once (rows 8 KB apart at 4096 keys), which some
-// placements of the rows in HBM serve far slower ([15, 4096, 4096] x
-// [5, 4096, 64] f16 on two hipMalloc'd probability tensors: 100 us in key
-// order, 88 us rotated; in key order the same launch has taken 86-107 us
-// from box to box).  Rows off the line grid keep key order (rotated:
-// 4093 keys 134.5 against 122.9 us).  Each output is still one fixed-order
-// f32 sum (its order depends only on the workgroup), so results repeat
-// exactly from run to run; sums of exactly representable products do not
-// depend on the order at all.
+// probability rows at once, which rows 4 or 8 KB apart (2048 or 4096 f16
+// keys) alias onto few HBM channels once about two workgroups a CU are in
+// flight ([15, 4096, 4096] x [5, 4096, 64] f16: 100 us in key order, 88 us
+// rotated; 32 heads x [2048, 4096]: 120 against 99 us).  Other row strides,
+// and grids of fewer workgroups, walk faster in key order (15 heads x
+// [2048, 4096]: 60 against 68.5 us; [4608, 4608]: 145 against 165 us).
+// Each output is still one fixed-order f32 sum (its order depends only on
+// the workgroup), so results repeat exactly from run to run; sums of exactly
+// representable products do not depend on the order at all.
 template <bool ROTATE>
 __device__ inline uint32_t walk_step(uint32_t i, uint32_t steps) {
     if constexpr (!ROTATE) return i;
@@ -262,8 +262,9 @@ __device__ inline uint32_t walk_step(uint32_t i, uint32_t steps) {
 
 // Rows of kv_len % 8 != 0 probabilities start off the 16-byte grid; their
 // chunks are read as unaligned 16-byte loads (get_scores_u), a row's last
-// partial chunk element by element.
-template <int NT, bool STREAM>
+// partial chunk element by element.  STREAM: non-temporal loads (rows on
+// the 128-byte line grid only); ROTATE: the staggered walk (walk_step).
+template <int NT, bool STREAM, bool ROTATE>
 __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ probs,
                                                      const half_t* __restrict__ v,
                                                      half_t* __restrict__ out, GqaParams p) {
@@ -340,16 +341,16 @@ __global__ __launch_bounds__(256) void k_gqa_pv_mfma(const half_t* __restrict__ 
 
     const uint32_t blocks = (p.kv_len + BN - 1) / BN;
     h8 pnext[P_LOADS], vnext[LOADS];
-    load_p(walk_step<STREAM>(0, blocks), pnext);
-    load_v(walk_step<STREAM>(0, blocks), vnext);
+    load_p(walk_step<ROTATE>(0, blocks), pnext);
+    load_v(walk_step<ROTATE>(0, blocks), vnext);
     store_p(0, pnext);
     store_v(vnext);
     __syncthreads();
     for (uint32_t blk = 0; blk < blocks; ++blk) {
         const bool more = blk + 1 < blocks;
         if (more) {  // next step's operands in flight during this step's products
-            load_p(walk_step<STREAM>(blk + 1, blocks), pnext);
-            load_v(walk_step<STREAM>(blk + 1, blocks), vnext);
+            load_p(walk_step<ROTATE>(blk + 1, blocks), pnext);
+            load_v(walk_step<ROTATE>(blk + 1, blocks), vnext);
         }
 #pragma unroll
         for (int c = 0; c < PC; ++c) {
@@ -877,12 +878,23 @@ rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, co
             if (grid > UINT32_MAX) return fail(RL_ERR_INVALID_SHAPE, "GQA PV grid exceeds u32");
             const dim3 g(static_cast<unsigned>(grid)), b(256);
             const bool lines = s.kv_len % 64 == 0;  // probability rows are whole 128-byte lines
+            // the staggered walk for rows 4 or 8 KB apart with >= 15/8
+            // workgroups a CU; streamed loads for line-grid rows when
+            // rotating or past 160 MB of probabilities (measured over 37
+            // shapes: below that the MALL keeps part of them between
+            // launches and plain loads win, 1024 x 4096 keys 60 -> 48 us)
+            const uint64_t row_bytes = s.kv_len * sizeof(T);
+            const bool rotate = lines && (row_bytes == 4096 || row_bytes == 8192) &&
+                                grid * 8 >= uint64_t(15) * uint64_t(ctx->num_cus);
+            const bool stream = lines && (rotate || plen * sizeof(T) > (uint64_t(160) << 20));
 #define RL_PV(NT)                                                                      \
     do {                                                                               \
-        if (lines)                                                                     \
-            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true>), g, b, pd, vd, od, p);            \
+        if (rotate)                                                                    \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true, true>), g, b, pd, vd, od, p);      \
+        else if (stream)                                                               \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, true, false>), g, b, pd, vd, od, p);     \
         else                                                                           \
-            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false>), g, b, pd, vd, od, p);           \
+            RL_LAUNCH(ctx, (k_gqa_pv_mfma<NT, false, false>), g, b, pd, vd, od, p);    \
     } while (0)
             switch (s.head_dim / 32) {
                 case 1: RL_PV(1); break;

@@ -229,7 +229,7 @@ def test_gqa_small_integers_match_the_oracle_bit_for_bit(ctx, dtype):
     or row kernels) and the oracle agree exactly -- also where the key count
     puts the score rows off the 16-byte grid (every element in its place)."""
     for hd, ql, kl in ((64, 40, 72), (48, 40, 72), (64, 130, 301), (128, 70, 1003), (32, 5, 9),
-                       (64, 300, 1024), (128, 130, 384)):  # line-grid rows: rotated PV walks
+                       (64, 300, 1024), (128, 130, 384)):  # line-grid rows, small grids: key order
         q = (np.arange(1 * 6 * ql * hd) % 7 - 3).reshape(1, 6, ql, hd).astype(dtype)
         k = (np.arange(1 * 2 * kl * hd) % 5 - 2).reshape(1, 2, kl, hd).astype(dtype)
         ctx.begin()
@@ -238,6 +238,28 @@ def test_gqa_small_integers_match_the_oracle_bit_for_bit(ctx, dtype):
         ctx.finish()
         assert np.array_equal(s.numpy(), o.gqa_qk(q, k))
         assert np.array_equal(pv.numpy(), o.gqa_pv((o.gqa_qk(q, k) / 64).astype(dtype), k))
+
+
+@pytest.mark.parametrize("kl,walk", [(2048, "rotated"), (1536, "key order, streamed")])
+def test_gqa_pv_line_grid_walks_bit_for_bit(ctx, kl, walk):
+    """P V f16 over probability rows on the 128-byte line grid at the sizes
+    where the matrix-core kernel changes its walk: rows 4 KB apart with 480
+    workgroups (16 heads x 30 query tiles, about two a CU) start each
+    workgroup's key walk at its own step; 3 KB rows over 189 MB of
+    probabilities walk in key order with streamed loads.  Small-integer
+    operands make every sum exact, so the result is the float64 product
+    rounded once to f16, element for element (the oracle's own arithmetic
+    at this size would take minutes on the host)."""
+    qh, kvh, ql, hd = 16, 4, 3840, 64
+    p = ((np.arange(qh * ql * kl, dtype=np.int64) % 7 - 3) / 64).astype(np.float16)
+    p = p.reshape(1, qh, ql, kl)
+    v = (np.arange(kvh * kl * hd) % 5 - 2).reshape(1, kvh, kl, hd).astype(np.float16)
+    ctx.begin()
+    got = ctx.gqa_pv(ctx.upload(p), ctx.upload(v)).numpy()
+    ctx.finish()
+    for h in range(qh):
+        want = (p[0, h].astype(np.float64) @ v[0, h // (qh // kvh)].astype(np.float64))
+        assert np.array_equal(got[0, h], want.astype(np.float16)), f"{walk}: head {h}"
 
 
 @pytest.mark.parametrize("dtype", [np.float16, np.float32])
