@@ -880,13 +880,12 @@ rl_status pv_entry(rl_context* ctx, const char* name, const rl_buffer* probs, co
             const bool lines = s.kv_len % 64 == 0;  // probability rows are whole 128-byte lines
             // the staggered walk for rows 4 or 8 KB apart with >= 15/8
             // workgroups a CU; streamed loads for line-grid rows when
-            // rotating or past 160 MB of probabilities (measured over 37
-            // shapes: below that the MALL keeps part of them between
-            // launches and plain loads win, 1024 x 4096 keys 60 -> 48 us)
+            // rotating or past kStreamReadBytes of probabilities (measured
+            // over 37 shapes)
             const uint64_t row_bytes = s.kv_len * sizeof(T);
             const bool rotate = lines && (row_bytes == 4096 || row_bytes == 8192) &&
                                 grid * 8 >= uint64_t(15) * uint64_t(ctx->num_cus);
-            const bool stream = lines && (rotate || plen * sizeof(T) > (uint64_t(160) << 20));
+            const bool stream = lines && (rotate || plen * sizeof(T) > kStreamReadBytes);
 #define RL_PV(NT)                                                                      \
     do {                                                                               \
         if (rotate)                                                                    \

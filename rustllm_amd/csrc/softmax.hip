@@ -303,7 +303,10 @@ __device__ inline float exp_packs(const h2v (&s)[NV][4], float (&ev)[NV][8], flo
     return sum;
 }
 
-template <int NV, int TPR, bool MASK, bool RAGGED>
+// CACHED: rows on the 16-byte grid read with plain loads (a launch reading
+// less than kStreamReadBytes); otherwise streamed.  Ragged rows always load
+// plainly.
+template <int NV, int TPR, bool MASK, bool RAGGED, bool CACHED>
 __global__ __launch_bounds__(kThreads) void k_softmax_rows_h2(const half_t* __restrict__ in,
                                                               half_t* __restrict__ out,
                                                               uint32_t row_base, uint32_t rows,
@@ -345,6 +348,8 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_h2(const half_t* __re
                 const uint64_t off = e0 + uint64_t(q) * N;
                 moved[k] = off + N > total;  // the buffer's last pack
                 raw[k] = load_u<half_t, N>(in + (moved[k] ? total - N : off));
+            } else if constexpr (CACHED) {
+                raw[k] = src[q];
             } else {
                 raw[k] = load_stream(src + q);
             }
@@ -565,6 +570,17 @@ __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ i
 
 // ---------------------------------------------------------------- launch
 
+// Elements a softmax launch reads: every row's kept keys (query qi of a
+// masked row keeps min(width, start + qi + 1)), summed per query_len rows.
+inline uint64_t softmax_read_bytes(uint64_t rows, uint64_t width, const MaskParams& mp,
+                                   bool mask) {
+    if (!mask) return rows * width;
+    const uint64_t q = mp.query_len.divisor, a = uint64_t(mp.start) + 1;
+    const uint64_t open = a > width ? 0 : std::min<uint64_t>(q, width - a + 1);  // unclamped
+    const uint64_t per_group = open * a + open * (open - 1) / 2 + (q - open) * width;
+    return (rows / q) * per_group + (rows % q) * width;
+}
+
 // Blocks for a grid-stride loop over `items` (rows or row groups).
 inline unsigned row_grid(uint64_t items) {
     return unsigned(items < (uint64_t(1) << 20) ? items : (uint64_t(1) << 20));
@@ -587,7 +603,9 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
     const uint64_t w_packs = ceil_div(width, N);
     const dim3 block(kThreads);
     // f16 rows whose scale is an f16 value take the first pass on pairs
-    // (k_softmax_rows_h2); the plain softmax's scale is 1.
+    // (k_softmax_rows_h2); the plain softmax's scale is 1.  Its rows on the
+    // 16-byte grid load plainly when the launch reads little (kept keys only).
+    const bool cached = softmax_read_bytes(rows, width, mp, MASK) * sizeof(T) <= kStreamReadBytes;
     bool pairs = false;
     h2v scale2 = {half_t(1.0f), half_t(1.0f)};
     if constexpr (sizeof(T) == 2) {
@@ -602,9 +620,14 @@ rl_status launch_softmax(rl_context* ctx, const char* name, const T* in, T* out,
             const uint64_t left = ceil_div(rows - base, kThreads / TPR);                         \
             const dim3 grid(unsigned(left < (uint64_t(1) << 30) ? left : (uint64_t(1) << 30)));  \
             if constexpr (sizeof(T) == 2) {                                                      \
+                if (pairs && !R && cached) {                                                     \
+                    RL_LAUNCH(ctx, (k_softmax_rows_h2<NV, TPR, MASK, R, true>), grid, block, in, \
+                              out, uint32_t(base), r32, w32, mp, scale2);                        \
+                    continue;                                                                    \
+                }                                                                                \
                 if (pairs) {                                                                     \
-                    RL_LAUNCH(ctx, (k_softmax_rows_h2<NV, TPR, MASK, R>), grid, block, in, out,  \
-                              uint32_t(base), r32, w32, mp, scale2);                             \
+                    RL_LAUNCH(ctx, (k_softmax_rows_h2<NV, TPR, MASK, R, false>), grid, block,    \
+                              in, out, uint32_t(base), r32, w32, mp, scale2);                    \
                     continue;                                                                    \
                 }                                                                                \
             }                                                                                    \
