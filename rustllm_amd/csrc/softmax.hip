@@ -520,6 +520,11 @@ __global__ __launch_bounds__(kThreads) void k_softmax_stream(const T* __restrict
 // ------------------------------------------------------ scale/mask alone
 
 // RAGGED: rows on the buffer's 16-byte pack grid as in k_softmax_rows.
+// Plain loads, streamed stores.  Streamed loads never won: level or slower
+// with the input cold or just written by a producer's streamed stores, and
+// far slower after a producer's plain stores -- how QK^T writes rows off the
+// 128-byte line grid ([15, 4093, 4093] f16 171.7 -> 155.7 us, 4088 keys
+// 161 -> 140, [15, 2047, 2047] cold 45 -> 35 us).
 template <typename T, int N, bool RAGGED>
 __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ in,
                                                          T* __restrict__ out, uint32_t rows,
@@ -539,7 +544,7 @@ __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ i
                 // lies in the buffer, this row's elements written one by one
                 V raw = {};
                 if (e0 - lead + uint64_t(p + 1) * N <= uint64_t(rows) * width) {
-                    raw = load_stream(src + p);
+                    raw = src[p];
                 } else {
 #pragma unroll
                     for (int j = 0; j < N; ++j)
@@ -558,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void k_scale_mask(const T* __restrict__ i
             }
             V o;
             if (p * N < kept + lead) {
-                V raw = load_stream(src + p);
+                V raw = src[p];
 #pragma unroll
                 for (int j = 0; j < N; ++j)
                     o[j] = (p * N + j < kept + lead) ? scale_to<T>(raw[j], mp.scale)
