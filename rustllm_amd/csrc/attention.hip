@@ -60,6 +60,9 @@ struct AttnParams {
     uint64_t kv_head_stride;  // elements between KV heads (kv_capacity * head_dim)
     float scale;           // attention scale
     float scale_log2;      // scale * log2(e)
+    uint32_t kchunks;      // key chunks per query tile (f16 MFMA kernel, PARTIAL)
+    float* part;           // PARTIAL: unnormalised outputs, [tile unit][query][head_dim]
+    float* part_ml;        // PARTIAL: (max in log2 units, sum) per [tile unit][query]
 };
 
 // ------------------------------------------------------------- MFMA kernel
@@ -138,7 +141,7 @@ constexpr float kRescaleSlack = 3.0f;
 // Otherwise blocks pass through registers into rows padded for the bank
 // layout (head size 96, whose 12 chunks a row do not swizzle onto 64 banks),
 // one block at a time.
-template <int NT, int QW, int KSPLIT, int BN, bool DMA>
+template <int NT, int QW, int KSPLIT, int BN, bool DMA, bool PARTIAL = false>
 __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
     half_t* __restrict__ out, AttnParams p) {
@@ -172,8 +175,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
     __shared__ __align__(16) unsigned char lds[LDS_BYTES];
     half_t* const kv_lds = reinterpret_cast<half_t*>(lds);
 
-    const uint32_t bh = blockIdx.x / p.pairs;
-    const uint32_t pair = blockIdx.x % p.pairs;
+    // PARTIAL: workgroup b takes key chunk b mod kchunks of its tile pair
+    // (the chunks of one pair are neighbours in the grid: one KV head)
+    const uint32_t chunk = PARTIAL ? blockIdx.x % p.kchunks : 0u;
+    const uint32_t unit_blk = PARTIAL ? blockIdx.x / p.kchunks : blockIdx.x;
+    const uint32_t bh = unit_blk / p.pairs;
+    const uint32_t pair = unit_blk % p.pairs;
     const uint32_t kv_heads = p.q_heads / p.group;
     const uint32_t kv_head = (bh / p.q_heads) * kv_heads + (bh % p.q_heads) / p.group;
     const half_t* kh = k + uint64_t(kv_head) * p.kv_head_stride;
@@ -238,6 +245,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
         const uint32_t keys = min(p.kv_len, p.start + q_last + 1);
         const uint32_t blocks = (keys + BN - 1) / BN;
         const uint32_t steps = (blocks + KSPLIT - 1) / KSPLIT;
+        // PARTIAL: this workgroup's share of the tile's steps, [s_begin, s_end)
+        const uint32_t s_begin = PARTIAL ? uint32_t(uint64_t(steps) * chunk / p.kchunks) : 0u;
+        const uint32_t s_end =
+            PARTIAL ? uint32_t(uint64_t(steps) * (chunk + 1) / p.kchunks) : steps;
 
         const uint32_t qw0 = q_first + qw * 32;  // first query of this wave
         const bool wave_active = qw0 < p.q_len;
@@ -330,11 +341,11 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
         };
 
         if constexpr (DMA) {
-            issue_step(0);
+            if (s_begin < s_end) issue_step(s_begin);
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         } else {
-            load_step(0);
+            load_step(s_begin);
             __syncthreads();  // the previous tile's LDS use is over
             store_step(0);
             __syncthreads();
@@ -343,11 +354,11 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
         // DMA: the blocks of step j + 1 stream into the other stage while
         // step j is computed (one barrier per step).  Otherwise they wait in
         // registers and are stored after the step's compute.
-        for (uint32_t step = 0; step < steps; ++step) {
+        for (uint32_t step = s_begin; step < s_end; ++step) {
             if constexpr (DMA) {
-                issue_step(step + 1);  // nothing past the last block
+                if (step + 1 < s_end) issue_step(step + 1);  // nothing past the last block
             } else {
-                if (step + 1 < steps) load_step(step + 1);
+                if (step + 1 < s_end) load_step(step + 1);
             }
             const uint32_t blk = step * KSPLIT + sub;
             const half_t* ks = kv_lds + ((step % NSTAGE) * KSPLIT + sub) * KV_HALVES;
@@ -434,7 +445,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                 __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed
             } else {
                 __syncthreads();
-                if (step + 1 < steps) store_step(0);
+                if (step + 1 < s_end) store_step(0);
             }
             __syncthreads();
         }
@@ -472,7 +483,26 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
             __syncthreads();  // the merge area is free again
         }
 
-        if (sub == 0) {
+        if (PARTIAL && sub == 0) {
+            // the chunk's (max, sum) and unnormalised f32 output of each query,
+            // merged by k_flash_combine
+            const float l_row = l + __shfl_xor(l, 32, 64);  // both halves of the query
+            if (q_valid) {
+                const uint64_t prow =
+                    ((uint64_t(bh) * p.tiles + tile) * p.kchunks + chunk) * TILE_Q + (qi - q_first);
+                float* po = p.part + prow * D + 4 * hs;
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        *reinterpret_cast<f32x4*>(po + t * 32 + 8 * g) =
+                            f32x4{o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]};
+                if (hs == 0) {
+                    p.part_ml[2 * prow] = m;
+                    p.part_ml[2 * prow + 1] = l_row;
+                }
+            }
+        } else if (sub == 0) {
             const float inv = 1.0f / (l + __shfl_xor(l, 32, 64));  // both halves of the query
             if (q_valid) {
                 // register r of tile t: element 32t + 8(r / 4) + 4hs + r % 4
@@ -489,6 +519,55 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
                 }
             }
         }
+    }
+}
+
+// The key chunks of a split launch of k_flash_attention merged, per query:
+// every chunk's (max m_c, sum l_c, unnormalised output o_c) rescaled to the
+// largest max M, out = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c (the
+// key-share merge of the kernel itself, over kchunks <= kFlashMaxChunks).
+// Workgroup = one query tile of a head; thread item = (query, 4 head
+// elements), 16-byte pieces of a row on consecutive lanes.  Every chunk's
+// loads are issued before any is used.  Some chunk holds key 0, which every
+// query sees, so M is finite.
+constexpr uint32_t kFlashMaxChunks = 16;
+template <int D, int TILE_Q>
+__global__ __launch_bounds__(256) void k_flash_combine(half_t* __restrict__ out, AttnParams p) {
+    constexpr uint32_t G = D / 4;
+    const uint32_t bh = blockIdx.x / p.tiles, tile = blockIdx.x % p.tiles;
+    const uint32_t q_first = tile * TILE_Q;
+    const uint32_t rows = min(uint32_t(TILE_Q), p.q_len - q_first);
+    const uint64_t unit0 = (uint64_t(bh) * p.tiles + tile) * p.kchunks;
+    for (uint32_t it = threadIdx.x; it < rows * G; it += 256) {
+        const uint32_t r = it / G, g = it % G;
+        float2 ml[kFlashMaxChunks];
+        f32x4 oc[kFlashMaxChunks];
+#pragma unroll
+        for (uint32_t c = 0; c < kFlashMaxChunks; ++c) {
+            const uint64_t prow = (unit0 + c) * TILE_Q + r;
+            if (c < p.kchunks) {
+                ml[c] = *reinterpret_cast<const float2*>(p.part_ml + 2 * prow);
+                oc[c] = *reinterpret_cast<const f32x4*>(p.part + prow * D + 4 * g);
+            } else {
+                ml[c] = make_float2(-INFINITY, 0.0f);
+                oc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+        float mmax = -INFINITY;
+#pragma unroll
+        for (uint32_t c = 0; c < kFlashMaxChunks; ++c) mmax = fmaxf(mmax, ml[c].x);
+        float lsum = 0.0f;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t c = 0; c < kFlashMaxChunks; ++c) {
+            const float w = mmax > ml[c].x ? __builtin_amdgcn_exp2f(ml[c].x - mmax) : 1.0f;
+            lsum += w * ml[c].y;
+            acc += w * oc[c];
+        }
+        const float inv = 1.0f / lsum;
+        const h4 o = {half_t(acc[0] * inv), half_t(acc[1] * inv), half_t(acc[2] * inv),
+                      half_t(acc[3] * inv)};
+        *reinterpret_cast<h4*>(out + (uint64_t(bh) * p.q_len + q_first + r) * D + 4 * g) = o;
     }
 }
 
@@ -1465,18 +1544,48 @@ rl_status validate_attention(const rl_buffer* q, const rl_buffer* k, const rl_bu
 // K and V then take 64, 128 and 128 KB of LDS for head sizes 32, 64, 128).
 constexpr int kFlashMaxBlockKeys = 128;
 constexpr int kFlashMaxKeySplit = 4;
-constexpr uint64_t kFlashFillBlocks = 192;  // about 3/4 of the CUs
+constexpr uint64_t kFlashFillBlocks = 192;      // f32: about 3/4 of the CUs
+constexpr uint64_t kFlashFillBlocksF16 = 96;    // f16: wide tiles from here on
 
 // Workgroup shape: 4 query waves x 2 key shares (128-query tiles) while that
-// gives about three quarters of the CUs a workgroup; otherwise 32-query
-// tiles, so that short or few-head prefills spread over more CUs: 1 query
-// wave x 2 key shares, or x 4 when the workgroups are still few or the head
-// is large (96, 128: more waves per workgroup keep all four SIMDs busy).
+// gives enough workgroups (`fill`); otherwise 32-query tiles, so that short
+// or few-head prefills spread over more CUs: 1 query wave x 2 key shares, or
+// x 4 when the workgroups are still few or the head is large (96, 128: more
+// waves per workgroup keep all four SIMDs busy).  f16, same box, all
+// launches of a call inside the events: the wide tiles win from about 96
+// workgroups (15 heads x [2048, 2048] causal 31.8 -> 28.7 us, [3072, 3072]
+// 71.8 -> 37.0, 8 heads x [4096, 4096] 52.1 -> 44.8) and lose below 64
+// (15 heads x [1024, 1024]: 19.1 against 14.2 us for 32-query tiles).
 enum class FlashShape { kWide, kNarrow2, kNarrow4 };
-FlashShape flash_shape(uint64_t heads, uint64_t q_len, uint64_t head_dim) {
-    if (heads * ((ceil_div(q_len, 128) + 1) / 2) >= kFlashFillBlocks) return FlashShape::kWide;
+FlashShape flash_shape(uint64_t heads, uint64_t q_len, uint64_t head_dim, uint64_t fill) {
+    if (heads * ((ceil_div(q_len, 128) + 1) / 2) >= fill) return FlashShape::kWide;
     if (head_dim >= 96 || heads * ((ceil_div(q_len, 32) + 1) / 2) < 256) return FlashShape::kNarrow4;
     return FlashShape::kNarrow2;
+}
+
+// Key chunks per 128-query tile for the f16 kernel (1 = no split), W the
+// wide tile pairs, steps the longest tile's key steps (two blocks each).
+// One workgroup a CU fits (its LDS), so chunks beyond 256 / W workgroups
+// queue behind the first wave: with 96 <= W <= 128 and at least 16 steps,
+// two chunks (8 heads x [4096, 4096] 44.8 -> 41.0 us, 15 heads x 2048
+// queries after 2048 cached keys 61.4 -> 49.4, 32 heads of 128 x 1024 after
+// 3072 105.3 -> 93.1); below 96 pairs only a prefill after cached keys,
+// whose every tile is long, splits, up to 256 / W chunks of two steps or
+// more (15 heads x 512 queries after 3584 keys: 50.4 us on 32-query tiles,
+// 32.7 in 8 chunks; 1024 after 3072: 48.4, 39.2 in 4).  Causal squares
+// with fewer pairs stay on the 32-query tiles (8 heads of 128 x [2048,
+// 2048]: 31.9 us against 43.6 in 4 chunks): each extra chunk writes and
+// merges another f32 copy of the output.
+uint32_t flash_key_chunks(uint64_t heads, uint64_t q_len, uint64_t kv_len, uint64_t start,
+                          uint64_t head_dim) {
+    const uint64_t wide = heads * ((ceil_div(q_len, 128) + 1) / 2);
+    const uint64_t bn = head_dim <= 64 ? 128 : 64;
+    const uint64_t keys = std::min<uint64_t>(kv_len, start + q_len);  // the longest tile's
+    const uint64_t steps = ceil_div(ceil_div(keys, bn), 2);
+    if (wide >= kFlashFillBlocksF16) return wide <= 128 && steps >= 16 ? 2 : 1;
+    if (start == 0 || steps < 16) return 1;
+    const uint64_t chunks = std::min<uint64_t>({256 / wide, 8, steps / 2});
+    return uint32_t(std::max<uint64_t>(chunks, 1));
 }
 
 // The matrix-core kernels by head size: f16 in key blocks of 128 (head
@@ -1501,6 +1610,26 @@ void launch_flash(rl_context* ctx, dim3 g, uint32_t nt, const half_t* q, const h
         }
     }
 }
+// The wide f16 kernel over key chunks (PARTIAL), then the merge.
+void launch_flash_split(rl_context* ctx, uint64_t heads, uint32_t nt, const half_t* q,
+                        const half_t* k, const half_t* v, half_t* o, const AttnParams& p) {
+    const dim3 g(static_cast<unsigned>(heads * p.pairs * p.kchunks)), b(64 * 4 * 2);
+    const dim3 gc(static_cast<unsigned>(heads * p.tiles)), bc(256);
+    if (nt == 1) {
+        RL_LAUNCH(ctx, (k_flash_attention<1, 4, 2, 128, true, true>), g, b, q, k, v, o, p);
+        RL_LAUNCH(ctx, (k_flash_combine<32, 128>), gc, bc, o, p);
+    } else if (nt == 2) {
+        RL_LAUNCH(ctx, (k_flash_attention<2, 4, 2, 128, true, true>), g, b, q, k, v, o, p);
+        RL_LAUNCH(ctx, (k_flash_combine<64, 128>), gc, bc, o, p);
+    } else if (nt == 3) {
+        RL_LAUNCH(ctx, (k_flash_attention<3, 4, 2, 64, false, true>), g, b, q, k, v, o, p);
+        RL_LAUNCH(ctx, (k_flash_combine<96, 128>), gc, bc, o, p);
+    } else {
+        RL_LAUNCH(ctx, (k_flash_attention<4, 4, 2, 64, true, true>), g, b, q, k, v, o, p);
+        RL_LAUNCH(ctx, (k_flash_combine<128, 128>), gc, bc, o, p);
+    }
+}
+
 template <int QW, int KS>
 void launch_flash(rl_context* ctx, dim3 g, uint32_t nt, const float* q, const float* k,
                   const float* v, float* o, const AttnParams& p) {
@@ -1723,7 +1852,32 @@ rl_status attention_entry(rl_context* ctx, const char* name, const rl_buffer* q,
         return st;
     }
     if (flash) {
-        const FlashShape shape = flash_shape(heads, s.q_len, s.head_dim);
+        if constexpr (std::is_same<T, half_t>::value) {
+            // Too few 128-query tile pairs to fill the CUs: keep the wide
+            // tiles and split each tile's key steps over workgroups
+            // (chunked prefill, short or few-head prefills), the pool holding
+            // the partials (not while a graph records, nor for the
+            // allocation-free entry).
+            const uint32_t chunks = flash_key_chunks(heads, s.q_len, s.kv_len, start, s.head_dim);
+            if (chunks > 1 && mode == DecodeScratch::kPool && !ctx->capturing) {
+                p.tiles = uint32_t(ceil_div(s.q_len, 128));
+                p.pairs = (p.tiles + 1) / 2;
+                p.kchunks = chunks;
+                const uint64_t units = heads * p.tiles * chunks * 128;
+                void* part = nullptr;
+                if (rl_status st = ctx->pool.allocate(units * (s.head_dim + 2) * sizeof(float), &part))
+                    return st;
+                p.part = static_cast<float*>(part);
+                p.part_ml = p.part + units * s.head_dim;
+                launch_flash_split(ctx, heads, uint32_t(s.head_dim / 32), qd, kd, vd, od, p);
+                const rl_status st = after_launch(ctx, name);
+                ctx->pool.release(part);  // stream-ordered: later users run after these launches
+                return st;
+            }
+        }
+        const FlashShape shape =
+            flash_shape(heads, s.q_len, s.head_dim,
+                        sizeof(T) == 2 ? kFlashFillBlocksF16 : kFlashFillBlocks);
         p.tiles = uint32_t(ceil_div(s.q_len, shape == FlashShape::kWide ? 128 : 32));
         p.pairs = (p.tiles + 1) / 2;
         const uint64_t grid = heads * p.pairs;

@@ -66,6 +66,13 @@ SHAPES = [
     (1, 2, 1, 33, 40, 40, 48, 7),        # head size off the matrix-core path
     (1, 2, 2, 17, 17, 20, 80, 0),
     (1, 2, 1, 9, 300, 300, 256, 291),
+    # f16: too few 128-query tile pairs, the key steps split over workgroups
+    # (partials merged by a second kernel)
+    (1, 15, 5, 512, 4096, 4096, 64, 3584),   # 8 key chunks: prefill after cached keys
+    (1, 48, 8, 512, 2048, 2048, 128, 1536),  # 96 tile pairs, D 128: 2 key chunks
+    (1, 6, 2, 256, 4096, 4096, 96, 3840),    # D 96 (register-staged blocks), 8 chunks
+    (1, 4, 2, 300, 5000, 5000, 32, 4700),    # D 32, ragged query tile and key count
+    (2, 4, 4, 200, 4100, 4160, 64, 3900),    # batch 2, cache rows past kv_len hold NaN
 ]
 
 # Few query rows per KV head over long key ranges: the split-key path
