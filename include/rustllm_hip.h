@@ -466,7 +466,11 @@ rl_status rl_embedding_f16(rl_context* ctx, const rl_buffer* weight, uint64_t vo
  * the scale/mask checks); also rejected: kv_capacity < kv_len and
  * head_dim > 512 when the matrix-core path (f16, head_dim 32/64/96/128)
  * does not apply.  Results differ from the four separate calls by their
- * intermediate roundings: scores and probabilities stay in f32 here. */
+ * intermediate roundings: scores and probabilities stay in f32 here.  f16
+ * launches with few 128-query tiles and long key ranges (a prefill after
+ * cached keys) split each tile's keys over workgroups: f32 partials in a
+ * pool block, merged by a second kernel (not while a graph records, where
+ * the one-pass kernels run). */
 rl_status rl_attention_f32(rl_context* ctx, const rl_buffer* q, const rl_buffer* k,
                            const rl_buffer* v, uint64_t batch, uint64_t q_heads,
                            uint64_t kv_heads, uint64_t q_len, uint64_t kv_len, uint64_t head_dim,
