@@ -1453,7 +1453,7 @@ def main():
     side = os.path.relpath(args.per_op_out, ROOT) if rows else None
 
     sm_traffic = measured_traffic("attention_softmax_f16 [15,4096,4096] causal")
-    roofline = {"bound": "hbm", "kernel": "k_softmax_rows_h2<4, 128, true, false>",
+    roofline = {"bound": "hbm", "kernel": "k_softmax_rows_h2<4, 128, true, false, false>",
                 "op": "causal scale/mask + softmax f16 [15,4096,4096]",
                 "achieved": round(sm_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(sm_gbs / PEAK_GBS, 4), "traffic": sm_traffic,
