@@ -1544,7 +1544,10 @@ rl_status validate_attention(const rl_buffer* q, const rl_buffer* k, const rl_bu
 // K and V then take 64, 128 and 128 KB of LDS for head sizes 32, 64, 128).
 constexpr int kFlashMaxBlockKeys = 128;
 constexpr int kFlashMaxKeySplit = 4;
-constexpr uint64_t kFlashFillBlocks = 192;      // f32: about 3/4 of the CUs
+// f32 (same box, all launches inside the events): the 32-query tiles win up to
+// at least 128 pairs (8 heads x [4096, 4096]: 203 against 308 us), the wide
+// tiles at 180 (15 heads x [3072, 3072]: 240 against 281 us)
+constexpr uint64_t kFlashFillBlocks = 180;
 constexpr uint64_t kFlashFillBlocksF16 = 96;    // f16: wide tiles from here on
 
 // Workgroup shape: 4 query waves x 2 key shares (128-query tiles) while that
