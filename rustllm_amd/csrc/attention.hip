@@ -1544,7 +1544,7 @@ rl_status validate_attention(const rl_buffer* q, const rl_buffer* k, const rl_bu
 // K and V then take 64, 128 and 128 KB of LDS for head sizes 32, 64, 128).
 constexpr int kFlashMaxBlockKeys = 128;
 constexpr int kFlashMaxKeySplit = 4;
-// f32 (same box, all launches inside the events): the 32-query tiles win up to
+// f32 (one MI355X, all launches inside the events): the 32-query tiles win up to
 // at least 128 pairs (8 heads x [4096, 4096]: 203 against 308 us), the wide
 // tiles at 180 (15 heads x [3072, 3072]: 240 against 281 us)
 constexpr uint64_t kFlashFillBlocks = 180;
@@ -1554,7 +1554,7 @@ constexpr uint64_t kFlashFillBlocksF16 = 96;    // f16: wide tiles from here on
 // gives enough workgroups (`fill`); otherwise 32-query tiles, so that short
 // or few-head prefills spread over more CUs: 1 query wave x 2 key shares, or
 // x 4 when the workgroups are still few or the head is large (96, 128: more
-// waves per workgroup keep all four SIMDs busy).  f16, same box, all
+// waves per workgroup keep all four SIMDs busy).  f16, one MI355X, all
 // launches of a call inside the events: the wide tiles win from about 96
 // workgroups (15 heads x [2048, 2048] causal 31.8 -> 28.7 us, [3072, 3072]
 // 71.8 -> 37.0, 8 heads x [4096, 4096] 52.1 -> 44.8) and lose below 64

@@ -73,7 +73,7 @@ struct CopyOp {  // cast.metal:10,18: the conversion happens on store/load
 // Launch shape of each op: 16-byte packs per thread and the store kind.
 // Measured on [4096, 1536] ([4096, 2560] for f16 SwiGLU) over 128-1024
 // threads per block x 1, 2, 4 packs per thread x non-temporal / plain
-// stores, two boxes agreeing within 1.5 points: about four loads in flight
+// stores, two MI355X hosts agreeing within 1.5 points: about four loads in flight
 // per thread pays where the math is light (f16 add 62% -> 69% of HBM peak,
 // f16 -> f32 cast 62% -> 71%, f32 SiLU 67% -> 72%), while the exp/rcp-heavy
 // f16 SwiGLU is best at one pack per thread.
@@ -108,7 +108,7 @@ struct MapShape<SiluF32Op, TIn, TOut> {
     static constexpr bool phased = false;
     static constexpr bool nt_store = true;
 };
-// Phased (loads, results, stores), four packs a thread: same-box back to
+// Phased (loads, results, stores), four packs a thread: one MI355X, back to
 // back, [4096, 1536] 5.84 us at two packs -> 5.55 us (eight: 7.0), [4096,
 // 2560] 9.16 -> 8.45 us; storing each pack as soon as it is computed is no
 // faster (5.85 at two, 5.44 at four).

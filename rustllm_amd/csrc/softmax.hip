@@ -348,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_h2(const half_t* __re
                 // first and last 128-byte lines with the next and previous
                 // wave loads, which then hit in L2 ([15, 4093, 4093]
                 // 149.6 -> 148.3 us, 4090 keys 139.3 -> 136.7, 4095 keys
-                // 151.8 -> 150.1, same box; streamed loads re-fetch them).
+                // 151.8 -> 150.1, one MI355X; streamed loads re-fetch them).
                 const uint64_t off = e0 + uint64_t(q) * N;
                 moved[k] = off + N > total;  // the buffer's last pack
                 raw[k] = load_u<half_t, N>(in + (moved[k] ? total - N : off));
