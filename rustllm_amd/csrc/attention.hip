@@ -526,20 +526,26 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void k_flash_attention(
 // every chunk's (max m_c, sum l_c, unnormalised output o_c) rescaled to the
 // largest max M, out = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c (the
 // key-share merge of the kernel itself, over kchunks <= kFlashMaxChunks).
-// Workgroup = one query tile of a head; thread item = (query, 4 head
-// elements), 16-byte pieces of a row on consecutive lanes.  Every chunk's
-// loads are issued before any is used.  Some chunk holds key 0, which every
-// query sees, so M is finite.
+// Workgroup = kCombineRows queries of a tile of a head (many workgroups: the
+// merge is a short dependent chain of loads per query); thread item =
+// (query, 4 head elements), 16-byte pieces of a row on consecutive lanes.
+// Every chunk's loads are issued before any is used.  Some chunk holds key
+// 0, which every query sees, so M is finite.
 constexpr uint32_t kFlashMaxChunks = 16;
+constexpr uint32_t kCombineRows = 16;
 template <int D, int TILE_Q>
 __global__ __launch_bounds__(256) void k_flash_combine(half_t* __restrict__ out, AttnParams p) {
     constexpr uint32_t G = D / 4;
-    const uint32_t bh = blockIdx.x / p.tiles, tile = blockIdx.x % p.tiles;
+    constexpr uint32_t PARTS = TILE_Q / kCombineRows;
+    const uint32_t part = blockIdx.x % PARTS, unit = blockIdx.x / PARTS;
+    const uint32_t bh = unit / p.tiles, tile = unit % p.tiles;
     const uint32_t q_first = tile * TILE_Q;
-    const uint32_t rows = min(uint32_t(TILE_Q), p.q_len - q_first);
+    const uint32_t r0 = part * kCombineRows;
+    if (q_first + r0 >= p.q_len) return;
+    const uint32_t rows = min(kCombineRows, p.q_len - q_first - r0);
     const uint64_t unit0 = (uint64_t(bh) * p.tiles + tile) * p.kchunks;
     for (uint32_t it = threadIdx.x; it < rows * G; it += 256) {
-        const uint32_t r = it / G, g = it % G;
+        const uint32_t r = r0 + it / G, g = it % G;
         float2 ml[kFlashMaxChunks];
         f32x4 oc[kFlashMaxChunks];
 #pragma unroll
@@ -1569,16 +1575,17 @@ FlashShape flash_shape(uint64_t heads, uint64_t q_len, uint64_t head_dim, uint64
 // Key chunks per 128-query tile for the f16 kernel (1 = no split), W the
 // wide tile pairs, steps the longest tile's key steps (two blocks each).
 // One workgroup a CU fits (its LDS), so chunks beyond 256 / W workgroups
-// queue behind the first wave: with 96 <= W <= 128 and at least 16 steps,
-// two chunks (8 heads x [4096, 4096] 44.8 -> 41.0 us, 15 heads x 2048
-// queries after 2048 cached keys 61.4 -> 49.4, 32 heads of 128 x 1024 after
-// 3072 105.3 -> 93.1); below 96 pairs only a prefill after cached keys,
-// whose every tile is long, splits, up to 256 / W chunks of two steps or
-// more (15 heads x 512 queries after 3584 keys: 50.4 us on 32-query tiles,
-// 32.7 in 8 chunks; 1024 after 3072: 48.4, 39.2 in 4).  Causal squares
-// with fewer pairs stay on the 32-query tiles (8 heads of 128 x [2048,
-// 2048]: 31.9 us against 43.6 in 4 chunks): each extra chunk writes and
-// merges another f32 copy of the output.
+// queue behind the first wave.  One MI355X, every launch of a call inside
+// the events, against what the shape took unsplit: with 96 <= W <= 128 and
+// at least 16 steps two chunks (8 heads x [4096, 4096] 45.0 -> 39.5 us on the
+// wide tiles, 15 heads x 2048 queries after 2048 cached keys 61.3 -> 47.8,
+// 32 heads of 128 x 1024 after 3072 105.8 -> 87.6); below 96 pairs only a
+// prefill after cached keys, whose every tile is long, splits, up to 256 / W
+// chunks of two steps or more (15 heads x 512 queries after 3584 keys: 51.1
+// us on 32-query tiles, 25.5 in 8 chunks; 1024 after 3072: 49.1, 34.2 in 4).
+// Causal squares with fewer pairs stay on the 32-query tiles (8 heads of 128
+// x [2048, 2048]: 31.8 us against 34.0 in 4 chunks; 15 x [1024, 1024]: 14.0
+// against 20.1): each chunk writes and merges another f32 copy of the output.
 uint32_t flash_key_chunks(uint64_t heads, uint64_t q_len, uint64_t kv_len, uint64_t start,
                           uint64_t head_dim) {
     const uint64_t wide = heads * ((ceil_div(q_len, 128) + 1) / 2);
@@ -1617,7 +1624,7 @@ void launch_flash(rl_context* ctx, dim3 g, uint32_t nt, const half_t* q, const h
 void launch_flash_split(rl_context* ctx, uint64_t heads, uint32_t nt, const half_t* q,
                         const half_t* k, const half_t* v, half_t* o, const AttnParams& p) {
     const dim3 g(static_cast<unsigned>(heads * p.pairs * p.kchunks)), b(64 * 4 * 2);
-    const dim3 gc(static_cast<unsigned>(heads * p.tiles)), bc(256);
+    const dim3 gc(static_cast<unsigned>(heads * p.tiles * (128 / kCombineRows))), bc(256);
     if (nt == 1) {
         RL_LAUNCH(ctx, (k_flash_attention<1, 4, 2, 128, true, true>), g, b, q, k, v, o, p);
         RL_LAUNCH(ctx, (k_flash_combine<32, 128>), gc, bc, o, p);
