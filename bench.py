@@ -228,6 +228,28 @@ def kernel_times_us(ctx, launches, reps, batch=True):
         len(launches) + reps
 
 
+def call_times_us(ctx, calls, reps, groups=3):
+    """Time per call of `reps` calls back to back (cycling through `calls`),
+    events recorded on the context's stream around each group of them: for
+    entry points that may enqueue more than one kernel (the per-launch stamps
+    of kernel_times_us see only the first)."""
+    for fn in calls:
+        fn()
+    ctx.finish()
+    out = []
+    for _ in range(groups):
+        start, stop = ctx.event(), ctx.event()
+        ctx.record(start)
+        for i in range(reps):
+            calls[i % len(calls)]()
+        ctx.record(stop)
+        ctx.finish()
+        out.append(ctx.elapsed_ms(start, stop) * 1e3 / reps)
+        ctx.destroy_event(start)
+        ctx.destroy_event(stop)
+    return out, None
+
+
 def graph_batch_us(ctx, launches, min_per_graph=32, replays=8):
     """us per launch of back-to-back launches replayed as a graph: one launch
     on each of the op's buffer sets (>= 1 GiB in total, so a replay streams
@@ -518,6 +540,25 @@ def attention_rows(ctx, qh, kvh, hd, tok, reps):
     log(f"    -> {row32['TFLOP/s']} TFLOP/s ({row32['pct_peak_mfma']}% of the dense f32 peak)")
     rows.append(row32)
     del sets32
+    # a prefill of 512 tokens after 4096 - 512 cached ones (f16, the layer's K
+    # and V): few 128-query tiles, so each tile's keys are split over
+    # workgroups and merged by a second kernel; timed per whole call
+    pre = tok // 8
+    qp = synth.normal(synth.seed_for("c5", "attn-q-prefill"), (1, qh, pre, hd), 0, 1, F16)
+    psets = [(ctx.upload(qp), ctx.empty(qp.shape, F16)) for _ in range(2)]
+    pflops = attention_flops(qh, pre, tok, hd, tok - pre)
+    rowp = op_row(f"layer.4 attention_f16 prefill of {pre} tokens after {tok - pre} cached "
+                  "(key chunks, every launch of a call timed)", "f16", [1, qh, pre, hd],
+                  (2 * qp.size + 2 * k.size) * 2,
+                  call_times_us(ctx, [lambda s=s: ctx.attention(s[0], sets[0][1], sets[0][2], 0.125,
+                                                                 tok - pre, None, s[1])
+                                      for s in psets], reps))
+    rowp.update({"flops": pflops, "TFLOP/s": round(pflops / (rowp["us"] * 1e-6) / 1e12, 1),
+                 "pct_peak_mfma": round(100 * pflops / (rowp["us"] * 1e-6) / 1e12 /
+                                        PEAK_F16_TFLOPS, 1)})
+    log(f"    -> {rowp['TFLOP/s']} TFLOP/s ({rowp['pct_peak_mfma']}% of the dense f16 peak)")
+    rows.append(rowp)
+    del psets
     # the reference's calls: scores written (503 MB), softmaxed, read back
     n_scores = qh * tok * tok
     unmasked = qh * (tok * (tok + 1) // 2)
