@@ -531,6 +531,21 @@ def test_fused_softmax_smollm_layer_f16(ctx):
         assert not got[h][upper].any()
 
 
+@pytest.mark.parametrize("dtype,scale", [(np.float32, 0.125), (np.float16, 0.1)])
+def test_fused_softmax_streamed_rows(ctx, dtype, scale):
+    """Rows on the 16-byte grid are read plainly when a launch reads at most
+    160 MB of kept keys and streamed above: 2048 queries after 2048 cached
+    keys over 15 heads keep 377 MB (f32) / 189 MB (f16) -- the streamed
+    variants of the row kernel (f32) and of the f16 rows at a scale that is
+    not an f16 value (0.1), against the oracle."""
+    rng = np.random.default_rng(synth.seed_for("streamed-rows", np.dtype(dtype).name))
+    x = rng.standard_normal((15, 2048, 4096), dtype=np.float32).astype(dtype)
+    d = ctx.upload(x)
+    got = run(ctx, lambda: ctx.attention_softmax(d, scale, 2048)).numpy()
+    del d
+    check_float(got, o.attention_softmax(x, scale, 2048), f"streamed rows {np.dtype(dtype).name}")
+
+
 # ------------------------------------------------------------------- RoPE
 
 @pytest.mark.parametrize("dtype", DT)
