@@ -118,6 +118,27 @@ struct MapShape<SiluF16Op, TIn, TOut> {
     static constexpr bool phased = true;
     static constexpr bool nt_store = true;
 };
+// A second launch shape for the large launches of an op, from `from_packs`
+// packs on (0: none).  f16 SwiGLU, one MI355X, back to back over 16 rotated
+// buffer sets, bit-identical: [4096, 2560] (1,310,720 packs) 12.0 us at one
+// pack a thread -> 11.4-11.55 us phased at four packs with plain stores
+// (three: 11.8-12.0, six: 12.6, eight: 12.3-12.5; four with streamed stores:
+// 12.2-12.3); [4096, 1536] (786,432 packs) 8.1 -> 8.1-8.3 us, so the
+// one-pack shape stays below 2^20 packs.
+template <typename Op, typename TIn, typename TOut>
+struct MapShapeBig {
+    static constexpr uint64_t from_packs = 0;
+    static constexpr int unroll = 1;
+    static constexpr bool nt_store = true;
+    static constexpr bool phased = false;
+};
+template <>
+struct MapShapeBig<SwigluF16Op, half_t, half_t> {
+    static constexpr uint64_t from_packs = uint64_t(1) << 20;
+    static constexpr int unroll = 4;
+    static constexpr bool nt_store = false;
+    static constexpr bool phased = true;
+};
 template <>
 struct MapShape<CopyOp, half_t, float> {  // widening cast: 8-byte loads
     static constexpr int unroll = 4;
@@ -530,6 +551,13 @@ rl_status launch_map(rl_context* ctx, const char* name, const void* a, const voi
             f.write[1] = uintptr_t(po) + n * sizeof(TOut);
             if (rl_status st = defer_fused(ctx, f)) return st;
             return after_launch(ctx, name);
+        }
+        using Big = MapShapeBig<Op, TIn, TOut>;
+        if constexpr (Big::from_packs != 0) {
+            if (n_packs >= Big::from_packs) {
+                RL_LAUNCH(ctx, (k_map<TIn, TOut, N, Big::unroll, ARITY, Big::nt_store, Big::phased, Op>), dim3(grid_for(n_packs, uint64_t(kThreads) * Big::unroll)), dim3(kThreads), pa, pb, po, n_packs, tail, op);
+                return after_launch(ctx, name);
+            }
         }
         RL_LAUNCH(ctx, (k_map<TIn, TOut, N, UNROLL, ARITY, NTS, PHASED, Op>), dim3(grid), dim3(kThreads), pa, pb, po, n_packs, tail, op);
     } else {

@@ -134,6 +134,26 @@ def test_silu_f16_in_place(ctx, n):
     ctx.graph_destroy(graph)
 
 
+@pytest.mark.parametrize("n", [8 << 20, 8 * ((1 << 20) + 1000) + 5, 4096 * 2560])
+def test_swiglu_f16_large_launch_shape(ctx, n):
+    """SwiGLU f16 from 2^20 packs of 8 on runs four packs a thread in three
+    phases (clamped loads, results, stores of owned packs only): at an exact
+    multiple of the block's packs, with a partial last block plus 5 elements
+    past the last pack, and at the layer's [4096, 2560] -- out of place and
+    written over the gate and over the up operand, each within 2 ulp of the
+    oracle."""
+    g = norm(("swiglu-big", "g"), (n,), np.float16, 0.0, 3.0)
+    u = norm(("swiglu-big", "u"), (n,), np.float16, 0.0, 2.0)
+    ref = o.swiglu(g, u)
+    dg, du = ctx.upload(g), ctx.upload(u)
+    check_float(run(ctx, lambda: ctx.swiglu(dg, du)).numpy(), ref, f"swiglu n={n}")
+    run(ctx, lambda: ctx.swiglu(dg, du, dg))
+    check_float(dg.numpy(), ref, f"swiglu over gate n={n}")
+    dg = ctx.upload(g)
+    run(ctx, lambda: ctx.swiglu(dg, du, du))
+    check_float(du.numpy(), ref, f"swiglu over up n={n}")
+
+
 def test_silu_swiglu_f16_every_half(ctx):
     """SiLU over all 65,536 halves (incl. +-inf, NaN, subnormals and the range
     where the sigmoid's reciprocal is subnormal), and SwiGLU with every half as
