@@ -76,7 +76,7 @@ struct CopyOp {  // cast.metal:10,18: the conversion happens on store/load
 // stores, two MI355X hosts agreeing within 1.5 points: about four loads in flight
 // per thread pays where the math is light (f16 add 62% -> 69% of HBM peak,
 // f16 -> f32 cast 62% -> 71%, f32 SiLU 67% -> 72%), while the exp/rcp-heavy
-// f16 SwiGLU is best at one pack per thread.
+// f16 SwiGLU is best at one pack per thread (below 2^20 packs: MapShapeBig).
 template <typename Op, typename TIn, typename TOut>
 struct MapShape {
     static constexpr int unroll = 1;
